@@ -1,0 +1,225 @@
+"""Benchmark: the 128->128 fp16 SubMConv3d layer over 500k surface voxels.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+One step is one forward of the layer over the whole batch, with its indice
+pairs cached under its ``indice_key`` (as a network reuses them), inputs
+already resident in HBM.  The pair build, the execution-order plan and the
+fused conv kernel are also timed on their own with HIP events on the stream
+they run on.  Prints ONE JSON line:
+  value         voxels/s of the layer (N_in / step time)
+  roofline      the conv kernel against MI355X's dense fp16 MFMA peak
+  cpu_baseline  the CPU oracle (a numpy port of the reference's CPU path)
+                timed on this host on the same workload
+Other workloads (``--workload``) are for exploration; the default is the one
+the headline metric is quoted on.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK = {  # MI355X published dense peaks
+    "float16": (2500.0, "TFLOP/s"), "bfloat16": (2500.0, "TFLOP/s"),
+    "float32": (157.3, "TFLOP/s"),
+}
+HBM_PEAK_GBS = 8000.0
+DTYPE_TAG = {"float32": "f32", "float16": "f16", "bfloat16": "bf16"}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="subm128_surface500k")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--verbose", action="store_true")
+    return ap.parse_args()
+
+
+def log(args, *a):
+    if args.verbose:
+        print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(w, feats, weight, bias, layer):
+    """Oracle (numpy port of the reference CPU path) on the whole workload, once."""
+    from oracle import conv as OC
+    from oracle import pairs as OP
+    try:
+        from threadpoolctl import threadpool_limits, threadpool_info
+    except ImportError:  # pragma: no cover
+        threadpool_limits = None
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    ctx = threadpool_limits(cores) if threadpool_limits else None
+    try:
+        t0 = time.perf_counter()
+        pr = OP.subm_pairs(w.indices, w.spatial_shape, w.batch_size, layer["kernel_size"],
+                           layer["dilation"])
+        t1 = time.perf_counter()
+        Wk = OC.normalize_weight(weight, layer["kernel_size"], layer["c_in"], layer["c_out"])
+        OC.conv_forward(feats, Wk, bias, pr.pairs_in, pr.pairs_out, len(w.indices), np.float32)
+        t2 = time.perf_counter()
+    finally:
+        if ctx is not None:
+            ctx.unpack() if hasattr(ctx, "unpack") else None
+    n = len(w.indices)
+    return {
+        "value": n / (t2 - t1), "unit": "voxels/s", "cores": cores, "kind": "port",
+        "sample": (f"whole workload once ({n} voxels, fp32 accumulate; numpy restatement of "
+                   "indices.py dense-table pair build + functional.py slot loop)"),
+        "pair_build_ms": (t1 - t0) * 1e3, "conv_ms": (t2 - t1) * 1e3,
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the sparse-conv path here runs on a single MI355X)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import trispconv.pytorch as spconv
+    from trispconv.pytorch import functional as Fn
+    from trispconv.pytorch.indices import generate_subm_indice_pairs, generate_strided_indice_pairs
+    from trispconv_amd import workloads
+
+    dev = torch.device("cuda:0")
+    w = workloads.make_workload(args.workload)
+    layer = w.layers[0]
+    dt = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}[w.dtype]
+    rng = np.random.default_rng(w.seed)
+    feats_np = workloads.features(rng, len(w.indices), layer["c_in"])
+    w_np, b_np = workloads.layer_params(rng, layer)
+    n_in = len(w.indices)
+
+    idx = torch.from_numpy(w.indices).to(dev)
+    feats = torch.from_numpy(feats_np).to(dev).to(dt)
+    key = "bench"
+    if layer["kind"] == "subm":
+        mod = spconv.SubMConv3d(layer["c_in"], layer["c_out"], layer["kernel_size"],
+                                dilation=layer["dilation"], indice_key=key)
+    else:
+        mod = spconv.SparseConv3d(layer["c_in"], layer["c_out"], layer["kernel_size"],
+                                  stride=layer["stride"], padding=layer["padding"],
+                                  dilation=layer["dilation"], indice_key=key)
+    with torch.no_grad():
+        mod.weight.copy_(torch.from_numpy(w_np))
+        mod.bias.copy_(torch.from_numpy(b_np))
+    mod = mod.to(dev).to(dt)
+    stream = torch.cuda.current_stream(dev)
+
+    def build_pairs():
+        if layer["kind"] == "subm":
+            return generate_subm_indice_pairs(idx, w.spatial_shape, w.batch_size,
+                                              layer["kernel_size"], layer["dilation"])
+        return generate_strided_indice_pairs(idx, w.spatial_shape, w.batch_size,
+                                             layer["kernel_size"], layer["stride"],
+                                             layer["padding"], layer["dilation"])
+
+    def event_ms(fn, reps):
+        """Median over reps of the stream time between events around fn()."""
+        times = []
+        for _ in range(reps):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            fn()
+            b.record(stream)
+            b.synchronize()
+            times.append(a.elapsed_time(b))
+        return float(np.median(times))
+
+    # ---- pair build (includes its one count read-back) and plan
+    for _ in range(2):
+        build_pairs()
+    pair_ms = event_ms(build_pairs, 10)
+    data = build_pairs()
+    n_out = len(data.out_indices)
+
+    def plan():
+        data._order = None
+        data.execution_order(n_out, dev)
+    plan()
+    plan_ms = event_ms(plan, 10)
+    P = int(data.pair_num.sum())
+    log(args, f"pairs P={P} n_out={n_out} pair_ms={pair_ms:.3f} plan_ms={plan_ms:.3f}")
+
+    # ---- the timed step: the layer with cached pairs
+    x = spconv.SparseConvTensor(feats, idx, list(w.spatial_shape), w.batch_size)
+    x.indice_dict[key] = data
+    packed = mod._packed_weight(dt)
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            y = mod(x)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            y = mod(x)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    step_ms = (t1 - t0) * 1e3 / args.steps
+
+    # ---- the conv kernel alone, HIP events on its stream
+    nbr = data.neighbour_map(n_out, dev)
+    order = data.execution_order(n_out, dev)
+    kern_ms = event_ms(lambda: Fn._run(feats, packed, mod.bias, nbr, order, n_out), 20)
+    flops = 2.0 * P * layer["c_in"] * layer["c_out"]
+    tflops = flops / (kern_ms * 1e-3) / 1e12
+    peak, unit = PEAK[w.dtype]
+    elem = 4 if w.dtype == "float32" else 2
+    # algorithmic bytes of one launch: input rows read once, output written
+    # once, the neighbour map and the order read once, the packed weight once
+    k_vol = int(np.prod(layer["kernel_size"]))
+    alg_bytes = (n_in * layer["c_in"] * elem + n_out * layer["c_out"] * elem
+                 + n_out * k_vol * 4 + n_out * 4 + k_vol * layer["c_in"] * layer["c_out"] * elem)
+
+    result = {
+        "metric": "voxels/sec + effective TFLOP/s per SubMConv3d layer; indice-pair build ms",
+        "value": n_in / (step_ms * 1e-3),
+        "unit": "voxels/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": step_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": DTYPE_TAG[w.dtype],
+        "data": "synthetic (seeded surface voxels, N(0,1) features, kaiming-uniform KRSC weights)",
+        "config": {"workload": w.name, "layer": f"{layer['kind']} {layer['kernel_size']} "
+                   f"{layer['c_in']}->{layer['c_out']}", "voxels": n_in,
+                   "spatial_shape": list(w.spatial_shape), "batch": w.batch_size, "pairs": P},
+        "tflops_effective": flops / (step_ms * 1e-3) / 1e12,
+        "pair_build_ms": pair_ms,
+        "plan_ms": plan_ms,
+        "conv_kernel_ms": kern_ms,
+        "roofline": {"bound": "mfma" if elem == 2 else "mfma", "achieved": tflops, "peak": peak,
+                     "unit": unit, "frac": tflops / peak, "traffic": None,
+                     "algorithmic_bytes": alg_bytes,
+                     "kernel": "conv_mfma_kernel" if elem == 2 else "conv_valu_kernel"},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(w, rounded(feats_np, dt), rounded(w_np, dt),
+                                              rounded(b_np, dt), layer)
+    print(json.dumps(result), flush=True)
+
+
+def rounded(a, dt):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dt).float().numpy()
+
+
+if __name__ == "__main__":
+    main()

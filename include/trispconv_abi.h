@@ -1,0 +1,153 @@
+/*
+ * trispconv_abi.h — C ABI of libtrispconv_hip.so, the MI355X (gfx950) backend
+ * behind the unchanged `trispconv.pytorch` API.
+ *
+ * Conventions
+ *   - Every pointer is caller-owned device memory (a torch tensor's data_ptr)
+ *     unless the comment says "host".  The library allocates nothing: each
+ *     builder has a *_workspace_bytes query and the caller passes that much
+ *     scratch.
+ *   - `stream` is a hipStream_t (torch.cuda.current_stream().cuda_stream).
+ *     All work is enqueued on it; no entry point synchronises.
+ *   - Return value: 0 = success, > 0 = invalid argument (message in
+ *     tsc_last_error()), < 0 = -(hipError_t) of a failed launch.
+ *   - Coordinates are int32 rows (b, z, y, x).  A slot k numbers the kernel
+ *     offsets (kz, ky, kx) lexicographically: k = (kz*kH + ky)*kW + kx.
+ *   - Pair tables are "padded": slot k owns entries [k*cap, k*cap + cnt[k]).
+ *   - A neighbour map `nbr` is [n_out][K] int32: the input row that feeds
+ *     output row o through slot k, or -1.
+ *
+ * Re-entrant; the only global state is the thread-local error string.
+ */
+#ifndef TRISPCONV_ABI_H
+#define TRISPCONV_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(__GNUC__)
+#define TSC_API __attribute__((visibility("default")))
+#else
+#define TSC_API
+#endif
+
+typedef void* tsc_stream_t; /* hipStream_t */
+
+enum tsc_status { TSC_OK = 0, TSC_EINVAL = 1, TSC_ERANGE = 2, TSC_EUNSUPPORTED = 3 };
+enum tsc_dtype { TSC_F32 = 0, TSC_F16 = 1, TSC_BF16 = 2 };
+/* bits of the device-side status word written by the builders */
+enum tsc_flags { TSC_FLAG_COORD_OUT_OF_GRID = 1, TSC_FLAG_BATCH_OUT_OF_RANGE = 2 };
+
+/* Thread-local description of the last non-zero return. */
+TSC_API const char* tsc_last_error(void);
+/* Bumped whenever a signature below changes. */
+TSC_API int tsc_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * Submanifold pairs.  Replaces generate_subm_indice_pairs
+ * (trispconv/pytorch/indices.py:67-140) including its dense lookup table
+ * (:54-64), which becomes an open-addressing hash of 2N..4N slots.
+ *
+ * Writes nbr [n][K]; pairs_in/pairs_out [K][n] (slot k: output rows r in
+ * ascending order, input row of each, exactly the reference's lists);
+ * counts [K+1]: counts[k] = pairs in slot k, counts[K] = status flags.
+ * ------------------------------------------------------------------------ */
+TSC_API int64_t tsc_subm_workspace_bytes(int64_t n, int32_t k_vol);
+TSC_API int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_size,
+                   const int32_t spatial[3] /* host */, const int32_t ksize[3] /* host */,
+                   const int32_t dilation[3] /* host */, void* ws, int64_t ws_bytes,
+                   int32_t* nbr, int32_t* pairs_in, int32_t* pairs_out, int32_t* counts,
+                   tsc_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Strided pairs.  Replaces generate_strided_indice_pairs
+ * (trispconv/pytorch/indices.py:143-259): candidate generation (:177-195),
+ * unique(sorted) of output keys (:215-229) and the per-slot split (:235-244).
+ * Two phases around the one host read of the counts:
+ *   count: counts [K+2]: counts[k] = pairs in slot k, counts[K] = n_out,
+ *          counts[K+1] = status flags.
+ *   fill:  out_coords [n_out][4] sorted by (b,z,y,x); nbr [n_out][K];
+ *          pairs_in/pairs_out [K][n] (slot k: input rows ascending, output
+ *          rank of each).  The workspace must be the one `count` filled.
+ * ------------------------------------------------------------------------ */
+TSC_API int64_t tsc_strided_workspace_bytes(int64_t n, int32_t k_vol, int32_t batch_size,
+                                    const int32_t out_spatial[3] /* host */);
+TSC_API int tsc_strided_count(const int32_t* coords, int64_t n, int32_t batch_size,
+                      const int32_t spatial[3], const int32_t ksize[3], const int32_t stride[3],
+                      const int32_t padding[3], const int32_t dilation[3],
+                      const int32_t out_spatial[3], void* ws, int64_t ws_bytes, int32_t* counts,
+                      tsc_stream_t stream);
+TSC_API int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_size,
+                     const int32_t spatial[3], const int32_t ksize[3], const int32_t stride[3],
+                     const int32_t padding[3], const int32_t dilation[3],
+                     const int32_t out_spatial[3], void* ws, int64_t ws_bytes, int64_t n_out,
+                     int32_t* out_coords, int32_t* nbr, int32_t* pairs_in, int32_t* pairs_out,
+                     tsc_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Inverse pairs.  Replaces the pair swap of SparseInverseConv3d
+ * (trispconv/pytorch/modules.py:175-212).  Input: the forward layer's padded
+ * tables (cap = forward n_in) and device pair counts.
+ *   count: counts[0] = number of participating forward inputs (= n_out).
+ *   fill:  out_coords [n_out][4] = forward input coords of participating
+ *          rows in ascending row order; nbr [n_out][K];
+ *          inv_pairs_out [K][cap] = compact id of each forward input
+ *          (the inverse's pairs_in are the forward's pairs_out, unchanged).
+ * ------------------------------------------------------------------------ */
+TSC_API int64_t tsc_inverse_workspace_bytes(int64_t n_fwd_in);
+TSC_API int tsc_inverse_count(const int32_t* fwd_pairs_in, const int32_t* fwd_counts, int32_t k_vol,
+                      int64_t cap, int64_t n_fwd_in, void* ws, int64_t ws_bytes, int32_t* counts,
+                      tsc_stream_t stream);
+TSC_API int tsc_inverse_fill(const int32_t* fwd_pairs_in, const int32_t* fwd_pairs_out,
+                     const int32_t* fwd_counts, int32_t k_vol, int64_t cap,
+                     const int32_t* fwd_in_coords, int64_t n_fwd_in, void* ws, int64_t ws_bytes,
+                     int64_t n_out, int32_t* out_coords, int32_t* nbr, int32_t* inv_pairs_out,
+                     tsc_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Execution order for the convolution: output rows sorted (stably) by the
+ * set of slots that feed them, so that rows processed together need the
+ * same weight slices.  No reference counterpart (the reference runs slot
+ * by slot); the order never changes any output value.
+ * ------------------------------------------------------------------------ */
+TSC_API int64_t tsc_plan_workspace_bytes(int64_t n_out, int32_t k_vol);
+TSC_API int tsc_conv_plan(const int32_t* nbr, int64_t n_out, int32_t k_vol, void* ws, int64_t ws_bytes,
+                  int32_t* order, tsc_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Weights.  Replaces normalize_spconv_weight (trispconv/pytorch/weight.py:8-50)
+ * and the fp32 upcast of the GPU branch (functional.py:34-36): reads the
+ * module's parameter and writes the kernel's layout in one pass.
+ *   layout 0 (KRSC):  W[k][ci][co] = w[((co*K + k)*c_in + ci)]
+ *   layout 1 (flat):  W[k][ci][co] = w[((k*c_in + ci)*c_out + co)]
+ *                     (the internal (K, C_in, C_out) layout, and the 1x1x1
+ *                      fold quirk, which re-reads KRSC storage this way)
+ * ------------------------------------------------------------------------ */
+TSC_API int64_t tsc_packed_weight_bytes(int32_t k_vol, int32_t c_in, int32_t c_out, int32_t dtype);
+TSC_API int tsc_pack_weight(const void* w, int32_t w_dtype, int32_t layout, int32_t k_vol, int32_t c_in,
+                    int32_t c_out, int32_t dtype, void* packed, tsc_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Fused gather -> GEMM -> scatter over all slots in one launch.  Replaces
+ * sparse_conv_forward (trispconv/pytorch/functional.py:14-51) and the Triton
+ * per-slot kernel (triton_kernels.py:16-135).  Output-stationary: each
+ * output row accumulates sum_k feat[nbr[o][k]] @ W[k] in fp32 with k
+ * ascending, adds bias in fp32 and is rounded once to `dtype`.  No atomics;
+ * results are bitwise reproducible and independent of `order`.
+ *   nbr == NULL means the identity map with k_vol == 1 (1x1x1 layers).
+ *   order == NULL means rows in index order.
+ *   bias may be NULL; bias_dtype is its element type.
+ * ------------------------------------------------------------------------ */
+TSC_API int tsc_conv_forward(const void* feat, int32_t dtype, int64_t n_in, int32_t c_in,
+                     const void* packed_w, const void* bias, int32_t bias_dtype,
+                     const int32_t* nbr, const int32_t* order, int64_t n_out, int32_t k_vol,
+                     int32_t c_out, void* out, tsc_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TRISPCONV_ABI_H */

@@ -1,0 +1,256 @@
+"""Fused convolution on the GPU against the fp64 oracle.
+
+Tolerance (max |out - ref| / max |ref|, oracle in fp64 over the rounded
+inputs and weights): 1e-5 for fp32, 1e-2 for fp16 and bf16.  Covers the VALU
+and MFMA kernels, every MFMA tile shape, ragged and wide channels, 1x1x1
+layers, the five workloads at full size (checked on a random subset of output
+rows), bitwise determinism and independence from the execution order.
+"""
+import numpy as np
+import pytest
+import torch
+
+import trispconv.pytorch as spconv
+from gpu_util import DEV, lists_np, needs_gpu, oracle_rows, rel_err, rounded, say, to_np
+from oracle import conv as OC
+from oracle import pairs as OP
+from trispconv.pytorch import functional as Fn
+from trispconv.pytorch.indices import generate_strided_indice_pairs, generate_subm_indice_pairs
+from trispconv_amd import workloads
+
+pytestmark = [pytest.mark.gpu, needs_gpu]
+
+TOL = {torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 1e-2}
+
+
+def _module(kind, c_in, c_out, k, s=1, p=0, d=1, key=None, dtype=torch.float32, seed=0, bias=True):
+    torch.manual_seed(seed)
+    if kind == "subm":
+        m = spconv.SubMConv3d(c_in, c_out, k, dilation=d, bias=bias, indice_key=key)
+    elif kind == "strided":
+        m = spconv.SparseConv3d(c_in, c_out, k, stride=s, padding=p, dilation=d, bias=bias,
+                                indice_key=key)
+    else:
+        m = spconv.SparseInverseConv3d(c_in, c_out, k, bias=bias, indice_key=key)
+    if bias:
+        with torch.no_grad():
+            m.bias.uniform_(-0.1, 0.1)
+    return m.to(DEV).to(dtype)
+
+
+def _tiny(seed, shape, B, n):
+    rng = np.random.default_rng(seed)
+    total = shape[0] * shape[1] * shape[2]
+    parts = []
+    for b in range(B):
+        cells = rng.choice(total, size=min(n, total), replace=False)
+        z, r = np.divmod(cells, shape[1] * shape[2])
+        y, x = np.divmod(r, shape[2])
+        parts.append(np.stack([np.full(len(cells), b), z, y, x], 1))
+    idx = np.concatenate(parts).astype(np.int32)
+    return idx[rng.permutation(len(idx))]
+
+
+def _check_layer(m, feats, idx, shape, B, dtype, rows=None, what=""):
+    """Run one subm/strided module on the GPU and compare with the oracle."""
+    say("conv layer:", what, m.__class__.__name__, m.in_channels, "->", m.out_channels, dtype,
+        feats.shape)
+    x = spconv.SparseConvTensor(torch.from_numpy(feats).to(DEV).to(dtype),
+                                torch.from_numpy(idx).to(DEV), list(shape), B)
+    y = m(x)
+    f64 = rounded(feats, dtype)
+    w = OC.normalize_weight(to_np(m.weight).astype(np.float64), m.kernel_size, m.in_channels,
+                            m.out_channels)
+    b = to_np(m.bias).astype(np.float64) if m.bias is not None else None
+    if m.subm:
+        pr = OP.subm_pairs(idx, shape, B, m.kernel_size, m.dilation)
+    else:
+        pr = OP.strided_pairs(idx, shape, B, m.kernel_size, m.stride, m.padding, m.dilation)
+    assert np.array_equal(y.indices.cpu().numpy(), pr.out_indices)
+    n_out = len(pr.out_indices)
+    if rows is None or rows >= n_out:
+        sel = np.arange(n_out)
+    else:
+        sel = np.sort(np.random.default_rng(1).choice(n_out, size=rows, replace=False))
+    ref = oracle_rows(f64, w, b, pr.pairs_in, pr.pairs_out, sel)
+    out = to_np(y.features)[sel]
+    err = rel_err(out, ref)
+    say("   rel err", err)
+    assert y.features.dtype == dtype and y.features.shape == (n_out, m.out_channels)
+    assert np.isfinite(out).all()
+    assert err <= TOL[dtype], f"{what}: rel err {err}"
+    return y
+
+
+# (c_in, c_out, dtype): VALU shapes (narrow / ragged / fp32) and every MFMA tile
+LAYER_CASES = [
+    (16, 16, torch.float32), (4, 6, torch.float32), (5, 7, torch.float32),
+    (16, 32, torch.float16), (4, 16, torch.bfloat16), (3, 8, torch.float16),
+    (32, 32, torch.float16), (32, 64, torch.bfloat16), (64, 32, torch.bfloat16),
+    (64, 64, torch.float16), (96, 96, torch.float16), (128, 128, torch.float16),
+    (128, 128, torch.bfloat16), (256, 128, torch.float16), (64, 256, torch.bfloat16),
+    (160, 192, torch.float16), (64, 64, torch.float32),
+]
+
+
+@pytest.mark.parametrize("c_in,c_out,dtype", LAYER_CASES)
+def test_subm_layer(c_in, c_out, dtype):
+    idx = _tiny(5, (20, 22, 24), 2, 2500)
+    feats = np.random.default_rng(6).standard_normal((len(idx), c_in)).astype(np.float32)
+    m = _module("subm", c_in, c_out, 3, dtype=dtype, seed=c_in + c_out)
+    _check_layer(m, feats, idx, (20, 22, 24), 2, dtype, what=f"subm {c_in}->{c_out}")
+
+
+@pytest.mark.parametrize("c_in,c_out,dtype", [(16, 32, torch.float32), (32, 64, torch.bfloat16),
+                                              (64, 128, torch.float16), (5, 3, torch.float16)])
+@pytest.mark.parametrize("k,s,p", [(3, 2, 1), (2, 2, 0), ((3, 1, 1), (2, 1, 1), 0)])
+def test_strided_layer(c_in, c_out, dtype, k, s, p):
+    idx = _tiny(7, (21, 18, 25), 2, 3000)
+    feats = np.random.default_rng(8).standard_normal((len(idx), c_in)).astype(np.float32)
+    m = _module("strided", c_in, c_out, k, s, p, dtype=dtype, seed=3)
+    _check_layer(m, feats, idx, (21, 18, 25), 2, dtype, what=f"strided {c_in}->{c_out} k{k}")
+
+
+@pytest.mark.parametrize("c_mid,c_out,dtype", [(64, 32, torch.bfloat16), (16, 8, torch.float32),
+                                               (128, 64, torch.float16)])
+def test_inverse_layer(c_mid, c_out, dtype):
+    shape = (16, 20, 18)
+    idx = _tiny(9, shape, 2, 2000)
+    down = _module("strided", c_out, c_mid, 3, 2, 1, key="k", dtype=dtype, seed=1)
+    up = _module("inverse", c_mid, c_out, 3, key="k", dtype=dtype, seed=2)
+    x = spconv.SparseConvTensor(torch.zeros(len(idx), c_out, device=DEV, dtype=dtype),
+                                torch.from_numpy(idx).to(DEV), list(shape), 2)
+    y = down(x)
+    mid = np.random.default_rng(10).standard_normal((len(y.indices), c_mid)).astype(np.float32)
+    z = up(y.replace_feature(torch.from_numpy(mid).to(DEV).to(dtype)))
+    fwd = OP.strided_pairs(idx, shape, 2, 3, 2, 1)
+    inv = OP.inverse_pairs(fwd)
+    assert np.array_equal(z.indices.cpu().numpy(), inv.out_indices)
+    assert z.spatial_shape == list(shape)
+    w = OC.normalize_weight(to_np(up.weight).astype(np.float64), (3, 3, 3), c_mid, c_out)
+    ref = OC.conv_forward(rounded(mid, dtype), w, to_np(up.bias).astype(np.float64),
+                          inv.pairs_in, inv.pairs_out, len(inv.out_indices))
+    err = rel_err(to_np(z.features), ref)
+    say("inverse rel err", err)
+    assert err <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_one_by_one_layers(dtype):
+    """SubM 1x1x1 (fold quirk) and the inverse 1x1x1 shortcut (dense product)."""
+    idx = _tiny(11, (12, 12, 12), 2, 700)
+    feats = np.random.default_rng(12).standard_normal((len(idx), 32)).astype(np.float32)
+    m = _module("subm", 32, 64, 1, dtype=dtype, seed=4)
+    y = _check_layer(m, feats, idx, (12, 12, 12), 2, dtype, what="subm 1x1x1")
+    fold = to_np(m.weight).astype(np.float64).reshape(-1).reshape(32, 64)
+    ref = rounded(feats, dtype) @ fold + to_np(m.bias).astype(np.float64)
+    assert rel_err(to_np(y.features), ref) <= TOL[dtype]
+    # inverse 1x1x1: coordinates and shape of the inverse input
+    down = _module("strided", 32, 64, 1, 2, 0, key="d", dtype=dtype, seed=5)
+    up = _module("inverse", 64, 16, 1, key="d", dtype=dtype, seed=6)
+    x = spconv.SparseConvTensor(torch.from_numpy(feats).to(DEV).to(dtype),
+                                torch.from_numpy(idx).to(DEV), [12, 12, 12], 2)
+    yd = down(x)
+    z = up(yd)
+    assert z.indices is yd.indices and z.spatial_shape == yd.spatial_shape
+    w0 = to_np(up.weight).astype(np.float64).reshape(-1).reshape(64, 16)
+    ref = to_np(yd.features).astype(np.float64) @ w0 + to_np(up.bias).astype(np.float64)
+    assert rel_err(to_np(z.features), ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("c_in,c_out,dtype", [(16, 16, torch.float32), (128, 128, torch.float16),
+                                              (64, 32, torch.bfloat16)])
+def test_deterministic_and_order_independent(c_in, c_out, dtype):
+    idx = _tiny(13, (30, 30, 30), 1, 9000)
+    x = torch.from_numpy(idx).to(DEV)
+    feats = torch.randn(len(idx), c_in, generator=torch.Generator().manual_seed(0)).to(DEV).to(dtype)
+    data = generate_subm_indice_pairs(x, (30, 30, 30), 1, 3)
+    m = _module("subm", c_in, c_out, 3, dtype=dtype, seed=7)
+    pw = m._packed_weight(dtype)
+    a = Fn.sparse_conv_forward(feats, pw, m.bias, data, len(idx))
+    b = Fn.sparse_conv_forward(feats, pw, m.bias, data, len(idx))
+    assert data._order is not None
+    c = Fn._run(feats, pw, m.bias, data.neighbour_map(len(idx), feats.device), None, len(idx))
+    rev = torch.flip(data._order, [0]).contiguous()
+    d = Fn._run(feats, pw, m.bias, data.neighbour_map(len(idx), feats.device), rev, len(idx))
+    assert torch.equal(a, b) and torch.equal(a, c) and torch.equal(a, d)
+
+
+def test_raw_internal_weight_and_user_built_indice_data():
+    """sparse_conv_forward with a (K, C_in, C_out) tensor and hand-made pair lists."""
+    idx = _tiny(14, (10, 10, 10), 1, 300)
+    x = torch.from_numpy(idx).to(DEV)
+    data = generate_subm_indice_pairs(x, (10, 10, 10), 1, 3)
+    feats = torch.randn(len(idx), 8, device=DEV)
+    W = torch.randn(27, 8, 12, device=DEV)
+    out = Fn.sparse_conv_forward(feats, W, None, data, len(idx))
+    from trispconv.pytorch.indices import IndiceData
+    hand = IndiceData(data.out_indices, [p.clone() for p in data.pairs_in],
+                      [p.clone() for p in data.pairs_out], data.pair_num, data.input_indices,
+                      (10, 10, 10), (10, 10, 10), (3, 3, 3), (1, 1, 1), (0, 0, 0), (1, 1, 1), True)
+    out2 = Fn.sparse_conv_forward(feats, W, None, hand, len(idx))
+    assert torch.equal(out, out2)
+    ref = OC.conv_forward(feats.cpu().numpy(), W.cpu().numpy(), None, lists_np(data.pairs_in),
+                          lists_np(data.pairs_out), len(idx))
+    assert rel_err(out.cpu().numpy(), ref) <= 1e-5
+
+
+@pytest.mark.parametrize("name", workloads.WORKLOAD_NAMES)
+def test_full_size_workloads(name):
+    """Each workload at full size, layer by layer on the GPU's own layer inputs."""
+    w = workloads.make_workload(name)
+    dtype = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}[w.dtype]
+    rng = np.random.default_rng(w.seed)
+    idx, shape = w.indices, tuple(w.spatial_shape)
+    feats = workloads.features(rng, len(idx), w.layers[0]["c_in"])
+    fwd_store = {}
+    for li, lay in enumerate(w.layers):
+        m = _module(lay["kind"], lay["c_in"], lay["c_out"], lay["kernel_size"], lay["stride"],
+                    lay["padding"], lay["dilation"], key=lay["indice_key"], dtype=dtype, seed=li)
+        if lay["kind"] == "inverse":
+            x_idx, x_shape, prev = fwd_store[lay["indice_key"]]
+            xin = spconv.SparseConvTensor(torch.from_numpy(feats).to(DEV).to(dtype),
+                                          torch.from_numpy(idx).to(DEV), list(shape), w.batch_size)
+            xin.indice_dict[lay["indice_key"]] = prev
+            y = m(xin)
+            exp_fwd = OP.strided_pairs(x_idx, x_shape, w.batch_size, prev.kernel_size, prev.stride,
+                                       prev.padding, prev.dilation)
+            inv = OP.inverse_pairs(exp_fwd)
+            assert np.array_equal(y.indices.cpu().numpy(), inv.out_indices)
+            sel = np.sort(rng.choice(len(inv.out_indices), size=min(4096, len(inv.out_indices)),
+                                     replace=False))
+            wt = OC.normalize_weight(to_np(m.weight).astype(np.float64), m.kernel_size,
+                                     m.in_channels, m.out_channels)
+            ref = oracle_rows(rounded(feats, dtype), wt, to_np(m.bias).astype(np.float64),
+                              inv.pairs_in, inv.pairs_out, sel)
+            err = rel_err(to_np(y.features)[sel], ref)
+            say(name, "inverse rel err", err)
+            assert err <= TOL[dtype]
+        else:
+            y = _check_layer(m, feats, idx, shape, w.batch_size, dtype, rows=4096,
+                             what=f"{name} layer {li}")
+            if lay["kind"] == "strided" and lay["indice_key"]:
+                key = lay["indice_key"]
+                fwd_store[key] = (idx, shape, y.indice_dict[key] if key in y.indice_dict else
+                                  generate_strided_indice_pairs(
+                                      torch.from_numpy(idx).to(DEV), shape, w.batch_size,
+                                      lay["kernel_size"], lay["stride"], lay["padding"],
+                                      lay["dilation"]))
+        # the next layer consumes this layer's output (ReLU keeps magnitudes sane)
+        out = torch.relu(y.features.float())
+        feats = out.cpu().numpy().astype(np.float32)
+        idx = y.indices.cpu().numpy()
+        shape = tuple(y.spatial_shape)
+        torch.cuda.synchronize()
+
+
+def test_plan_is_a_stable_sort_by_slot_mask():
+    idx = _tiny(15, (40, 40, 40), 2, 6000)
+    x = torch.from_numpy(idx).to(DEV)
+    data = generate_subm_indice_pairs(x, (40, 40, 40), 2, 3)
+    n = len(idx)
+    order = data.execution_order(n, x.device).cpu().numpy().astype(np.int64)
+    nbr = data.neighbour_map(n, x.device).cpu().numpy()
+    mask = ((nbr >= 0).astype(np.int64) << np.arange(27)).sum(1)
+    expect = np.lexsort((np.arange(n), mask))
+    assert np.array_equal(order, expect)

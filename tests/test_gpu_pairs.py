@@ -1,0 +1,149 @@
+"""Indice pairs on the GPU are bit-exact against the oracle.
+
+Checks pair lists (order and values), pair_num, output coordinates and their
+row order for submanifold, strided and inverse builds: on the reference's
+golden-fixture inputs, on tiny inputs with unusual kernels, on empty and
+single-voxel inputs, and on the five workloads at their full sizes.
+"""
+import numpy as np
+import pytest
+import torch
+
+import golden_io
+from gpu_util import DEV, lists_np, needs_gpu, say
+from oracle import pairs as OP
+from trispconv.pytorch.indices import (generate_inverse_indice_pairs,
+                                       generate_strided_indice_pairs, generate_subm_indice_pairs)
+from trispconv_amd import workloads
+
+pytestmark = [pytest.mark.gpu, needs_gpu]
+
+
+def _check_lists(got, exp, what):
+    g_in, g_out = lists_np(got.pairs_in), lists_np(got.pairs_out)
+    assert len(g_in) == len(exp.pairs_in), what
+    assert got.pair_num.dtype == torch.int64 and got.pair_num.device.type == "cpu"
+    assert np.array_equal(got.pair_num.numpy(), exp.pair_num), what
+    for k in range(len(exp.pairs_in)):
+        assert np.array_equal(g_in[k], exp.pairs_in[k]), f"{what}: pairs_in[{k}]"
+        assert np.array_equal(g_out[k], exp.pairs_out[k]), f"{what}: pairs_out[{k}]"
+
+
+def _subm(idx, shape, B, k, d, what):
+    say("subm pairs:", what, idx.shape, shape, k, d)
+    got = generate_subm_indice_pairs(torch.from_numpy(idx).to(DEV), shape, B, k, d)
+    exp = OP.subm_pairs(idx, shape, B, k, d)
+    _check_lists(got, exp, what)
+    assert got.subm and got.output_spatial_shape == tuple(shape)
+    return got
+
+
+def _strided(idx, shape, B, k, s, p, d, what):
+    say("strided pairs:", what, idx.shape, shape, k, s, p, d)
+    x = torch.from_numpy(idx).to(DEV)
+    got = generate_strided_indice_pairs(x, shape, B, k, s, p, d)
+    exp = OP.strided_pairs(idx, shape, B, k, s, p, d)
+    assert got.output_spatial_shape == tuple(exp.output_spatial_shape), what
+    assert np.array_equal(got.out_indices.cpu().numpy(), exp.out_indices), f"{what}: out_indices"
+    _check_lists(got, exp, what)
+    return got, exp
+
+
+def _inverse(got_fwd, exp_fwd, what):
+    say("inverse pairs:", what)
+    got = generate_inverse_indice_pairs(got_fwd)
+    exp = OP.inverse_pairs(exp_fwd)
+    assert np.array_equal(got.out_indices.cpu().numpy(), exp.out_indices), f"{what}: out_indices"
+    _check_lists(got, exp, what)
+    return got
+
+
+def _tiny(seed, shape, B, n):
+    rng = np.random.default_rng(seed)
+    total = shape[0] * shape[1] * shape[2]
+    parts = []
+    for b in range(B):
+        cells = rng.choice(total, size=min(n, total), replace=False)
+        z, r = np.divmod(cells, shape[1] * shape[2])
+        y, x = np.divmod(r, shape[2])
+        parts.append(np.stack([np.full(len(cells), b), z, y, x], 1))
+    idx = np.concatenate(parts).astype(np.int32)
+    return idx[rng.permutation(len(idx))]
+
+
+@pytest.mark.parametrize("name", golden_io.fixture_names())
+def test_pairs_on_fixture_inputs(name):
+    a, m = golden_io.load(name)
+    k, s, p, d = m["kernel_size"], m["stride"], m["padding"], m["dilation"]
+    B = m["batch_size"]
+    if m["conv_type"] == "subm":
+        _subm(a["indices"], tuple(m["spatial_shape"]), B, k, d, name)
+    elif m["conv_type"] == "strided":
+        _strided(a["indices"], tuple(m["spatial_shape"]), B, k, s, p, d, name)
+    else:
+        g, e = _strided(a["down_in_indices"], tuple(m["down_in_spatial_shape"]), B, k, s, p, d,
+                        name + "/fwd")
+        if e.kernel_size != (1, 1, 1):
+            _inverse(g, e, name)
+
+
+@pytest.mark.parametrize("k,d", [(3, 1), (3, 2), (1, 1), ((3, 1, 3), (1, 2, 1)), ((2, 3, 2), 1),
+                                 (5, 1), ((7, 3, 3), 1)])
+def test_subm_pairs_unusual_kernels(k, d):
+    idx = _tiny(17, (9, 10, 11), 2, 300)
+    _subm(idx, (9, 10, 11), 2, k, d, f"k={k} d={d}")
+
+
+@pytest.mark.parametrize("k,s,p,d", [(3, 2, 1, 1), (2, 2, 0, 1), (2, 1, 0, 1), (3, 1, 1, 2),
+                                     ((3, 1, 1), (2, 1, 1), 0, 1), (3, (2, 1, 2), (1, 0, 1), 1),
+                                     (1, 2, 0, 1), (5, 3, 2, 1)])
+def test_strided_and_inverse_pairs_unusual(k, s, p, d):
+    idx = _tiny(23, (9, 10, 11), 3, 250)
+    g, e = _strided(idx, (9, 10, 11), 3, k, s, p, d, f"k={k} s={s} p={p} d={d}")
+    if e.kernel_size != (1, 1, 1):
+        _inverse(g, e, f"inverse k={k} s={s} p={p} d={d}")
+
+
+def test_empty_and_single_inputs():
+    empty = np.zeros((0, 4), np.int32)
+    _subm(empty, (4, 4, 4), 1, 3, 1, "empty subm")
+    g, e = _strided(empty, (4, 4, 4), 1, 3, 2, 1, 1, "empty strided")
+    assert g.out_indices.shape == (0, 4)
+    one = np.array([[0, 2, 2, 2]], np.int32)
+    _subm(one, (4, 4, 4), 1, 3, 1, "single subm")
+    g, e = _strided(one, (4, 4, 4), 1, 3, 2, 1, 1, "single strided")
+    _inverse(g, e, "single inverse")
+    # no candidate at all: stride 2, k=1, odd coordinates only
+    odd = np.array([[0, 1, 1, 1], [0, 3, 1, 3]], np.int32)
+    g, e = _strided(odd, (5, 5, 5), 1, 1, 2, 0, 1, "no candidates")
+    assert g.out_indices.shape == (0, 4) and int(g.pair_num.sum()) == 0
+
+
+def test_repeated_coordinates_later_row_wins():
+    idx = np.array([[0, 1, 1, 1], [0, 1, 1, 2], [0, 1, 1, 1], [0, 2, 2, 2], [0, 1, 1, 2]], np.int32)
+    _subm(idx, (4, 4, 4), 1, 3, 1, "duplicates")
+
+
+def test_out_of_grid_coordinates_raise():
+    idx = torch.tensor([[0, 1, 1, 1], [0, 9, 1, 1]], dtype=torch.int32, device=DEV)
+    with pytest.raises(IndexError):
+        generate_subm_indice_pairs(idx, (4, 4, 4), 1, 3)
+    idx = torch.tensor([[0, 1, 1, 1], [3, 1, 1, 1]], dtype=torch.int32, device=DEV)
+    with pytest.raises(IndexError):
+        generate_subm_indice_pairs(idx, (4, 4, 4), 2, 3)
+    with pytest.raises(IndexError):
+        generate_strided_indice_pairs(idx, (4, 4, 4), 2, 3, 2, 1)
+
+
+@pytest.mark.parametrize("name", workloads.WORKLOAD_NAMES)
+def test_pairs_full_size_workloads(name):
+    w = workloads.make_workload(name)
+    idx, shape, B = w.indices, w.spatial_shape, w.batch_size
+    lay = w.layers[0]
+    if lay["kind"] == "subm":
+        _subm(idx, shape, B, lay["kernel_size"], lay["dilation"], name)
+    else:
+        g, e = _strided(idx, shape, B, lay["kernel_size"], lay["stride"], lay["padding"],
+                        lay["dilation"], name)
+        if len(w.layers) > 1 and w.layers[1]["kind"] == "inverse":
+            _inverse(g, e, name + "/inverse")

@@ -1,0 +1,203 @@
+"""Host-side behaviour that needs no GPU: the tensor carrier, constructors,
+error paths, weight layout, the C-ABI library's exports and the workloads.
+
+Mirrors the CPU-checkable parts of the reference's tests/test_tensor.py,
+test_indices_strided.py:119-127 and modules.py:46-51 / :149-155.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import trispconv.pytorch as spconv
+from trispconv.pytorch.weight import normalize_spconv_weight
+from trispconv_amd import _lib as L
+from trispconv_amd import workloads
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def make_sparse(B=1, N=8, C=4, D=8, H=8, W=8, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    coords = torch.randint(0, min(D, H, W), (N, 3), dtype=torch.int32, generator=g)
+    idx = torch.cat([torch.zeros(N, 1, dtype=torch.int32), coords], dim=1)
+    return spconv.SparseConvTensor(torch.randn(N, C, generator=g), idx, [D, H, W], B)
+
+
+# ----------------------------------------------------------- tensor carrier
+def test_construction():
+    x = make_sparse()
+    assert x.features.shape == (8, 4)
+    assert x.indices.shape == (8, 4)
+    assert x.spatial_shape == [8, 8, 8]
+    assert x.batch_size == 1
+
+
+def test_constructor_asserts():
+    with pytest.raises(AssertionError):
+        spconv.SparseConvTensor(torch.zeros(3), torch.zeros(3, 4, dtype=torch.int32), [2, 2, 2], 1)
+    with pytest.raises(AssertionError):
+        spconv.SparseConvTensor(torch.zeros(3, 2), torch.zeros(3, 4, dtype=torch.int64), [2, 2, 2], 1)
+
+
+def test_replace_feature_shares_indices_and_dict():
+    x = make_sparse()
+    y = x.replace_feature(torch.ones(8, 4))
+    assert torch.equal(y.features, torch.ones(8, 4))
+    assert y.indices is x.indices
+    assert y.indice_dict is x.indice_dict
+    assert not torch.equal(x.features, torch.ones(8, 4))
+
+
+def test_features_setter_raises():
+    x = make_sparse()
+    with pytest.raises(AttributeError):
+        x.features = torch.zeros(8, 4)
+
+
+def test_dense_shape_and_values():
+    x = make_sparse(B=2, N=10, C=3, D=4, H=5, W=6)
+    idx = x.indices.clone()
+    idx[:5, 0] = 0
+    idx[5:, 0] = 1
+    x2 = spconv.SparseConvTensor(x.features, idx, [4, 5, 6], 2)
+    d = x2.dense()
+    assert d.shape == (2, 3, 4, 5, 6)
+    assert x2.dense(channels_first=False).shape == (2, 4, 5, 6, 3)
+    i = idx.long()
+    # last duplicate wins; check a row whose coordinate is unique
+    keys = ((i[:, 0] * 4 + i[:, 1]) * 5 + i[:, 2]) * 6 + i[:, 3]
+    uniq = [r for r in range(10) if (keys == keys[r]).sum() == 1]
+    r = uniq[0]
+    assert torch.equal(d[i[r, 0], :, i[r, 1], i[r, 2], i[r, 3]], x.features[r])
+
+
+def test_find_indice_pair():
+    x = make_sparse()
+    assert x.find_indice_pair("nonexistent") is None
+    assert x.find_indice_pair(None) is None
+    x.indice_dict["k"] = "sentinel"
+    assert x.find_indice_pair("k") == "sentinel"
+
+
+# ----------------------------------------------------------- constructors
+def test_constructor_errors():
+    with pytest.raises(NotImplementedError):
+        spconv.SparseConvolution(2, 4, 4, 3)
+    with pytest.raises(NotImplementedError):
+        spconv.SparseConvolution(3, 4, 4, 3, groups=2)
+    with pytest.raises(NotImplementedError):
+        spconv.SparseConvolution(3, 4, 4, 3, transposed=True)
+
+
+def test_module_parameters_krsc_and_forced_fields():
+    m = spconv.SubMConv3d(4, 6, 3, stride=2, padding=1)
+    assert m.weight.shape == (6, 3, 3, 3, 4)
+    assert m.stride == (1, 1, 1) and m.padding == (0, 0, 0) and m.subm
+    assert torch.equal(m.bias, torch.zeros(6))
+    inv = spconv.SparseInverseConv3d(4, 6, (3, 1, 3), bias=False)
+    assert inv.inverse and inv.bias is None and inv.kernel_size == (3, 1, 3)
+    # kaiming-uniform bound over the (C_out, K*C_in) view
+    bound = (6.0 / (27 * 4)) ** 0.5
+    assert float(m.weight.abs().max()) <= bound + 1e-7
+
+
+def test_inverse_requires_key_before_any_gpu_work():
+    x = spconv.SparseConvTensor(torch.randn(5, 4), torch.zeros(5, 4, dtype=torch.int32), [8, 8, 8], 1)
+    with pytest.raises(ValueError):
+        spconv.SparseInverseConv3d(4, 4, 3)(x)
+    with pytest.raises(KeyError):
+        spconv.SparseInverseConv3d(4, 4, 3, indice_key="missing")(x)
+
+
+def test_cpu_tensors_are_refused():
+    x = make_sparse(C=4)
+    with pytest.raises(RuntimeError, match="GPU"):
+        spconv.SubMConv3d(4, 4, 3)(x)
+
+
+def test_sparse_sequential_names():
+    from collections import OrderedDict
+    seq = spconv.SparseSequential(OrderedDict(a=torch.nn.ReLU(), b=torch.nn.Identity()))
+    assert [n for n, _ in seq.named_children()] == ["a", "b"]
+    seq2 = spconv.SparseSequential(torch.nn.ReLU(), extra=torch.nn.Identity())
+    assert [n for n, _ in seq2.named_children()] == ["0", "extra"]
+    # dense modules act on features, the carrier keeps its coordinates
+    x = make_sparse()
+    y = seq2(x)
+    assert torch.equal(y.features, torch.relu(x.features)) and y.indices is x.indices
+
+
+# ----------------------------------------------------------- weight layout
+def test_normalize_weight_layouts():
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(6, 3, 2, 3, 4, generator=g)
+    W = normalize_spconv_weight(w, (3, 2, 3), 4, 6)
+    assert W.shape == (18, 4, 6)
+    assert torch.equal(W[(2 * 2 + 1) * 3 + 2], w[:, 2, 1, 2, :].T)
+    w1 = torch.randn(6, 1, 1, 1, 4, generator=g)
+    assert torch.equal(normalize_spconv_weight(w1, (1, 1, 1), 4, 6)[0], w1.reshape(-1).view(4, 6))
+    assert torch.equal(normalize_spconv_weight(w1.reshape(6, 4), (1, 1, 1), 4, 6)[0],
+                       w1.reshape(-1).view(4, 6))
+    assert torch.equal(normalize_spconv_weight(W, (3, 2, 3), 4, 6), W)
+    with pytest.raises(ValueError):
+        normalize_spconv_weight(torch.zeros(5, 5), (3, 3, 3), 4, 6)
+
+
+# ----------------------------------------------------------- C ABI
+def _declared_symbols():
+    text = (ROOT / "include" / "trispconv_abi.h").read_text()
+    return sorted(set(re.findall(r"TSC_API\s+[\w\s\*]+?\b(tsc_\w+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = L.lib()
+    declared = _declared_symbols()
+    assert declared, "no declarations parsed"
+    assert declared == L.exported_symbols()
+    for name in declared:
+        assert getattr(lib, name) is not None
+    assert lib.tsc_abi_version() == L.ABI_VERSION
+
+
+def test_workspace_queries_are_host_only():
+    lib = L.lib()
+    assert lib.tsc_subm_workspace_bytes(500_000, 27) >= 1_048_576 * 8
+    assert lib.tsc_strided_workspace_bytes(1000, 27, 2, L.i3((21, 800, 704))) > 2 * 21 * 800 * 704 // 8
+    assert lib.tsc_inverse_workspace_bytes(1000) >= 8000
+    assert lib.tsc_plan_workspace_bytes(1000, 27) >= 16000
+    # MFMA-eligible layers pack 2-byte weights, others fp32
+    assert lib.tsc_packed_weight_bytes(27, 128, 128, L.F16) == 27 * 128 * 128 * 2
+    assert lib.tsc_packed_weight_bytes(27, 16, 16, L.F32) == 27 * 16 * 16 * 4
+
+
+def test_argument_errors_return_codes_without_gpu():
+    lib = L.lib()
+    rc = lib.tsc_subm_pairs(None, -1, 1, L.i3((4, 4, 4)), L.i3((3, 3, 3)), L.i3((1, 1, 1)), None,
+                            0, None, None, None, None, None)
+    assert rc == 1 and b"out of range" in lib.tsc_last_error()
+    rc = lib.tsc_strided_count(None, 10, 1, L.i3((8, 8, 8)), L.i3((3, 3, 3)), L.i3((2, 2, 2)),
+                               L.i3((1, 1, 1)), L.i3((1, 1, 1)), L.i3((5, 5, 5)), None, 0, None,
+                               None)
+    assert rc == 1 and b"output shape" in lib.tsc_last_error()
+    rc = lib.tsc_conv_forward(None, 7, 1, 1, None, None, 0, None, None, 1, 1, 1, None, None)
+    assert rc == 1 and b"dtype" in lib.tsc_last_error()
+    with pytest.raises(ValueError):
+        L.check(1, "probe")
+
+
+# ----------------------------------------------------------- workloads
+@pytest.mark.parametrize("name", workloads.WORKLOAD_NAMES)
+def test_workloads_unique_in_grid(name):
+    w = workloads.make_workload(name, scale=0.02)
+    idx = w.indices
+    assert idx.dtype == np.int32 and idx.shape[1] == 4
+    D, H, W = w.spatial_shape
+    assert (idx[:, 0] >= 0).all() and (idx[:, 0] < w.batch_size).all()
+    assert (idx[:, 1] < D).all() and (idx[:, 2] < H).all() and (idx[:, 3] < W).all()
+    assert (idx >= 0).all()
+    keys = ((idx[:, 0].astype(np.int64) * D + idx[:, 1]) * H + idx[:, 2]) * W + idx[:, 3]
+    assert len(np.unique(keys)) == len(keys)

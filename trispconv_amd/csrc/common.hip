@@ -1,0 +1,209 @@
+// Error reporting, fills and the two scans shared by the pair builders.
+#include "common.hpp"
+
+#include <cstdarg>
+
+namespace tsc {
+
+namespace {
+thread_local std::string g_error;
+}
+
+int set_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+const char* last_error() { return g_error.c_str(); }
+
+// ------------------------------------------------------------------ fills --
+__global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+__global__ void fill_u64_kernel(unsigned long long* p, int64_t n, unsigned long long v) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+static int fill_grid(int64_t n) {
+  int64_t g = ceil_div(n, 256);
+  return static_cast<int>(g < 4096 ? (g < 1 ? 1 : g) : 4096);
+}
+
+int fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s) {
+  if (n <= 0) return 0;
+  fill_u32_kernel<<<fill_grid(n), 256, 0, s>>>(p, n, v);
+  TSC_LAUNCH_CHECK("fill_u32");
+  return 0;
+}
+
+int fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hipStream_t s) {
+  if (n <= 0) return 0;
+  fill_u64_kernel<<<fill_grid(n), 256, 0, s>>>(p, n, v);
+  TSC_LAUNCH_CHECK("fill_u64");
+  return 0;
+}
+
+// ------------------------------------------------------------ block scan --
+// Inclusive scan across a wave with shuffles.
+__device__ __forceinline__ uint32_t wave_inclusive(uint32_t v) {
+  const int l = __lane_id();
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    uint32_t t = __shfl_up(v, d, kWave);
+    if (l >= d) v += t;
+  }
+  return v;
+}
+
+// Exclusive scan across the block (blockDim.x a multiple of 64, <= 1024).
+// Returns the thread's exclusive prefix; *block_total receives the sum.
+__device__ uint32_t block_exclusive(uint32_t v, uint32_t* s_wave, uint32_t* block_total) {
+  const int w = threadIdx.x / kWave;
+  const int nw = blockDim.x / kWave;
+  uint32_t inc = wave_inclusive(v);
+  if (__lane_id() == kWave - 1) s_wave[w] = inc;
+  __syncthreads();
+  if (w == 0) {
+    uint32_t t = __lane_id() < nw ? s_wave[__lane_id()] : 0u;
+    uint32_t ti = wave_inclusive(t);
+    if (__lane_id() < nw) s_wave[__lane_id()] = ti - t;  // exclusive wave offsets
+    if (__lane_id() == nw - 1) s_wave[32] = ti;
+  }
+  __syncthreads();
+  uint32_t res = s_wave[w] + inc - v;
+  *block_total = s_wave[32];
+  __syncthreads();
+  return res;
+}
+
+// ---------------------------------------------------- per-slot block scan --
+__global__ void __launch_bounds__(1024) scan_slot_blocks_kernel(const int32_t* __restrict__ cnt,
+                                                                int32_t* __restrict__ off,
+                                                                int32_t* __restrict__ totals,
+                                                                int nblk) {
+  __shared__ uint32_t s_wave[33];
+  const int k = blockIdx.x;
+  const int32_t* c = cnt + (int64_t)k * nblk;
+  int32_t* o = off + (int64_t)k * nblk;
+  uint32_t carry = 0;
+  for (int base = 0; base < nblk; base += blockDim.x) {
+    const int i = base + threadIdx.x;
+    uint32_t v = i < nblk ? static_cast<uint32_t>(c[i]) : 0u;
+    uint32_t tot;
+    uint32_t ex = block_exclusive(v, s_wave, &tot);
+    if (i < nblk) o[i] = static_cast<int32_t>(carry + ex);
+    carry += tot;
+  }
+  if (threadIdx.x == 0) totals[k] = static_cast<int32_t>(carry);
+}
+
+int scan_slot_blocks(const int32_t* cnt, int32_t* off, int32_t* totals, int K, int nblk,
+                     hipStream_t s) {
+  scan_slot_blocks_kernel<<<K, 1024, 0, s>>>(cnt, off, totals, nblk);
+  TSC_LAUNCH_CHECK("scan_slot_blocks");
+  return 0;
+}
+
+// ---------------------------------------------------- device-wide scan --
+constexpr int kScanThreads = 256;
+constexpr int kScanItems = 16;                       // per thread
+constexpr int kScanTile = kScanThreads * kScanItems; // per block
+
+__device__ __forceinline__ uint32_t scan_value(const uint32_t* src, int kind, int64_t i) {
+  uint32_t v = src[i];
+  if (kind == 0) return __popc(v);
+  if (kind == 1) return v != 0u ? 1u : 0u;
+  return v;
+}
+
+__global__ void __launch_bounds__(kScanThreads) scan_reduce_kernel(const uint32_t* __restrict__ src,
+                                                                   int kind, int64_t n,
+                                                                   uint32_t* __restrict__ sums) {
+  __shared__ uint32_t s_wave[33];
+  const int64_t base = blockIdx.x * (int64_t)kScanTile;
+  uint32_t acc = 0;
+#pragma unroll 4
+  for (int j = 0; j < kScanItems; ++j) {
+    const int64_t i = base + j * kScanThreads + threadIdx.x;  // coalesced
+    if (i < n) acc += scan_value(src, kind, i);
+  }
+  uint32_t tot;
+  block_exclusive(acc, s_wave, &tot);
+  if (threadIdx.x == 0) sums[blockIdx.x] = tot;
+}
+
+__global__ void __launch_bounds__(1024) scan_sums_kernel(uint32_t* __restrict__ sums, int64_t nblk,
+                                                         int32_t* __restrict__ total) {
+  __shared__ uint32_t s_wave[33];
+  uint32_t carry = 0;
+  for (int64_t b = 0; b < nblk; b += blockDim.x) {
+    const int64_t i = b + threadIdx.x;
+    uint32_t v = i < nblk ? sums[i] : 0u;
+    uint32_t tot;
+    uint32_t ex = block_exclusive(v, s_wave, &tot);
+    if (i < nblk) sums[i] = carry + ex;
+    carry += tot;
+  }
+  if (threadIdx.x == 0 && total) *total = static_cast<int32_t>(carry);
+}
+
+__global__ void __launch_bounds__(kScanThreads) scan_apply_kernel(const uint32_t* __restrict__ src,
+                                                                  int kind, int64_t n,
+                                                                  const uint32_t* __restrict__ sums,
+                                                                  uint32_t* __restrict__ out) {
+  __shared__ uint32_t s_wave[33];
+  // each thread owns kScanItems consecutive items so the prefix stays in order
+  const int64_t base = blockIdx.x * (int64_t)kScanTile + threadIdx.x * (int64_t)kScanItems;
+  uint32_t v[kScanItems];
+  uint32_t acc = 0;
+#pragma unroll
+  for (int j = 0; j < kScanItems; ++j) {
+    const int64_t i = base + j;
+    v[j] = i < n ? scan_value(src, kind, i) : 0u;
+    acc += v[j];
+  }
+  uint32_t tot;
+  uint32_t run = sums[blockIdx.x] + block_exclusive(acc, s_wave, &tot);
+#pragma unroll
+  for (int j = 0; j < kScanItems; ++j) {
+    const int64_t i = base + j;
+    if (i < n) out[i] = run;
+    run += v[j];
+  }
+}
+
+int64_t scan_scratch_words(int64_t n) { return ceil_div(n > 0 ? n : 1, kScanTile); }
+
+int exclusive_scan_u32(const uint32_t* src, int kind, int64_t n, uint32_t* out, int32_t* total,
+                       uint32_t* scratch, hipStream_t s) {
+  if (n <= 0) {
+    if (total) {
+      int rc = fill_u32(reinterpret_cast<uint32_t*>(total), 1, 0u, s);
+      if (rc) return rc;
+    }
+    return 0;
+  }
+  const int64_t nblk = ceil_div(n, kScanTile);
+  scan_reduce_kernel<<<nblk, kScanThreads, 0, s>>>(src, kind, n, scratch);
+  TSC_LAUNCH_CHECK("scan_reduce");
+  scan_sums_kernel<<<1, 1024, 0, s>>>(scratch, nblk, total);
+  TSC_LAUNCH_CHECK("scan_sums");
+  scan_apply_kernel<<<nblk, kScanThreads, 0, s>>>(src, kind, n, scratch, out);
+  TSC_LAUNCH_CHECK("scan_apply");
+  return 0;
+}
+
+}  // namespace tsc
+
+extern "C" const char* tsc_last_error(void) { return tsc::last_error(); }
+extern "C" int tsc_abi_version(void) { return 1; }

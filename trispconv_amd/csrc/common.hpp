@@ -1,0 +1,161 @@
+// Shared device/host helpers for libtrispconv_hip: error reporting, launch
+// checks, integer geometry, the coordinate hash and wave-level primitives.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/trispconv_abi.h"
+
+namespace tsc {
+
+// ---------------------------------------------------------------- errors --
+int set_error(int code, const char* fmt, ...);
+const char* last_error();
+
+#define TSC_REQUIRE(cond, ...)                                        \
+  do {                                                                \
+    if (!(cond)) return ::tsc::set_error(TSC_EINVAL, __VA_ARGS__);    \
+  } while (0)
+
+#define TSC_LAUNCH_CHECK(what)                                                     \
+  do {                                                                             \
+    hipError_t e_ = hipGetLastError();                                             \
+    if (e_ != hipSuccess)                                                          \
+      return ::tsc::set_error(-static_cast<int>(e_), "%s: %s", what,               \
+                              hipGetErrorString(e_));                              \
+  } while (0)
+
+constexpr int kWave = 64;
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t align_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+// Carves typed sub-buffers out of one caller-provided workspace; every
+// carve is 256-byte aligned.
+struct Carver {
+  char* base;
+  int64_t used = 0;
+  explicit Carver(void* p) : base(static_cast<char*>(p)) {}
+  template <typename T>
+  T* take(int64_t count) {
+    T* p = reinterpret_cast<T*>(base ? base + used : nullptr);
+    used += align_up(count * static_cast<int64_t>(sizeof(T)), 256);
+    return p;
+  }
+};
+
+// --------------------------------------------------------------- geometry --
+struct Box {            // 3-D extents or per-axis parameters, z-y-x order
+  int32_t z, y, x;
+};
+
+inline Box box(const int32_t* v) { return Box{v[0], v[1], v[2]}; }
+
+// slot k -> (kz, ky, kx) for a kD x kH x kW kernel
+__device__ __forceinline__ void slot_to_zyx(int k, const Box& ks, int& kz, int& ky, int& kx) {
+  kx = k % ks.x;
+  int r = k / ks.x;
+  ky = r % ks.y;
+  kz = r / ks.y;
+}
+
+// ------------------------------------------------------------------ hash --
+// Open addressing, linear probing, power-of-two capacity, one 64-bit word per
+// slot: (key << 32) | row.  Keys are the packed (b,z,y,x) cell id, which the
+// host guarantees to be < 2^32 - 1, so an all-ones word marks an empty slot.
+constexpr uint64_t kEmpty = ~0ull;
+
+__device__ __forceinline__ uint32_t hash32(uint32_t k) {
+  // murmur3 finaliser
+  k ^= k >> 16;
+  k *= 0x85ebca6bu;
+  k ^= k >> 13;
+  k *= 0xc2b2ae35u;
+  k ^= k >> 16;
+  return k;
+}
+
+__device__ __forceinline__ void hash_insert(unsigned long long* table, uint32_t mask,
+                                            uint32_t key, uint32_t row) {
+  const unsigned long long word = (static_cast<unsigned long long>(key) << 32) | row;
+  uint32_t h = hash32(key) & mask;
+  while (true) {
+    unsigned long long old = atomicCAS(&table[h], static_cast<unsigned long long>(kEmpty), word);
+    if (old == kEmpty) return;
+    if (static_cast<uint32_t>(old >> 32) == key) {
+      // repeated coordinate: the larger row id wins, as a sequential
+      // "table[key] = row" over rows in order would leave it
+      atomicMax(&table[h], word);
+      return;
+    }
+    h = (h + 1) & mask;
+  }
+}
+
+__device__ __forceinline__ int32_t hash_find(const unsigned long long* __restrict__ table,
+                                             uint32_t mask, uint32_t key) {
+  uint32_t h = hash32(key) & mask;
+  while (true) {
+    unsigned long long w = table[h];
+    if (w == kEmpty) return -1;
+    if (static_cast<uint32_t>(w >> 32) == key) return static_cast<int32_t>(w & 0xffffffffu);
+    h = (h + 1) & mask;
+  }
+}
+
+// ------------------------------------------------------------ wave tools --
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ uint64_t lanes_below() {
+  const int l = __lane_id();
+  return l == 0 ? 0ull : (~0ull >> (64 - l));
+}
+
+__device__ __forceinline__ int rank_in_wave(uint64_t ballot) {
+  return __popcll(ballot & lanes_below());
+}
+
+// ------------------------------------------------------------ conversions --
+template <typename T> __device__ __forceinline__ float to_f32(T v);
+template <> __device__ __forceinline__ float to_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ float to_f32<__half>(__half v) { return __half2float(v); }
+template <> __device__ __forceinline__ float to_f32<__hip_bfloat16>(__hip_bfloat16 v) {
+  return __bfloat162float(v);
+}
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ __half from_f32<__half>(float v) { return __float2half_rn(v); }
+template <> __device__ __forceinline__ __hip_bfloat16 from_f32<__hip_bfloat16>(float v) {
+  return __float2bfloat16(v);  // round to nearest even
+}
+
+inline int dtype_bytes(int dt) { return dt == TSC_F32 ? 4 : 2; }
+inline bool dtype_ok(int dt) { return dt == TSC_F32 || dt == TSC_F16 || dt == TSC_BF16; }
+
+// ------------------------------------------------------ shared kernels --
+__global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v);
+__global__ void fill_u64_kernel(unsigned long long* p, int64_t n, unsigned long long v);
+int fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s);
+int fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hipStream_t s);
+
+// Per-slot, per-block counts -> exclusive offsets along blocks, plus totals.
+// cnt and off are [K][nblk]; totals[k] receives the sum of slot k.
+int scan_slot_blocks(const int32_t* cnt, int32_t* off, int32_t* totals, int K, int nblk,
+                     hipStream_t s);
+
+// Exclusive scan of n uint32 values produced by `kind` from `src`:
+//   kind 0: popcount(src[i])   kind 1: src[i] != 0   kind 2: src[i]
+// out[i] receives the prefix, *total the sum (device pointer, may be null).
+// Scratch: scan_scratch_words(n) uint32 words.
+int64_t scan_scratch_words(int64_t n);
+int exclusive_scan_u32(const uint32_t* src, int kind, int64_t n, uint32_t* out, int32_t* total,
+                       uint32_t* scratch, hipStream_t s);
+
+}  // namespace tsc

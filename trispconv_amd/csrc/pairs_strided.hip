@@ -1,0 +1,288 @@
+// Strided indice pairs on the GPU.
+//
+// Reference algorithm: trispconv/pytorch/indices.py:143-259.  For slot
+// k = (kz,ky,kx) in product order and each input row i in ascending order,
+// c = coord(i) + pad - k*dil is a candidate when, on every axis, c is a
+// multiple of the stride and 0 <= c/stride < out_dim; its output is
+// o = (b_i, c/stride).  The output set is the sorted unique set of all
+// candidate cells; a pair's output id is its cell's rank in that set.
+//
+// MI355X design: instead of concatenating candidates and running a sort-based
+// unique (indices.py:215-229), every candidate sets one bit in an occupancy
+// bitmap over the output grid (B*oD*oH*oW bits: 1/64 of the reference's
+// int64-per-cell dense table).  An exclusive scan of the words' popcounts then
+// gives each cell's rank in sorted order directly, so output coordinates come
+// out sorted by (b,z,y,x) and ranks need no sort and no search.  Pair lists are
+// compacted per slot in ascending input order with the same block-offset +
+// wave-ballot scheme as the submanifold builder.
+#include "common.hpp"
+
+namespace tsc {
+namespace {
+
+constexpr int kRows = 256;
+
+struct StridedGeom {
+  int32_t B;
+  Box ks, st, pad, dil, out;
+};
+
+// Candidate output cell of input coordinate c for slot (kz,ky,kx); -1 if none.
+__device__ __forceinline__ int64_t candidate(const StridedGeom& g, const int4& c, int kz, int ky,
+                                             int kx) {
+  const int cz = c.y + g.pad.z - kz * g.dil.z;
+  const int cy = c.z + g.pad.y - ky * g.dil.y;
+  const int cx = c.w + g.pad.x - kx * g.dil.x;
+  // divisibility does not depend on the sign, and c < 0 gives c/s < 0 (out of
+  // range) under floor division, so testing c >= 0 first is equivalent to the
+  // reference's floor-mod / floor-div test
+  if (cz < 0 || cy < 0 || cx < 0) return -1;
+  if (cz % g.st.z || cy % g.st.y || cx % g.st.x) return -1;
+  const int oz = cz / g.st.z, oy = cy / g.st.y, ox = cx / g.st.x;
+  if (oz >= g.out.z || oy >= g.out.y || ox >= g.out.x) return -1;
+  return ((static_cast<int64_t>(c.x) * g.out.z + oz) * g.out.y + oy) * g.out.x + ox;
+}
+
+__global__ void __launch_bounds__(kRows) strided_mark_kernel(const int4* __restrict__ coords,
+                                                             int64_t n, int K, StridedGeom g,
+                                                             uint32_t* bitmap,
+                                                             int32_t* __restrict__ blk_cnt,
+                                                             int nblk, int32_t* status) {
+  __shared__ int32_t s_cnt[kRows / kWave][64];
+  const int t = threadIdx.x;
+  const int w = t / kWave;
+  const int64_t i = blockIdx.x * (int64_t)kRows + t;
+  const bool valid = i < n;
+  int4 c = valid ? coords[i] : make_int4(-1, 0, 0, 0);
+  bool ok = valid && c.x >= 0 && c.x < g.B;
+  if (valid && !ok) atomicOr(status, TSC_FLAG_BATCH_OUT_OF_RANGE);
+  for (int k = 0; k < K; ++k) {
+    int kz, ky, kx;
+    slot_to_zyx(k, g.ks, kz, ky, kx);
+    const int64_t cell = ok ? candidate(g, c, kz, ky, kx) : -1;
+    if (cell >= 0) atomicOr(&bitmap[cell >> 5], 1u << (cell & 31));
+    const uint64_t hits = __ballot(cell >= 0);
+    if (__lane_id() == 0) {
+      if (k < 64)
+        s_cnt[w][k] = __popcll(hits);
+      else
+        atomicAdd(&blk_cnt[(int64_t)k * nblk + blockIdx.x], (int)__popcll(hits));
+    }
+  }
+  __syncthreads();
+  if (t < K && t < 64) {
+    int s = 0;
+#pragma unroll
+    for (int ww = 0; ww < kRows / kWave; ++ww) s += s_cnt[ww][t];
+    blk_cnt[(int64_t)t * nblk + blockIdx.x] = s;
+  }
+}
+
+// One thread per bitmap word: decode every set bit, in ascending order, into
+// its (b, z, y, x) row at the word's prefix rank.
+__global__ void __launch_bounds__(256) strided_emit_kernel(const uint32_t* __restrict__ bitmap,
+                                                           const uint32_t* __restrict__ wprefix,
+                                                           int64_t nwords, StridedGeom g,
+                                                           int4* __restrict__ out_coords,
+                                                           int64_t n_out) {
+  const int64_t wi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (wi >= nwords) return;
+  uint32_t bits = bitmap[wi];
+  uint32_t rank = wprefix[wi];
+  const int64_t plane = (int64_t)g.out.y * g.out.x;
+  const int64_t vol = plane * g.out.z;
+  while (bits) {
+    const int b = __ffs(bits) - 1;
+    bits &= bits - 1;
+    const int64_t cell = (wi << 5) + b;
+    const int64_t bb = cell / vol;
+    const int64_t rem = cell - bb * vol;
+    const int64_t z = rem / plane;
+    const int64_t r2 = rem - z * plane;
+    const int64_t y = r2 / g.out.x;
+    const int64_t x = r2 - y * g.out.x;
+    if (rank < n_out) out_coords[rank] = make_int4((int)bb, (int)z, (int)y, (int)x);
+    ++rank;
+  }
+}
+
+__global__ void __launch_bounds__(kRows) strided_fill_kernel(const int4* __restrict__ coords,
+                                                             int64_t n, int K, StridedGeom g,
+                                                             const uint32_t* __restrict__ bitmap,
+                                                             const uint32_t* __restrict__ wprefix,
+                                                             const int32_t* __restrict__ blk_off,
+                                                             int nblk, int64_t cap, int64_t n_out,
+                                                             int32_t* __restrict__ nbr,
+                                                             int32_t* __restrict__ pairs_in,
+                                                             int32_t* __restrict__ pairs_out) {
+  __shared__ int32_t s_wcnt[kRows / kWave][64];
+  const int t = threadIdx.x;
+  const int w = t / kWave;
+  const int64_t i = blockIdx.x * (int64_t)kRows + t;
+  const bool valid = i < n;
+  int4 c = valid ? coords[i] : make_int4(-1, 0, 0, 0);
+  const bool ok = valid && c.x >= 0 && c.x < g.B;
+  for (int kb = 0; kb < K; kb += 64) {
+    const int kend = (K - kb) < 64 ? (K - kb) : 64;
+    for (int kk = 0; kk < kend; ++kk) {
+      int kz, ky, kx;
+      slot_to_zyx(kb + kk, g.ks, kz, ky, kx);
+      const int64_t cell = ok ? candidate(g, c, kz, ky, kx) : -1;
+      const uint64_t hits = __ballot(cell >= 0);
+      if (__lane_id() == 0) s_wcnt[w][kk] = __popcll(hits);
+    }
+    __syncthreads();
+    for (int kk = 0; kk < kend; ++kk) {
+      const int k = kb + kk;
+      int kz, ky, kx;
+      slot_to_zyx(k, g.ks, kz, ky, kx);
+      const int64_t cell = ok ? candidate(g, c, kz, ky, kx) : -1;
+      const uint64_t hits = __ballot(cell >= 0);
+      int base = blk_off[(int64_t)k * nblk + blockIdx.x];
+      for (int ww = 0; ww < w; ++ww) base += s_wcnt[ww][kk];
+      if (cell >= 0) {
+        const int64_t word = cell >> 5;
+        const uint32_t below = bitmap[word] & ((1u << (cell & 31)) - 1u);
+        const int32_t rank = static_cast<int32_t>(wprefix[word] + __popc(below));
+        const int64_t slot_pos = base + rank_in_wave(hits);
+        // both bounds hold by construction; the test keeps a bad count from
+        // turning into an out-of-bounds write
+        if (slot_pos < cap && rank < n_out) {
+          pairs_in[(int64_t)k * cap + slot_pos] = static_cast<int32_t>(i);
+          pairs_out[(int64_t)k * cap + slot_pos] = rank;
+          nbr[(int64_t)rank * K + k] = static_cast<int32_t>(i);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+struct Layout {
+  int64_t cells, nwords, nblk;
+};
+
+Layout layout(int64_t n, int32_t batch, const int32_t* out) {
+  Layout L;
+  L.cells = (int64_t)batch * out[0] * out[1] * out[2];
+  L.nwords = ceil_div(L.cells > 0 ? L.cells : 1, 32);
+  L.nblk = ceil_div(n > 0 ? n : 1, kRows);
+  return L;
+}
+
+struct Buffers {
+  uint32_t* bitmap;
+  uint32_t* wprefix;
+  uint32_t* scratch;
+  int32_t* blk_cnt;
+  int32_t* blk_off;
+};
+
+Buffers carve(void* ws, const Layout& L, int K, int64_t* used) {
+  Carver c(ws);
+  Buffers b;
+  b.bitmap = c.take<uint32_t>(L.nwords);
+  b.wprefix = c.take<uint32_t>(L.nwords);
+  b.scratch = c.take<uint32_t>(scan_scratch_words(L.nwords));
+  b.blk_cnt = c.take<int32_t>(L.nblk * K);
+  b.blk_off = c.take<int32_t>(L.nblk * K);
+  if (used) *used = c.used;
+  return b;
+}
+
+int check_geom(int64_t n, int32_t batch, const int32_t* spatial, const int32_t* ksize,
+               const int32_t* stride, const int32_t* padding, const int32_t* dilation,
+               const int32_t* out_spatial, StridedGeom* g) {
+  TSC_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "strided: n=%lld out of range", (long long)n);
+  TSC_REQUIRE(batch > 0, "strided: batch_size must be positive");
+  for (int a = 0; a < 3; ++a) {
+    TSC_REQUIRE(spatial[a] > 0 && ksize[a] > 0 && stride[a] > 0 && dilation[a] > 0 &&
+                    padding[a] >= 0,
+                "strided: invalid geometry on axis %d", a);
+    const int num = spatial[a] + 2 * padding[a] - dilation[a] * (ksize[a] - 1) - 1;
+    TSC_REQUIRE(num >= 0, "strided: kernel extent exceeds the padded input on axis %d", a);
+    const int expect = num / stride[a] + 1;
+    TSC_REQUIRE(out_spatial[a] == expect,
+                "strided: output shape %d on axis %d, expected %d", out_spatial[a], a, expect);
+  }
+  const int64_t cells = (int64_t)batch * out_spatial[0] * out_spatial[1] * out_spatial[2];
+  TSC_REQUIRE(cells <= (int64_t(1) << 37),
+              "strided: output grid of %lld cells exceeds the 2^37-cell bitmap limit",
+              (long long)cells);
+  *g = StridedGeom{batch, box(ksize), box(stride), box(padding), box(dilation), box(out_spatial)};
+  return 0;
+}
+
+}  // namespace
+}  // namespace tsc
+
+using namespace tsc;
+
+extern "C" int64_t tsc_strided_workspace_bytes(int64_t n, int32_t k_vol, int32_t batch_size,
+                                               const int32_t out_spatial[3]) {
+  int64_t used = 0;
+  carve(nullptr, layout(n, batch_size, out_spatial), k_vol, &used);
+  return used;
+}
+
+extern "C" int tsc_strided_count(const int32_t* coords, int64_t n, int32_t batch_size,
+                                 const int32_t spatial[3], const int32_t ksize[3],
+                                 const int32_t stride[3], const int32_t padding[3],
+                                 const int32_t dilation[3], const int32_t out_spatial[3], void* ws,
+                                 int64_t ws_bytes, int32_t* counts, tsc_stream_t stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  StridedGeom g;
+  int rc = check_geom(n, batch_size, spatial, ksize, stride, padding, dilation, out_spatial, &g);
+  if (rc) return rc;
+  const int K = ksize[0] * ksize[1] * ksize[2];
+  TSC_REQUIRE(K <= 4096, "strided: kernel volume %d too large", K);
+  const Layout L = layout(n, batch_size, out_spatial);
+  int64_t need = 0;
+  carve(nullptr, L, K, &need);
+  TSC_REQUIRE(ws && ws_bytes >= need, "strided: workspace too small (%lld < %lld)",
+              (long long)ws_bytes, (long long)need);
+  TSC_REQUIRE(counts != nullptr, "strided: counts is null");
+  Buffers b = carve(ws, L, K, nullptr);
+  if ((rc = fill_u32(reinterpret_cast<uint32_t*>(counts), K + 2, 0u, s))) return rc;
+  if ((rc = fill_u32(b.bitmap, L.nwords, 0u, s))) return rc;
+  if (n == 0) return 0;
+  TSC_REQUIRE(coords != nullptr, "strided: coords is null");
+  if (K > 64 && (rc = fill_u32(reinterpret_cast<uint32_t*>(b.blk_cnt), L.nblk * K, 0u, s)))
+    return rc;
+  strided_mark_kernel<<<L.nblk, kRows, 0, s>>>(reinterpret_cast<const int4*>(coords), n, K, g,
+                                               b.bitmap, b.blk_cnt, (int)L.nblk, counts + K + 1);
+  TSC_LAUNCH_CHECK("strided_mark");
+  if ((rc = scan_slot_blocks(b.blk_cnt, b.blk_off, counts, K, (int)L.nblk, s))) return rc;
+  return exclusive_scan_u32(b.bitmap, 0, L.nwords, b.wprefix, counts + K, b.scratch, s);
+}
+
+extern "C" int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_size,
+                                const int32_t spatial[3], const int32_t ksize[3],
+                                const int32_t stride[3], const int32_t padding[3],
+                                const int32_t dilation[3], const int32_t out_spatial[3], void* ws,
+                                int64_t ws_bytes, int64_t n_out, int32_t* out_coords, int32_t* nbr,
+                                int32_t* pairs_in, int32_t* pairs_out, tsc_stream_t stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  StridedGeom g;
+  int rc = check_geom(n, batch_size, spatial, ksize, stride, padding, dilation, out_spatial, &g);
+  if (rc) return rc;
+  const int K = ksize[0] * ksize[1] * ksize[2];
+  const Layout L = layout(n, batch_size, out_spatial);
+  int64_t need = 0;
+  carve(nullptr, L, K, &need);
+  TSC_REQUIRE(ws && ws_bytes >= need, "strided: workspace too small");
+  TSC_REQUIRE(n_out >= 0 && n_out <= L.cells, "strided: n_out=%lld invalid", (long long)n_out);
+  if (n == 0 || n_out == 0) return 0;
+  TSC_REQUIRE(coords && out_coords && nbr && pairs_in && pairs_out, "strided: null pointer");
+  Buffers b = carve(ws, L, K, nullptr);
+  strided_emit_kernel<<<ceil_div(L.nwords, 256), 256, 0, s>>>(b.bitmap, b.wprefix, L.nwords, g,
+                                                             reinterpret_cast<int4*>(out_coords),
+                                                             n_out);
+  TSC_LAUNCH_CHECK("strided_emit");
+  if ((rc = fill_u32(reinterpret_cast<uint32_t*>(nbr), n_out * K, 0xffffffffu, s))) return rc;
+  strided_fill_kernel<<<L.nblk, kRows, 0, s>>>(reinterpret_cast<const int4*>(coords), n, K, g,
+                                               b.bitmap, b.wprefix, b.blk_off, (int)L.nblk, n, n_out,
+                                               nbr, pairs_in, pairs_out);
+  TSC_LAUNCH_CHECK("strided_fill");
+  return 0;
+}

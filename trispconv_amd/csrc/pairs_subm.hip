@@ -1,0 +1,240 @@
+// Submanifold indice pairs on the GPU.
+//
+// Reference algorithm: trispconv/pytorch/indices.py:67-140.  For slot k (kernel
+// offsets in (kz,ky,kx) lexicographic order, measured from the kernel centre)
+// and every output row r in ascending order, the pair (in = j, out = r) exists
+// when coord(r) + offset_k lies inside the grid and is the coordinate of row j.
+//
+// MI355X design: the reference's dense grid-sized lookup table (:54-64) becomes
+// an open-addressing hash of 2N..4N 64-bit slots (8-16 MB at 500k voxels, so
+// it stays in L2 / Infinity Cache).  One probe kernel writes the [N][K]
+// neighbour map the convolution consumes and per-(slot, block) hit counts;
+// a per-slot scan of those counts gives each block its write offset, and a
+// fill kernel emits every slot's pair list in ascending output-row order with
+// wave ballots, so the lists come out in exactly the reference's order.
+#include "common.hpp"
+
+namespace tsc {
+namespace {
+
+constexpr int kRows = 256;  // output rows per block in probe and fill
+
+struct SubmGeom {
+  int32_t B;
+  Box shape, ks, dil;
+  uint32_t mask;  // hash capacity - 1
+};
+
+__device__ __forceinline__ bool in_grid(const SubmGeom& g, int b, int z, int y, int x) {
+  return b >= 0 && b < g.B && z >= 0 && z < g.shape.z && y >= 0 && y < g.shape.y && x >= 0 &&
+         x < g.shape.x;
+}
+
+__device__ __forceinline__ uint32_t cell_key(const SubmGeom& g, int b, int z, int y, int x) {
+  return ((static_cast<uint32_t>(b) * g.shape.z + z) * g.shape.y + y) * g.shape.x + x;
+}
+
+__global__ void __launch_bounds__(256) subm_insert_kernel(const int4* __restrict__ coords,
+                                                          int64_t n, SubmGeom g,
+                                                          unsigned long long* table,
+                                                          int32_t* status) {
+  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  const int4 c = coords[r];  // (b, z, y, x)
+  if (!in_grid(g, c.x, c.y, c.z, c.w)) {
+    atomicOr(status, (c.x < 0 || c.x >= g.B) ? TSC_FLAG_BATCH_OUT_OF_RANGE
+                                              : TSC_FLAG_COORD_OUT_OF_GRID);
+    return;
+  }
+  hash_insert(table, g.mask, cell_key(g, c.x, c.y, c.z, c.w), static_cast<uint32_t>(r));
+}
+
+// One thread per output row; K lookups each.  With STAGED the block's
+// [kRows][K] slice of the map is assembled in LDS and written out coalesced.
+template <bool STAGED>
+__global__ void __launch_bounds__(kRows) subm_probe_kernel(const int4* __restrict__ coords,
+                                                           int64_t n, int K, SubmGeom g,
+                                                           const unsigned long long* __restrict__ table,
+                                                           int32_t* __restrict__ nbr,
+                                                           int32_t* __restrict__ blk_cnt,
+                                                           int nblk) {
+  extern __shared__ int32_t s_nbr[];           // [kRows][K] when STAGED
+  __shared__ int32_t s_cnt[kRows / kWave][64];  // per wave, per slot (K <= 64 counted here)
+  const int t = threadIdx.x;
+  const int w = t / kWave;
+  const int64_t row0 = blockIdx.x * (int64_t)kRows;
+  const int64_t r = row0 + t;
+  const bool valid = r < n;
+  int4 c = valid ? coords[r] : make_int4(-1, 0, 0, 0);
+  const bool self_ok = valid && in_grid(g, c.x, c.y, c.z, c.w);
+
+  for (int k = 0; k < K; ++k) {
+    int kz, ky, kx;
+    slot_to_zyx(k, g.ks, kz, ky, kx);
+    const int z = c.y + (kz - g.ks.z / 2) * g.dil.z;
+    const int y = c.z + (ky - g.ks.y / 2) * g.dil.y;
+    const int x = c.w + (kx - g.ks.x / 2) * g.dil.x;
+    int32_t j = -1;
+    if (self_ok && in_grid(g, c.x, z, y, x)) j = hash_find(table, g.mask, cell_key(g, c.x, z, y, x));
+    const uint64_t hits = __ballot(j >= 0);
+    if (STAGED) {
+      s_nbr[t * K + k] = j;
+    } else if (valid) {
+      nbr[r * K + k] = j;
+    }
+    // per-wave hit count of this slot, accumulated through LDS
+    if (__lane_id() == 0) {
+      if (k < 64) {
+        s_cnt[w][k] = __popcll(hits);
+      } else {
+        // K > 64: fold straight into the global count
+        atomicAdd(&blk_cnt[(int64_t)k * nblk + blockIdx.x], (int)__popcll(hits));
+      }
+    }
+  }
+  __syncthreads();
+  if (t < K && t < 64) {
+    int s = 0;
+#pragma unroll
+    for (int ww = 0; ww < kRows / kWave; ++ww) s += s_cnt[ww][t];
+    blk_cnt[(int64_t)t * nblk + blockIdx.x] = s;
+  }
+  if (STAGED) {
+    const int64_t rows = (n - row0) < kRows ? (n - row0) : kRows;
+    const int64_t total = rows * K;
+    int32_t* dst = nbr + row0 * K;
+    for (int64_t i = t; i < total; i += kRows) dst[i] = s_nbr[i];
+  }
+}
+
+// Emits pairs_in/pairs_out for every slot from the neighbour map.  Rows keep
+// ascending order inside a slot: blocks own consecutive row ranges (block
+// offsets from the per-slot scan), waves own consecutive sub-ranges (offsets
+// from per-wave counts) and lanes are ranked by ballot.
+template <bool STAGED>
+__global__ void __launch_bounds__(kRows) subm_fill_kernel(const int32_t* __restrict__ nbr, int64_t n,
+                                                          int K,
+                                                          const int32_t* __restrict__ blk_off,
+                                                          int nblk, int64_t cap,
+                                                          int32_t* __restrict__ pairs_in,
+                                                          int32_t* __restrict__ pairs_out) {
+  extern __shared__ int32_t s_nbr[];
+  __shared__ int32_t s_wcnt[kRows / kWave][64];
+  const int t = threadIdx.x;
+  const int w = t / kWave;
+  const int64_t row0 = blockIdx.x * (int64_t)kRows;
+  const int64_t r = row0 + t;
+  const bool valid = r < n;
+  if (STAGED) {
+    const int64_t rows = (n - row0) < kRows ? (n - row0) : kRows;
+    const int64_t total = rows * K;
+    const int32_t* src = nbr + row0 * K;
+    for (int64_t i = t; i < total; i += kRows) s_nbr[i] = src[i];
+    __syncthreads();
+  }
+  for (int kb = 0; kb < K; kb += 64) {
+    const int kend = (K - kb) < 64 ? (K - kb) : 64;
+    for (int kk = 0; kk < kend; ++kk) {
+      const int k = kb + kk;
+      const int32_t j = valid ? (STAGED ? s_nbr[t * K + k] : nbr[r * K + k]) : -1;
+      const uint64_t hits = __ballot(j >= 0);
+      if (__lane_id() == 0) s_wcnt[w][kk] = __popcll(hits);
+    }
+    __syncthreads();
+    for (int kk = 0; kk < kend; ++kk) {
+      const int k = kb + kk;
+      const int32_t j = valid ? (STAGED ? s_nbr[t * K + k] : nbr[r * K + k]) : -1;
+      const uint64_t hits = __ballot(j >= 0);
+      int base = blk_off[(int64_t)k * nblk + blockIdx.x];
+      for (int ww = 0; ww < w; ++ww) base += s_wcnt[ww][kk];
+      const int64_t slot_pos = base + rank_in_wave(hits);
+      if (j >= 0 && slot_pos < cap) {  // slot_pos < cap holds by construction
+        pairs_in[(int64_t)k * cap + slot_pos] = j;
+        pairs_out[(int64_t)k * cap + slot_pos] = static_cast<int32_t>(r);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+}  // namespace
+
+static int64_t subm_capacity(int64_t n) {
+  int64_t cap = 1024;
+  while (cap < 2 * n) cap <<= 1;
+  return cap;
+}
+
+// LDS staging of a block's map slice while it stays within 48 KB.
+static bool staged(int K) { return K <= 48; }
+
+}  // namespace tsc
+
+using namespace tsc;
+
+extern "C" int64_t tsc_subm_workspace_bytes(int64_t n, int32_t k_vol) {
+  Carver c(nullptr);
+  const int64_t nblk = ceil_div(n > 0 ? n : 1, kRows);
+  c.take<unsigned long long>(subm_capacity(n));
+  c.take<int32_t>(nblk * k_vol);  // block counts
+  c.take<int32_t>(nblk * k_vol);  // block offsets
+  return c.used;
+}
+
+extern "C" int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_size,
+                              const int32_t spatial[3], const int32_t ksize[3],
+                              const int32_t dilation[3], void* ws, int64_t ws_bytes, int32_t* nbr,
+                              int32_t* pairs_in, int32_t* pairs_out, int32_t* counts,
+                              tsc_stream_t stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  TSC_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "subm: n=%lld out of range", (long long)n);
+  TSC_REQUIRE(batch_size > 0, "subm: batch_size must be positive");
+  const Box shape = box(spatial), ks = box(ksize), dil = box(dilation);
+  TSC_REQUIRE(shape.z > 0 && shape.y > 0 && shape.x > 0, "subm: spatial shape must be positive");
+  TSC_REQUIRE(ks.z > 0 && ks.y > 0 && ks.x > 0 && dil.z > 0 && dil.y > 0 && dil.x > 0,
+              "subm: kernel size and dilation must be positive");
+  const int64_t cells = (int64_t)batch_size * shape.z * shape.y * shape.x;
+  TSC_REQUIRE(cells < 0xffffffffll,
+              "subm: batch*D*H*W = %lld cells exceeds the 32-bit cell id range", (long long)cells);
+  const int K = ks.z * ks.y * ks.x;
+  TSC_REQUIRE(K <= 4096, "subm: kernel volume %d too large", K);
+  TSC_REQUIRE(ws_bytes >= tsc_subm_workspace_bytes(n, K), "subm: workspace too small");
+  TSC_REQUIRE(counts != nullptr, "subm: counts is null");
+
+  int rc = fill_u32(reinterpret_cast<uint32_t*>(counts), K + 1, 0u, s);
+  if (rc) return rc;
+  if (n == 0) return 0;
+  TSC_REQUIRE(coords && nbr && pairs_in && pairs_out && ws, "subm: null pointer");
+
+  const int64_t cap = subm_capacity(n);
+  const int nblk = static_cast<int>(ceil_div(n, kRows));
+  Carver c(ws);
+  auto* table = c.take<unsigned long long>(cap);
+  auto* blk_cnt = c.take<int32_t>((int64_t)nblk * K);
+  auto* blk_off = c.take<int32_t>((int64_t)nblk * K);
+
+  SubmGeom g{batch_size, shape, ks, dil, static_cast<uint32_t>(cap - 1)};
+  if ((rc = fill_u64(table, cap, kEmpty, s))) return rc;
+  if (K > 64 && (rc = fill_u32(reinterpret_cast<uint32_t*>(blk_cnt), (int64_t)nblk * K, 0u, s)))
+    return rc;
+  subm_insert_kernel<<<ceil_div(n, 256), 256, 0, s>>>(reinterpret_cast<const int4*>(coords), n, g,
+                                                      table, counts + K);
+  TSC_LAUNCH_CHECK("subm_insert");
+  const size_t lds = staged(K) ? (size_t)kRows * K * sizeof(int32_t) : 0;
+  if (staged(K))
+    subm_probe_kernel<true><<<nblk, kRows, lds, s>>>(reinterpret_cast<const int4*>(coords), n, K,
+                                                     g, table, nbr, blk_cnt, nblk);
+  else
+    subm_probe_kernel<false><<<nblk, kRows, 0, s>>>(reinterpret_cast<const int4*>(coords), n, K,
+                                                    g, table, nbr, blk_cnt, nblk);
+  TSC_LAUNCH_CHECK("subm_probe");
+  if ((rc = scan_slot_blocks(blk_cnt, blk_off, counts, K, nblk, s))) return rc;
+  if (staged(K))
+    subm_fill_kernel<true><<<nblk, kRows, lds, s>>>(nbr, n, K, blk_off, nblk, n, pairs_in,
+                                                    pairs_out);
+  else
+    subm_fill_kernel<false><<<nblk, kRows, 0, s>>>(nbr, n, K, blk_off, nblk, n, pairs_in,
+                                                   pairs_out);
+  TSC_LAUNCH_CHECK("subm_fill");
+  return 0;
+}

@@ -1,0 +1,65 @@
+"""``sparse_conv_forward`` — one fused HIP launch over every kernel slot.
+
+Contract of trispconv/pytorch/functional.py:14-51 (GPU semantics): the output
+is zero-initialised, slot contributions feat[pairs_in[k]] @ W[k] are added to
+rows pairs_out[k] for k ascending in fp32 (fp16/bf16 operands upcast,
+:34-36), the bias is added in fp32 and the result is rounded once to the
+features' dtype (:48-51).  The per-slot loop of the reference (:40-46) and its
+Triton kernel become ``tsc_conv_forward``.
+"""
+from __future__ import annotations
+
+from typing import Optional, Union
+
+import torch
+
+from .. import _lib as L
+from .indices import IndiceData
+from .weight import PackedWeight, pack_weight
+
+
+def _run(features: torch.Tensor, packed: PackedWeight, bias: Optional[torch.Tensor],
+         nbr: Optional[torch.Tensor], order: Optional[torch.Tensor], n_out: int) -> torch.Tensor:
+    L.require_gpu(features, "sparse_conv_forward")
+    feats = features.contiguous()
+    if feats.data_ptr() % 16:
+        feats = feats.clone()  # rows are read as 16-byte vectors
+    if feats.dtype != packed.dtype:
+        raise TypeError(f"weight packed for {packed.dtype}, features are {feats.dtype}")
+    if feats.shape[1] != packed.c_in:
+        raise ValueError(f"features have {feats.shape[1]} channels, weight expects {packed.c_in}")
+    out = torch.empty((n_out, packed.c_out), dtype=feats.dtype, device=feats.device)
+    b = None
+    if bias is not None:
+        b = bias.detach().to(feats.device).contiguous()
+        if b.numel() != packed.c_out:
+            raise ValueError(f"bias has {b.numel()} entries, expected {packed.c_out}")
+    lib = L.lib()
+    L.check(lib.tsc_conv_forward(
+        feats.data_ptr(), L.dtype_code(feats.dtype), feats.shape[0], packed.c_in,
+        packed.data.data_ptr(), L.ptr(b), L.dtype_code(b.dtype) if b is not None else 0,
+        L.ptr(nbr), L.ptr(order), n_out, packed.k_vol, packed.c_out, out.data_ptr(),
+        L.stream_of(feats)), "sparse_conv_forward")
+    return out
+
+
+def sparse_conv_forward(features: torch.Tensor, weight: Union[torch.Tensor, PackedWeight],
+                        bias: Optional[torch.Tensor], indice_data: IndiceData,
+                        N_out: int) -> torch.Tensor:
+    """Sparse convolution forward; ``weight`` is (K, C_in, C_out) or a PackedWeight."""
+    L.require_gpu(features, "sparse_conv_forward")
+    if not isinstance(weight, PackedWeight):
+        K, c_in, c_out = weight.shape
+        weight = pack_weight(weight, (K, 1, 1), c_in, c_out, features.dtype)
+    nbr = indice_data.neighbour_map(N_out, features.device)
+    order = indice_data.execution_order(N_out, features.device)
+    return _run(features, weight, bias, nbr, order, N_out)
+
+
+def dense_forward(features: torch.Tensor, weight: PackedWeight,
+                  bias: Optional[torch.Tensor]) -> torch.Tensor:
+    """features @ W[0] (+ bias) through the same kernel with the identity map.
+
+    Used by the inverse 1x1x1 path (modules.py:162-173).
+    """
+    return _run(features, weight, bias, None, None, features.shape[0])

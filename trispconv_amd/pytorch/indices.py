@@ -1,0 +1,275 @@
+"""Indice-pair generation on the GPU (submanifold, strided, inverse).
+
+Public names and semantics follow trispconv/pytorch/indices.py:10-259 and the
+inverse remap of modules.py:175-212; the work runs in libtrispconv_hip.so.
+
+``IndiceData`` keeps the reference's fields.  Pair lists are stored on the
+device as padded int32 tables (slot k owns ``[k, :pair_num[k]]``) next to the
+output-major neighbour map the convolution reads; the reference-style lists
+of K int64 tensors are materialised on first access to ``pairs_in`` /
+``pairs_out``.  ``pair_num`` is a CPU int64 tensor, as in the reference
+(indices.py:131), read with the one device-to-host copy each build makes.
+"""
+from __future__ import annotations
+
+from typing import List, Optional, Sequence, Tuple
+
+import torch
+
+from .. import _lib as L
+
+__all__ = [
+    "IndiceData",
+    "generate_subm_indice_pairs",
+    "generate_strided_indice_pairs",
+    "generate_inverse_indice_pairs",
+]
+
+# Below this many output rows the execution-order sort costs more than it saves.
+_PLAN_MIN_ROWS = 2048
+
+
+def _to3(x) -> Tuple[int, int, int]:
+    """indices.py:26-29."""
+    if isinstance(x, int):
+        return (x, x, x)
+    return tuple(int(v) for v in x)
+
+
+def _output_spatial_shape(in_shape, kernel_size, stride, padding, dilation) -> Tuple[int, int, int]:
+    """(S + 2p - d(k-1) - 1) // s + 1 per axis — indices.py:32-42."""
+    return tuple((s + 2 * p - d * (k - 1) - 1) // st + 1
+                 for s, k, st, p, d in zip(in_shape, kernel_size, stride, padding, dilation))
+
+
+def _encode_coords(indices: torch.Tensor, D: int, H: int, W: int) -> torch.Tensor:
+    """(b, z, y, x) -> b*DHW + z*HW + y*W + x as int64 — indices.py:45-51."""
+    i = indices.long()
+    return i[:, 0] * (D * H * W) + i[:, 1] * (H * W) + i[:, 2] * W + i[:, 3]
+
+
+class IndiceData:
+    """Pairs of one layer (indices.py:10-23), backed by device tables."""
+
+    def __init__(self, out_indices: torch.Tensor, pairs_in: Optional[List[torch.Tensor]],
+                 pairs_out: Optional[List[torch.Tensor]], pair_num: torch.Tensor,
+                 input_indices: torch.Tensor, input_spatial_shape, output_spatial_shape,
+                 kernel_size, stride, padding, dilation, subm: bool):
+        self.out_indices = out_indices
+        self.input_indices = input_indices
+        self.input_spatial_shape = tuple(input_spatial_shape)
+        self.output_spatial_shape = tuple(output_spatial_shape)
+        self.kernel_size = tuple(kernel_size)
+        self.stride = tuple(stride)
+        self.padding = tuple(padding)
+        self.dilation = tuple(dilation)
+        self.subm = subm
+        self.pair_num = pair_num
+        self._pairs_in = pairs_in
+        self._pairs_out = pairs_out
+        # device tables
+        self._pin: Optional[torch.Tensor] = None    # [K][cap] int32
+        self._pout: Optional[torch.Tensor] = None   # [K][cap] int32
+        self._cnt: Optional[torch.Tensor] = None    # [K] int32 on the device
+        self._nbr: Optional[torch.Tensor] = None    # [n_out][K] int32
+        self._order: Optional[torch.Tensor] = None  # [n_out] int32 execution order
+        self._inverse_cache: Optional["IndiceData"] = None
+
+    # --------------------------------------------------- construction
+    @classmethod
+    def _from_tables(cls, *, out_indices, input_indices, input_spatial_shape, output_spatial_shape,
+                     kernel_size, stride, padding, dilation, subm, pin, pout, cnt_dev,
+                     pair_num, nbr) -> "IndiceData":
+        d = cls(out_indices, None, None, pair_num, input_indices, input_spatial_shape,
+                output_spatial_shape, kernel_size, stride, padding, dilation, subm)
+        d._pin, d._pout, d._cnt, d._nbr = pin, pout, cnt_dev, nbr
+        return d
+
+    # --------------------------------------------------- reference fields
+    @property
+    def K(self) -> int:
+        k = self.kernel_size
+        return int(k[0]) * int(k[1]) * int(k[2])
+
+    @property
+    def pairs_in(self) -> List[torch.Tensor]:
+        if self._pairs_in is None:
+            self._pairs_in = self._slot_views(self._pin)
+        return self._pairs_in
+
+    @pairs_in.setter
+    def pairs_in(self, value: List[torch.Tensor]) -> None:
+        self._pairs_in = value
+        self._drop_tables()
+
+    @property
+    def pairs_out(self) -> List[torch.Tensor]:
+        if self._pairs_out is None:
+            self._pairs_out = self._slot_views(self._pout)
+        return self._pairs_out
+
+    @pairs_out.setter
+    def pairs_out(self, value: List[torch.Tensor]) -> None:
+        self._pairs_out = value
+        self._drop_tables()
+
+    def _slot_views(self, table: Optional[torch.Tensor]) -> List[torch.Tensor]:
+        if table is None:
+            raise RuntimeError("IndiceData has neither pair lists nor device tables")
+        counts = [int(c) for c in self.pair_num.tolist()]
+        return [table[k, :c].long() for k, c in enumerate(counts)]
+
+    def _drop_tables(self) -> None:
+        self._pin = self._pout = self._cnt = self._nbr = self._order = None
+        self._inverse_cache = None
+
+    # --------------------------------------------------- convolution inputs
+    def neighbour_map(self, n_out: int, device) -> torch.Tensor:
+        """[n_out][K] int32: input row feeding output row o through slot k, or -1."""
+        if self._nbr is None:
+            # user-built lists: scatter them into a map (each slot maps an
+            # output at most once, as every generator guarantees)
+            K = self.K
+            nbr = torch.full((n_out, K), -1, dtype=torch.int32, device=device)
+            for k, (pi, po) in enumerate(zip(self.pairs_in, self.pairs_out)):
+                if pi.numel():
+                    nbr[po.to(device).long(), k] = pi.to(device).int()
+            self._nbr = nbr
+        return self._nbr
+
+    def execution_order(self, n_out: int, device) -> Optional[torch.Tensor]:
+        """Rows sorted by their slot-occupancy mask (built once, cached)."""
+        if n_out < _PLAN_MIN_ROWS:
+            return None
+        if self._order is None:
+            nbr = self.neighbour_map(n_out, device)
+            lib = L.lib()
+            ws = L.workspace(lib.tsc_plan_workspace_bytes(n_out, self.K), device)
+            order = torch.empty(n_out, dtype=torch.int32, device=device)
+            L.check(lib.tsc_conv_plan(nbr.data_ptr(), n_out, self.K, ws.data_ptr(), ws.numel(),
+                                      order.data_ptr(), L.stream_of(nbr)), "conv plan")
+            self._order = order
+        return self._order
+
+    def __repr__(self) -> str:
+        return (f"IndiceData(subm={self.subm}, K={self.K}, n_out={len(self.out_indices)}, "
+                f"pairs={int(self.pair_num.sum()) if self.pair_num.numel() else 0})")
+
+
+def _coords(indices: torch.Tensor, what: str) -> torch.Tensor:
+    L.require_gpu(indices, what)
+    if indices.ndim != 2 or indices.shape[1] != 4:
+        raise ValueError(f"{what}: indices must be (N, 4) (b, z, y, x), got {tuple(indices.shape)}")
+    coords = indices.to(torch.int32).contiguous()
+    if coords.data_ptr() % 16:
+        coords = coords.clone()  # the kernels read each row as one 16-byte vector
+    return coords
+
+
+def _raise_status(status: int, what: str) -> None:
+    if status & L.FLAG_BATCH_OUT_OF_RANGE:
+        raise IndexError(f"{what}: batch index outside [0, batch_size)")
+    if status & L.FLAG_COORD_OUT_OF_GRID:
+        raise IndexError(f"{what}: coordinate outside the spatial shape")
+
+
+def generate_subm_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size: int, kernel_size,
+                               dilation=1) -> IndiceData:
+    """Submanifold pairs: output set == input set (indices.py:67-140)."""
+    coords = _coords(indices, "generate_subm_indice_pairs")
+    ks, dil = _to3(kernel_size), _to3(dilation)
+    shape = tuple(int(v) for v in spatial_shape)
+    K = ks[0] * ks[1] * ks[2]
+    n = coords.shape[0]
+    dev = coords.device
+    lib = L.lib()
+    ws = L.workspace(lib.tsc_subm_workspace_bytes(n, K), dev)
+    nbr = torch.empty((n, K), dtype=torch.int32, device=dev)
+    pin = torch.empty((K, n), dtype=torch.int32, device=dev)
+    pout = torch.empty((K, n), dtype=torch.int32, device=dev)
+    counts = torch.empty(K + 1, dtype=torch.int32, device=dev)
+    L.check(lib.tsc_subm_pairs(coords.data_ptr(), n, int(batch_size), L.i3(shape), L.i3(ks),
+                               L.i3(dil), ws.data_ptr(), ws.numel(), nbr.data_ptr(),
+                               pin.data_ptr(), pout.data_ptr(), counts.data_ptr(),
+                               L.stream_of(coords)), "generate_subm_indice_pairs")
+    host = counts.cpu()
+    _raise_status(int(host[K]), "generate_subm_indice_pairs")
+    return IndiceData._from_tables(
+        out_indices=indices, input_indices=indices, input_spatial_shape=spatial_shape,
+        output_spatial_shape=spatial_shape, kernel_size=ks, stride=(1, 1, 1),
+        padding=(0, 0, 0), dilation=dil, subm=True, pin=pin, pout=pout, cnt_dev=counts[:K],
+        pair_num=host[:K].long(), nbr=nbr)
+
+
+def generate_strided_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size: int,
+                                  kernel_size, stride=1, padding=0, dilation=1) -> IndiceData:
+    """Strided pairs and the sorted new active set (indices.py:143-259)."""
+    coords = _coords(indices, "generate_strided_indice_pairs")
+    ks, st, pd, dil = _to3(kernel_size), _to3(stride), _to3(padding), _to3(dilation)
+    shape = tuple(int(v) for v in spatial_shape)
+    out_shape = _output_spatial_shape(shape, ks, st, pd, dil)
+    K = ks[0] * ks[1] * ks[2]
+    n = coords.shape[0]
+    dev = coords.device
+    if min(out_shape) <= 0:
+        raise ValueError(f"generate_strided_indice_pairs: empty output shape {out_shape}")
+    lib = L.lib()
+    ws = L.workspace(lib.tsc_strided_workspace_bytes(n, K, int(batch_size), L.i3(out_shape)), dev)
+    counts = torch.empty(K + 2, dtype=torch.int32, device=dev)
+    geo = (L.i3(shape), L.i3(ks), L.i3(st), L.i3(pd), L.i3(dil), L.i3(out_shape))
+    stream = L.stream_of(coords)
+    L.check(lib.tsc_strided_count(coords.data_ptr(), n, int(batch_size), *geo, ws.data_ptr(),
+                                  ws.numel(), counts.data_ptr(), stream),
+            "generate_strided_indice_pairs")
+    host = counts.cpu()
+    _raise_status(int(host[K + 1]), "generate_strided_indice_pairs")
+    n_out = int(host[K])
+    out_coords = torch.empty((n_out, 4), dtype=torch.int32, device=dev)
+    nbr = torch.empty((n_out, K), dtype=torch.int32, device=dev)
+    pin = torch.empty((K, n), dtype=torch.int32, device=dev)
+    pout = torch.empty((K, n), dtype=torch.int32, device=dev)
+    L.check(lib.tsc_strided_fill(coords.data_ptr(), n, int(batch_size), *geo, ws.data_ptr(),
+                                 ws.numel(), n_out, out_coords.data_ptr(), nbr.data_ptr(),
+                                 pin.data_ptr(), pout.data_ptr(), stream),
+            "generate_strided_indice_pairs")
+    return IndiceData._from_tables(
+        out_indices=out_coords, input_indices=indices, input_spatial_shape=shape,
+        output_spatial_shape=out_shape, kernel_size=ks, stride=st, padding=pd, dilation=dil,
+        subm=False, pin=pin, pout=pout, cnt_dev=counts[:K], pair_num=host[:K].long(), nbr=nbr)
+
+
+def generate_inverse_indice_pairs(fwd: IndiceData) -> IndiceData:
+    """Pairs of the inverse of a strided layer (modules.py:175-212).
+
+    Output rows: forward input rows with at least one forward pair, ascending;
+    slot k reads forward outputs pairs_out[k] and writes the compact id of
+    forward input pairs_in[k]; pair_num is the forward's.
+    """
+    if fwd._pin is None:
+        raise ValueError("inverse pairs need a forward IndiceData built on the GPU")
+    dev = fwd._pin.device
+    K = fwd.K
+    cap = fwd._pin.shape[1]
+    n_in = len(fwd.input_indices)
+    lib = L.lib()
+    ws = L.workspace(lib.tsc_inverse_workspace_bytes(n_in), dev)
+    counts = torch.empty(1, dtype=torch.int32, device=dev)
+    stream = L.stream_of(fwd._pin)
+    L.check(lib.tsc_inverse_count(fwd._pin.data_ptr(), fwd._cnt.data_ptr(), K, cap, n_in,
+                                  ws.data_ptr(), ws.numel(), counts.data_ptr(), stream),
+            "inverse pairs")
+    n_out = int(counts.cpu()[0])
+    in_coords = _coords(fwd.input_indices, "inverse pairs")
+    out_coords = torch.empty((n_out, 4), dtype=torch.int32, device=dev)
+    nbr = torch.empty((n_out, K), dtype=torch.int32, device=dev)
+    inv_pout = torch.empty((K, cap), dtype=torch.int32, device=dev)
+    L.check(lib.tsc_inverse_fill(fwd._pin.data_ptr(), fwd._pout.data_ptr(), fwd._cnt.data_ptr(), K,
+                                 cap, in_coords.data_ptr(), n_in, ws.data_ptr(), ws.numel(), n_out,
+                                 out_coords.data_ptr(), nbr.data_ptr(), inv_pout.data_ptr(),
+                                 stream), "inverse pairs")
+    return IndiceData._from_tables(
+        out_indices=out_coords, input_indices=fwd.out_indices,
+        input_spatial_shape=fwd.output_spatial_shape,
+        output_spatial_shape=fwd.input_spatial_shape, kernel_size=fwd.kernel_size,
+        stride=fwd.stride, padding=fwd.padding, dilation=fwd.dilation, subm=False,
+        pin=fwd._pout, pout=inv_pout, cnt_dev=fwd._cnt, pair_num=fwd.pair_num, nbr=nbr)
