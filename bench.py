@@ -43,6 +43,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="subm128_surface500k")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="first run one device-to-device copy of this many MiB (a known-size "
+                         "kernel to scale FETCH_SIZE / WRITE_SIZE counters by)")
     ap.add_argument("--verbose", action="store_true")
     return ap.parse_args()
 
@@ -96,6 +99,12 @@ def main():
     from trispconv_amd import workloads
 
     dev = torch.device("cuda:0")
+    if args.copy_probe_mib:
+        src = torch.ones(args.copy_probe_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     w = workloads.make_workload(args.workload)
     layer = w.layers[0]
     dt = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}[w.dtype]

@@ -14,8 +14,8 @@
  *   - Coordinates are int32 rows (b, z, y, x).  A slot k numbers the kernel
  *     offsets (kz, ky, kx) lexicographically: k = (kz*kH + ky)*kW + kx.
  *   - Pair tables are "padded": slot k owns entries [k*cap, k*cap + cnt[k]).
- *   - A neighbour map `nbr` is [n_out][K] int32: the input row that feeds
- *     output row o through slot k, or -1.
+ *   - A neighbour map `nbr` is slot-major [K][n_out] int32: entry (k, o) is
+ *     the input row that feeds output row o through slot k, or -1.
  *
  * Re-entrant; the only global state is the thread-local error string.
  */
@@ -52,7 +52,7 @@ TSC_API int tsc_abi_version(void);
  * (trispconv/pytorch/indices.py:67-140) including its dense lookup table
  * (:54-64), which becomes an open-addressing hash of 2N..4N slots.
  *
- * Writes nbr [n][K]; pairs_in/pairs_out [K][n] (slot k: output rows r in
+ * Writes nbr [K][n]; pairs_in/pairs_out [K][n] (slot k: output rows r in
  * ascending order, input row of each, exactly the reference's lists);
  * counts [K+1]: counts[k] = pairs in slot k, counts[K] = status flags.
  * ------------------------------------------------------------------------ */
@@ -70,7 +70,7 @@ TSC_API int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_size,
  * Two phases around the one host read of the counts:
  *   count: counts [K+2]: counts[k] = pairs in slot k, counts[K] = n_out,
  *          counts[K+1] = status flags.
- *   fill:  out_coords [n_out][4] sorted by (b,z,y,x); nbr [n_out][K];
+ *   fill:  out_coords [n_out][4] sorted by (b,z,y,x); nbr [K][n_out];
  *          pairs_in/pairs_out [K][n] (slot k: input rows ascending, output
  *          rank of each).  The workspace must be the one `count` filled.
  * ------------------------------------------------------------------------ */
@@ -94,7 +94,7 @@ TSC_API int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_siz
  * tables (cap = forward n_in) and device pair counts.
  *   count: counts[0] = number of participating forward inputs (= n_out).
  *   fill:  out_coords [n_out][4] = forward input coords of participating
- *          rows in ascending row order; nbr [n_out][K];
+ *          rows in ascending row order; nbr [K][n_out];
  *          inv_pairs_out [K][cap] = compact id of each forward input
  *          (the inverse's pairs_in are the forward's pairs_out, unchanged).
  * ------------------------------------------------------------------------ */
@@ -109,14 +109,18 @@ TSC_API int tsc_inverse_fill(const int32_t* fwd_pairs_in, const int32_t* fwd_pai
                      tsc_stream_t stream);
 
 /* ------------------------------------------------------------------------
- * Execution order for the convolution: output rows sorted (stably) by the
- * set of slots that feed them, so that rows processed together need the
- * same weight slices.  No reference counterpart (the reference runs slot
- * by slot); the order never changes any output value.
+ * Execution order for the convolution: output rows in Morton order, cut into
+ * regions of region_rows rows, each region sorted (stably) by the set of
+ * slots that feed its rows — rows processed together then need the same
+ * weight slices and gather nearby inputs.  No reference counterpart (the
+ * reference runs slot by slot); the order never changes any output value.
+ *   out_coords [n_out][4] are the output rows' (b, z, y, x).
  * ------------------------------------------------------------------------ */
 TSC_API int64_t tsc_plan_workspace_bytes(int64_t n_out, int32_t k_vol);
-TSC_API int tsc_conv_plan(const int32_t* nbr, int64_t n_out, int32_t k_vol, void* ws, int64_t ws_bytes,
-                  int32_t* order, tsc_stream_t stream);
+TSC_API int tsc_conv_plan(const int32_t* nbr, const int32_t* out_coords, int64_t n_out,
+                  int32_t k_vol, int32_t batch_size, const int32_t out_spatial[3] /* host */,
+                  int64_t region_rows, void* ws, int64_t ws_bytes, int32_t* order,
+                  tsc_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Weights.  Replaces normalize_spconv_weight (trispconv/pytorch/weight.py:8-50)
@@ -135,7 +139,7 @@ TSC_API int tsc_pack_weight(const void* w, int32_t w_dtype, int32_t layout, int3
  * Fused gather -> GEMM -> scatter over all slots in one launch.  Replaces
  * sparse_conv_forward (trispconv/pytorch/functional.py:14-51) and the Triton
  * per-slot kernel (triton_kernels.py:16-135).  Output-stationary: each
- * output row accumulates sum_k feat[nbr[o][k]] @ W[k] in fp32 with k
+ * output row accumulates sum_k feat[nbr[k][o]] @ W[k] in fp32 with k
  * ascending, adds bias in fp32 and is rounded once to `dtype`.  No atomics;
  * results are bitwise reproducible and independent of `order`.
  *   nbr == NULL means the identity map with k_vol == 1 (1x1x1 layers).

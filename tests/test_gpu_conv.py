@@ -244,13 +244,19 @@ def test_full_size_workloads(name):
         torch.cuda.synchronize()
 
 
-def test_plan_is_a_stable_sort_by_slot_mask():
+@pytest.mark.parametrize("row_bytes", [256, 2048])
+def test_plan_regions_are_mask_sorted_permutations(row_bytes):
+    """The execution order is a permutation of the output rows whose regions
+    (consecutive runs of region_rows rows) are each sorted by slot mask."""
     idx = _tiny(15, (40, 40, 40), 2, 6000)
     x = torch.from_numpy(idx).to(DEV)
     data = generate_subm_indice_pairs(x, (40, 40, 40), 2, 3)
     n = len(idx)
-    order = data.execution_order(n, x.device).cpu().numpy().astype(np.int64)
+    order = data.execution_order(n, x.device, row_bytes).cpu().numpy().astype(np.int64)
+    region = data._order_region
+    assert np.array_equal(np.sort(order), np.arange(n))
     nbr = data.neighbour_map(n, x.device).cpu().numpy()
-    mask = ((nbr >= 0).astype(np.int64) << np.arange(27)).sum(1)
-    expect = np.lexsort((np.arange(n), mask))
-    assert np.array_equal(order, expect)
+    mask = ((nbr.T >= 0).astype(np.int64) << np.arange(27)).sum(1)[order]
+    for r0 in range(0, n, region):
+        m = mask[r0:r0 + region]
+        assert (np.diff(m) >= 0).all(), f"region at {r0} not sorted by mask"

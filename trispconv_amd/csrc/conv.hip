@@ -32,7 +32,9 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 enum Path { kValu = 0, kMfma16 = 1 };
 
-int pick_ck(int c_in) { return c_in % 128 == 0 ? 128 : (c_in % 64 == 0 ? 64 : 32); }
+// 64-channel chunks keep accumulators plus double-buffered operands within
+// 256 registers, so two workgroups (8 waves) share a CU.
+int pick_ck(int c_in) { return c_in % 64 == 0 ? 64 : 32; }
 int pick_bn(int c_out) { return c_out % 128 == 0 ? 128 : (c_out % 64 == 0 ? 64 : 32); }
 
 Path pick_path(int dtype, int c_in, int c_out, int K) {
@@ -109,7 +111,7 @@ __global__ void __launch_bounds__(256) conv_valu_kernel(
 #pragma unroll
   for (int c = 0; c < CO; ++c) acc[c] = 0.f;
   for (int k = 0; k < K; ++k) {
-    const int32_t j = valid ? (nbr ? nbr[o * K + k] : static_cast<int32_t>(o)) : -1;
+    const int32_t j = valid ? (nbr ? nbr[(int64_t)k * n_out + o] : static_cast<int32_t>(o)) : -1;
     if (__ballot(j >= 0) == 0ull) continue;  // no lane of the wave uses slot k
     const T* x = feat + (int64_t)(j >= 0 ? j : 0) * c_in;
     const float* wk = W + (int64_t)k * c_in * c_out + co0;
@@ -146,33 +148,64 @@ template <> struct MfmaOp<__hip_bfloat16> {
 
 constexpr int kTileRows = 256;  // 4 waves x 64 rows
 
+// 16 bytes per lane, global memory -> LDS without passing through registers
+// (global_load_lds_dwordx4): lane l of the wave writes lds_base + 16*l.  The
+// builtin exists only for the device; the host pass sees an empty body.
+__device__ __forceinline__ void copy16_to_lds(const uint4* src, uint4* lds_base) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
+#else
+  (void)src;
+  (void)lds_base;
+#endif
+}
+
+// Operand source for absent neighbours: lanes whose output row has no input
+// through the current slot read zeros from here instead of branching around
+// their loads (64 bytes per lane are read at most).
+__device__ __attribute__((aligned(256))) uint4 g_zero_row[16];
+// s_waitcnt immediate for "vmcnt(0)", leaving expcnt / lgkmcnt unconstrained
+constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xf << 8);
+
 template <typename T, int BN, int CK>
-__global__ void __launch_bounds__(256, 1) conv_mfma_kernel(
+__global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
     const T* __restrict__ feat, int c_in, const T* __restrict__ W, const void* bias, int bias_dt,
     const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int64_t n_out, int K,
     int c_out, T* __restrict__ out) {
   using Op = MfmaOp<T>;
   using V = typename Op::V;
-  constexpr int STEPS = CK / 16;
-  constexpr int NB = BN / 32;
-  constexpr int SLAB = BN * CK;                  // elements of one weight stage
-  constexpr int SLAB_VECS = SLAB / 8;            // 16-byte vectors per stage
-  constexpr int WV = (SLAB_VECS + 255) / 256;    // vectors per thread per stage
+  constexpr int STEPS = CK / 16;                 // 16-deep MFMA steps per chunk
+  constexpr int NB = BN / 32;                    // 32-wide column blocks
+  constexpr int SLAB_VECS = BN * CK / 8;         // 16-byte vectors of one weight stage
+  constexpr int WV = SLAB_VECS >= 256 ? SLAB_VECS / 256 : 1;
+  constexpr bool FULL = SLAB_VECS % 256 == 0;
+  static_assert(!FULL || SLAB_VECS / 256 == WV, "slab split");
 
   __shared__ __attribute__((aligned(16))) uint4 s_w[2][SLAB_VECS];
-  __shared__ int32_t s_orow[kTileRows];
-  __shared__ uint32_t s_mask[4];
+  __shared__ __attribute__((aligned(16))) int32_t s_orow[kTileRows];
+  __shared__ uint32_t s_mask[8];      // per 32-row block
   extern __shared__ int32_t s_nbr[];  // [K][kTileRows]
 
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
   const int h = lane >> 5;
-  const int64_t tile0 = blockIdx.x * (int64_t)kTileRows;
-  const int nbt = blockIdx.y;
+  // XCD-aware placement: workgroups are dispatched round-robin over the 8
+  // XCDs, so give XCD x a contiguous run of (tile, column tile) items; all
+  // column tiles of a row tile, and neighbouring row tiles of the execution
+  // order, then share that XCD's L2.
+  const int ncol = c_out / BN;
+  int64_t item;
+  {
+    const int64_t nwg = gridDim.x, lin = blockIdx.x;
+    const int64_t per = nwg / 8, rem = nwg % 8, x = lin % 8;
+    item = x * per + (x < rem ? x : rem) + lin / 8;
+  }
+  const int64_t tile0 = (item / ncol) * kTileRows;
+  const int nbt = static_cast<int>(item % ncol);
   const int nch = c_in / CK;
 
-  // ---- tile set-up: output rows, their neighbour lists and slot masks
+  // ---- tile set-up: output rows, their slot lists and slot masks
   {
     const int64_t tr = tile0 + t;
     const int32_t orow = tr < n_out ? (order ? order[tr] : static_cast<int32_t>(tr)) : -1;
@@ -180,17 +213,20 @@ __global__ void __launch_bounds__(256, 1) conv_mfma_kernel(
     uint32_t m = 0;
     for (int k = 0; k < K; ++k) {
       int32_t j = -1;
-      if (orow >= 0) j = nbr ? nbr[(int64_t)orow * K + k] : orow;
+      if (orow >= 0) j = nbr ? nbr[(int64_t)k * n_out + orow] : orow;
       s_nbr[k * kTileRows + t] = j;
       m |= (j >= 0 ? 1u : 0u) << (k & 31);
     }
+    // OR over each 32-row half-wave: the rows one MFMA row block covers
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m |= __shfl_xor(m, off, kWave);
-    if (lane == 0) s_mask[wave] = m;
+    for (int off = 16; off > 0; off >>= 1) m |= __shfl_xor(m, off, kWave);
+    if ((lane & 31) == 0) s_mask[wave * 2 + h] = m;
   }
   __syncthreads();
-  const uint32_t umask = s_mask[0] | s_mask[1] | s_mask[2] | s_mask[3];
-  const uint32_t wmask = s_mask[wave];
+  uint32_t umask = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) umask |= s_mask[i];
+  const uint32_t bmask0 = s_mask[wave * 2], bmask1 = s_mask[wave * 2 + 1];
   const int r0 = wave * 64 + (lane & 31);  // tile rows of this lane's A operands
   const int r1 = r0 + 32;
 
@@ -202,10 +238,6 @@ __global__ void __launch_bounds__(256, 1) conv_mfma_kernel(
 
   const uint4* Wv = reinterpret_cast<const uint4*>(W);
   const int nbt_all = c_out / 32;
-  auto slab_src = [&](int k, int c) {
-    const int64_t e = (((int64_t)k * nch + c) * nbt_all + (int64_t)nbt * NB) * STEPS * 64;  // vec idx
-    return Wv + e;
-  };
 
   f32x16 acc[2][NB];
 #pragma unroll
@@ -216,48 +248,58 @@ __global__ void __launch_bounds__(256, 1) conv_mfma_kernel(
       for (int i = 0; i < 16; ++i) acc[rb][nb][i] = 0.f;
 
   uint4 a_cur[2][STEPS], a_nxt[2][STEPS];
-  uint4 wreg[WV];
 
-  auto load_a = [&](uint4 (&a)[2][STEPS], int k, int c) {
-    const int32_t j0 = s_nbr[k * kTileRows + r0];
-    const int32_t j1 = s_nbr[k * kTileRows + r1];
-    const int coff = c * CK + h * (CK / 2);
-#pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
-      a[0][s] = j0 >= 0 ? *reinterpret_cast<const uint4*>(feat + (int64_t)j0 * c_in + coff + s * 8)
-                        : make_uint4(0, 0, 0, 0);
-      a[1][s] = j1 >= 0 ? *reinterpret_cast<const uint4*>(feat + (int64_t)j1 * c_in + coff + s * 8)
-                        : make_uint4(0, 0, 0, 0);
-    }
-  };
+// Weight slab of stage (KK, CC) -> s_w[BUF], straight from global memory
+// into LDS (global_load_lds_dwordx4: lane l of a wave lands at base + 16*l).
+#define TSC_LOAD_W(KK, CC, BUF)                                                               \
+  {                                                                                           \
+    const uint4* src_ =                                                                       \
+        Wv + (((int64_t)(KK) * nch + (CC)) * nbt_all + (int64_t)nbt * NB) * STEPS * 64;        \
+    _Pragma("unroll") for (int v = 0; v < WV; ++v) {                                          \
+      if (FULL || v * 256 + t < SLAB_VECS)                                                    \
+        copy16_to_lds(src_ + v * 256 + t, &s_w[BUF][v * 256 + wave * 64]);                    \
+    }                                                                                         \
+  }
+#define TSC_LOAD_A(DST, KK, CC)                                                               \
+  {                                                                                           \
+    const int32_t j0_ = s_nbr[(KK) * kTileRows + r0];                                         \
+    const int32_t j1_ = s_nbr[(KK) * kTileRows + r1];                                         \
+    const int coff_ = (CC) * CK + h * (CK / 2);                                               \
+    const uint4* p0_ = j0_ >= 0 ? reinterpret_cast<const uint4*>(feat + (int64_t)j0_ * c_in + coff_) \
+                                : g_zero_row;                                                  \
+    const uint4* p1_ = j1_ >= 0 ? reinterpret_cast<const uint4*>(feat + (int64_t)j1_ * c_in + coff_) \
+                                : g_zero_row;                                                  \
+    _Pragma("unroll") for (int s_ = 0; s_ < STEPS; ++s_) {                                    \
+      DST[0][s_] = p0_[s_];                                                                   \
+      DST[1][s_] = p1_[s_];                                                                   \
+    }                                                                                         \
+  }
 
   int k = (umask & 1u) ? 0 : next_k(0);
   int c = 0;
   int buf = 0;
   if (k < K) {
-    const uint4* src = slab_src(k, c);
-#pragma unroll
-    for (int v = 0; v < WV; ++v)
-      if (v * 256 + t < SLAB_VECS) s_w[0][v * 256 + t] = src[v * 256 + t];
-    load_a(a_cur, k, c);
+    TSC_LOAD_W(k, c, 0);
+    TSC_LOAD_A(a_cur, k, c);
   }
+  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
   __syncthreads();
   while (k < K) {
-    // next stage
     int kn = k, cn = c + 1;
     if (cn == nch) {
       cn = 0;
       kn = next_k(k);
     }
     const bool more = kn < K;
-    if (more) {
-      const uint4* src = slab_src(kn, cn);
-#pragma unroll
-      for (int v = 0; v < WV; ++v)
-        if (v * 256 + t < SLAB_VECS) wreg[v] = src[v * 256 + t];
-      load_a(a_nxt, kn, cn);
-    }
-    if (wmask & (1u << (k & 31))) {
+    // gathers for the next stage go out before this stage's MFMAs; the weight
+    // slab copy (global -> LDS) is issued after them so that no LDS write is
+    // in flight while the MFMA operands are read from LDS
+    if (more) TSC_LOAD_A(a_nxt, kn, cn);
+    // a 32-row block with no input through slot k skips its MFMAs (its
+    // operands are zero and would add exact zeros)
+    const uint32_t kbit = 1u << (k & 31);
+    const bool use0 = (bmask0 & kbit) != 0, use1 = (bmask1 & kbit) != 0;
+    if (use0 || use1) {
       const uint4* sw = s_w[buf];
 #pragma unroll
       for (int s = 0; s < STEPS; ++s) {
@@ -266,16 +308,15 @@ __global__ void __launch_bounds__(256, 1) conv_mfma_kernel(
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
           const V b = __builtin_bit_cast(V, sw[(nb * STEPS + s) * 64 + lane]);
-          acc[0][nb] = Op::run(a0, b, acc[0][nb]);
-          acc[1][nb] = Op::run(a1, b, acc[1][nb]);
+          if (use0) acc[0][nb] = Op::run(a0, b, acc[0][nb]);
+          if (use1) acc[1][nb] = Op::run(a1, b, acc[1][nb]);
         }
       }
     }
-    if (more) {
-#pragma unroll
-      for (int v = 0; v < WV; ++v)
-        if (v * 256 + t < SLAB_VECS) s_w[buf ^ 1][v * 256 + t] = wreg[v];
-    }
+    if (more) TSC_LOAD_W(kn, cn, buf ^ 1);
+    // the next stage's weight slab (and operands) must have landed before any
+    // wave reads it
+    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
     __syncthreads();
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
@@ -285,10 +326,18 @@ __global__ void __launch_bounds__(256, 1) conv_mfma_kernel(
     k = kn;
     c = cn;
   }
+#undef TSC_LOAD_W
+#undef TSC_LOAD_A
 
   // ---- epilogue: + bias, round once, store each output element once.
   // 32x32 accumulator layout: register i of lane l holds row
   // (i/4)*8 + (l/32)*4 + i%4 and column l%32 of the block.
+  int4 orows[2][4];  // rows (rb, g): 4 consecutive rows starting at wave*64 + rb*32 + g*8 + h*4
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      orows[rb][g] = *reinterpret_cast<const int4*>(&s_orow[wave * 64 + rb * 32 + g * 8 + h * 4]);
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const int col = nbt * BN + nb * 32 + (lane & 31);
@@ -297,8 +346,8 @@ __global__ void __launch_bounds__(256, 1) conv_mfma_kernel(
     for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int row = wave * 64 + rb * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
-        const int32_t orow = s_orow[row];
+        const int4 q = orows[rb][i >> 2];
+        const int32_t orow = (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w;
         if (orow >= 0) out[(int64_t)orow * c_out + col] = from_f32<T>(acc[rb][nb][i] + bv);
       }
     }
@@ -309,7 +358,8 @@ template <typename T, int BN, int CK>
 int launch_mfma(const void* feat, int c_in, const void* W, const void* bias, int bias_dt,
                 const int32_t* nbr, const int32_t* order, int64_t n_out, int K, int c_out,
                 void* out, hipStream_t s) {
-  dim3 grid(static_cast<unsigned>(ceil_div(n_out, kTileRows)), static_cast<unsigned>(c_out / BN));
+  const int64_t items = ceil_div(n_out, kTileRows) * (c_out / BN);
+  dim3 grid(static_cast<unsigned>(items));
   const size_t lds = (size_t)K * kTileRows * sizeof(int32_t);
   conv_mfma_kernel<T, BN, CK><<<grid, 256, lds, s>>>(
       static_cast<const T*>(feat), c_in, static_cast<const T*>(W), bias, bias_dt, nbr, order, n_out,
@@ -327,13 +377,10 @@ int dispatch_mfma(const void* feat, int c_in, const void* W, const void* bias, i
   if (bn == BN_ && ck == CK_)                                                                \
     return launch_mfma<T, BN_, CK_>(feat, c_in, W, bias, bias_dt, nbr, order, n_out, K, c_out, \
                                     out, s);
-  TSC_MFMA_CASE(128, 128)
   TSC_MFMA_CASE(128, 64)
   TSC_MFMA_CASE(128, 32)
-  TSC_MFMA_CASE(64, 128)
   TSC_MFMA_CASE(64, 64)
   TSC_MFMA_CASE(64, 32)
-  TSC_MFMA_CASE(32, 128)
   TSC_MFMA_CASE(32, 64)
   TSC_MFMA_CASE(32, 32)
 #undef TSC_MFMA_CASE

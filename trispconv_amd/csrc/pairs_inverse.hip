@@ -48,7 +48,7 @@ __global__ void __launch_bounds__(256) inverse_fill_kernel(const int32_t* __rest
   const int64_t e = (int64_t)k * cap + j;
   const int32_t o = static_cast<int32_t>(id_map[fwd_pin[e]]);
   inv_pout[e] = o;
-  if (o < n_out) nbr[(int64_t)o * K + k] = fwd_pout[e];  // holds by construction
+  if (o < n_out) nbr[(int64_t)k * n_out + o] = fwd_pout[e];  // holds by construction
 }
 
 struct Buffers {

@@ -150,7 +150,7 @@ __global__ void __launch_bounds__(kRows) strided_fill_kernel(const int4* __restr
         if (slot_pos < cap && rank < n_out) {
           pairs_in[(int64_t)k * cap + slot_pos] = static_cast<int32_t>(i);
           pairs_out[(int64_t)k * cap + slot_pos] = rank;
-          nbr[(int64_t)rank * K + k] = static_cast<int32_t>(i);
+          nbr[(int64_t)k * n_out + rank] = static_cast<int32_t>(i);
         }
       }
     }

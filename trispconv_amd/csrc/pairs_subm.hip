@@ -7,8 +7,8 @@
 //
 // MI355X design: the reference's dense grid-sized lookup table (:54-64) becomes
 // an open-addressing hash of 2N..4N 64-bit slots (8-16 MB at 500k voxels, so
-// it stays in L2 / Infinity Cache).  One probe kernel writes the [N][K]
-// neighbour map the convolution consumes and per-(slot, block) hit counts;
+// it stays in L2 / Infinity Cache).  One probe kernel writes the slot-major
+// [K][N] neighbour map the convolution consumes and per-(slot, block) hit counts;
 // a per-slot scan of those counts gives each block its write offset, and a
 // fill kernel emits every slot's pair list in ascending output-row order with
 // wave ballots, so the lists come out in exactly the reference's order.
@@ -49,61 +49,77 @@ __global__ void __launch_bounds__(256) subm_insert_kernel(const int4* __restrict
   hash_insert(table, g.mask, cell_key(g, c.x, c.y, c.z, c.w), static_cast<uint32_t>(r));
 }
 
-// One thread per output row; K lookups each.  With STAGED the block's
-// [kRows][K] slice of the map is assembled in LDS and written out coalesced.
-template <bool STAGED>
+// One thread per output row.  Slots are processed in groups of kGroup: the
+// first probe of every slot in the group is issued before any is inspected,
+// so a thread keeps kGroup independent hash reads in flight; collisions are
+// then followed slot by slot.  The map is slot-major ([K][n]), so for each
+// slot a wave writes 64 consecutive entries.
+constexpr int kGroup = 16;
+
 __global__ void __launch_bounds__(kRows) subm_probe_kernel(const int4* __restrict__ coords,
                                                            int64_t n, int K, SubmGeom g,
                                                            const unsigned long long* __restrict__ table,
                                                            int32_t* __restrict__ nbr,
                                                            int32_t* __restrict__ blk_cnt,
                                                            int nblk) {
-  extern __shared__ int32_t s_nbr[];           // [kRows][K] when STAGED
-  __shared__ int32_t s_cnt[kRows / kWave][64];  // per wave, per slot (K <= 64 counted here)
+  __shared__ int32_t s_cnt[kRows / kWave][64];  // per wave, per slot (slots < 64)
   const int t = threadIdx.x;
   const int w = t / kWave;
-  const int64_t row0 = blockIdx.x * (int64_t)kRows;
-  const int64_t r = row0 + t;
+  const int64_t r = blockIdx.x * (int64_t)kRows + t;
   const bool valid = r < n;
-  int4 c = valid ? coords[r] : make_int4(-1, 0, 0, 0);
+  const int4 c = valid ? coords[r] : make_int4(-1, 0, 0, 0);
   const bool self_ok = valid && in_grid(g, c.x, c.y, c.z, c.w);
 
-  for (int k = 0; k < K; ++k) {
-    int kz, ky, kx;
-    slot_to_zyx(k, g.ks, kz, ky, kx);
-    const int z = c.y + (kz - g.ks.z / 2) * g.dil.z;
-    const int y = c.z + (ky - g.ks.y / 2) * g.dil.y;
-    const int x = c.w + (kx - g.ks.x / 2) * g.dil.x;
-    int32_t j = -1;
-    if (self_ok && in_grid(g, c.x, z, y, x)) j = hash_find(table, g.mask, cell_key(g, c.x, z, y, x));
-    const uint64_t hits = __ballot(j >= 0);
-    if (STAGED) {
-      s_nbr[t * K + k] = j;
-    } else if (valid) {
-      nbr[r * K + k] = j;
+  for (int kb = 0; kb < K; kb += kGroup) {
+    uint32_t key[kGroup], h[kGroup];
+    unsigned long long word[kGroup];
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) {
+      const int k = kb + i;
+      int kz, ky, kx;
+      slot_to_zyx(k < K ? k : 0, g.ks, kz, ky, kx);
+      const int z = c.y + (kz - g.ks.z / 2) * g.dil.z;
+      const int y = c.z + (ky - g.ks.y / 2) * g.dil.y;
+      const int x = c.w + (kx - g.ks.x / 2) * g.dil.x;
+      const bool look = self_ok && k < K && in_grid(g, c.x, z, y, x);
+      key[i] = look ? cell_key(g, c.x, z, y, x) : 0u;
+      h[i] = hash32(key[i]) & g.mask;
+      // unconditional read (slot h is always inside the table) so the group's
+      // reads issue back to back; a slot that needs no lookup is then marked
+      // empty
+      const unsigned long long wv = table[h[i]];
+      word[i] = look ? wv : kEmpty;
     }
-    // per-wave hit count of this slot, accumulated through LDS
-    if (__lane_id() == 0) {
-      if (k < 64) {
-        s_cnt[w][k] = __popcll(hits);
-      } else {
-        // K > 64: fold straight into the global count
-        atomicAdd(&blk_cnt[(int64_t)k * nblk + blockIdx.x], (int)__popcll(hits));
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) {
+      const int k = kb + i;
+      int32_t j = -1;
+      while (word[i] != kEmpty) {
+        if (static_cast<uint32_t>(word[i] >> 32) == key[i]) {
+          j = static_cast<int32_t>(word[i] & 0xffffffffu);
+          break;
+        }
+        h[i] = (h[i] + 1) & g.mask;
+        word[i] = table[h[i]];
+      }
+      if (k < K) {
+        const uint64_t hits = __ballot(j >= 0);
+        if (valid) nbr[(int64_t)k * n + r] = j;
+        if (__lane_id() == 0) {
+          if (k < 64)
+            s_cnt[w][k] = __popcll(hits);
+          else  // K > 64: fold straight into the global count
+            atomicAdd(&blk_cnt[(int64_t)k * nblk + blockIdx.x], (int)__popcll(hits));
+        }
       }
     }
   }
   __syncthreads();
   if (t < K && t < 64) {
-    int s = 0;
+    int sum = 0;
 #pragma unroll
-    for (int ww = 0; ww < kRows / kWave; ++ww) s += s_cnt[ww][t];
-    blk_cnt[(int64_t)t * nblk + blockIdx.x] = s;
-  }
-  if (STAGED) {
-    const int64_t rows = (n - row0) < kRows ? (n - row0) : kRows;
-    const int64_t total = rows * K;
-    int32_t* dst = nbr + row0 * K;
-    for (int64_t i = t; i < total; i += kRows) dst[i] = s_nbr[i];
+    for (int ww = 0; ww < kRows / kWave; ++ww) sum += s_cnt[ww][t];
+    blk_cnt[(int64_t)t * nblk + blockIdx.x] = sum;
   }
 }
 
@@ -111,39 +127,28 @@ __global__ void __launch_bounds__(kRows) subm_probe_kernel(const int4* __restric
 // ascending order inside a slot: blocks own consecutive row ranges (block
 // offsets from the per-slot scan), waves own consecutive sub-ranges (offsets
 // from per-wave counts) and lanes are ranked by ballot.
-template <bool STAGED>
 __global__ void __launch_bounds__(kRows) subm_fill_kernel(const int32_t* __restrict__ nbr, int64_t n,
                                                           int K,
                                                           const int32_t* __restrict__ blk_off,
                                                           int nblk, int64_t cap,
                                                           int32_t* __restrict__ pairs_in,
                                                           int32_t* __restrict__ pairs_out) {
-  extern __shared__ int32_t s_nbr[];
   __shared__ int32_t s_wcnt[kRows / kWave][64];
   const int t = threadIdx.x;
   const int w = t / kWave;
-  const int64_t row0 = blockIdx.x * (int64_t)kRows;
-  const int64_t r = row0 + t;
+  const int64_t r = blockIdx.x * (int64_t)kRows + t;
   const bool valid = r < n;
-  if (STAGED) {
-    const int64_t rows = (n - row0) < kRows ? (n - row0) : kRows;
-    const int64_t total = rows * K;
-    const int32_t* src = nbr + row0 * K;
-    for (int64_t i = t; i < total; i += kRows) s_nbr[i] = src[i];
-    __syncthreads();
-  }
   for (int kb = 0; kb < K; kb += 64) {
     const int kend = (K - kb) < 64 ? (K - kb) : 64;
     for (int kk = 0; kk < kend; ++kk) {
-      const int k = kb + kk;
-      const int32_t j = valid ? (STAGED ? s_nbr[t * K + k] : nbr[r * K + k]) : -1;
+      const int32_t j = valid ? nbr[(int64_t)(kb + kk) * n + r] : -1;
       const uint64_t hits = __ballot(j >= 0);
       if (__lane_id() == 0) s_wcnt[w][kk] = __popcll(hits);
     }
     __syncthreads();
     for (int kk = 0; kk < kend; ++kk) {
       const int k = kb + kk;
-      const int32_t j = valid ? (STAGED ? s_nbr[t * K + k] : nbr[r * K + k]) : -1;
+      const int32_t j = valid ? nbr[(int64_t)k * n + r] : -1;
       const uint64_t hits = __ballot(j >= 0);
       int base = blk_off[(int64_t)k * nblk + blockIdx.x];
       for (int ww = 0; ww < w; ++ww) base += s_wcnt[ww][kk];
@@ -164,9 +169,6 @@ static int64_t subm_capacity(int64_t n) {
   while (cap < 2 * n) cap <<= 1;
   return cap;
 }
-
-// LDS staging of a block's map slice while it stays within 48 KB.
-static bool staged(int K) { return K <= 48; }
 
 }  // namespace tsc
 
@@ -220,21 +222,11 @@ extern "C" int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_si
   subm_insert_kernel<<<ceil_div(n, 256), 256, 0, s>>>(reinterpret_cast<const int4*>(coords), n, g,
                                                       table, counts + K);
   TSC_LAUNCH_CHECK("subm_insert");
-  const size_t lds = staged(K) ? (size_t)kRows * K * sizeof(int32_t) : 0;
-  if (staged(K))
-    subm_probe_kernel<true><<<nblk, kRows, lds, s>>>(reinterpret_cast<const int4*>(coords), n, K,
-                                                     g, table, nbr, blk_cnt, nblk);
-  else
-    subm_probe_kernel<false><<<nblk, kRows, 0, s>>>(reinterpret_cast<const int4*>(coords), n, K,
-                                                    g, table, nbr, blk_cnt, nblk);
+  subm_probe_kernel<<<nblk, kRows, 0, s>>>(reinterpret_cast<const int4*>(coords), n, K, g, table,
+                                           nbr, blk_cnt, nblk);
   TSC_LAUNCH_CHECK("subm_probe");
   if ((rc = scan_slot_blocks(blk_cnt, blk_off, counts, K, nblk, s))) return rc;
-  if (staged(K))
-    subm_fill_kernel<true><<<nblk, kRows, lds, s>>>(nbr, n, K, blk_off, nblk, n, pairs_in,
-                                                    pairs_out);
-  else
-    subm_fill_kernel<false><<<nblk, kRows, 0, s>>>(nbr, n, K, blk_off, nblk, n, pairs_in,
-                                                   pairs_out);
+  subm_fill_kernel<<<nblk, kRows, 0, s>>>(nbr, n, K, blk_off, nblk, n, pairs_in, pairs_out);
   TSC_LAUNCH_CHECK("subm_fill");
   return 0;
 }

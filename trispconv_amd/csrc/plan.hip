@@ -1,18 +1,31 @@
 // Execution order for the fused convolution.
 //
-// The convolution kernel computes tiles of output rows and, for each slot k,
-// runs the MFMA work for the whole tile if any row of the tile has an input
-// through k.  Rows whose neighbour sets differ therefore waste work when they
-// share a tile.  This builder sorts output rows by their slot-occupancy mask
-// (bit k set when nbr[o][k] >= 0; slots beyond 32 fold onto bit k mod 32)
-// with a stable LSD radix sort, so tiles mostly hold rows with one mask.
-// Output values do not depend on the order: every row's fp32 accumulation
+// The convolution kernel computes tiles of output rows.  Two things make a
+// tile cheap:
+//   * its rows need the same kernel slots — for each slot k the MFMA work of a
+//     32-row block is skipped only when no row of the block has an input
+//     through k, so rows with different slot sets waste matrix-core work;
+//   * its rows, and the tiles an XCD runs around the same time, gather from
+//     nearby input rows — the gathered rows then come from that XCD's L2
+//     instead of HBM.
+// The order built here serves both: output rows are put in Morton (z-order)
+// order, cut into regions of `region_rows` consecutive rows (sized so one
+// region's input rows fit an XCD's L2), and sorted inside each region by
+// their slot-occupancy mask (bit k set when nbr[k][o] >= 0; slots beyond 32
+// fold onto bit k mod 32), ties kept in Morton order.
+//
+// Output values never depend on the order: every row's fp32 accumulation
 // sees the same slots in the same ascending order and absent slots add zero.
 //
-// Radix sort: 8-bit digits; per pass one histogram kernel (per-block digit
-// counts, stored digit-major), one exclusive scan over all counts and one
-// stable scatter in which each wave ranks equal digits with eight ballots.
+// Sorting: stable LSD radix passes with 8-bit digits.  Each pass is a
+// histogram kernel (per-block digit counts, digit-major), one exclusive scan
+// of all counts and a stable scatter in which each wave ranks equal digits
+// with eight ballots.  The first sort orders rows by their Morton code; the
+// second carries Morton positions as values and takes its digits from the
+// mask at that position, then from the region (position / region_rows).
 #include "common.hpp"
+
+#include <utility>
 
 namespace tsc {
 namespace {
@@ -22,20 +35,81 @@ constexpr int kItems = 8;                     // per thread per block
 constexpr int kTile = kThreads * kItems;      // items per block
 constexpr int kRadix = 256;
 
-__global__ void __launch_bounds__(256) mask_kernel(const int32_t* __restrict__ nbr, int64_t n, int K,
-                                                   uint32_t* __restrict__ keys,
-                                                   uint32_t* __restrict__ vals) {
+// Digit sources of a pass.
+enum DigitSrc { kFromKey = 0, kFromMaskAtValue = 1, kFromRegionOfValue = 2 };
+
+struct Digits {
+  int src;
+  int shift;
+  const uint32_t* keys;      // kFromKey: keys[i]
+  const uint32_t* mask_pos;  // kFromMaskAtValue: mask_pos[value]
+  uint32_t region_rows;      // kFromRegionOfValue: value / region_rows
+};
+
+__device__ __forceinline__ uint32_t digit_of(const Digits& d, int64_t i, uint32_t value) {
+  uint32_t k;
+  if (d.src == kFromKey)
+    k = d.keys[i];
+  else if (d.src == kFromMaskAtValue)
+    k = d.mask_pos[value];
+  else
+    k = value / d.region_rows;
+  return (k >> d.shift) & 0xffu;
+}
+
+// Spreads the low 10 bits of v to every third bit.
+__device__ __forceinline__ uint32_t spread3(uint32_t v) {
+  v &= 0x3ffu;
+  v = (v | (v << 16)) & 0x030000ffu;
+  v = (v | (v << 8)) & 0x0300f00fu;
+  v = (v | (v << 4)) & 0x030c30c3u;
+  v = (v | (v << 2)) & 0x09249249u;
+  return v;
+}
+
+// Morton code of each output row: the sample index in the bits at and above
+// batch_shift, then the leading bits of the 30-bit z-order code of
+// (z, y, x) >> coarse (coarse chosen by the host so the largest axis fits 10
+// bits).
+__global__ void __launch_bounds__(256) spatial_key_kernel(const int4* __restrict__ coords, int64_t n,
+                                                          int coarse, int batch_shift,
+                                                          uint32_t* __restrict__ keys,
+                                                          uint32_t* __restrict__ vals) {
   const int64_t o = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (o >= n) return;
-  const int32_t* row = nbr + o * K;
-  uint32_t m = 0;
-  for (int k = 0; k < K; ++k) m |= (row[k] >= 0 ? 1u : 0u) << (k & 31);
-  keys[o] = m;
+  const int4 c = coords[o];
+  const uint32_t m = (spread3(static_cast<uint32_t>(c.y) >> coarse) << 2) |
+                     (spread3(static_cast<uint32_t>(c.z) >> coarse) << 1) |
+                     spread3(static_cast<uint32_t>(c.w) >> coarse);
+  const uint32_t spatial = batch_shift >= 30 ? m : (m >> (30 - batch_shift));
+  keys[o] = (batch_shift >= 32 ? 0u : (static_cast<uint32_t>(c.x) << batch_shift)) | spatial;
   vals[o] = static_cast<uint32_t>(o);
 }
 
-__global__ void __launch_bounds__(kThreads) radix_hist_kernel(const uint32_t* __restrict__ keys,
-                                                              int64_t n, int shift,
+// mask_pos[i] = slot mask of output row rows[i]; vals[i] = i.
+__global__ void __launch_bounds__(256) mask_at_pos_kernel(const int32_t* __restrict__ nbr, int64_t n,
+                                                          int K, const uint32_t* __restrict__ rows,
+                                                          uint32_t* __restrict__ mask_pos,
+                                                          uint32_t* __restrict__ vals) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint32_t o = rows[i];
+  uint32_t m = 0;
+  for (int k = 0; k < K; ++k) m |= (nbr[(int64_t)k * n + o] >= 0 ? 1u : 0u) << (k & 31);
+  mask_pos[i] = m;
+  vals[i] = static_cast<uint32_t>(i);
+}
+
+__global__ void __launch_bounds__(256) gather_rows_kernel(const uint32_t* __restrict__ pos,
+                                                          const uint32_t* __restrict__ rows,
+                                                          int64_t n, int32_t* __restrict__ order) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  order[i] = static_cast<int32_t>(rows[pos[i]]);
+}
+
+__global__ void __launch_bounds__(kThreads) radix_hist_kernel(const uint32_t* __restrict__ vals,
+                                                              int64_t n, Digits d,
                                                               uint32_t* __restrict__ hist,
                                                               int nblk) {
   __shared__ uint32_t s_h[kRadix];
@@ -45,7 +119,7 @@ __global__ void __launch_bounds__(kThreads) radix_hist_kernel(const uint32_t* __
 #pragma unroll
   for (int j = 0; j < kItems; ++j) {
     const int64_t i = base + j * kThreads + threadIdx.x;
-    if (i < n) atomicAdd(&s_h[(keys[i] >> shift) & 0xffu], 1u);
+    if (i < n) atomicAdd(&s_h[digit_of(d, i, vals[i])], 1u);
   }
   __syncthreads();
   hist[(int64_t)threadIdx.x * nblk + blockIdx.x] = s_h[threadIdx.x];
@@ -53,7 +127,7 @@ __global__ void __launch_bounds__(kThreads) radix_hist_kernel(const uint32_t* __
 
 __global__ void __launch_bounds__(kThreads) radix_scatter_kernel(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n,
-    int shift, const uint32_t* __restrict__ hist_off, int nblk, uint32_t* __restrict__ keys_out,
+    Digits d, const uint32_t* __restrict__ hist_off, int nblk, uint32_t* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out) {
   __shared__ uint32_t s_run[kRadix];                   // placed so far, per digit
   __shared__ uint32_t s_wc[kThreads / kWave][kRadix];  // this round, per wave, per digit
@@ -67,24 +141,24 @@ __global__ void __launch_bounds__(kThreads) radix_scatter_kernel(
     __syncthreads();
     const int64_t i = base + j * kThreads + t;  // items stay in index order
     const bool valid = i < n;
-    const uint32_t key = valid ? keys_in[i] : 0u;
     const uint32_t val = valid ? vals_in[i] : 0u;
-    const uint32_t d = (key >> shift) & 0xffu;
+    const uint32_t key = (valid && keys_in) ? keys_in[i] : 0u;
+    const uint32_t dg = valid ? digit_of(d, i, val) : 0u;
     // lanes of this wave holding the same digit
     uint64_t peers = __ballot(valid);
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
-      const uint64_t ones = __ballot((d >> b) & 1u);
-      peers &= ((d >> b) & 1u) ? ones : ~ones;
+      const uint64_t ones = __ballot((dg >> b) & 1u);
+      peers &= ((dg >> b) & 1u) ? ones : ~ones;
     }
     const int rank = rank_in_wave(peers);
-    if (valid && rank == 0) s_wc[w][d] = __popcll(peers);
+    if (valid && rank == 0) s_wc[w][dg] = __popcll(peers);
     __syncthreads();
     if (valid) {
-      uint32_t pos = s_run[d] + rank;
-      for (int ww = 0; ww < w; ++ww) pos += s_wc[ww][d];
+      uint32_t pos = s_run[dg] + rank;
+      for (int ww = 0; ww < w; ++ww) pos += s_wc[ww][dg];
       if (pos < n) {  // always true when the digit offsets are consistent
-        keys_out[pos] = key;
+        if (keys_out) keys_out[pos] = key;
         vals_out[pos] = val;
       }
     }
@@ -98,7 +172,7 @@ __global__ void __launch_bounds__(kThreads) radix_scatter_kernel(
 }
 
 struct Buffers {
-  uint32_t *keys_a, *vals_a, *keys_b, *vals_b, *hist, *hist_off, *scratch;
+  uint32_t *keys_a, *keys_b, *vals_a, *vals_b, *rows, *mask_pos, *hist, *hist_off, *scratch;
 };
 
 Buffers carve(void* ws, int64_t n, int64_t* used) {
@@ -107,13 +181,36 @@ Buffers carve(void* ws, int64_t n, int64_t* used) {
   const int64_t nblk = ceil_div(m, kTile);
   Buffers b;
   b.keys_a = c.take<uint32_t>(m);
-  b.vals_a = c.take<uint32_t>(m);
   b.keys_b = c.take<uint32_t>(m);
+  b.vals_a = c.take<uint32_t>(m);
   b.vals_b = c.take<uint32_t>(m);
+  b.rows = c.take<uint32_t>(m);
+  b.mask_pos = c.take<uint32_t>(m);
   b.hist = c.take<uint32_t>(nblk * kRadix);
   b.hist_off = c.take<uint32_t>(nblk * kRadix);
   b.scratch = c.take<uint32_t>(scan_scratch_words(nblk * kRadix));
   if (used) *used = c.used;
+  return b;
+}
+
+// One stable pass: (keys, vals) in -> out, digits from d.
+int radix_pass(const Buffers& b, const uint32_t* keys_in, const uint32_t* vals_in,
+               uint32_t* keys_out, uint32_t* vals_out, int64_t n, const Digits& d,
+               hipStream_t s) {
+  const int nblk = static_cast<int>(ceil_div(n, kTile));
+  radix_hist_kernel<<<nblk, kThreads, 0, s>>>(vals_in, n, d, b.hist, nblk);
+  TSC_LAUNCH_CHECK("plan_hist");
+  int rc = exclusive_scan_u32(b.hist, 2, (int64_t)nblk * kRadix, b.hist_off, nullptr, b.scratch, s);
+  if (rc) return rc;
+  radix_scatter_kernel<<<nblk, kThreads, 0, s>>>(keys_in, vals_in, n, d, b.hist_off, nblk, keys_out,
+                                                 vals_out);
+  TSC_LAUNCH_CHECK("plan_scatter");
+  return 0;
+}
+
+int bits_for(uint64_t v) {  // bits needed to hold values 0..v
+  int b = 0;
+  while (b < 64 && (uint64_t(1) << b) <= v) ++b;
   return b;
 }
 
@@ -129,39 +226,65 @@ extern "C" int64_t tsc_plan_workspace_bytes(int64_t n_out, int32_t k_vol) {
   return used;
 }
 
-extern "C" int tsc_conv_plan(const int32_t* nbr, int64_t n_out, int32_t k_vol, void* ws,
-                             int64_t ws_bytes, int32_t* order, tsc_stream_t stream) {
+extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* out_coords, int64_t n_out,
+                             int32_t k_vol, int32_t batch_size, const int32_t out_spatial[3],
+                             int64_t region_rows, void* ws, int64_t ws_bytes, int32_t* order,
+                             tsc_stream_t stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   TSC_REQUIRE(n_out >= 0 && n_out < (int64_t(1) << 31), "plan: n_out out of range");
-  TSC_REQUIRE(k_vol > 0, "plan: invalid kernel volume");
+  TSC_REQUIRE(k_vol > 0 && batch_size > 0, "plan: invalid kernel volume or batch size");
+  TSC_REQUIRE(region_rows > 0 && region_rows < (int64_t(1) << 31),
+              "plan: region_rows must be positive");
+  TSC_REQUIRE(out_spatial && out_spatial[0] > 0 && out_spatial[1] > 0 && out_spatial[2] > 0,
+              "plan: spatial shape must be positive");
   if (n_out == 0) return 0;
-  TSC_REQUIRE(nbr && order && ws, "plan: null pointer");
+  TSC_REQUIRE(nbr && out_coords && order && ws, "plan: null pointer");
   TSC_REQUIRE(ws_bytes >= tsc_plan_workspace_bytes(n_out, k_vol), "plan: workspace too small");
   Buffers b = carve(ws, n_out, nullptr);
-  const int nblk = static_cast<int>(ceil_div(n_out, kTile));
-  mask_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(nbr, n_out, k_vol, b.keys_a, b.vals_a);
-  TSC_LAUNCH_CHECK("plan_mask");
-  const int bits = k_vol < 32 ? k_vol : 32;
-  const int passes = (bits + 7) / 8;
-  uint32_t *ki = b.keys_a, *vi = b.vals_a, *ko = b.keys_b, *vo = b.vals_b;
-  for (int p = 0; p < passes; ++p) {
-    const int shift = 8 * p;
-    if (p == passes - 1) {
-      // the last pass writes the values straight into the caller's order
-      vo = reinterpret_cast<uint32_t*>(order);
-    }
-    radix_hist_kernel<<<nblk, kThreads, 0, s>>>(ki, n_out, shift, b.hist, nblk);
-    TSC_LAUNCH_CHECK("plan_hist");
-    int rc = exclusive_scan_u32(b.hist, 2, (int64_t)nblk * kRadix, b.hist_off, nullptr, b.scratch, s);
-    if (rc) return rc;
-    radix_scatter_kernel<<<nblk, kThreads, 0, s>>>(ki, vi, n_out, shift, b.hist_off, nblk, ko, vo);
-    TSC_LAUNCH_CHECK("plan_scatter");
-    uint32_t* tk = ki;
-    ki = ko;
-    ko = tk;
-    uint32_t* tv = vi;
-    vi = vo;
-    vo = tv;
+  int rc;
+
+  // ---- sort 1: rows by Morton code
+  int extent = out_spatial[0];
+  if (out_spatial[1] > extent) extent = out_spatial[1];
+  if (out_spatial[2] > extent) extent = out_spatial[2];
+  const int axis_bits = bits_for(static_cast<uint64_t>(extent - 1));
+  const int coarse = axis_bits > 10 ? axis_bits - 10 : 0;
+  int batch_bits = bits_for(static_cast<uint64_t>(batch_size - 1));
+  if (batch_bits > 16) batch_bits = 16;  // more samples than that only coarsen the order
+  const int batch_shift = 32 - batch_bits;
+  spatial_key_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(
+      reinterpret_cast<const int4*>(out_coords), n_out, coarse, batch_shift, b.keys_a, b.vals_a);
+  TSC_LAUNCH_CHECK("plan_spatial_key");
+  uint32_t *ki = b.keys_a, *ko = b.keys_b, *vi = b.vals_a, *vo = b.vals_b;
+  for (int p = 0; p < 4; ++p) {
+    const Digits d{kFromKey, 8 * p, ki, nullptr, 1u};
+    uint32_t* vdst = (p == 3) ? b.rows : vo;  // the last pass leaves rows in Morton order
+    if ((rc = radix_pass(b, ki, vi, ko, vdst, n_out, d, s))) return rc;
+    std::swap(ki, ko);
+    std::swap(vi, vo);
   }
+
+  // ---- sort 2: Morton positions by (region, mask), stable
+  mask_at_pos_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(nbr, n_out, k_vol, b.rows, b.mask_pos,
+                                                          b.vals_a);
+  TSC_LAUNCH_CHECK("plan_mask");
+  vi = b.vals_a;
+  vo = b.vals_b;
+  const int mask_bits = k_vol < 32 ? k_vol : 32;
+  const int64_t regions = ceil_div(n_out, region_rows);
+  const int region_bits = bits_for(static_cast<uint64_t>(regions - 1));
+  for (int p = 0; p < (mask_bits + 7) / 8; ++p) {
+    const Digits d{kFromMaskAtValue, 8 * p, nullptr, b.mask_pos, 1u};
+    if ((rc = radix_pass(b, nullptr, vi, nullptr, vo, n_out, d, s))) return rc;
+    std::swap(vi, vo);
+  }
+  for (int p = 0; p < (region_bits + 7) / 8; ++p) {
+    const Digits d{kFromRegionOfValue, 8 * p, nullptr, nullptr,
+                   static_cast<uint32_t>(region_rows)};
+    if ((rc = radix_pass(b, nullptr, vi, nullptr, vo, n_out, d, s))) return rc;
+    std::swap(vi, vo);
+  }
+  gather_rows_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(vi, b.rows, n_out, order);
+  TSC_LAUNCH_CHECK("plan_gather");
   return 0;
 }

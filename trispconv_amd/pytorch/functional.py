@@ -52,7 +52,8 @@ def sparse_conv_forward(features: torch.Tensor, weight: Union[torch.Tensor, Pack
         K, c_in, c_out = weight.shape
         weight = pack_weight(weight, (K, 1, 1), c_in, c_out, features.dtype)
     nbr = indice_data.neighbour_map(N_out, features.device)
-    order = indice_data.execution_order(N_out, features.device)
+    order = indice_data.execution_order(N_out, features.device,
+                                        weight.c_in * features.element_size())
     return _run(features, weight, bias, nbr, order, N_out)
 
 

@@ -27,6 +27,9 @@ __all__ = [
 
 # Below this many output rows the execution-order sort costs more than it saves.
 _PLAN_MIN_ROWS = 2048
+# L2 per XCD on MI355X: the execution order keeps one region's gathered rows
+# within it.
+_L2_BYTES = 4 << 20
 
 
 def _to3(x) -> Tuple[int, int, int]:
@@ -71,18 +74,21 @@ class IndiceData:
         self._pin: Optional[torch.Tensor] = None    # [K][cap] int32
         self._pout: Optional[torch.Tensor] = None   # [K][cap] int32
         self._cnt: Optional[torch.Tensor] = None    # [K] int32 on the device
-        self._nbr: Optional[torch.Tensor] = None    # [n_out][K] int32
+        self._nbr: Optional[torch.Tensor] = None    # [K][n_out] int32
         self._order: Optional[torch.Tensor] = None  # [n_out] int32 execution order
         self._inverse_cache: Optional["IndiceData"] = None
+        self._order_region = 0
+        self._batch_size: Optional[int] = None
 
     # --------------------------------------------------- construction
     @classmethod
     def _from_tables(cls, *, out_indices, input_indices, input_spatial_shape, output_spatial_shape,
                      kernel_size, stride, padding, dilation, subm, pin, pout, cnt_dev,
-                     pair_num, nbr) -> "IndiceData":
+                     pair_num, nbr, batch_size) -> "IndiceData":
         d = cls(out_indices, None, None, pair_num, input_indices, input_spatial_shape,
                 output_spatial_shape, kernel_size, stride, padding, dilation, subm)
         d._pin, d._pout, d._cnt, d._nbr = pin, pout, cnt_dev, nbr
+        d._batch_size = batch_size
         return d
 
     # --------------------------------------------------- reference fields
@@ -125,31 +131,46 @@ class IndiceData:
 
     # --------------------------------------------------- convolution inputs
     def neighbour_map(self, n_out: int, device) -> torch.Tensor:
-        """[n_out][K] int32: input row feeding output row o through slot k, or -1."""
+        """[K][n_out] int32: input row feeding output row o through slot k, or -1."""
         if self._nbr is None:
             # user-built lists: scatter them into a map (each slot maps an
             # output at most once, as every generator guarantees)
             K = self.K
-            nbr = torch.full((n_out, K), -1, dtype=torch.int32, device=device)
+            nbr = torch.full((K, n_out), -1, dtype=torch.int32, device=device)
             for k, (pi, po) in enumerate(zip(self.pairs_in, self.pairs_out)):
                 if pi.numel():
-                    nbr[po.to(device).long(), k] = pi.to(device).int()
+                    nbr[k, po.to(device).long()] = pi.to(device).int()
             self._nbr = nbr
         return self._nbr
 
-    def execution_order(self, n_out: int, device) -> Optional[torch.Tensor]:
-        """Rows sorted by their slot-occupancy mask (built once, cached)."""
+    def execution_order(self, n_out: int, device, row_bytes: int = 256) -> Optional[torch.Tensor]:
+        """Processing order of the output rows for the fused convolution.
+
+        Morton order cut into regions whose gathered input rows (``row_bytes``
+        each) fit one XCD's 4 MiB L2, each region sorted by slot mask.  Built
+        once per region size and cached; None for small layers.
+        """
         if n_out < _PLAN_MIN_ROWS:
             return None
-        if self._order is None:
+        region = int(min(max(_L2_BYTES // max(int(row_bytes), 1), 2048), 1 << 16))
+        if self._order is None or self._order_region != region:
             nbr = self.neighbour_map(n_out, device)
+            coords = _coords(self.out_indices, "conv plan")
             lib = L.lib()
             ws = L.workspace(lib.tsc_plan_workspace_bytes(n_out, self.K), device)
             order = torch.empty(n_out, dtype=torch.int32, device=device)
-            L.check(lib.tsc_conv_plan(nbr.data_ptr(), n_out, self.K, ws.data_ptr(), ws.numel(),
-                                      order.data_ptr(), L.stream_of(nbr)), "conv plan")
-            self._order = order
+            L.check(lib.tsc_conv_plan(nbr.data_ptr(), coords.data_ptr(), n_out, self.K,
+                                      self._batch_bound(), L.i3(self.output_spatial_shape), region,
+                                      ws.data_ptr(), ws.numel(), order.data_ptr(),
+                                      L.stream_of(nbr)), "conv plan")
+            self._order, self._order_region = order, region
         return self._order
+
+    def _batch_bound(self) -> int:
+        if self._batch_size is None:
+            oi = self.out_indices
+            self._batch_size = int(oi[:, 0].max()) + 1 if len(oi) else 1
+        return max(int(self._batch_size), 1)
 
     def __repr__(self) -> str:
         return (f"IndiceData(subm={self.subm}, K={self.K}, n_out={len(self.out_indices)}, "
@@ -184,7 +205,7 @@ def generate_subm_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size:
     dev = coords.device
     lib = L.lib()
     ws = L.workspace(lib.tsc_subm_workspace_bytes(n, K), dev)
-    nbr = torch.empty((n, K), dtype=torch.int32, device=dev)
+    nbr = torch.empty((K, n), dtype=torch.int32, device=dev)
     pin = torch.empty((K, n), dtype=torch.int32, device=dev)
     pout = torch.empty((K, n), dtype=torch.int32, device=dev)
     counts = torch.empty(K + 1, dtype=torch.int32, device=dev)
@@ -198,7 +219,7 @@ def generate_subm_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size:
         out_indices=indices, input_indices=indices, input_spatial_shape=spatial_shape,
         output_spatial_shape=spatial_shape, kernel_size=ks, stride=(1, 1, 1),
         padding=(0, 0, 0), dilation=dil, subm=True, pin=pin, pout=pout, cnt_dev=counts[:K],
-        pair_num=host[:K].long(), nbr=nbr)
+        pair_num=host[:K].long(), nbr=nbr, batch_size=int(batch_size))
 
 
 def generate_strided_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size: int,
@@ -225,7 +246,7 @@ def generate_strided_indice_pairs(indices: torch.Tensor, spatial_shape, batch_si
     _raise_status(int(host[K + 1]), "generate_strided_indice_pairs")
     n_out = int(host[K])
     out_coords = torch.empty((n_out, 4), dtype=torch.int32, device=dev)
-    nbr = torch.empty((n_out, K), dtype=torch.int32, device=dev)
+    nbr = torch.empty((K, n_out), dtype=torch.int32, device=dev)
     pin = torch.empty((K, n), dtype=torch.int32, device=dev)
     pout = torch.empty((K, n), dtype=torch.int32, device=dev)
     L.check(lib.tsc_strided_fill(coords.data_ptr(), n, int(batch_size), *geo, ws.data_ptr(),
@@ -235,7 +256,8 @@ def generate_strided_indice_pairs(indices: torch.Tensor, spatial_shape, batch_si
     return IndiceData._from_tables(
         out_indices=out_coords, input_indices=indices, input_spatial_shape=shape,
         output_spatial_shape=out_shape, kernel_size=ks, stride=st, padding=pd, dilation=dil,
-        subm=False, pin=pin, pout=pout, cnt_dev=counts[:K], pair_num=host[:K].long(), nbr=nbr)
+        subm=False, pin=pin, pout=pout, cnt_dev=counts[:K], pair_num=host[:K].long(), nbr=nbr,
+        batch_size=int(batch_size))
 
 
 def generate_inverse_indice_pairs(fwd: IndiceData) -> IndiceData:
@@ -261,7 +283,7 @@ def generate_inverse_indice_pairs(fwd: IndiceData) -> IndiceData:
     n_out = int(counts.cpu()[0])
     in_coords = _coords(fwd.input_indices, "inverse pairs")
     out_coords = torch.empty((n_out, 4), dtype=torch.int32, device=dev)
-    nbr = torch.empty((n_out, K), dtype=torch.int32, device=dev)
+    nbr = torch.empty((K, n_out), dtype=torch.int32, device=dev)
     inv_pout = torch.empty((K, cap), dtype=torch.int32, device=dev)
     L.check(lib.tsc_inverse_fill(fwd._pin.data_ptr(), fwd._pout.data_ptr(), fwd._cnt.data_ptr(), K,
                                  cap, in_coords.data_ptr(), n_in, ws.data_ptr(), ws.numel(), n_out,
@@ -272,4 +294,5 @@ def generate_inverse_indice_pairs(fwd: IndiceData) -> IndiceData:
         input_spatial_shape=fwd.output_spatial_shape,
         output_spatial_shape=fwd.input_spatial_shape, kernel_size=fwd.kernel_size,
         stride=fwd.stride, padding=fwd.padding, dilation=fwd.dilation, subm=False,
-        pin=fwd._pout, pout=inv_pout, cnt_dev=fwd._cnt, pair_num=fwd.pair_num, nbr=nbr)
+        pin=fwd._pout, pout=inv_pout, cnt_dev=fwd._cnt, pair_num=fwd.pair_num, nbr=nbr,
+        batch_size=fwd._batch_size)
