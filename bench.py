@@ -159,7 +159,7 @@ def main():
 
     def plan():
         data._order = None
-        data.execution_order(n_out, dev)
+        data.execution_order(n_out, dev, layer["c_in"] * (4 if w.dtype == "float32" else 2))
     plan()
     plan_ms = event_ms(plan, 10)
     P = int(data.pair_num.sum())
@@ -181,9 +181,12 @@ def main():
     step_ms = (t1 - t0) * 1e3 / args.steps
 
     # ---- the conv kernel alone, HIP events on its stream
-    nbr = data.neighbour_map(n_out, dev)
-    order = data.execution_order(n_out, dev)
-    kern_ms = event_ms(lambda: Fn._run(feats, packed, mod.bias, nbr, order, n_out), 20)
+    order = data.execution_order(n_out, dev, layer["c_in"] * feats.element_size())
+    if order is not None:
+        conv_args = (data.ordered_map(), order, n_out, True)
+    else:
+        conv_args = (data.neighbour_map(n_out, dev), None, n_out, False)
+    kern_ms = event_ms(lambda: Fn._run(feats, packed, mod.bias, *conv_args), 20)
     flops = 2.0 * P * layer["c_in"] * layer["c_out"]
     tflops = flops / (kern_ms * 1e-3) / 1e12
     peak, unit = PEAK[w.dtype]

@@ -115,12 +115,15 @@ TSC_API int tsc_inverse_fill(const int32_t* fwd_pairs_in, const int32_t* fwd_pai
  * weight slices and gather nearby inputs.  No reference counterpart (the
  * reference runs slot by slot); the order never changes any output value.
  *   out_coords [n_out][4] are the output rows' (b, z, y, x).
+ *   order [n_out] receives the processing order; nbr_ordered [K][n_out]
+ *   (may be NULL) the map permuted into that order: entry (k, t) is
+ *   nbr[k][order[t]], so the convolution reads it contiguously.
  * ------------------------------------------------------------------------ */
 TSC_API int64_t tsc_plan_workspace_bytes(int64_t n_out, int32_t k_vol);
 TSC_API int tsc_conv_plan(const int32_t* nbr, const int32_t* out_coords, int64_t n_out,
                   int32_t k_vol, int32_t batch_size, const int32_t out_spatial[3] /* host */,
                   int64_t region_rows, void* ws, int64_t ws_bytes, int32_t* order,
-                  tsc_stream_t stream);
+                  int32_t* nbr_ordered, tsc_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Weights.  Replaces normalize_spconv_weight (trispconv/pytorch/weight.py:8-50)
@@ -144,12 +147,15 @@ TSC_API int tsc_pack_weight(const void* w, int32_t w_dtype, int32_t layout, int3
  * results are bitwise reproducible and independent of `order`.
  *   nbr == NULL means the identity map with k_vol == 1 (1x1x1 layers).
  *   order == NULL means rows in index order.
+ *   nbr_ordered != 0 means nbr is the plan's permuted map (entry (k, t)
+ *   belongs to output row order[t]).
  *   bias may be NULL; bias_dtype is its element type.
  * ------------------------------------------------------------------------ */
 TSC_API int tsc_conv_forward(const void* feat, int32_t dtype, int64_t n_in, int32_t c_in,
                      const void* packed_w, const void* bias, int32_t bias_dtype,
-                     const int32_t* nbr, const int32_t* order, int64_t n_out, int32_t k_vol,
-                     int32_t c_out, void* out, tsc_stream_t stream);
+                     const int32_t* nbr, const int32_t* order, int32_t nbr_ordered,
+                     int64_t n_out, int32_t k_vol, int32_t c_out, void* out,
+                     tsc_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -158,6 +158,36 @@ def test_one_by_one_layers(dtype):
     assert rel_err(to_np(z.features), ref) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("c_in,c_out", [(32, 96), (64, 192), (32, 256), (96, 64), (64, 64)])
+@pytest.mark.parametrize("n", [1500, 6000])
+def test_every_bias_dtype_and_column_tile(c_in, c_out, dtype, n):
+    """A bias of any dtype on every MFMA tile shape, with several column tiles
+    per row tile, with (n=6000) and without (n=1500) an execution order."""
+    shape = (24, 24, 24)
+    idx = _tiny(15, shape, 1, n)
+    x = torch.from_numpy(idx).to(DEV)
+    data = generate_subm_indice_pairs(x, shape, 1, 3)
+    rng = np.random.default_rng(16)
+    feats = rng.standard_normal((len(idx), c_in)).astype(np.float32)
+    W = (rng.standard_normal((27, c_in, c_out)) / np.sqrt(27 * c_in)).astype(np.float32)
+    bias = rng.uniform(-1, 1, c_out).astype(np.float32)
+    f = torch.from_numpy(feats).to(DEV).to(dtype)
+    pw = Fn.pack_weight(torch.from_numpy(W).to(DEV), (3, 3, 3), c_in, c_out, dtype)
+    pr = OP.subm_pairs(idx, shape, 1, 3, 1)
+    w64 = rounded(W, dtype)
+    for bdt in (None, torch.float32, torch.float16, torch.bfloat16):
+        b = None if bdt is None else torch.from_numpy(bias).to(DEV).to(bdt)
+        say("bias dtype", bdt, "features", dtype, c_in, "->", c_out, "rows", len(idx))
+        out = Fn.sparse_conv_forward(f, pw, b, data, len(idx))
+        ref = OC.conv_forward(rounded(feats, dtype), w64,
+                              None if b is None else to_np(b).astype(np.float64),
+                              pr.pairs_in, pr.pairs_out, len(idx))
+        got = to_np(out)
+        assert np.isfinite(got).all()
+        assert rel_err(got, ref) <= TOL[dtype], f"bias {bdt}: rel err {rel_err(got, ref)}"
+
+
 @pytest.mark.parametrize("c_in,c_out,dtype", [(16, 16, torch.float32), (128, 128, torch.float16),
                                               (64, 32, torch.bfloat16)])
 def test_deterministic_and_order_independent(c_in, c_out, dtype):

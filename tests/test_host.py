@@ -183,7 +183,7 @@ def test_argument_errors_return_codes_without_gpu():
                                L.i3((1, 1, 1)), L.i3((1, 1, 1)), L.i3((5, 5, 5)), None, 0, None,
                                None)
     assert rc == 1 and b"output shape" in lib.tsc_last_error()
-    rc = lib.tsc_conv_forward(None, 7, 1, 1, None, None, 0, None, None, 1, 1, 1, None, None)
+    rc = lib.tsc_conv_forward(None, 7, 1, 1, None, None, 0, None, None, 0, 1, 1, 1, None, None)
     assert rc == 1 and b"dtype" in lib.tsc_last_error()
     with pytest.raises(ValueError):
         L.check(1, "probe")

@@ -23,6 +23,8 @@
 //     addresses, slots skipped when no lane of the wave needs them.
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace tsc {
 namespace {
 
@@ -32,8 +34,8 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 enum Path { kValu = 0, kMfma16 = 1 };
 
-// 64-channel chunks keep accumulators plus double-buffered operands within
-// 256 registers, so two workgroups (8 waves) share a CU.
+// 64-channel chunks: a ring of four operand buffers (64 registers each at
+// 64 rows per wave) plus the AGPR accumulators fit one wave per SIMD.
 int pick_ck(int c_in) { return c_in % 64 == 0 ? 64 : 32; }
 int pick_bn(int c_out) { return c_out % 128 == 0 ? 128 : (c_out % 64 == 0 ? 64 : 32); }
 
@@ -48,6 +50,20 @@ __device__ __forceinline__ float load_any(const void* p, int dt, int64_t i) {
   if (dt == TSC_F32) return static_cast<const float*>(p)[i];
   if (dt == TSC_F16) return __half2float(static_cast<const __half*>(p)[i]);
   return __bfloat162float(static_cast<const __hip_bfloat16*>(p)[i]);
+}
+
+// Bias entry i as fp32 without a branch on the dtype: two 16-bit reads that
+// are in bounds for every dtype (the halves of an fp32, or the same 16-bit
+// entry twice), then selects.  A three-way branch here, in the epilogue, once
+// led the compiler to leave the output address undefined on the bf16 arm.
+__device__ __forceinline__ float load_bias(const void* p, int dt, int64_t i) {
+  const uint16_t* q = static_cast<const uint16_t*>(p);
+  const bool wide = dt == TSC_F32;
+  const uint32_t lo = q[wide ? 2 * i : i];
+  const uint32_t hi = q[wide ? 2 * i + 1 : i];
+  const uint32_t bits = wide ? (lo | (hi << 16)) : (dt == TSC_BF16 ? lo << 16 : 0u);
+  const float h = __half2float(__ushort_as_half(static_cast<unsigned short>(lo)));
+  return dt == TSC_F16 ? h : __uint_as_float(bits);
 }
 
 __device__ __forceinline__ float src_weight(const void* w, int dt, int layout, int K, int c_in,
@@ -101,8 +117,8 @@ __global__ void pack_mfma_kernel(const void* w, int w_dt, int layout, int K, int
 template <typename T, int CO>
 __global__ void __launch_bounds__(256) conv_valu_kernel(
     const T* __restrict__ feat, int c_in, const float* __restrict__ W, const void* bias, int bias_dt,
-    const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int64_t n_out, int K,
-    int c_out, T* __restrict__ out) {
+    const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int nbr_ordered,
+    int64_t n_out, int K, int c_out, T* __restrict__ out) {
   const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   const int co0 = blockIdx.y * CO;
   const bool valid = t < n_out;
@@ -111,7 +127,8 @@ __global__ void __launch_bounds__(256) conv_valu_kernel(
 #pragma unroll
   for (int c = 0; c < CO; ++c) acc[c] = 0.f;
   for (int k = 0; k < K; ++k) {
-    const int32_t j = valid ? (nbr ? nbr[(int64_t)k * n_out + o] : static_cast<int32_t>(o)) : -1;
+    const int64_t col = nbr_ordered ? t : o;  // the map's column of this row
+    const int32_t j = valid ? (nbr ? nbr[(int64_t)k * n_out + col] : static_cast<int32_t>(o)) : -1;
     if (__ballot(j >= 0) == 0ull) continue;  // no lane of the wave uses slot k
     const T* x = feat + (int64_t)(j >= 0 ? j : 0) * c_in;
     const float* wk = W + (int64_t)k * c_in * c_out + co0;
@@ -126,7 +143,7 @@ __global__ void __launch_bounds__(256) conv_valu_kernel(
   T* dst = out + o * c_out + co0;
 #pragma unroll
   for (int c = 0; c < CO; ++c) {
-    const float b = bias ? load_any(bias, bias_dt, co0 + c) : 0.f;
+    const float b = bias ? load_bias(bias, bias_dt, co0 + c) : 0.f;
     dst[c] = from_f32<T>(acc[c] + b);
   }
 }
@@ -148,43 +165,41 @@ template <> struct MfmaOp<__hip_bfloat16> {
 
 constexpr int kTileRows = 256;  // 4 waves x 64 rows
 
-// 16 bytes per lane, global memory -> LDS without passing through registers
-// (global_load_lds_dwordx4): lane l of the wave writes lds_base + 16*l.  The
-// builtin exists only for the device; the host pass sees an empty body.
-__device__ __forceinline__ void copy16_to_lds(const uint4* src, uint4* lds_base) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
-#else
-  (void)src;
-  (void)lds_base;
-#endif
-}
-
 // Operand source for absent neighbours: lanes whose output row has no input
 // through the current slot read zeros from here instead of branching around
 // their loads (64 bytes per lane are read at most).
 __device__ __attribute__((aligned(256))) uint4 g_zero_row[16];
-// s_waitcnt immediate for "vmcnt(0)", leaving expcnt / lgkmcnt unconstrained
-constexpr int kWaitVmcnt0 = (0x7 << 4) | (0xf << 8);
 
+template <int N> using Slot = std::integral_constant<int, N>;
+
+// One workgroup (4 waves, one per SIMD) per CU; each wave owns 64 rows x BN
+// columns of a 256-row tile.  The work of a tile is a sequence of stages
+// (slot k present in the tile, 64- or 32-channel input chunk c).  Gathered
+// input rows are loaded straight into MFMA operand registers RING-1 stages
+// ahead (a ring of RING register buffers, so RING-1 stages of gathers are in
+// flight while one computes); the stage's weight slab is loaded into registers
+// one stage ahead and written to an LDS double buffer after the MFMAs, so all
+// four waves share one copy.  fp32 accumulators live in AGPRs.
 template <typename T, int BN, int CK>
-__global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
+__global__ void __launch_bounds__(256, 1) conv_mfma_kernel(
     const T* __restrict__ feat, int c_in, const T* __restrict__ W, const void* bias, int bias_dt,
-    const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int64_t n_out, int K,
-    int c_out, T* __restrict__ out) {
+    const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int nbr_ordered,
+    int64_t n_out, int K, int c_out, T* __restrict__ out) {
   using Op = MfmaOp<T>;
   using V = typename Op::V;
+  constexpr int RING = 4;                        // operand buffers (RING-1 stages in flight)
   constexpr int STEPS = CK / 16;                 // 16-deep MFMA steps per chunk
   constexpr int NB = BN / 32;                    // 32-wide column blocks
   constexpr int SLAB_VECS = BN * CK / 8;         // 16-byte vectors of one weight stage
   constexpr int WV = SLAB_VECS >= 256 ? SLAB_VECS / 256 : 1;
   constexpr bool FULL = SLAB_VECS % 256 == 0;
-  static_assert(!FULL || SLAB_VECS / 256 == WV, "slab split");
+  static_assert(WV <= 4, "weight slab too large for the register stage");
 
   __shared__ __attribute__((aligned(16))) uint4 s_w[2][SLAB_VECS];
   __shared__ __attribute__((aligned(16))) int32_t s_orow[kTileRows];
+  __shared__ float s_bias[BN];        // this column tile's bias in fp32 (0 without one)
   __shared__ uint32_t s_mask[8];      // per 32-row block
-  extern __shared__ int32_t s_nbr[];  // [K][kTileRows]
+  extern __shared__ int32_t s_nbr[];  // [K][kTileRows]; output staging at the end
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -194,28 +209,45 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
   // XCDs, so give XCD x a contiguous run of (tile, column tile) items; all
   // column tiles of a row tile, and neighbouring row tiles of the execution
   // order, then share that XCD's L2.
-  const int ncol = c_out / BN;
-  int64_t item;
+  const uint32_t ncol = static_cast<uint32_t>(c_out / BN);
+  uint32_t item;  // the launch keeps the grid below 2^31 workgroups
   {
-    const int64_t nwg = gridDim.x, lin = blockIdx.x;
-    const int64_t per = nwg / 8, rem = nwg % 8, x = lin % 8;
+    const uint32_t nwg = gridDim.x, lin = blockIdx.x;
+    const uint32_t per = nwg / 8, rem = nwg % 8, x = lin % 8;
     item = x * per + (x < rem ? x : rem) + lin / 8;
   }
-  const int64_t tile0 = (item / ncol) * kTileRows;
+  const int64_t tile0 = static_cast<int64_t>(item / ncol) * kTileRows;
   const int nbt = static_cast<int>(item % ncol);
   const int nch = c_in / CK;
 
-  // ---- tile set-up: output rows, their slot lists and slot masks
+  // ---- tile set-up: output rows, their slot lists and slot masks.  The map
+  // entries are read eight slots at a time, all eight loads in flight before
+  // any is used (rows past the end read row 0 and are then discarded).
   {
     const int64_t tr = tile0 + t;
     const int32_t orow = tr < n_out ? (order ? order[tr] : static_cast<int32_t>(tr)) : -1;
     s_orow[t] = orow;
+    // column of the map holding this row: its processing position when the map
+    // was permuted into the execution order (contiguous reads), else the row
+    const int64_t src_row = orow >= 0 ? (nbr_ordered ? tr : orow) : 0;
+    if (t < BN) s_bias[t] = bias ? load_bias(bias, bias_dt, (int64_t)nbt * BN + t) : 0.f;
     uint32_t m = 0;
-    for (int k = 0; k < K; ++k) {
-      int32_t j = -1;
-      if (orow >= 0) j = nbr ? nbr[(int64_t)k * n_out + orow] : orow;
-      s_nbr[k * kTileRows + t] = j;
-      m |= (j >= 0 ? 1u : 0u) << (k & 31);
+    for (int k0 = 0; k0 < K; k0 += 8) {
+      int32_t jv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int k = k0 + i < K ? k0 + i : K - 1;
+        jv[i] = nbr ? nbr[(int64_t)k * n_out + src_row] : static_cast<int32_t>(orow >= 0 ? orow : 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int k = k0 + i;
+        const int32_t j = orow >= 0 ? jv[i] : -1;
+        if (k < K) {
+          s_nbr[k * kTileRows + t] = j;
+          m |= (j >= 0 ? 1u : 0u) << (k & 31);
+        }
+      }
     }
     // OR over each 32-row half-wave: the rows one MFMA row block covers
 #pragma unroll
@@ -226,14 +258,19 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
   uint32_t umask = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) umask |= s_mask[i];
-  const uint32_t bmask0 = s_mask[wave * 2], bmask1 = s_mask[wave * 2 + 1];
+  // wave-uniform values kept in scalar registers
+  umask = __builtin_amdgcn_readfirstlane(umask);
+  const uint32_t wmask = __builtin_amdgcn_readfirstlane(s_mask[wave * 2] | s_mask[wave * 2 + 1]);
   const int r0 = wave * 64 + (lane & 31);  // tile rows of this lane's A operands
   const int r1 = r0 + 32;
 
-  auto next_k = [&](int k) {
+  // stage (k, c) -> the next stage; k == K marks the end
+  auto advance = [&](int& k, int& c) {
+    if (k >= K) return;
+    if (++c < nch) return;
+    c = 0;
     for (++k; k < K; ++k)
-      if (umask & (1u << (k & 31))) return k;
-    return K;
+      if (umask & (1u << (k & 31))) return;
   };
 
   const uint4* Wv = reinterpret_cast<const uint4*>(W);
@@ -247,136 +284,167 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[rb][nb][i] = 0.f;
 
-  uint4 a_cur[2][STEPS], a_nxt[2][STEPS];
+  uint4 ring[RING][2][STEPS];
+  uint4 wr0, wr1, wr2, wr3;
 
-// Weight slab of stage (KK, CC) -> s_w[BUF], straight from global memory
-// into LDS (global_load_lds_dwordx4: lane l of a wave lands at base + 16*l).
-#define TSC_LOAD_W(KK, CC, BUF)                                                               \
-  {                                                                                           \
-    const uint4* src_ =                                                                       \
-        Wv + (((int64_t)(KK) * nch + (CC)) * nbt_all + (int64_t)nbt * NB) * STEPS * 64;        \
-    _Pragma("unroll") for (int v = 0; v < WV; ++v) {                                          \
-      if (FULL || v * 256 + t < SLAB_VECS)                                                    \
-        copy16_to_lds(src_ + v * 256 + t, &s_w[BUF][v * 256 + wave * 64]);                    \
-    }                                                                                         \
-  }
-#define TSC_LOAD_A(DST, KK, CC)                                                               \
-  {                                                                                           \
-    const int32_t j0_ = s_nbr[(KK) * kTileRows + r0];                                         \
-    const int32_t j1_ = s_nbr[(KK) * kTileRows + r1];                                         \
-    const int coff_ = (CC) * CK + h * (CK / 2);                                               \
-    const uint4* p0_ = j0_ >= 0 ? reinterpret_cast<const uint4*>(feat + (int64_t)j0_ * c_in + coff_) \
-                                : g_zero_row;                                                  \
-    const uint4* p1_ = j1_ >= 0 ? reinterpret_cast<const uint4*>(feat + (int64_t)j1_ * c_in + coff_) \
-                                : g_zero_row;                                                  \
-    _Pragma("unroll") for (int s_ = 0; s_ < STEPS; ++s_) {                                    \
-      DST[0][s_] = p0_[s_];                                                                   \
-      DST[1][s_] = p1_[s_];                                                                   \
-    }                                                                                         \
-  }
-
-  int k = (umask & 1u) ? 0 : next_k(0);
-  int c = 0;
-  int buf = 0;
-  if (k < K) {
-    TSC_LOAD_W(k, c, 0);
-    TSC_LOAD_A(a_cur, k, c);
-  }
-  __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
-  __syncthreads();
-  while (k < K) {
-    int kn = k, cn = c + 1;
-    if (cn == nch) {
-      cn = 0;
-      kn = next_k(k);
+  // Loads are issued whether or not the stage exists (past the last stage they
+  // re-read stage 0 or the zero row), keeping the loop body straight-line so
+  // the compiler's wait counters see each operand's true age.
+  auto load_w = [&](int k, int c) {
+    if (k >= K) k = c = 0;
+    const uint4* src = Wv + (((int64_t)k * nch + c) * nbt_all + (int64_t)nbt * NB) * STEPS * 64 + t;
+    if (FULL || t < SLAB_VECS) wr0 = src[0];
+    if constexpr (WV > 1) wr1 = src[256];
+    if constexpr (WV > 2) wr2 = src[512];
+    if constexpr (WV > 3) wr3 = src[768];
+  };
+  auto store_w = [&](uint4* dst) {
+    if (FULL || t < SLAB_VECS) dst[t] = wr0;
+    if constexpr (WV > 1) dst[256 + t] = wr1;
+    if constexpr (WV > 2) dst[512 + t] = wr2;
+    if constexpr (WV > 3) dst[768 + t] = wr3;
+  };
+  auto load_a = [&](auto slot, int k, int c) {
+    constexpr int S = decltype(slot)::value;
+    const bool live = k < K;
+    const int32_t j0 = live ? s_nbr[k * kTileRows + r0] : -1;
+    const int32_t j1 = live ? s_nbr[k * kTileRows + r1] : -1;
+    const int coff = c * CK + h * (CK / 2);
+    const uint4* p0 = j0 >= 0 ? reinterpret_cast<const uint4*>(feat + (int64_t)j0 * c_in + coff)
+                              : g_zero_row;
+    const uint4* p1 = j1 >= 0 ? reinterpret_cast<const uint4*>(feat + (int64_t)j1 * c_in + coff)
+                              : g_zero_row;
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+      ring[S][0][s] = p0[s];
+      ring[S][1][s] = p1[s];
     }
-    const bool more = kn < K;
-    // gathers for the next stage go out before this stage's MFMAs; the weight
-    // slab copy (global -> LDS) is issued after them so that no LDS write is
-    // in flight while the MFMA operands are read from LDS
-    if (more) TSC_LOAD_A(a_nxt, kn, cn);
+  };
+  auto compute = [&](auto slot, int k, const uint4* sw) {
+    constexpr int S = decltype(slot)::value;
     // a 32-row block with no input through slot k skips its MFMAs (its
     // operands are zero and would add exact zeros)
-    const uint32_t kbit = 1u << (k & 31);
-    const bool use0 = (bmask0 & kbit) != 0, use1 = (bmask1 & kbit) != 0;
-    if (use0 || use1) {
-      const uint4* sw = s_w[buf];
+    // A wave whose 64 rows have no input through slot k skips the stage's
+    // MFMAs (past the last stage nothing is computed).  The test is a single
+    // uniform branch around all accumulators, so they stay in place.
+    const uint32_t kbit = k < K ? 1u << (k & 31) : 0u;
+    if (!(wmask & kbit)) return;
 #pragma unroll
-      for (int s = 0; s < STEPS; ++s) {
-        const V a0 = __builtin_bit_cast(V, a_cur[0][s]);
-        const V a1 = __builtin_bit_cast(V, a_cur[1][s]);
+    for (int s = 0; s < STEPS; ++s) {
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          const V b = __builtin_bit_cast(V, sw[(nb * STEPS + s) * 64 + lane]);
-          if (use0) acc[0][nb] = Op::run(a0, b, acc[0][nb]);
-          if (use1) acc[1][nb] = Op::run(a1, b, acc[1][nb]);
-        }
+      for (int nb = 0; nb < NB; ++nb) {
+        const V b = __builtin_bit_cast(V, sw[(nb * STEPS + s) * 64 + lane]);
+        acc[0][nb] = Op::run(__builtin_bit_cast(V, ring[S][0][s]), b, acc[0][nb]);
+        acc[1][nb] = Op::run(__builtin_bit_cast(V, ring[S][1][s]), b, acc[1][nb]);
       }
     }
-    if (more) TSC_LOAD_W(kn, cn, buf ^ 1);
-    // the next stage's weight slab (and operands) must have landed before any
-    // wave reads it
-    __builtin_amdgcn_s_waitcnt(kWaitVmcnt0);
+  };
+
+  // stage descriptors: current (kc, cc), next (kw, cw) and RING-1 ahead (ka, ca)
+  int kc = 0, cc = 0;
+  if (!(umask & 1u)) {
+    kc = -1;
+    cc = nch - 1;
+    advance(kc, cc);
+  }
+  int kw = kc, cw = cc;
+  advance(kw, cw);
+  int ka = kw, ca = cw;
+  // prologue: operands of the first RING-1 stages, weights of the first
+  load_a(Slot<0>{}, kc, cc);
+  load_w(kc, cc);
+  store_w(s_w[0]);
+  load_a(Slot<1>{}, ka, ca);
+  advance(ka, ca);
+  load_a(Slot<2>{}, ka, ca);
+  advance(ka, ca);  // now RING-1 = 3 stages ahead of kc
+  __syncthreads();
+
+  auto body = [&](auto slot) {
+    constexpr int S = decltype(slot)::value;
+    load_w(kw, cw);                                    // weights, 1 stage ahead
+    load_a(Slot<(S + RING - 1) % RING>{}, ka, ca);     // operands, 3 stages ahead
+    compute(Slot<S>{}, kc, s_w[S & 1]);
+    store_w(s_w[(S + 1) & 1]);
     __syncthreads();
+    kc = kw;
+    cc = cw;
+    advance(kw, cw);
+    advance(ka, ca);
+  };
+  // four bodies per trip keep every ring slot a fixed register set; bodies
+  // past the last stage load harmless data and compute nothing
+  while (kc < K) {
+    body(Slot<0>{});
+    body(Slot<1>{});
+    body(Slot<2>{});
+    body(Slot<3>{});
+  }
+
+  // ---- epilogue: + bias, round once, store each output element once.
+  // The tile is transposed through LDS so that every lane writes 16-byte
+  // pieces of output rows (whole rows per group of lanes) instead of single
+  // elements.  32x32 accumulator layout: register i of lane l holds row
+  // (i/4)*8 + (l/32)*4 + i%4 and column l%32 of the block.
+  constexpr int ROW_BYTES = BN * (int)sizeof(T);
+  constexpr int STRIDE = ROW_BYTES + 16;            // padded LDS row
+  constexpr int CHUNKS = ROW_BYTES / 16;            // 16-byte pieces per row
+  __syncthreads();                                  // s_nbr is free again
+  char* stage = reinterpret_cast<char*>(s_nbr) + wave * 64 * STRIDE;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int cl = nb * 32 + (lane & 31);
+    const float bv = s_bias[cl];
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-      for (int s = 0; s < STEPS; ++s) a_cur[rb][s] = a_nxt[rb][s];
-    buf ^= 1;
-    k = kn;
-    c = cn;
-  }
-#undef TSC_LOAD_W
-#undef TSC_LOAD_A
-
-  // ---- epilogue: + bias, round once, store each output element once.
-  // 32x32 accumulator layout: register i of lane l holds row
-  // (i/4)*8 + (l/32)*4 + i%4 and column l%32 of the block.
-  int4 orows[2][4];  // rows (rb, g): 4 consecutive rows starting at wave*64 + rb*32 + g*8 + h*4
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-    for (int g = 0; g < 4; ++g)
-      orows[rb][g] = *reinterpret_cast<const int4*>(&s_orow[wave * 64 + rb * 32 + g * 8 + h * 4]);
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int col = nbt * BN + nb * 32 + (lane & 31);
-    const float bv = bias ? load_any(bias, bias_dt, col) : 0.f;
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-#pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int4 q = orows[rb][i >> 2];
-        const int32_t orow = (i & 3) == 0 ? q.x : (i & 3) == 1 ? q.y : (i & 3) == 2 ? q.z : q.w;
-        if (orow >= 0) out[(int64_t)orow * c_out + col] = from_f32<T>(acc[rb][nb][i] + bv);
+        const int row = rb * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
+        *reinterpret_cast<T*>(stage + row * STRIDE + cl * (int)sizeof(T)) =
+            from_f32<T>(acc[rb][nb][i] + bv);
       }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < CHUNKS; ++q) {
+    const int piece = q * 64 + lane;
+    const int row = piece / CHUNKS, ch = piece % CHUNKS;
+    const int32_t orow = s_orow[wave * 64 + row];
+    if (orow >= 0) {
+      const uint4 v = *reinterpret_cast<const uint4*>(stage + row * STRIDE + ch * 16);
+      *reinterpret_cast<uint4*>(out + (int64_t)orow * c_out + nbt * BN + ch * (16 / (int)sizeof(T))) = v;
     }
   }
 }
 
 template <typename T, int BN, int CK>
 int launch_mfma(const void* feat, int c_in, const void* W, const void* bias, int bias_dt,
-                const int32_t* nbr, const int32_t* order, int64_t n_out, int K, int c_out,
-                void* out, hipStream_t s) {
+                const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
+                int c_out, void* out, hipStream_t s) {
   const int64_t items = ceil_div(n_out, kTileRows) * (c_out / BN);
+  TSC_REQUIRE(items < (int64_t(1) << 31), "conv: %lld workgroups exceed the grid limit",
+              static_cast<long long>(items));
   dim3 grid(static_cast<unsigned>(items));
-  const size_t lds = (size_t)K * kTileRows * sizeof(int32_t);
+  // dynamic LDS: the tile's slot lists, later reused to stage the output
+  const size_t lds_nbr = (size_t)K * kTileRows * sizeof(int32_t);
+  const size_t lds_out = (size_t)kTileRows * (BN * sizeof(T) + 16);
+  const size_t lds = lds_nbr > lds_out ? lds_nbr : lds_out;
   conv_mfma_kernel<T, BN, CK><<<grid, 256, lds, s>>>(
-      static_cast<const T*>(feat), c_in, static_cast<const T*>(W), bias, bias_dt, nbr, order, n_out,
-      K, c_out, static_cast<T*>(out));
+      static_cast<const T*>(feat), c_in, static_cast<const T*>(W), bias, bias_dt, nbr, order,
+      nbr_ordered, n_out, K, c_out, static_cast<T*>(out));
   TSC_LAUNCH_CHECK("conv_mfma");
   return 0;
 }
 
 template <typename T>
 int dispatch_mfma(const void* feat, int c_in, const void* W, const void* bias, int bias_dt,
-                  const int32_t* nbr, const int32_t* order, int64_t n_out, int K, int c_out,
-                  void* out, hipStream_t s) {
+                  const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
+                  int c_out, void* out, hipStream_t s) {
   const int bn = pick_bn(c_out), ck = pick_ck(c_in);
 #define TSC_MFMA_CASE(BN_, CK_)                                                              \
   if (bn == BN_ && ck == CK_)                                                                \
-    return launch_mfma<T, BN_, CK_>(feat, c_in, W, bias, bias_dt, nbr, order, n_out, K, c_out, \
-                                    out, s);
+    return launch_mfma<T, BN_, CK_>(feat, c_in, W, bias, bias_dt, nbr, order, nbr_ordered, \
+                                    n_out, K, c_out, out, s);
   TSC_MFMA_CASE(128, 64)
   TSC_MFMA_CASE(128, 32)
   TSC_MFMA_CASE(64, 64)
@@ -389,24 +457,25 @@ int dispatch_mfma(const void* feat, int c_in, const void* W, const void* bias, i
 
 template <typename T, int CO>
 int launch_valu(const void* feat, int c_in, const void* W, const void* bias, int bias_dt,
-                const int32_t* nbr, const int32_t* order, int64_t n_out, int K, int c_out,
-                void* out, hipStream_t s) {
+                const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
+                int c_out, void* out, hipStream_t s) {
   dim3 grid(static_cast<unsigned>(ceil_div(n_out, 256)), static_cast<unsigned>(c_out / CO));
   conv_valu_kernel<T, CO><<<grid, 256, 0, s>>>(static_cast<const T*>(feat), c_in,
                                                static_cast<const float*>(W), bias, bias_dt, nbr,
-                                               order, n_out, K, c_out, static_cast<T*>(out));
+                                               order, nbr_ordered, n_out, K, c_out,
+                                               static_cast<T*>(out));
   TSC_LAUNCH_CHECK("conv_valu");
   return 0;
 }
 
 template <typename T>
 int dispatch_valu(const void* feat, int c_in, const void* W, const void* bias, int bias_dt,
-                  const int32_t* nbr, const int32_t* order, int64_t n_out, int K, int c_out,
-                  void* out, hipStream_t s) {
+                  const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
+                  int c_out, void* out, hipStream_t s) {
 #define TSC_VALU_CASE(CO_)                                                                   \
   if (c_out % CO_ == 0)                                                                      \
-    return launch_valu<T, CO_>(feat, c_in, W, bias, bias_dt, nbr, order, n_out, K, c_out, out, \
-                               s);
+    return launch_valu<T, CO_>(feat, c_in, W, bias, bias_dt, nbr, order, nbr_ordered, n_out, K, \
+                               c_out, out, s);
   TSC_VALU_CASE(32)
   TSC_VALU_CASE(16)
   TSC_VALU_CASE(8)
@@ -456,8 +525,9 @@ extern "C" int tsc_pack_weight(const void* w, int32_t w_dtype, int32_t layout, i
 
 extern "C" int tsc_conv_forward(const void* feat, int32_t dtype, int64_t n_in, int32_t c_in,
                                 const void* packed_w, const void* bias, int32_t bias_dtype,
-                                const int32_t* nbr, const int32_t* order, int64_t n_out,
-                                int32_t k_vol, int32_t c_out, void* out, tsc_stream_t stream) {
+                                const int32_t* nbr, const int32_t* order, int32_t nbr_ordered,
+                                int64_t n_out, int32_t k_vol, int32_t c_out, void* out,
+                                tsc_stream_t stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   TSC_REQUIRE(dtype_ok(dtype), "conv: unsupported dtype %d", dtype);
   TSC_REQUIRE(!bias || dtype_ok(bias_dtype), "conv: unsupported bias dtype %d", bias_dtype);
@@ -466,6 +536,7 @@ extern "C" int tsc_conv_forward(const void* feat, int32_t dtype, int64_t n_in, i
               "conv: row counts out of range");
   TSC_REQUIRE(nbr || k_vol == 1, "conv: identity map needs k_vol == 1");
   TSC_REQUIRE(nbr || n_in >= n_out, "conv: identity map needs n_in >= n_out");
+  TSC_REQUIRE(!nbr_ordered || (order && nbr), "conv: an ordered map needs its order");
   if (n_out == 0) return 0;
   TSC_REQUIRE(packed_w && out && (feat || n_in == 0), "conv: null pointer");
   if (n_in == 0) {
@@ -475,20 +546,21 @@ extern "C" int tsc_conv_forward(const void* feat, int32_t dtype, int64_t n_in, i
   const Path path = pick_path(dtype, c_in, c_out, k_vol);
   if (path == kMfma16) {
     TSC_REQUIRE((reinterpret_cast<uintptr_t>(feat) & 15) == 0 &&
-                    (reinterpret_cast<uintptr_t>(packed_w) & 15) == 0,
-                "conv: feature and weight buffers must be 16-byte aligned");
+                    (reinterpret_cast<uintptr_t>(packed_w) & 15) == 0 &&
+                    (reinterpret_cast<uintptr_t>(out) & 15) == 0,
+                "conv: feature, weight and output buffers must be 16-byte aligned");
     if (dtype == TSC_F16)
-      return dispatch_mfma<__half>(feat, c_in, packed_w, bias, bias_dtype, nbr, order, n_out,
-                                   k_vol, c_out, out, s);
+      return dispatch_mfma<__half>(feat, c_in, packed_w, bias, bias_dtype, nbr, order, nbr_ordered,
+                                   n_out, k_vol, c_out, out, s);
     return dispatch_mfma<__hip_bfloat16>(feat, c_in, packed_w, bias, bias_dtype, nbr, order,
-                                         n_out, k_vol, c_out, out, s);
+                                         nbr_ordered, n_out, k_vol, c_out, out, s);
   }
   if (dtype == TSC_F32)
-    return dispatch_valu<float>(feat, c_in, packed_w, bias, bias_dtype, nbr, order, n_out, k_vol,
-                                c_out, out, s);
+    return dispatch_valu<float>(feat, c_in, packed_w, bias, bias_dtype, nbr, order, nbr_ordered,
+                                n_out, k_vol, c_out, out, s);
   if (dtype == TSC_F16)
-    return dispatch_valu<__half>(feat, c_in, packed_w, bias, bias_dtype, nbr, order, n_out, k_vol,
-                                 c_out, out, s);
-  return dispatch_valu<__hip_bfloat16>(feat, c_in, packed_w, bias, bias_dtype, nbr, order, n_out,
-                                       k_vol, c_out, out, s);
+    return dispatch_valu<__half>(feat, c_in, packed_w, bias, bias_dtype, nbr, order, nbr_ordered,
+                                 n_out, k_vol, c_out, out, s);
+  return dispatch_valu<__hip_bfloat16>(feat, c_in, packed_w, bias, bias_dtype, nbr, order,
+                                       nbr_ordered, n_out, k_vol, c_out, out, s);
 }

@@ -108,6 +108,24 @@ __global__ void __launch_bounds__(256) gather_rows_kernel(const uint32_t* __rest
   order[i] = static_cast<int32_t>(rows[pos[i]]);
 }
 
+// nbr_ordered[k][t] = nbr[k][order[t]]; eight slots' reads in flight at once.
+__global__ void __launch_bounds__(256) permute_map_kernel(const int32_t* __restrict__ nbr,
+                                                          const int32_t* __restrict__ order,
+                                                          int64_t n, int K,
+                                                          int32_t* __restrict__ out) {
+  const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (t >= n) return;
+  const int64_t o = order[t];
+  for (int k0 = 0; k0 < K; k0 += 8) {
+    int32_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = nbr[(int64_t)(k0 + i < K ? k0 + i : K - 1) * n + o];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (k0 + i < K) out[(int64_t)(k0 + i) * n + t] = v[i];
+  }
+}
+
 __global__ void __launch_bounds__(kThreads) radix_hist_kernel(const uint32_t* __restrict__ vals,
                                                               int64_t n, Digits d,
                                                               uint32_t* __restrict__ hist,
@@ -229,7 +247,7 @@ extern "C" int64_t tsc_plan_workspace_bytes(int64_t n_out, int32_t k_vol) {
 extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* out_coords, int64_t n_out,
                              int32_t k_vol, int32_t batch_size, const int32_t out_spatial[3],
                              int64_t region_rows, void* ws, int64_t ws_bytes, int32_t* order,
-                             tsc_stream_t stream) {
+                             int32_t* nbr_ordered, tsc_stream_t stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   TSC_REQUIRE(n_out >= 0 && n_out < (int64_t(1) << 31), "plan: n_out out of range");
   TSC_REQUIRE(k_vol > 0 && batch_size > 0, "plan: invalid kernel volume or batch size");
@@ -286,5 +304,9 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* out_coords, int6
   }
   gather_rows_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(vi, b.rows, n_out, order);
   TSC_LAUNCH_CHECK("plan_gather");
+  if (nbr_ordered) {
+    permute_map_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(nbr, order, n_out, k_vol, nbr_ordered);
+    TSC_LAUNCH_CHECK("plan_permute_map");
+  }
   return 0;
 }

@@ -19,7 +19,8 @@ from .weight import PackedWeight, pack_weight
 
 
 def _run(features: torch.Tensor, packed: PackedWeight, bias: Optional[torch.Tensor],
-         nbr: Optional[torch.Tensor], order: Optional[torch.Tensor], n_out: int) -> torch.Tensor:
+         nbr: Optional[torch.Tensor], order: Optional[torch.Tensor], n_out: int,
+         nbr_ordered: bool = False) -> torch.Tensor:
     L.require_gpu(features, "sparse_conv_forward")
     feats = features.contiguous()
     if feats.data_ptr() % 16:
@@ -38,7 +39,8 @@ def _run(features: torch.Tensor, packed: PackedWeight, bias: Optional[torch.Tens
     L.check(lib.tsc_conv_forward(
         feats.data_ptr(), L.dtype_code(feats.dtype), feats.shape[0], packed.c_in,
         packed.data.data_ptr(), L.ptr(b), L.dtype_code(b.dtype) if b is not None else 0,
-        L.ptr(nbr), L.ptr(order), n_out, packed.k_vol, packed.c_out, out.data_ptr(),
+        L.ptr(nbr), L.ptr(order), int(nbr_ordered), n_out, packed.k_vol, packed.c_out,
+        out.data_ptr(),
         L.stream_of(feats)), "sparse_conv_forward")
     return out
 
@@ -54,7 +56,9 @@ def sparse_conv_forward(features: torch.Tensor, weight: Union[torch.Tensor, Pack
     nbr = indice_data.neighbour_map(N_out, features.device)
     order = indice_data.execution_order(N_out, features.device,
                                         weight.c_in * features.element_size())
-    return _run(features, weight, bias, nbr, order, N_out)
+    if order is not None:
+        return _run(features, weight, bias, indice_data.ordered_map(), order, N_out, True)
+    return _run(features, weight, bias, nbr, None, N_out)
 
 
 def dense_forward(features: torch.Tensor, weight: PackedWeight,

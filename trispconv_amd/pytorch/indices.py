@@ -78,6 +78,7 @@ class IndiceData:
         self._order: Optional[torch.Tensor] = None  # [n_out] int32 execution order
         self._inverse_cache: Optional["IndiceData"] = None
         self._order_region = 0
+        self._nbr_ordered: Optional[torch.Tensor] = None
         self._batch_size: Optional[int] = None
 
     # --------------------------------------------------- construction
@@ -127,6 +128,7 @@ class IndiceData:
 
     def _drop_tables(self) -> None:
         self._pin = self._pout = self._cnt = self._nbr = self._order = None
+        self._nbr_ordered = None
         self._inverse_cache = None
 
     # --------------------------------------------------- convolution inputs
@@ -159,12 +161,17 @@ class IndiceData:
             lib = L.lib()
             ws = L.workspace(lib.tsc_plan_workspace_bytes(n_out, self.K), device)
             order = torch.empty(n_out, dtype=torch.int32, device=device)
+            nbr_ordered = torch.empty_like(nbr)
             L.check(lib.tsc_conv_plan(nbr.data_ptr(), coords.data_ptr(), n_out, self.K,
                                       self._batch_bound(), L.i3(self.output_spatial_shape), region,
                                       ws.data_ptr(), ws.numel(), order.data_ptr(),
-                                      L.stream_of(nbr)), "conv plan")
-            self._order, self._order_region = order, region
+                                      nbr_ordered.data_ptr(), L.stream_of(nbr)), "conv plan")
+            self._order, self._order_region, self._nbr_ordered = order, region, nbr_ordered
         return self._order
+
+    def ordered_map(self) -> Optional[torch.Tensor]:
+        """The neighbour map permuted into the execution order (None without one)."""
+        return self._nbr_ordered if self._order is not None else None
 
     def _batch_bound(self) -> int:
         if self._batch_size is None:
