@@ -3,13 +3,18 @@
     python -m trispconv_amd.profiling trace  <out_dir>            # kernel-trace stats
     python -m trispconv_amd.profiling pmc    <out_dir> [--kernel SUBSTR]
     python -m trispconv_amd.profiling calib  <out_dir> --bytes N  [--kernel SUBSTR]
+    python -m trispconv_amd.profiling traffic --fetch DIR --write DIR --trace DIR
+            --kernel SUBSTR --calib-kernel SUBSTR --calib-bytes N [--algorithmic-bytes B]
 
 ``out_dir`` is a rocprofv3 ``-d`` directory written with ``--output-format
 csv``.  ``trace`` prints per-kernel call count and average / min / max /
 total duration; ``pmc`` prints the per-dispatch average of every collected
 counter for the kernels whose name contains SUBSTR; ``calib`` prints the
 counter value per byte for a copy kernel of known size (the FETCH_SIZE /
-WRITE_SIZE scale factor).
+WRITE_SIZE scale factor); ``traffic`` combines a FETCH_SIZE pass, a WRITE_SIZE
+pass (each holding one copy-like kernel that reads and writes N bytes) and a
+kernel trace into HBM bytes per launch of one kernel, scaled by what the
+counters read for the copy.
 """
 from __future__ import annotations
 
@@ -69,14 +74,59 @@ def calib(out_dir: Path, kernel: str, nbytes: int) -> None:
               f" ({n} dispatches)")
 
 
+def _avg_duration_us(trace_dir: Path, kernel: str):
+    durs = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            for r in _rows(trace_dir, "kernel_trace.csv") if kernel in r["Kernel_Name"]]
+    return (sum(durs) / len(durs), len(durs)) if durs else (float("nan"), 0)
+
+
+def traffic(fetch_dir: Path, write_dir: Path, trace_dir: Path, kernel: str, calib_kernel: str,
+            calib_bytes: int, algorithmic: float) -> None:
+    """FETCH_SIZE and WRITE_SIZE are in KiB per dispatch; each is divided by
+    what it reads per byte of the copy-like calibration kernel."""
+    f_k, nf = _pmc(fetch_dir, kernel)["FETCH_SIZE"]
+    w_k, nw = _pmc(write_dir, kernel)["WRITE_SIZE"]
+    f_c, _ = _pmc(fetch_dir, calib_kernel)["FETCH_SIZE"]
+    w_c, _ = _pmc(write_dir, calib_kernel)["WRITE_SIZE"]
+    f_scale = f_c * 1024.0 / calib_bytes
+    w_scale = w_c * 1024.0 / calib_bytes
+    fetch_b = f_k * 1024.0 / f_scale
+    write_b = w_k * 1024.0 / w_scale
+    avg_us, nt = _avg_duration_us(trace_dir, kernel)
+    print(f"kernel: {kernel}")
+    print(f"kernel_avg_us: {avg_us:.2f}")
+    print(f"kernel_trace_dispatches: {nt}")
+    print(f"fetch_kib_per_dispatch: {f_k:.1f}   (avg over {nf} dispatches)")
+    print(f"write_kib_per_dispatch: {w_k:.1f}   (avg over {nw} dispatches)")
+    print(f"calib_fetch_counter_per_byte: {f_scale:.4f}   ({calib_kernel}, {calib_bytes} bytes)")
+    print(f"calib_write_counter_per_byte: {w_scale:.4f}")
+    print(f"fetch_bytes_per_launch: {fetch_b:.0f}")
+    print(f"write_bytes_per_launch: {write_b:.0f}")
+    print(f"traffic_bytes_per_launch: {fetch_b + write_b:.0f}")
+    if algorithmic:
+        print(f"algorithmic_bytes_per_launch: {algorithmic:.0f}")
+        print(f"traffic_over_algorithmic: {(fetch_b + write_b) / algorithmic:.3f}")
+    if avg_us == avg_us and avg_us > 0:
+        print(f"hbm_gbs_at_avg_duration: {(fetch_b + write_b) / (avg_us * 1e3):.1f}")
+
+
 def main(argv=None) -> None:
     ap = argparse.ArgumentParser()
-    ap.add_argument("mode", choices=["trace", "pmc", "calib"])
-    ap.add_argument("out_dir", type=Path)
+    ap.add_argument("mode", choices=["trace", "pmc", "calib", "traffic"])
+    ap.add_argument("out_dir", type=Path, nargs="?")
     ap.add_argument("--kernel", default="")
     ap.add_argument("--bytes", type=int, default=0)
+    ap.add_argument("--fetch", type=Path)
+    ap.add_argument("--write", type=Path)
+    ap.add_argument("--trace", type=Path)
+    ap.add_argument("--calib-kernel", default="")
+    ap.add_argument("--calib-bytes", type=int, default=0)
+    ap.add_argument("--algorithmic-bytes", type=float, default=0.0)
     a = ap.parse_args(argv)
-    if a.mode == "trace":
+    if a.mode == "traffic":
+        traffic(a.fetch, a.write, a.trace, a.kernel, a.calib_kernel, a.calib_bytes,
+                a.algorithmic_bytes)
+    elif a.mode == "trace":
         trace(a.out_dir)
     elif a.mode == "pmc":
         pmc(a.out_dir, a.kernel)
