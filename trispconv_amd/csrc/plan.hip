@@ -86,17 +86,33 @@ __global__ void __launch_bounds__(256) spatial_key_kernel(const int4* __restrict
   vals[o] = static_cast<uint32_t>(o);
 }
 
+// mask_row[o] = slot mask of output row o.  Lanes take consecutive rows, so
+// every slot's map column is read coalesced; eight slots' loads in flight.
+__global__ void __launch_bounds__(256) row_mask_kernel(const int32_t* __restrict__ nbr, int64_t n,
+                                                       int K, uint32_t* __restrict__ mask_row) {
+  const int64_t o = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (o >= n) return;
+  uint32_t m = 0;
+  for (int k0 = 0; k0 < K; k0 += 8) {
+    int32_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = nbr[(int64_t)(k0 + i < K ? k0 + i : K - 1) * n + o];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (k0 + i < K) m |= (v[i] >= 0 ? 1u : 0u) << ((k0 + i) & 31);
+  }
+  mask_row[o] = m;
+}
+
 // mask_pos[i] = slot mask of output row rows[i]; vals[i] = i.
-__global__ void __launch_bounds__(256) mask_at_pos_kernel(const int32_t* __restrict__ nbr, int64_t n,
-                                                          int K, const uint32_t* __restrict__ rows,
+__global__ void __launch_bounds__(256) mask_at_pos_kernel(const uint32_t* __restrict__ mask_row,
+                                                          int64_t n,
+                                                          const uint32_t* __restrict__ rows,
                                                           uint32_t* __restrict__ mask_pos,
                                                           uint32_t* __restrict__ vals) {
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const uint32_t o = rows[i];
-  uint32_t m = 0;
-  for (int k = 0; k < K; ++k) m |= (nbr[(int64_t)k * n + o] >= 0 ? 1u : 0u) << (k & 31);
-  mask_pos[i] = m;
+  mask_pos[i] = mask_row[rows[i]];
   vals[i] = static_cast<uint32_t>(i);
 }
 
@@ -108,21 +124,22 @@ __global__ void __launch_bounds__(256) gather_rows_kernel(const uint32_t* __rest
   order[i] = static_cast<int32_t>(rows[pos[i]]);
 }
 
-// nbr_ordered[k][t] = nbr[k][order[t]]; eight slots' reads in flight at once.
+// nbr_ordered[k][t] = nbr[k][order[t]].  blockIdx.y is the slot: blocks are
+// dispatched x-fastest, so the blocks in flight share one slot's column and
+// its gathered entries stay in cache; four positions per thread.
 __global__ void __launch_bounds__(256) permute_map_kernel(const int32_t* __restrict__ nbr,
                                                           const int32_t* __restrict__ order,
-                                                          int64_t n, int K,
+                                                          int64_t n, int vec,
                                                           int32_t* __restrict__ out) {
-  const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (t >= n) return;
-  const int64_t o = order[t];
-  for (int k0 = 0; k0 < K; k0 += 8) {
-    int32_t v[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) v[i] = nbr[(int64_t)(k0 + i < K ? k0 + i : K - 1) * n + o];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      if (k0 + i < K) out[(int64_t)(k0 + i) * n + t] = v[i];
+  const int64_t t0 = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) * 4;
+  if (t0 >= n) return;
+  const int32_t* col = nbr + (int64_t)blockIdx.y * n;
+  int32_t* dst = out + (int64_t)blockIdx.y * n;
+  if (vec && t0 + 4 <= n) {
+    const int4 o = *reinterpret_cast<const int4*>(order + t0);
+    *reinterpret_cast<int4*>(dst + t0) = make_int4(col[o.x], col[o.y], col[o.z], col[o.w]);
+  } else {
+    for (int64_t t = t0; t < n && t < t0 + 4; ++t) dst[t] = col[order[t]];
   }
 }
 
@@ -283,7 +300,10 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* out_coords, int6
   }
 
   // ---- sort 2: Morton positions by (region, mask), stable
-  mask_at_pos_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(nbr, n_out, k_vol, b.rows, b.mask_pos,
+  // the sort-1 keys are dead now: keys_a holds each row's slot mask
+  row_mask_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(nbr, n_out, k_vol, b.keys_a);
+  TSC_LAUNCH_CHECK("plan_row_mask");
+  mask_at_pos_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(b.keys_a, n_out, b.rows, b.mask_pos,
                                                           b.vals_a);
   TSC_LAUNCH_CHECK("plan_mask");
   vi = b.vals_a;
@@ -305,7 +325,11 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* out_coords, int6
   gather_rows_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(vi, b.rows, n_out, order);
   TSC_LAUNCH_CHECK("plan_gather");
   if (nbr_ordered) {
-    permute_map_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(nbr, order, n_out, k_vol, nbr_ordered);
+    // int4 accesses need 16-byte aligned rows of the map and of the order
+    const bool vec = (n_out & 3) == 0 && (reinterpret_cast<uintptr_t>(order) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(nbr_ordered) & 15) == 0;
+    dim3 grid(static_cast<unsigned>(ceil_div(ceil_div(n_out, 4), 256)), static_cast<unsigned>(k_vol));
+    permute_map_kernel<<<grid, 256, 0, s>>>(nbr, order, n_out, vec ? 1 : 0, nbr_ordered);
     TSC_LAUNCH_CHECK("plan_permute_map");
   }
   return 0;
