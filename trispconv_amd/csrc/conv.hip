@@ -181,13 +181,13 @@ template <int N> using Slot = std::integral_constant<int, N>;
 // one stage ahead and written to an LDS double buffer after the MFMAs, so all
 // four waves share one copy.  fp32 accumulators live in AGPRs.
 template <typename T, int BN, int CK>
-__global__ void __launch_bounds__(256, 1) conv_mfma_kernel(
+__global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
     const T* __restrict__ feat, int c_in, const T* __restrict__ W, const void* bias, int bias_dt,
     const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int nbr_ordered,
     int64_t n_out, int K, int c_out, T* __restrict__ out) {
   using Op = MfmaOp<T>;
   using V = typename Op::V;
-  constexpr int RING = 4;                        // operand buffers (RING-1 stages in flight)
+  constexpr int RING = 2;                        // operand buffers: this stage and the next
   constexpr int STEPS = CK / 16;                 // 16-deep MFMA steps per chunk
   constexpr int NB = BN / 32;                    // 32-wide column blocks
   constexpr int SLAB_VECS = BN * CK / 8;         // 16-byte vectors of one weight stage
@@ -198,7 +198,7 @@ __global__ void __launch_bounds__(256, 1) conv_mfma_kernel(
   __shared__ __attribute__((aligned(16))) uint4 s_w[2][SLAB_VECS];
   __shared__ __attribute__((aligned(16))) int32_t s_orow[kTileRows];
   __shared__ float s_bias[BN];        // this column tile's bias in fp32 (0 without one)
-  __shared__ uint32_t s_mask[8];      // per 32-row block
+  __shared__ uint64_t s_mask[4];      // per wave: slots its rows use (K <= 64)
   extern __shared__ int32_t s_nbr[];  // [K][kTileRows]; output staging at the end
 
   const int t = threadIdx.x;
@@ -231,7 +231,7 @@ __global__ void __launch_bounds__(256, 1) conv_mfma_kernel(
     // was permuted into the execution order (contiguous reads), else the row
     const int64_t src_row = orow >= 0 ? (nbr_ordered ? tr : orow) : 0;
     if (t < BN) s_bias[t] = bias ? load_bias(bias, bias_dt, (int64_t)nbt * BN + t) : 0.f;
-    uint32_t m = 0;
+    uint64_t m = 0;
     for (int k0 = 0; k0 < K; k0 += 8) {
       int32_t jv[8];
 #pragma unroll
@@ -245,36 +245,49 @@ __global__ void __launch_bounds__(256, 1) conv_mfma_kernel(
         const int32_t j = orow >= 0 ? jv[i] : -1;
         if (k < K) {
           s_nbr[k * kTileRows + t] = j;
-          m |= (j >= 0 ? 1u : 0u) << (k & 31);
+          m |= (j >= 0 ? uint64_t(1) : uint64_t(0)) << k;
         }
       }
     }
-    // OR over each 32-row half-wave: the rows one MFMA row block covers
+    // OR over the wave (two 32-bit halves)
+    uint32_t lo = static_cast<uint32_t>(m), hi = static_cast<uint32_t>(m >> 32);
 #pragma unroll
-    for (int off = 16; off > 0; off >>= 1) m |= __shfl_xor(m, off, kWave);
-    if ((lane & 31) == 0) s_mask[wave * 2 + h] = m;
+    for (int off = 32; off > 0; off >>= 1) {
+      lo |= __shfl_xor(lo, off, kWave);
+      hi |= __shfl_xor(hi, off, kWave);
+    }
+    if (lane == 0) s_mask[wave] = (static_cast<uint64_t>(hi) << 32) | lo;
   }
   __syncthreads();
-  uint32_t umask = 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) umask |= s_mask[i];
-  // wave-uniform values kept in scalar registers
-  umask = __builtin_amdgcn_readfirstlane(umask);
-  const uint32_t wmask = __builtin_amdgcn_readfirstlane(s_mask[wave * 2] | s_mask[wave * 2 + 1]);
+  // the tile's slots, wave-uniform (scalar registers)
+  const uint64_t umask_v = s_mask[0] | s_mask[1] | s_mask[2] | s_mask[3];
+  const uint64_t umask =
+      (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(umask_v >> 32))) << 32) |
+      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(umask_v));
   const int r0 = wave * 64 + (lane & 31);  // tile rows of this lane's A operands
   const int r1 = r0 + 32;
 
-  // stage (k, c) -> the next stage; k == K marks the end
+  // stage (k, c) -> the next stage: the next chunk of slot k, else chunk 0
+  // of the tile's next slot; k == K marks the end.  Branch-free (bit scan),
+  // so a loop body is one scheduling region.  k may start at -1.
   auto advance = [&](int& k, int& c) {
-    if (k >= K) return;
-    if (++c < nch) return;
-    c = 0;
-    for (++k; k < K; ++k)
-      if (umask & (1u << (k & 31))) return;
+    const bool done = k >= K;
+    const bool more_c = c + 1 < nch;
+    const uint64_t above = k + 1 < 64 ? umask >> (k + 1) : 0;
+    const int nk = above ? k + 1 + __builtin_ctzll(above) : K;
+    const int k2 = done ? K : (more_c ? k : nk);
+    c = done ? c : (more_c ? c + 1 : 0);
+    k = k2;
   };
 
   const uint4* Wv = reinterpret_cast<const uint4*>(W);
   const int nbt_all = c_out / 32;
+  // the zero row's address, held in scalar registers for the whole kernel
+  // (otherwise it is reloaded from the GOT, with a wait, in every stage)
+  uint64_t zero_addr = reinterpret_cast<uint64_t>(g_zero_row);
+  asm volatile("" : "+s"(zero_addr));
+  const uint4* zero_row =
+      (const uint4*)reinterpret_cast<const __attribute__((address_space(1))) uint4*>(zero_addr);
 
   f32x16 acc[2][NB];
 #pragma unroll
@@ -284,51 +297,51 @@ __global__ void __launch_bounds__(256, 1) conv_mfma_kernel(
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[rb][nb][i] = 0.f;
 
-  uint4 ring[RING][2][STEPS];
-  uint4 wr0, wr1, wr2, wr3;
+  uint4 ring[RING][2][STEPS];  // gathered operands: this stage and the next
+  uint4 w0, w1, w2, w3;        // this thread's share of the next weight slab
 
   // Loads are issued whether or not the stage exists (past the last stage they
-  // re-read stage 0 or the zero row), keeping the loop body straight-line so
-  // the compiler's wait counters see each operand's true age.
+  // re-read stage 0 or the zero row), keeping the loop body straight-line.
   auto load_w = [&](int k, int c) {
     if (k >= K) k = c = 0;
     const uint4* src = Wv + (((int64_t)k * nch + c) * nbt_all + (int64_t)nbt * NB) * STEPS * 64 + t;
-    if (FULL || t < SLAB_VECS) wr0 = src[0];
-    if constexpr (WV > 1) wr1 = src[256];
-    if constexpr (WV > 2) wr2 = src[512];
-    if constexpr (WV > 3) wr3 = src[768];
+    if (FULL || t < SLAB_VECS) w0 = src[0];
+    if constexpr (WV > 1) w1 = src[256];
+    if constexpr (WV > 2) w2 = src[512];
+    if constexpr (WV > 3) w3 = src[768];
   };
   auto store_w = [&](uint4* dst) {
-    if (FULL || t < SLAB_VECS) dst[t] = wr0;
-    if constexpr (WV > 1) dst[256 + t] = wr1;
-    if constexpr (WV > 2) dst[512 + t] = wr2;
-    if constexpr (WV > 3) dst[768 + t] = wr3;
+    if (FULL || t < SLAB_VECS) dst[t] = w0;
+    if constexpr (WV > 1) dst[256 + t] = w1;
+    if constexpr (WV > 2) dst[512 + t] = w2;
+    if constexpr (WV > 3) dst[768 + t] = w3;
   };
   auto load_a = [&](auto slot, int k, int c) {
     constexpr int S = decltype(slot)::value;
     const bool live = k < K;
-    const int32_t j0 = live ? s_nbr[k * kTileRows + r0] : -1;
-    const int32_t j1 = live ? s_nbr[k * kTileRows + r1] : -1;
+    const int kk = live ? k : K - 1;  // reads stay in the table; dead stages use -1
+    const int32_t e0 = s_nbr[kk * kTileRows + r0];
+    const int32_t e1 = s_nbr[kk * kTileRows + r1];
+    const int32_t j0 = live ? e0 : -1;
+    const int32_t j1 = live ? e1 : -1;
     const int coff = c * CK + h * (CK / 2);
     const uint4* p0 = j0 >= 0 ? reinterpret_cast<const uint4*>(feat + (int64_t)j0 * c_in + coff)
-                              : g_zero_row;
+                              : zero_row;
     const uint4* p1 = j1 >= 0 ? reinterpret_cast<const uint4*>(feat + (int64_t)j1 * c_in + coff)
-                              : g_zero_row;
+                              : zero_row;
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
       ring[S][0][s] = p0[s];
       ring[S][1][s] = p1[s];
     }
   };
-  auto compute = [&](auto slot, int k, const uint4* sw) {
+  // Every wave runs every stage of its tile: a stage lasts as long as its
+  // busiest wave anyway (the waves share the weight slab through LDS), and a
+  // body without branches keeps each stage one scheduling region.  Rows
+  // without input through the stage's slot (and bodies past the last stage)
+  // multiply the zero row and add exact zeros.
+  auto compute = [&](auto slot, const uint4* sw) {
     constexpr int S = decltype(slot)::value;
-    // a 32-row block with no input through slot k skips its MFMAs (its
-    // operands are zero and would add exact zeros)
-    // A wave whose 64 rows have no input through slot k skips the stage's
-    // MFMAs (past the last stage nothing is computed).  The test is a single
-    // uniform branch around all accumulators, so they stay in place.
-    const uint32_t kbit = k < K ? 1u << (k & 31) : 0u;
-    if (!(wmask & kbit)) return;
 #pragma unroll
     for (int s = 0; s < STEPS; ++s) {
 #pragma unroll
@@ -340,79 +353,67 @@ __global__ void __launch_bounds__(256, 1) conv_mfma_kernel(
     }
   };
 
-  // stage descriptors: current (kc, cc), next (kw, cw) and RING-1 ahead (ka, ca)
-  int kc = 0, cc = 0;
-  if (!(umask & 1u)) {
-    kc = -1;
-    cc = nch - 1;
-    advance(kc, cc);
-  }
-  int kw = kc, cw = cc;
-  advance(kw, cw);
-  int ka = kw, ca = cw;
-  // prologue: operands of the first RING-1 stages, weights of the first
-  load_a(Slot<0>{}, kc, cc);
+  // current stage (kc, cc) and the next one (kn, cn)
+  int kc = -1, cc = nch - 1;
+  advance(kc, cc);  // the tile's first slot
+  int kn = kc, cn = cc;
+  advance(kn, cn);
   load_w(kc, cc);
+  load_a(Slot<0>{}, kc, cc);
   store_w(s_w[0]);
-  load_a(Slot<1>{}, ka, ca);
-  advance(ka, ca);
-  load_a(Slot<2>{}, ka, ca);
-  advance(ka, ca);  // now RING-1 = 3 stages ahead of kc
   __syncthreads();
 
+  // Two waves per SIMD (two workgroups per CU): while one wave waits for its
+  // gathers or at the barrier, the other's MFMAs keep the matrix core busy.
   auto body = [&](auto slot) {
     constexpr int S = decltype(slot)::value;
-    load_w(kw, cw);                                    // weights, 1 stage ahead
-    load_a(Slot<(S + RING - 1) % RING>{}, ka, ca);     // operands, 3 stages ahead
-    compute(Slot<S>{}, kc, s_w[S & 1]);
-    store_w(s_w[(S + 1) & 1]);
+    load_w(kn, cn);                           // next stage's weights
+    load_a(Slot<(S + 1) % RING>{}, kn, cn);   // next stage's operands
+    compute(Slot<S>{}, s_w[S]);
+    store_w(s_w[(S + 1) % RING]);
     __syncthreads();
-    kc = kw;
-    cc = cw;
-    advance(kw, cw);
-    advance(ka, ca);
+    kc = kn;
+    cc = cn;
+    advance(kn, cn);
   };
-  // four bodies per trip keep every ring slot a fixed register set; bodies
-  // past the last stage load harmless data and compute nothing
   while (kc < K) {
     body(Slot<0>{});
     body(Slot<1>{});
-    body(Slot<2>{});
-    body(Slot<3>{});
   }
 
   // ---- epilogue: + bias, round once, store each output element once.
-  // The tile is transposed through LDS so that every lane writes 16-byte
-  // pieces of output rows (whole rows per group of lanes) instead of single
+  // Each wave transposes its accumulators through LDS, 32 rows at a time, so
+  // that lanes write 16-byte pieces of output rows instead of single
   // elements.  32x32 accumulator layout: register i of lane l holds row
   // (i/4)*8 + (l/32)*4 + i%4 and column l%32 of the block.
   constexpr int ROW_BYTES = BN * (int)sizeof(T);
   constexpr int STRIDE = ROW_BYTES + 16;            // padded LDS row
   constexpr int CHUNKS = ROW_BYTES / 16;            // 16-byte pieces per row
-  __syncthreads();                                  // s_nbr is free again
-  char* stage = reinterpret_cast<char*>(s_nbr) + wave * 64 * STRIDE;
+  char* stage = reinterpret_cast<char*>(s_nbr) + wave * 32 * STRIDE;
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int cl = nb * 32 + (lane & 31);
-    const float bv = s_bias[cl];
+  for (int rb = 0; rb < 2; ++rb) {
+    __syncthreads();                                // the staging area is free
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int nb = 0; nb < NB; ++nb) {
+      const int cl = nb * 32 + (lane & 31);
+      const float bv = s_bias[cl];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int row = rb * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
+        const int row = (i >> 2) * 8 + h * 4 + (i & 3);
         *reinterpret_cast<T*>(stage + row * STRIDE + cl * (int)sizeof(T)) =
             from_f32<T>(acc[rb][nb][i] + bv);
       }
-  }
-  __syncthreads();
+    }
+    __syncthreads();
 #pragma unroll
-  for (int q = 0; q < CHUNKS; ++q) {
-    const int piece = q * 64 + lane;
-    const int row = piece / CHUNKS, ch = piece % CHUNKS;
-    const int32_t orow = s_orow[wave * 64 + row];
-    if (orow >= 0) {
-      const uint4 v = *reinterpret_cast<const uint4*>(stage + row * STRIDE + ch * 16);
-      *reinterpret_cast<uint4*>(out + (int64_t)orow * c_out + nbt * BN + ch * (16 / (int)sizeof(T))) = v;
+    for (int q = 0; q < CHUNKS / 2; ++q) {
+      const int piece = q * 64 + lane;
+      const int row = piece / CHUNKS, ch = piece % CHUNKS;
+      const int32_t orow = s_orow[wave * 64 + rb * 32 + row];
+      if (orow >= 0) {
+        const uint4 v = *reinterpret_cast<const uint4*>(stage + row * STRIDE + ch * 16);
+        *reinterpret_cast<uint4*>(out + (int64_t)orow * c_out + nbt * BN + ch * (16 / (int)sizeof(T))) = v;
+      }
     }
   }
 }
@@ -427,7 +428,7 @@ int launch_mfma(const void* feat, int c_in, const void* W, const void* bias, int
   dim3 grid(static_cast<unsigned>(items));
   // dynamic LDS: the tile's slot lists, later reused to stage the output
   const size_t lds_nbr = (size_t)K * kTileRows * sizeof(int32_t);
-  const size_t lds_out = (size_t)kTileRows * (BN * sizeof(T) + 16);
+  const size_t lds_out = (size_t)(kTileRows / 2) * (BN * sizeof(T) + 16);  // 32 rows per wave
   const size_t lds = lds_nbr > lds_out ? lds_nbr : lds_out;
   conv_mfma_kernel<T, BN, CK><<<grid, 256, lds, s>>>(
       static_cast<const T*>(feat), c_in, static_cast<const T*>(W), bias, bias_dt, nbr, order,
