@@ -39,8 +39,10 @@ DTYPE_TAG = {"float32": "f32", "float16": "f16", "bfloat16": "bf16"}
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=5)
+    # the GPU needs some tens of milliseconds of load to reach its steady clock:
+    # 100 warm-up steps of this layer take ~40 ms
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--workload", default="subm128_surface500k")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-probe-mib", type=int, default=0,

@@ -6,13 +6,13 @@
 //     32-row block is skipped only when no row of the block has an input
 //     through k, so rows with different slot sets waste matrix-core work;
 //   * its rows, and the tiles an XCD runs around the same time, gather from
-//     nearby input rows — the gathered rows then come from that XCD's L2
-//     instead of HBM.
+//     nearby input rows — the gathered rows then come from cache instead of
+//     HBM.
 // The order built here serves both: output rows are put in Morton (z-order)
-// order, cut into regions of `region_rows` consecutive rows (sized so one
-// region's input rows fit an XCD's L2), and sorted inside each region by
-// their slot-occupancy mask (bit k set when nbr[k][o] >= 0; slots beyond 32
-// fold onto bit k mod 32), ties kept in Morton order.
+// order, cut into regions of `region_rows` consecutive rows (the caller sizes
+// them so one region's input rows fit in cache), and sorted inside each
+// region by their slot-occupancy mask (bit k set when nbr[k][o] >= 0; slots
+// beyond 32 fold onto bit k mod 32), ties kept in Morton order.
 //
 // Output values never depend on the order: every row's fp32 accumulation
 // sees the same slots in the same ascending order and absent slots add zero.
