@@ -50,13 +50,16 @@ TSC_API int tsc_abi_version(void);
 /* ------------------------------------------------------------------------
  * Submanifold pairs.  Replaces generate_subm_indice_pairs
  * (trispconv/pytorch/indices.py:67-140) including its dense lookup table
- * (:54-64), which becomes an open-addressing hash of 2N..4N slots.
+ * (:54-64), which becomes an occupancy bitmap with per-word ranks (grids of
+ * up to about 32 cells per voxel) or an open-addressing hash of 2N..4N slots.
+ * The workspace depends on the grid (batch_size * D * H * W cells).
  *
  * Writes nbr [K][n]; pairs_in/pairs_out [K][n] (slot k: output rows r in
  * ascending order, input row of each, exactly the reference's lists);
  * counts [K+1]: counts[k] = pairs in slot k, counts[K] = status flags.
  * ------------------------------------------------------------------------ */
-TSC_API int64_t tsc_subm_workspace_bytes(int64_t n, int32_t k_vol);
+TSC_API int64_t tsc_subm_workspace_bytes(int64_t n, int32_t k_vol, int32_t batch_size,
+                                         const int32_t spatial[3] /* host */);
 TSC_API int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_size,
                    const int32_t spatial[3] /* host */, const int32_t ksize[3] /* host */,
                    const int32_t dilation[3] /* host */, void* ws, int64_t ws_bytes,

@@ -124,6 +124,36 @@ def test_repeated_coordinates_later_row_wins():
     _subm(idx, (4, 4, 4), 1, 3, 1, "duplicates")
 
 
+def _clustered_with_duplicates(seed, shape, B, n, box, dups):
+    """n voxels per sample inside a box-sized corner of the grid (so they have
+    neighbours), plus `dups` repeats of random rows, shuffled."""
+    rng = np.random.default_rng(seed)
+    parts = []
+    for b in range(B):
+        cells = rng.choice(box ** 3, size=n, replace=False)
+        z, r = np.divmod(cells, box * box)
+        y, x = np.divmod(r, box)
+        off = rng.integers(0, [shape[0] - box + 1, shape[1] - box + 1, shape[2] - box + 1])
+        parts.append(np.stack([np.full(n, b), z + off[0], y + off[1], x + off[2]], 1))
+    idx = np.concatenate(parts).astype(np.int32)
+    idx = np.concatenate([idx, idx[rng.choice(len(idx), size=dups)]])
+    return idx[rng.permutation(len(idx))]
+
+
+# The submanifold builder looks cells up in an occupancy bitmap when the grid
+# has at most about 32 cells per voxel (8 words per voxel + 2^20 words), and in
+# a hash table otherwise; both must give the same lists, repeated coordinates
+# included.
+@pytest.mark.parametrize("shape,what", [((20, 24, 28), "bitmap"), ((320, 320, 200), "hash")])
+def test_subm_lookup_paths_with_duplicates(shape, what):
+    B, n = 2, 3000
+    idx = _clustered_with_duplicates(31, shape, B, n, 16, 300)
+    words = -(-B * shape[0] * shape[1] * shape[2] // 32)
+    assert (words <= 8 * len(idx) + (1 << 20)) == (what == "bitmap")
+    _subm(idx, shape, B, 3, 1, f"{what} path")
+    _subm(idx, shape, B, (3, 1, 3), (1, 2, 1), f"{what} path, 3x1x3 dilated")
+
+
 def test_out_of_grid_coordinates_raise():
     idx = torch.tensor([[0, 1, 1, 1], [0, 9, 1, 1]], dtype=torch.int32, device=DEV)
     with pytest.raises(IndexError):

@@ -165,7 +165,13 @@ def test_library_exports_every_declared_symbol():
 
 def test_workspace_queries_are_host_only():
     lib = L.lib()
-    assert lib.tsc_subm_workspace_bytes(500_000, 27) >= 1_048_576 * 8
+    # dense enough for the occupancy bitmap: two words per 32 cells + rank->row
+    assert lib.tsc_subm_workspace_bytes(500_000, 27, 1, L.i3((256, 256, 256))) >= \
+        2 * (256 ** 3 // 32) * 4 + 500_000 * 4
+    # very sparse grid: the hash (2N..4N 8-byte slots), far below the bitmap
+    sparse = lib.tsc_subm_workspace_bytes(60_000, 27, 4, L.i3((41, 1600, 1408)))
+    assert 1 << 20 <= sparse < 4 * 41 * 1600 * 1408 // 8
+    assert lib.tsc_subm_workspace_bytes(10, 27, 0, L.i3((4, 4, 4))) == -1
     assert lib.tsc_strided_workspace_bytes(1000, 27, 2, L.i3((21, 800, 704))) > 2 * 21 * 800 * 704 // 8
     assert lib.tsc_inverse_workspace_bytes(1000) >= 8000
     assert lib.tsc_plan_workspace_bytes(1000, 27) >= 16000

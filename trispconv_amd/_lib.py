@@ -31,7 +31,7 @@ _i32 = ctypes.c_int32
 _SIGNATURES = {
     "tsc_last_error": (ctypes.c_char_p, []),
     "tsc_abi_version": (ctypes.c_int, []),
-    "tsc_subm_workspace_bytes": (_i64, [_i64, _i32]),
+    "tsc_subm_workspace_bytes": (_i64, [_i64, _i32, _i32, c_i32p]),
     "tsc_subm_pairs": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, _vp, _i64,
                                       _vp, _vp, _vp, _vp, _vp]),
     "tsc_strided_workspace_bytes": (_i64, [_i64, _i32, _i32, c_i32p]),
@@ -52,7 +52,7 @@ _SIGNATURES = {
                                         _i64, _i32, _i32, _vp, _vp]),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lib: Optional[ctypes.CDLL] = None
 

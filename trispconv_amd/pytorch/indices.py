@@ -214,7 +214,11 @@ def generate_subm_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size:
     n = coords.shape[0]
     dev = coords.device
     lib = L.lib()
-    ws = L.workspace(lib.tsc_subm_workspace_bytes(n, K), dev)
+    ws_bytes = lib.tsc_subm_workspace_bytes(n, K, int(batch_size), L.i3(shape))
+    if ws_bytes < 0:
+        raise ValueError(f"generate_subm_indice_pairs: invalid batch size {batch_size} or "
+                         f"spatial shape {shape}")
+    ws = L.workspace(ws_bytes, dev)
     nbr = torch.empty((K, n), dtype=torch.int32, device=dev)
     pin = torch.empty((K, n), dtype=torch.int32, device=dev)
     pout = torch.empty((K, n), dtype=torch.int32, device=dev)
