@@ -153,10 +153,17 @@ def main():
             times.append(a.elapsed_time(b))
         return float(np.median(times))
 
-    # ---- pair build (includes its one count read-back) and plan
+    # ---- pair build (includes its one count read-back) and plan.  The build
+    # makes what the convolution consumes (the neighbour map and pair_num);
+    # the reference-format padded pair tables are made on first access and
+    # timed separately.
     for _ in range(2):
         build_pairs()
     pair_ms = event_ms(build_pairs, 10)
+
+    def build_with_tables():
+        build_pairs()._ensure_tables()
+    tables_ms = event_ms(build_with_tables, 10)
     data = build_pairs()
     n_out = len(data.out_indices)
 
@@ -196,6 +203,7 @@ def main():
     # algorithmic bytes of one launch: input rows read once, output written
     # once, the neighbour map and the order read once, the packed weight once
     k_vol = int(np.prod(layer["kernel_size"]))
+    pb_bytes = 16 * n_in + 8 * n_in + 8 * k_vol * n_in + 8 * P
     alg_bytes = (n_in * layer["c_in"] * elem + n_out * layer["c_out"] * elem
                  + n_out * k_vol * 4 + n_out * 4 + k_vol * layer["c_in"] * layer["c_out"] * elem)
 
@@ -217,6 +225,11 @@ def main():
                    "spatial_shape": list(w.spatial_shape), "batch": w.batch_size, "pairs": P},
         "tflops_effective": flops / (step_ms * 1e-3) / 1e12,
         "pair_build_ms": pair_ms,
+        "pair_build_with_tables_ms": tables_ms,
+        # 16N coords + 8N insert + 8KN probes + 8P pair tables (the build's
+        # algorithmic bytes, as a hash build of this layer would move them)
+        "pair_build_hbm": {"algorithmic_bytes": pb_bytes, "gbs": pb_bytes / (pair_ms * 1e6),
+                           "frac": pb_bytes / (pair_ms * 1e6) / HBM_PEAK_GBS},
         "plan_ms": plan_ms,
         "conv_kernel_ms": kern_ms,
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": peak,

@@ -54,17 +54,36 @@ TSC_API int tsc_abi_version(void);
  * up to about 32 cells per voxel) or an open-addressing hash of 2N..4N slots.
  * The workspace depends on the grid (batch_size * D * H * W cells).
  *
- * Writes nbr [K][n]; pairs_in/pairs_out [K][n] (slot k: output rows r in
- * ascending order, input row of each, exactly the reference's lists);
- * counts [K+1]: counts[k] = pairs in slot k, counts[K] = status flags.
+ * Writes the neighbour map as columns: nbr [K][n], column t belongs to row
+ * cols_row[t] (a permutation of the rows when every coordinate is in the
+ * grid; -1 marks unused columns).  counts [K+2]: counts[k] = pairs in slot k
+ * (pair_num), counts[K] = status flags, counts[K+1] = 1 when the columns are
+ * in (b,z,y,x) order (bitmap path), 0 when they are the rows in order (hash
+ * path, cols_row[t] = t).  The reference's pair lists follow from the map
+ * with tsc_map_to_rows and tsc_pairs_from_map.
  * ------------------------------------------------------------------------ */
 TSC_API int64_t tsc_subm_workspace_bytes(int64_t n, int32_t k_vol, int32_t batch_size,
                                          const int32_t spatial[3] /* host */);
 TSC_API int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_size,
-                   const int32_t spatial[3] /* host */, const int32_t ksize[3] /* host */,
-                   const int32_t dilation[3] /* host */, void* ws, int64_t ws_bytes,
-                   int32_t* nbr, int32_t* pairs_in, int32_t* pairs_out, int32_t* counts,
-                   tsc_stream_t stream);
+                           const int32_t spatial[3] /* host */, const int32_t ksize[3] /* host */,
+                           const int32_t dilation[3] /* host */, void* ws, int64_t ws_bytes,
+                           int32_t* cols_row, int32_t* nbr, int32_t* counts, tsc_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Pair lists from a neighbour map (the reference's IndiceData.pairs_in /
+ * pairs_out, indices.py:123-124).
+ *   tsc_map_to_rows: nbr_rows[k][cols_row[t]] = nbr_cols[k][t] for the
+ *     n_cols columns (entries of rows no column names are left untouched).
+ *   tsc_pairs_from_map: padded pairs_in/pairs_out [K][cap] from a row-major
+ *     map [K][n]: slot k lists its pairs in ascending output row.
+ * ------------------------------------------------------------------------ */
+TSC_API int tsc_map_to_rows(const int32_t* nbr_cols, const int32_t* cols_row, int64_t n_cols,
+                            int64_t n_rows, int32_t k_vol, int32_t* nbr_rows,
+                            tsc_stream_t stream);
+TSC_API int64_t tsc_pairs_from_map_workspace_bytes(int64_t n, int32_t k_vol);
+TSC_API int tsc_pairs_from_map(const int32_t* nbr, int64_t n, int32_t k_vol, int64_t cap,
+                               void* ws, int64_t ws_bytes, int32_t* pairs_in,
+                               int32_t* pairs_out, tsc_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Strided pairs.  Replaces generate_strided_indice_pairs
@@ -112,21 +131,25 @@ TSC_API int tsc_inverse_fill(const int32_t* fwd_pairs_in, const int32_t* fwd_pai
                      tsc_stream_t stream);
 
 /* ------------------------------------------------------------------------
- * Execution order for the convolution: output rows in Morton order, cut into
+ * Execution order for the convolution: output rows in spatial order, cut into
  * regions of region_rows rows, each region sorted (stably) by the set of
  * slots that feed its rows — rows processed together then need the same
  * weight slices and gather nearby inputs.  No reference counterpart (the
  * reference runs slot by slot); the order never changes any output value.
- *   out_coords [n_out][4] are the output rows' (b, z, y, x).
- *   order [n_out] receives the processing order; nbr_ordered [K][n_out]
- *   (may be NULL) the map permuted into that order: entry (k, t) is
- *   nbr[k][order[t]], so the convolution reads it contiguously.
+ *   nbr [K][n_out] is a map by columns: column t belongs to row cols_row[t]
+ *   (cols_row == NULL: column t is row t).  raster != 0 says the columns are
+ *   already in (b,z,y,x) order (the submanifold builder's bitmap path);
+ *   otherwise they are put in Morton order of out_coords [n_out][4].
+ *   order [n_out] receives the processing order (rows); nbr_ordered
+ *   [K][n_out] (may be NULL) the map permuted into that order: entry (k, t)
+ *   belongs to row order[t], so the convolution reads it contiguously.
  * ------------------------------------------------------------------------ */
 TSC_API int64_t tsc_plan_workspace_bytes(int64_t n_out, int32_t k_vol);
-TSC_API int tsc_conv_plan(const int32_t* nbr, const int32_t* out_coords, int64_t n_out,
-                  int32_t k_vol, int32_t batch_size, const int32_t out_spatial[3] /* host */,
-                  int64_t region_rows, void* ws, int64_t ws_bytes, int32_t* order,
-                  int32_t* nbr_ordered, tsc_stream_t stream);
+TSC_API int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_t raster,
+                          const int32_t* out_coords, int64_t n_out, int32_t k_vol,
+                          int32_t batch_size, const int32_t out_spatial[3] /* host */,
+                          int64_t region_rows, void* ws, int64_t ws_bytes, int32_t* order,
+                          int32_t* nbr_ordered, tsc_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Weights.  Replaces normalize_spconv_weight (trispconv/pytorch/weight.py:8-50)

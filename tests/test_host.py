@@ -165,9 +165,10 @@ def test_library_exports_every_declared_symbol():
 
 def test_workspace_queries_are_host_only():
     lib = L.lib()
-    # dense enough for the occupancy bitmap: two words per 32 cells + rank->row
+    # dense enough for the occupancy bitmap: a word and its rank per 32 cells
     assert lib.tsc_subm_workspace_bytes(500_000, 27, 1, L.i3((256, 256, 256))) >= \
-        2 * (256 ** 3 // 32) * 4 + 500_000 * 4
+        2 * (256 ** 3 // 32) * 4
+    assert lib.tsc_pairs_from_map_workspace_bytes(500_000, 27) >= 2 * 27 * (500_000 // 256) * 4
     # very sparse grid: the hash (2N..4N 8-byte slots), far below the bitmap
     sparse = lib.tsc_subm_workspace_bytes(60_000, 27, 4, L.i3((41, 1600, 1408)))
     assert 1 << 20 <= sparse < 4 * 41 * 1600 * 1408 // 8
@@ -183,7 +184,7 @@ def test_workspace_queries_are_host_only():
 def test_argument_errors_return_codes_without_gpu():
     lib = L.lib()
     rc = lib.tsc_subm_pairs(None, -1, 1, L.i3((4, 4, 4)), L.i3((3, 3, 3)), L.i3((1, 1, 1)), None,
-                            0, None, None, None, None, None)
+                            0, None, None, None, None)
     assert rc == 1 and b"out of range" in lib.tsc_last_error()
     rc = lib.tsc_strided_count(None, 10, 1, L.i3((8, 8, 8)), L.i3((3, 3, 3)), L.i3((2, 2, 2)),
                                L.i3((1, 1, 1)), L.i3((1, 1, 1)), L.i3((5, 5, 5)), None, 0, None,

@@ -33,7 +33,10 @@ _SIGNATURES = {
     "tsc_abi_version": (ctypes.c_int, []),
     "tsc_subm_workspace_bytes": (_i64, [_i64, _i32, _i32, c_i32p]),
     "tsc_subm_pairs": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, _vp, _i64,
-                                      _vp, _vp, _vp, _vp, _vp]),
+                                      _vp, _vp, _vp, _vp]),
+    "tsc_map_to_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _vp, _vp]),
+    "tsc_pairs_from_map_workspace_bytes": (_i64, [_i64, _i32]),
+    "tsc_pairs_from_map": (ctypes.c_int, [_vp, _i64, _i32, _i64, _vp, _i64, _vp, _vp, _vp]),
     "tsc_strided_workspace_bytes": (_i64, [_i64, _i32, _i32, c_i32p]),
     "tsc_strided_count": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, c_i32p, c_i32p,
                                          c_i32p, _vp, _i64, _vp, _vp]),
@@ -44,15 +47,15 @@ _SIGNATURES = {
     "tsc_inverse_fill": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i64, _vp, _i64, _vp, _i64, _i64,
                                         _vp, _vp, _vp, _vp]),
     "tsc_plan_workspace_bytes": (_i64, [_i64, _i32]),
-    "tsc_conv_plan": (ctypes.c_int, [_vp, _vp, _i64, _i32, _i32, c_i32p, _i64, _vp, _i64, _vp,
-                                     _vp, _vp]),
+    "tsc_conv_plan": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i64, _i32, _i32, c_i32p, _i64, _vp,
+                                     _i64, _vp, _vp, _vp]),
     "tsc_packed_weight_bytes": (_i64, [_i32, _i32, _i32, _i32]),
     "tsc_pack_weight": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp]),
     "tsc_conv_forward": (ctypes.c_int, [_vp, _i32, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32,
                                         _i64, _i32, _i32, _vp, _vp]),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lib: Optional[ctypes.CDLL] = None
 

@@ -5,22 +5,24 @@
 // and every output row r in ascending order, the pair (in = j, out = r) exists
 // when coord(r) + offset_k lies inside the grid and is the coordinate of row j.
 //
-// MI355X design: the reference's dense grid-sized lookup table (:54-64) becomes
-// one of two compact structures, chosen by how dense the active set is:
+// MI355X design.  The build produces what the convolution consumes: the
+// neighbour map as columns ([K][n], column t belongs to row cols_row[t]) and
+// the per-slot pair counts.  The reference's dense grid-sized lookup table
+// (:54-64) becomes one of two compact structures, chosen by how dense the
+// active set is:
 //   * occupancy bitmap (grids of up to about 32 cells per voxel): one bit per
 //     cell, an exclusive popcount scan of its words (each occupied cell's rank
-//     in (b,z,y,x) order) and rank -> row.  The neighbour lookups then run in
-//     rank order — a wave handles 64 neighbouring occupied cells, so its
-//     bitmap and rank reads share cache lines — and write the map rows they
-//     own; a row-order pass copies the entries of duplicate rows;
+//     in (b,z,y,x) order) and rank -> row.  Columns are the occupied cells in
+//     rank order (then any earlier rows of repeated coordinates), so a wave's
+//     64 lookups touch neighbouring cells and share cache lines, and its map
+//     writes are contiguous;
 //   * open-addressing hash of 2N..4N 64-bit slots otherwise, probed in row
-//     order.
-// Both write the slot-major [K][N] neighbour map the convolution consumes and
-// per-(slot, block) hit counts; a per-slot scan of those counts gives each
-// block its write offset, and a fill kernel emits every slot's pair list in
-// ascending output-row order with wave ballots, so the lists come out in
-// exactly the reference's order.  Repeated coordinates resolve to the later
-// row, as the reference's table scatter leaves them.
+//     order (columns are rows).
+// The reference's pair lists are derived from the map only when asked for
+// (tsc_map_to_rows, tsc_pairs_from_map): per-(slot, block) counts, a per-slot
+// scan and a wave-ballot compaction put every slot's list in ascending
+// output-row order, exactly the reference's order.  Repeated coordinates
+// resolve to the later row, as the reference's table scatter leaves them.
 #include "common.hpp"
 
 namespace tsc {
@@ -169,20 +171,46 @@ __global__ void __launch_bounds__(256) subm_rank_kernel(const int4* __restrict__
             static_cast<int32_t>(r));
 }
 
-// One thread per occupied cell, in rank order: the thread's row (the cell's
-// last row) gets its K neighbours.  Eight slots' bitmap and prefix reads are
-// in flight together, then their rank -> row reads.
+// Columns of repeated coordinates: a row whose cell's last row is another
+// row gets a column after the n_unique cell columns (in no particular order;
+// the values computed for it do not depend on where it sits).
+__global__ void __launch_bounds__(256) subm_place_kernel(const int4* __restrict__ coords, int64_t n,
+                                                         SubmGeom g,
+                                                         const uint32_t* __restrict__ words,
+                                                         const uint32_t* __restrict__ word_rank,
+                                                         const int32_t* __restrict__ n_unique,
+                                                         int32_t* cols_row, int32_t* n_extra) {
+  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  const int4 c = coords[r];
+  if (!in_grid(g, c.x, c.y, c.z, c.w)) return;
+  const uint32_t cell = cell_key(g, c.x, c.y, c.z, c.w);
+  const uint32_t rank = cell_rank(words[cell >> 5], word_rank[cell >> 5], cell);
+  if (cols_row[rank] != static_cast<int32_t>(r)) {
+    const int32_t col = *n_unique + atomicAdd(n_extra, 1);
+    cols_row[col] = static_cast<int32_t>(r);  // col < rows in the grid <= n
+  }
+}
+
+// One thread per map column (an occupied cell in rank order, or a repeated
+// row after them): the column gets its row's K neighbours.  Eight slots'
+// bitmap and prefix reads are in flight together, then their rank -> row
+// reads.  Hits are counted per slot: per wave by ballot, per block in LDS,
+// then one atomic per block and slot.
 constexpr int kLook = 8;
 
-__global__ void __launch_bounds__(256) subm_probe_rank_kernel(
+__global__ void __launch_bounds__(256) subm_probe_cols_kernel(
     const int4* __restrict__ coords, int64_t n, int K, SubmGeom g,
     const uint32_t* __restrict__ words, const uint32_t* __restrict__ word_rank,
-    const int32_t* __restrict__ rank_row, const int32_t* __restrict__ n_unique,
-    int32_t* __restrict__ nbr) {
-  const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (t >= *n_unique) return;
-  const int32_t row = rank_row[t];
-  const int4 c = coords[row];
+    const int32_t* __restrict__ cols_row, const int32_t* __restrict__ n_unique,
+    const int32_t* __restrict__ n_extra, int32_t* __restrict__ nbr, int32_t* __restrict__ counts) {
+  __shared__ int32_t s_cnt[64];
+  const int t = threadIdx.x;
+  if (t < 64) s_cnt[t] = 0;
+  __syncthreads();
+  const int64_t col = blockIdx.x * (int64_t)blockDim.x + t;
+  const bool live = col < *n_unique + *n_extra;  // the other columns are empty
+  const int4 c = live ? coords[cols_row[col]] : make_int4(0, 0, 0, 0);
   for (int k0 = 0; k0 < K; k0 += kLook) {
     uint32_t cell[kLook], wv[kLook], wr[kLook];
     bool look[kLook];
@@ -194,7 +222,7 @@ __global__ void __launch_bounds__(256) subm_probe_rank_kernel(
       const int z = c.y + (kz - g.ks.z / 2) * g.dil.z;
       const int y = c.z + (ky - g.ks.y / 2) * g.dil.y;
       const int x = c.w + (kx - g.ks.x / 2) * g.dil.x;
-      look[i] = k < K && in_grid(g, c.x, z, y, x);
+      look[i] = live && k < K && in_grid(g, c.x, z, y, x);
       cell[i] = look[i] ? cell_key(g, c.x, z, y, x) : 0u;
       wv[i] = words[cell[i] >> 5];  // word 0 exists: unconditional reads
       wr[i] = word_rank[cell[i] >> 5];
@@ -203,40 +231,40 @@ __global__ void __launch_bounds__(256) subm_probe_rank_kernel(
 #pragma unroll
     for (int i = 0; i < kLook; ++i) {
       const bool hit = look[i] && ((wv[i] >> (cell[i] & 31)) & 1u);
-      jr[i] = rank_row[hit ? cell_rank(wv[i], wr[i], cell[i]) : 0u];  // rank 0 exists
+      // a hit's rank is below n_unique <= n; a miss reads column 0
+      jr[i] = cols_row[hit ? cell_rank(wv[i], wr[i], cell[i]) : 0u];
       if (!hit) jr[i] = -1;
     }
 #pragma unroll
-    for (int i = 0; i < kLook; ++i)
-      if (k0 + i < K) nbr[(int64_t)(k0 + i) * n + row] = jr[i];
+    for (int i = 0; i < kLook; ++i) {
+      const int k = k0 + i;
+      if (k >= K) continue;
+      if (col < n) nbr[(int64_t)k * n + col] = jr[i];
+      const uint64_t hits = __ballot(jr[i] >= 0);
+      if (__lane_id() == 0 && hits) {
+        if (k < 64)
+          atomicAdd(&s_cnt[k], (int)__popcll(hits));
+        else
+          atomicAdd(&counts[k], (int)__popcll(hits));
+      }
+    }
   }
+  __syncthreads();
+  if (t < K && t < 64 && s_cnt[t]) atomicAdd(&counts[t], s_cnt[t]);
 }
 
-// Row order: rows that share a cell with a later row copy that row's map
-// entries, rows outside the grid get -1 (the call reports them), and every
-// block counts its hits per slot for the compaction offsets.
-__global__ void __launch_bounds__(kRows) subm_finish_kernel(
-    const int4* __restrict__ coords, int64_t n, int K, SubmGeom g,
-    const uint32_t* __restrict__ words, const uint32_t* __restrict__ word_rank,
-    const int32_t* __restrict__ rank_row, int32_t* __restrict__ nbr, int32_t* __restrict__ blk_cnt,
-    int nblk) {
+// Row-order hit counts per (slot, block) of a row-major map, for the
+// compaction offsets of the pair lists.
+__global__ void __launch_bounds__(kRows) map_count_kernel(const int32_t* __restrict__ nbr, int64_t n,
+                                                          int K, int32_t* __restrict__ blk_cnt,
+                                                          int nblk) {
   __shared__ int32_t s_cnt[kRows / kWave][64];
   const int t = threadIdx.x;
   const int w = t / kWave;
   const int64_t r = blockIdx.x * (int64_t)kRows + t;
   const bool valid = r < n;
-  const int4 c = valid ? coords[r] : make_int4(-1, 0, 0, 0);
-  const bool ok = valid && in_grid(g, c.x, c.y, c.z, c.w);
-  int64_t src = r;
-  if (ok) {
-    const uint32_t cell = cell_key(g, c.x, c.y, c.z, c.w);
-    src = rank_row[cell_rank(words[cell >> 5], word_rank[cell >> 5], cell)];
-  }
-  const bool copy = ok && src != r;
   for (int k = 0; k < K; ++k) {
-    int32_t j = -1;
-    if (ok) j = nbr[(int64_t)k * n + src];
-    if (valid && (copy || !ok)) nbr[(int64_t)k * n + r] = j;
+    const int32_t j = valid ? nbr[(int64_t)k * n + r] : -1;
     const uint64_t hits = __ballot(j >= 0);
     if (__lane_id() == 0) {
       if (k < 64)
@@ -252,6 +280,19 @@ __global__ void __launch_bounds__(kRows) subm_finish_kernel(
     for (int ww = 0; ww < kRows / kWave; ++ww) sum += s_cnt[ww][t];
     blk_cnt[(int64_t)t * nblk + blockIdx.x] = sum;
   }
+}
+
+// nbr_rows[k][cols_row[t]] = nbr_cols[k][t]: the map back in row order.
+// blockIdx.y is the slot, so the blocks in flight share one slot's rows.
+__global__ void __launch_bounds__(256) map_to_rows_kernel(const int32_t* __restrict__ nbr_cols,
+                                                          const int32_t* __restrict__ cols_row,
+                                                          int64_t n_cols, int64_t n_rows,
+                                                          int32_t* __restrict__ nbr_rows) {
+  const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (t >= n_cols) return;
+  const int32_t r = cols_row[t];
+  if (r < 0 || r >= n_rows) return;
+  nbr_rows[(int64_t)blockIdx.y * n_rows + r] = nbr_cols[(int64_t)blockIdx.y * n_cols + t];
 }
 
 // Emits pairs_in/pairs_out for every slot from the neighbour map.  Rows keep
@@ -310,7 +351,7 @@ static bool subm_use_bitmap(int64_t n, int64_t cells) {
 struct SubmWork {
   unsigned long long* table;
   uint32_t *words, *word_rank, *scan_scratch;
-  int32_t *rank_row, *n_unique, *blk_cnt, *blk_off;
+  int32_t *n_unique, *n_extra, *blk_cnt, *blk_off;
 };
 
 static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, int64_t* used) {
@@ -323,15 +364,20 @@ static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, int64_t* u
     w.words = c.take<uint32_t>(nw);
     w.word_rank = c.take<uint32_t>(nw);
     w.scan_scratch = c.take<uint32_t>(scan_scratch_words(nw));
-    w.rank_row = c.take<int32_t>(m);
     w.n_unique = c.take<int32_t>(1);
+    w.n_extra = c.take<int32_t>(1);
   } else {
     w.table = c.take<unsigned long long>(subm_capacity(m));
+    w.blk_cnt = c.take<int32_t>(nblk * K);
+    w.blk_off = c.take<int32_t>(nblk * K);
   }
-  w.blk_cnt = c.take<int32_t>(nblk * K);
-  w.blk_off = c.take<int32_t>(nblk * K);
   if (used) *used = c.used;
   return w;
+}
+
+__global__ void iota_kernel(int32_t* p, int64_t n) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i < n) p[i] = static_cast<int32_t>(i);
 }
 
 }  // namespace tsc
@@ -350,8 +396,8 @@ extern "C" int64_t tsc_subm_workspace_bytes(int64_t n, int32_t k_vol, int32_t ba
 
 extern "C" int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_size,
                               const int32_t spatial[3], const int32_t ksize[3],
-                              const int32_t dilation[3], void* ws, int64_t ws_bytes, int32_t* nbr,
-                              int32_t* pairs_in, int32_t* pairs_out, int32_t* counts,
+                              const int32_t dilation[3], void* ws, int64_t ws_bytes,
+                              int32_t* cols_row, int32_t* nbr, int32_t* counts,
                               tsc_stream_t stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   TSC_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "subm: n=%lld out of range", (long long)n);
@@ -370,44 +416,100 @@ extern "C" int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_si
               "subm: workspace too small");
   TSC_REQUIRE(counts != nullptr, "subm: counts is null");
 
-  int rc = fill_u32(reinterpret_cast<uint32_t*>(counts), K + 1, 0u, s);
+  int rc = fill_u32(reinterpret_cast<uint32_t*>(counts), K + 2, 0u, s);
   if (rc) return rc;
   if (n == 0) return 0;
-  TSC_REQUIRE(coords && nbr && pairs_in && pairs_out && ws, "subm: null pointer");
+  TSC_REQUIRE(coords && cols_row && nbr && ws, "subm: null pointer");
 
   const int nblk = static_cast<int>(ceil_div(n, kRows));
   const SubmWork w = subm_carve(ws, n, K, cells, nullptr);
   const int4* c4 = reinterpret_cast<const int4*>(coords);
-  if (K > 64 && (rc = fill_u32(reinterpret_cast<uint32_t*>(w.blk_cnt), (int64_t)nblk * K, 0u, s)))
-    return rc;
   if (w.words) {
+    // columns in (b,z,y,x) order: tell the caller
+    if ((rc = fill_u32(reinterpret_cast<uint32_t*>(counts + K + 1), 1, 1u, s))) return rc;
     const int64_t nw = ceil_div(cells, 32);
     SubmGeom g{batch_size, shape, ks, dil, 0u};
     if ((rc = fill_u32(w.words, nw, 0u, s))) return rc;
+    if ((rc = fill_u32(reinterpret_cast<uint32_t*>(w.n_extra), 1, 0u, s))) return rc;
     subm_mark_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.words, counts + K);
     TSC_LAUNCH_CHECK("subm_mark");
     if ((rc = exclusive_scan_u32(w.words, 0, nw, w.word_rank, w.n_unique, w.scan_scratch, s)))
       return rc;
-    if ((rc = fill_u32(reinterpret_cast<uint32_t*>(w.rank_row), n, 0xffffffffu, s))) return rc;
-    subm_rank_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.words, w.word_rank, w.rank_row);
+    if ((rc = fill_u32(reinterpret_cast<uint32_t*>(cols_row), n, 0xffffffffu, s))) return rc;
+    subm_rank_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.words, w.word_rank, cols_row);
     TSC_LAUNCH_CHECK("subm_rank");
-    subm_probe_rank_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, K, g, w.words, w.word_rank,
-                                                            w.rank_row, w.n_unique, nbr);
-    TSC_LAUNCH_CHECK("subm_probe_rank");
-    subm_finish_kernel<<<nblk, kRows, 0, s>>>(c4, n, K, g, w.words, w.word_rank, w.rank_row, nbr,
-                                              w.blk_cnt, nblk);
-    TSC_LAUNCH_CHECK("subm_finish");
+    subm_place_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.words, w.word_rank, w.n_unique,
+                                                       cols_row, w.n_extra);
+    TSC_LAUNCH_CHECK("subm_place");
+    subm_probe_cols_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, K, g, w.words, w.word_rank,
+                                                            cols_row, w.n_unique, w.n_extra, nbr,
+                                                            counts);
+    TSC_LAUNCH_CHECK("subm_probe_cols");
   } else {
     const int64_t cap = subm_capacity(n);
     SubmGeom g{batch_size, shape, ks, dil, static_cast<uint32_t>(cap - 1)};
+    if (K > 64 &&
+        (rc = fill_u32(reinterpret_cast<uint32_t*>(w.blk_cnt), (int64_t)nblk * K, 0u, s)))
+      return rc;
     if ((rc = fill_u64(w.table, cap, kEmpty, s))) return rc;
+    iota_kernel<<<ceil_div(n, 256), 256, 0, s>>>(cols_row, n);
+    TSC_LAUNCH_CHECK("subm_iota");
     subm_insert_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.table, counts + K);
     TSC_LAUNCH_CHECK("subm_insert");
     subm_probe_kernel<<<nblk, kRows, 0, s>>>(c4, n, K, g, w.table, nbr, w.blk_cnt, nblk);
     TSC_LAUNCH_CHECK("subm_probe");
+    if ((rc = scan_slot_blocks(w.blk_cnt, w.blk_off, counts, K, nblk, s))) return rc;
   }
-  if ((rc = scan_slot_blocks(w.blk_cnt, w.blk_off, counts, K, nblk, s))) return rc;
-  subm_fill_kernel<<<nblk, kRows, 0, s>>>(nbr, n, K, w.blk_off, nblk, n, pairs_in, pairs_out);
-  TSC_LAUNCH_CHECK("subm_fill");
+  return 0;
+}
+
+extern "C" int tsc_map_to_rows(const int32_t* nbr_cols, const int32_t* cols_row, int64_t n_cols,
+                               int64_t n_rows, int32_t k_vol, int32_t* nbr_rows,
+                               tsc_stream_t stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  TSC_REQUIRE(n_cols >= 0 && n_rows >= 0 && k_vol > 0 && k_vol <= 65535,
+              "map_to_rows: invalid sizes");
+  if (n_cols == 0 || n_rows == 0) return 0;
+  TSC_REQUIRE(nbr_cols && cols_row && nbr_rows, "map_to_rows: null pointer");
+  dim3 grid(static_cast<unsigned>(ceil_div(n_cols, 256)), static_cast<unsigned>(k_vol));
+  map_to_rows_kernel<<<grid, 256, 0, s>>>(nbr_cols, cols_row, n_cols, n_rows, nbr_rows);
+  TSC_LAUNCH_CHECK("map_to_rows");
+  return 0;
+}
+
+extern "C" int64_t tsc_pairs_from_map_workspace_bytes(int64_t n, int32_t k_vol) {
+  if (n < 0 || k_vol <= 0) return -1;
+  Carver c(nullptr);
+  const int64_t nblk = ceil_div(n > 0 ? n : 1, kRows);
+  c.take<int32_t>(nblk * k_vol);  // block counts
+  c.take<int32_t>(nblk * k_vol);  // block offsets
+  c.take<int32_t>(k_vol);         // slot totals
+  return c.used;
+}
+
+extern "C" int tsc_pairs_from_map(const int32_t* nbr, int64_t n, int32_t k_vol, int64_t cap,
+                                  void* ws, int64_t ws_bytes, int32_t* pairs_in,
+                                  int32_t* pairs_out, tsc_stream_t stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  TSC_REQUIRE(n >= 0 && n < (int64_t(1) << 31) && k_vol > 0 && k_vol <= 4096 && cap >= 0,
+              "pairs_from_map: invalid sizes");
+  TSC_REQUIRE(ws_bytes >= tsc_pairs_from_map_workspace_bytes(n, k_vol),
+              "pairs_from_map: workspace too small");
+  if (n == 0) return 0;
+  TSC_REQUIRE(nbr && ws && pairs_in && pairs_out, "pairs_from_map: null pointer");
+  const int nblk = static_cast<int>(ceil_div(n, kRows));
+  Carver c(ws);
+  auto* blk_cnt = c.take<int32_t>((int64_t)nblk * k_vol);
+  auto* blk_off = c.take<int32_t>((int64_t)nblk * k_vol);
+  auto* totals = c.take<int32_t>(k_vol);
+  int rc;
+  if (k_vol > 64 &&
+      (rc = fill_u32(reinterpret_cast<uint32_t*>(blk_cnt), (int64_t)nblk * k_vol, 0u, s)))
+    return rc;
+  map_count_kernel<<<nblk, kRows, 0, s>>>(nbr, n, k_vol, blk_cnt, nblk);
+  TSC_LAUNCH_CHECK("pairs_count");
+  if ((rc = scan_slot_blocks(blk_cnt, blk_off, totals, k_vol, nblk, s))) return rc;
+  subm_fill_kernel<<<nblk, kRows, 0, s>>>(nbr, n, k_vol, blk_off, nblk, cap, pairs_in, pairs_out);
+  TSC_LAUNCH_CHECK("pairs_fill");
   return 0;
 }

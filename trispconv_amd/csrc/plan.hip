@@ -67,23 +67,34 @@ __device__ __forceinline__ uint32_t spread3(uint32_t v) {
   return v;
 }
 
-// Morton code of each output row: the sample index in the bits at and above
-// batch_shift, then the leading bits of the 30-bit z-order code of
+// Morton code of each map column's row: the sample index in the bits at and
+// above batch_shift, then the leading bits of the 30-bit z-order code of
 // (z, y, x) >> coarse (coarse chosen by the host so the largest axis fits 10
-// bits).
-__global__ void __launch_bounds__(256) spatial_key_kernel(const int4* __restrict__ coords, int64_t n,
-                                                          int coarse, int batch_shift,
+// bits).  Columns without a row sort last.
+__global__ void __launch_bounds__(256) spatial_key_kernel(const int4* __restrict__ coords,
+                                                          const int32_t* __restrict__ cols_row,
+                                                          int64_t n, int coarse, int batch_shift,
                                                           uint32_t* __restrict__ keys,
                                                           uint32_t* __restrict__ vals) {
   const int64_t o = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (o >= n) return;
-  const int4 c = coords[o];
+  vals[o] = static_cast<uint32_t>(o);
+  const int32_t row = cols_row ? cols_row[o] : static_cast<int32_t>(o);
+  if (row < 0) {
+    keys[o] = 0xffffffffu;
+    return;
+  }
+  const int4 c = coords[row];
   const uint32_t m = (spread3(static_cast<uint32_t>(c.y) >> coarse) << 2) |
                      (spread3(static_cast<uint32_t>(c.z) >> coarse) << 1) |
                      spread3(static_cast<uint32_t>(c.w) >> coarse);
   const uint32_t spatial = batch_shift >= 30 ? m : (m >> (30 - batch_shift));
   keys[o] = (batch_shift >= 32 ? 0u : (static_cast<uint32_t>(c.x) << batch_shift)) | spatial;
-  vals[o] = static_cast<uint32_t>(o);
+}
+
+__global__ void __launch_bounds__(256) iota_u32_kernel(uint32_t* p, int64_t n) {
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i < n) p[i] = static_cast<uint32_t>(i);
 }
 
 // mask_row[o] = slot mask of output row o.  Lanes take consecutive rows, so
@@ -116,19 +127,24 @@ __global__ void __launch_bounds__(256) mask_at_pos_kernel(const uint32_t* __rest
   vals[i] = static_cast<uint32_t>(i);
 }
 
+// perm[i] = map column processed at position i; order[i] = its row.
 __global__ void __launch_bounds__(256) gather_rows_kernel(const uint32_t* __restrict__ pos,
-                                                          const uint32_t* __restrict__ rows,
-                                                          int64_t n, int32_t* __restrict__ order) {
+                                                          const uint32_t* __restrict__ cols,
+                                                          const int32_t* __restrict__ cols_row,
+                                                          int64_t n, uint32_t* __restrict__ perm,
+                                                          int32_t* __restrict__ order) {
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (i >= n) return;
-  order[i] = static_cast<int32_t>(rows[pos[i]]);
+  const uint32_t col = cols[pos[i]];
+  perm[i] = col;
+  order[i] = cols_row ? cols_row[col] : static_cast<int32_t>(col);
 }
 
-// nbr_ordered[k][t] = nbr[k][order[t]].  blockIdx.y is the slot: blocks are
+// nbr_ordered[k][t] = nbr[k][perm[t]].  blockIdx.y is the slot: blocks are
 // dispatched x-fastest, so the blocks in flight share one slot's column and
 // its gathered entries stay in cache; four positions per thread.
 __global__ void __launch_bounds__(256) permute_map_kernel(const int32_t* __restrict__ nbr,
-                                                          const int32_t* __restrict__ order,
+                                                          const uint32_t* __restrict__ order,
                                                           int64_t n, int vec,
                                                           int32_t* __restrict__ out) {
   const int64_t t0 = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) * 4;
@@ -136,7 +152,7 @@ __global__ void __launch_bounds__(256) permute_map_kernel(const int32_t* __restr
   const int32_t* col = nbr + (int64_t)blockIdx.y * n;
   int32_t* dst = out + (int64_t)blockIdx.y * n;
   if (vec && t0 + 4 <= n) {
-    const int4 o = *reinterpret_cast<const int4*>(order + t0);
+    const uint4 o = *reinterpret_cast<const uint4*>(order + t0);
     *reinterpret_cast<int4*>(dst + t0) = make_int4(col[o.x], col[o.y], col[o.z], col[o.w]);
   } else {
     for (int64_t t = t0; t < n && t < t0 + 4; ++t) dst[t] = col[order[t]];
@@ -261,8 +277,9 @@ extern "C" int64_t tsc_plan_workspace_bytes(int64_t n_out, int32_t k_vol) {
   return used;
 }
 
-extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* out_coords, int64_t n_out,
-                             int32_t k_vol, int32_t batch_size, const int32_t out_spatial[3],
+extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_t raster,
+                             const int32_t* out_coords, int64_t n_out, int32_t k_vol,
+                             int32_t batch_size, const int32_t out_spatial[3],
                              int64_t region_rows, void* ws, int64_t ws_bytes, int32_t* order,
                              int32_t* nbr_ordered, tsc_stream_t stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -273,41 +290,49 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* out_coords, int6
   TSC_REQUIRE(out_spatial && out_spatial[0] > 0 && out_spatial[1] > 0 && out_spatial[2] > 0,
               "plan: spatial shape must be positive");
   if (n_out == 0) return 0;
-  TSC_REQUIRE(nbr && out_coords && order && ws, "plan: null pointer");
+  TSC_REQUIRE(nbr && order && ws && (raster || out_coords), "plan: null pointer");
   TSC_REQUIRE(ws_bytes >= tsc_plan_workspace_bytes(n_out, k_vol), "plan: workspace too small");
   Buffers b = carve(ws, n_out, nullptr);
   int rc;
 
-  // ---- sort 1: rows by Morton code
-  int extent = out_spatial[0];
-  if (out_spatial[1] > extent) extent = out_spatial[1];
-  if (out_spatial[2] > extent) extent = out_spatial[2];
-  const int axis_bits = bits_for(static_cast<uint64_t>(extent - 1));
-  const int coarse = axis_bits > 10 ? axis_bits - 10 : 0;
-  int batch_bits = bits_for(static_cast<uint64_t>(batch_size - 1));
-  if (batch_bits > 16) batch_bits = 16;  // more samples than that only coarsen the order
-  const int batch_shift = 32 - batch_bits;
-  spatial_key_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(
-      reinterpret_cast<const int4*>(out_coords), n_out, coarse, batch_shift, b.keys_a, b.vals_a);
-  TSC_LAUNCH_CHECK("plan_spatial_key");
-  uint32_t *ki = b.keys_a, *ko = b.keys_b, *vi = b.vals_a, *vo = b.vals_b;
-  for (int p = 0; p < 4; ++p) {
-    const Digits d{kFromKey, 8 * p, ki, nullptr, 1u};
-    uint32_t* vdst = (p == 3) ? b.rows : vo;  // the last pass leaves rows in Morton order
-    if ((rc = radix_pass(b, ki, vi, ko, vdst, n_out, d, s))) return rc;
-    std::swap(ki, ko);
-    std::swap(vi, vo);
+  // ---- sort 1: map columns by the Morton code of their rows (columns that
+  // are already in (b,z,y,x) order keep it)
+  if (raster) {
+    iota_u32_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(b.rows, n_out);
+    TSC_LAUNCH_CHECK("plan_iota");
+  } else {
+    int extent = out_spatial[0];
+    if (out_spatial[1] > extent) extent = out_spatial[1];
+    if (out_spatial[2] > extent) extent = out_spatial[2];
+    const int axis_bits = bits_for(static_cast<uint64_t>(extent - 1));
+    const int coarse = axis_bits > 10 ? axis_bits - 10 : 0;
+    int batch_bits = bits_for(static_cast<uint64_t>(batch_size - 1));
+    if (batch_bits > 16) batch_bits = 16;  // more samples than that only coarsen the order
+    const int batch_shift = 32 - batch_bits;
+    spatial_key_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(
+        reinterpret_cast<const int4*>(out_coords), cols_row, n_out, coarse, batch_shift, b.keys_a,
+        b.vals_a);
+    TSC_LAUNCH_CHECK("plan_spatial_key");
+    uint32_t *ki = b.keys_a, *ko = b.keys_b, *vi = b.vals_a, *vo = b.vals_b;
+    for (int p = 0; p < 4; ++p) {
+      const Digits d{kFromKey, 8 * p, ki, nullptr, 1u};
+      uint32_t* vdst = (p == 3) ? b.rows : vo;  // the last pass leaves columns in Morton order
+      if ((rc = radix_pass(b, ki, vi, ko, vdst, n_out, d, s))) return rc;
+      std::swap(ki, ko);
+      std::swap(vi, vo);
+    }
   }
 
   // ---- sort 2: Morton positions by (region, mask), stable
-  // the sort-1 keys are dead now: keys_a holds each row's slot mask
+  // the sort-1 keys are dead now: keys_a holds each column's slot mask,
+  // keys_b the final column permutation
   row_mask_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(nbr, n_out, k_vol, b.keys_a);
   TSC_LAUNCH_CHECK("plan_row_mask");
   mask_at_pos_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(b.keys_a, n_out, b.rows, b.mask_pos,
                                                           b.vals_a);
   TSC_LAUNCH_CHECK("plan_mask");
-  vi = b.vals_a;
-  vo = b.vals_b;
+  uint32_t* vi = b.vals_a;
+  uint32_t* vo = b.vals_b;
   const int mask_bits = k_vol < 32 ? k_vol : 32;
   const int64_t regions = ceil_div(n_out, region_rows);
   const int region_bits = bits_for(static_cast<uint64_t>(regions - 1));
@@ -322,14 +347,14 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* out_coords, int6
     if ((rc = radix_pass(b, nullptr, vi, nullptr, vo, n_out, d, s))) return rc;
     std::swap(vi, vo);
   }
-  gather_rows_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(vi, b.rows, n_out, order);
+  gather_rows_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(vi, b.rows, cols_row, n_out, b.keys_b,
+                                                          order);
   TSC_LAUNCH_CHECK("plan_gather");
   if (nbr_ordered) {
     // int4 accesses need 16-byte aligned rows of the map and of the order
-    const bool vec = (n_out & 3) == 0 && (reinterpret_cast<uintptr_t>(order) & 15) == 0 &&
-                     (reinterpret_cast<uintptr_t>(nbr_ordered) & 15) == 0;
+    const bool vec = (n_out & 3) == 0 && (reinterpret_cast<uintptr_t>(nbr_ordered) & 15) == 0;
     dim3 grid(static_cast<unsigned>(ceil_div(ceil_div(n_out, 4), 256)), static_cast<unsigned>(k_vol));
-    permute_map_kernel<<<grid, 256, 0, s>>>(nbr, order, n_out, vec ? 1 : 0, nbr_ordered);
+    permute_map_kernel<<<grid, 256, 0, s>>>(nbr, b.keys_b, n_out, vec ? 1 : 0, nbr_ordered);
     TSC_LAUNCH_CHECK("plan_permute_map");
   }
   return 0;

@@ -53,12 +53,9 @@ def sparse_conv_forward(features: torch.Tensor, weight: Union[torch.Tensor, Pack
     if not isinstance(weight, PackedWeight):
         K, c_in, c_out = weight.shape
         weight = pack_weight(weight, (K, 1, 1), c_in, c_out, features.dtype)
-    nbr = indice_data.neighbour_map(N_out, features.device)
-    order = indice_data.execution_order(N_out, features.device,
-                                        weight.c_in * features.element_size())
-    if order is not None:
-        return _run(features, weight, bias, indice_data.ordered_map(), order, N_out, True)
-    return _run(features, weight, bias, nbr, None, N_out)
+    nbr, order, ordered = indice_data.conv_operands(N_out, features.device,
+                                                    weight.c_in * features.element_size())
+    return _run(features, weight, bias, nbr, order, N_out, ordered)
 
 
 def dense_forward(features: torch.Tensor, weight: PackedWeight,

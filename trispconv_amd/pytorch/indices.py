@@ -77,7 +77,12 @@ class IndiceData:
         self._pin: Optional[torch.Tensor] = None    # [K][cap] int32
         self._pout: Optional[torch.Tensor] = None   # [K][cap] int32
         self._cnt: Optional[torch.Tensor] = None    # [K] int32 on the device
-        self._nbr: Optional[torch.Tensor] = None    # [K][n_out] int32
+        self._nbr: Optional[torch.Tensor] = None    # [K][n_out] int32, by output row
+        # the builder's map by columns: column t belongs to row _cols_row[t];
+        # _raster says the columns are in (b,z,y,x) order
+        self._map_cols: Optional[torch.Tensor] = None
+        self._cols_row: Optional[torch.Tensor] = None
+        self._raster = False
         self._order: Optional[torch.Tensor] = None  # [n_out] int32 execution order
         self._inverse_cache: Optional["IndiceData"] = None
         self._order_region = 0
@@ -88,10 +93,12 @@ class IndiceData:
     @classmethod
     def _from_tables(cls, *, out_indices, input_indices, input_spatial_shape, output_spatial_shape,
                      kernel_size, stride, padding, dilation, subm, pin, pout, cnt_dev,
-                     pair_num, nbr, batch_size) -> "IndiceData":
+                     pair_num, nbr, batch_size, map_cols=None, cols_row=None,
+                     raster=False) -> "IndiceData":
         d = cls(out_indices, None, None, pair_num, input_indices, input_spatial_shape,
                 output_spatial_shape, kernel_size, stride, padding, dilation, subm)
         d._pin, d._pout, d._cnt, d._nbr = pin, pout, cnt_dev, nbr
+        d._map_cols, d._cols_row, d._raster = map_cols, cols_row, bool(raster)
         d._batch_size = batch_size
         return d
 
@@ -104,6 +111,7 @@ class IndiceData:
     @property
     def pairs_in(self) -> List[torch.Tensor]:
         if self._pairs_in is None:
+            self._ensure_tables()
             self._pairs_in = self._slot_views(self._pin)
         return self._pairs_in
 
@@ -115,6 +123,7 @@ class IndiceData:
     @property
     def pairs_out(self) -> List[torch.Tensor]:
         if self._pairs_out is None:
+            self._ensure_tables()
             self._pairs_out = self._slot_views(self._pout)
         return self._pairs_out
 
@@ -129,14 +138,43 @@ class IndiceData:
         counts = [int(c) for c in self.pair_num.tolist()]
         return [table[k, :c].long() for k, c in enumerate(counts)]
 
+    def _ensure_tables(self) -> None:
+        """Padded pair tables from the builder's map (made on first use: the
+        convolution itself reads the map)."""
+        if self._pin is not None or self._map_cols is None:
+            return
+        n_out = len(self.out_indices)
+        nbr = self.neighbour_map(n_out, self._map_cols.device)
+        lib = L.lib()
+        K = self.K
+        ws = L.workspace(lib.tsc_pairs_from_map_workspace_bytes(n_out, K), nbr.device)
+        pin = torch.empty((K, max(n_out, 1)), dtype=torch.int32, device=nbr.device)
+        pout = torch.empty_like(pin)
+        L.check(lib.tsc_pairs_from_map(nbr.data_ptr(), n_out, K, pin.shape[1], ws.data_ptr(),
+                                       ws.numel(), pin.data_ptr(), pout.data_ptr(),
+                                       L.stream_of(nbr)), "pair lists")
+        self._pin, self._pout = pin, pout
+        self._cnt = self.pair_num.to(device=nbr.device, dtype=torch.int32)
+
     def _drop_tables(self) -> None:
         self._pin = self._pout = self._cnt = self._nbr = self._order = None
+        self._map_cols = self._cols_row = None
+        self._raster = False
         self._nbr_ordered = None
         self._inverse_cache = None
 
     # --------------------------------------------------- convolution inputs
     def neighbour_map(self, n_out: int, device) -> torch.Tensor:
         """[K][n_out] int32: input row feeding output row o through slot k, or -1."""
+        if self._nbr is None and self._map_cols is not None:
+            if not self._raster:  # the builder's columns are the rows in order
+                self._nbr = self._map_cols
+            else:
+                nbr = torch.full((self.K, n_out), -1, dtype=torch.int32, device=device)
+                L.check(L.lib().tsc_map_to_rows(self._map_cols.data_ptr(), self._cols_row.data_ptr(),
+                                                self._map_cols.shape[1], n_out, self.K,
+                                                nbr.data_ptr(), L.stream_of(nbr)), "map to rows")
+                self._nbr = nbr
         if self._nbr is None:
             # user-built lists: scatter them into a map (each slot maps an
             # output at most once, as every generator guarantees)
@@ -159,18 +197,33 @@ class IndiceData:
             return None
         region = int(min(max(_REGION_BYTES // max(int(row_bytes), 1), 2048), 1 << 30))
         if self._order is None or self._order_region != region:
-            nbr = self.neighbour_map(n_out, device)
-            coords = _coords(self.out_indices, "conv plan")
+            if self._map_cols is not None:  # the builder's columns, maybe in spatial order
+                nbr, cols_row, raster = self._map_cols, self._cols_row, self._raster
+            else:
+                nbr, cols_row, raster = self.neighbour_map(n_out, device), None, False
+            coords = None if raster else _coords(self.out_indices, "conv plan")
             lib = L.lib()
             ws = L.workspace(lib.tsc_plan_workspace_bytes(n_out, self.K), device)
             order = torch.empty(n_out, dtype=torch.int32, device=device)
             nbr_ordered = torch.empty_like(nbr)
-            L.check(lib.tsc_conv_plan(nbr.data_ptr(), coords.data_ptr(), n_out, self.K,
-                                      self._batch_bound(), L.i3(self.output_spatial_shape), region,
-                                      ws.data_ptr(), ws.numel(), order.data_ptr(),
-                                      nbr_ordered.data_ptr(), L.stream_of(nbr)), "conv plan")
+            L.check(lib.tsc_conv_plan(nbr.data_ptr(), L.ptr(cols_row), int(raster), L.ptr(coords),
+                                      n_out, self.K, self._batch_bound(),
+                                      L.i3(self.output_spatial_shape), region, ws.data_ptr(),
+                                      ws.numel(), order.data_ptr(), nbr_ordered.data_ptr(),
+                                      L.stream_of(nbr)), "conv plan")
             self._order, self._order_region, self._nbr_ordered = order, region, nbr_ordered
         return self._order
+
+    def conv_operands(self, n_out: int, device, row_bytes: int = 256):
+        """(map, order, ordered) for the fused convolution: the planned order
+        and its permuted map; for small layers the builder's own spatial
+        column order when it has one; else the row-major map."""
+        order = self.execution_order(n_out, device, row_bytes)
+        if order is not None:
+            return self._nbr_ordered, order, True
+        if self._map_cols is not None and self._raster:
+            return self._map_cols, self._cols_row, True
+        return self.neighbour_map(n_out, device), None, False
 
     def ordered_map(self) -> Optional[torch.Tensor]:
         """The neighbour map permuted into the execution order (None without one)."""
@@ -219,21 +272,23 @@ def generate_subm_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size:
         raise ValueError(f"generate_subm_indice_pairs: invalid batch size {batch_size} or "
                          f"spatial shape {shape}")
     ws = L.workspace(ws_bytes, dev)
-    nbr = torch.empty((K, n), dtype=torch.int32, device=dev)
-    pin = torch.empty((K, n), dtype=torch.int32, device=dev)
-    pout = torch.empty((K, n), dtype=torch.int32, device=dev)
-    counts = torch.empty(K + 1, dtype=torch.int32, device=dev)
+    # the map by columns (in (b,z,y,x) order when the bitmap path runs); the
+    # reference's pair lists are derived from it on first access
+    cols_row = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+    map_cols = torch.empty((K, n), dtype=torch.int32, device=dev)
+    counts = torch.empty(K + 2, dtype=torch.int32, device=dev)
     L.check(lib.tsc_subm_pairs(coords.data_ptr(), n, int(batch_size), L.i3(shape), L.i3(ks),
-                               L.i3(dil), ws.data_ptr(), ws.numel(), nbr.data_ptr(),
-                               pin.data_ptr(), pout.data_ptr(), counts.data_ptr(),
-                               L.stream_of(coords)), "generate_subm_indice_pairs")
+                               L.i3(dil), ws.data_ptr(), ws.numel(), cols_row.data_ptr(),
+                               map_cols.data_ptr(), counts.data_ptr(), L.stream_of(coords)),
+            "generate_subm_indice_pairs")
     host = counts.cpu()
     _raise_status(int(host[K]), "generate_subm_indice_pairs")
     return IndiceData._from_tables(
         out_indices=indices, input_indices=indices, input_spatial_shape=spatial_shape,
         output_spatial_shape=spatial_shape, kernel_size=ks, stride=(1, 1, 1),
-        padding=(0, 0, 0), dilation=dil, subm=True, pin=pin, pout=pout, cnt_dev=counts[:K],
-        pair_num=host[:K].long(), nbr=nbr, batch_size=int(batch_size))
+        padding=(0, 0, 0), dilation=dil, subm=True, pin=None, pout=None, cnt_dev=None,
+        pair_num=host[:K].long(), nbr=None, batch_size=int(batch_size), map_cols=map_cols,
+        cols_row=cols_row[:n], raster=bool(host[K + 1]))
 
 
 def generate_strided_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size: int,
@@ -281,6 +336,7 @@ def generate_inverse_indice_pairs(fwd: IndiceData) -> IndiceData:
     slot k reads forward outputs pairs_out[k] and writes the compact id of
     forward input pairs_in[k]; pair_num is the forward's.
     """
+    fwd._ensure_tables()
     if fwd._pin is None:
         raise ValueError("inverse pairs need a forward IndiceData built on the GPU")
     dev = fwd._pin.device
