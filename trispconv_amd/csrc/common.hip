@@ -182,6 +182,37 @@ __global__ void __launch_bounds__(kScanThreads) scan_apply_kernel(const uint32_t
   }
 }
 
+// Inputs of up to kSmallScan items are scanned by one workgroup in a single
+// launch (chunks of 1024 x 16 consecutive items, carried across chunks).
+constexpr int kSmallItems = 16;
+constexpr int64_t kSmallScan = 65536;
+
+__global__ void __launch_bounds__(1024) scan_small_kernel(const uint32_t* __restrict__ src, int kind,
+                                                          int64_t n, uint32_t* __restrict__ out,
+                                                          int32_t* __restrict__ total) {
+  __shared__ uint32_t s_wave[33];
+  uint32_t carry = 0;
+  for (int64_t base = 0; base < n; base += 1024 * kSmallItems) {
+    const int64_t b0 = base + threadIdx.x * (int64_t)kSmallItems;
+    uint32_t v[kSmallItems];
+    uint32_t acc = 0;
+#pragma unroll
+    for (int j = 0; j < kSmallItems; ++j) {
+      v[j] = b0 + j < n ? scan_value(src, kind, b0 + j) : 0u;
+      acc += v[j];
+    }
+    uint32_t tot;
+    uint32_t run = carry + block_exclusive(acc, s_wave, &tot);
+#pragma unroll
+    for (int j = 0; j < kSmallItems; ++j) {
+      if (b0 + j < n) out[b0 + j] = run;
+      run += v[j];
+    }
+    carry += tot;
+  }
+  if (threadIdx.x == 0 && total) *total = static_cast<int32_t>(carry);
+}
+
 int64_t scan_scratch_words(int64_t n) { return ceil_div(n > 0 ? n : 1, kScanTile); }
 
 int exclusive_scan_u32(const uint32_t* src, int kind, int64_t n, uint32_t* out, int32_t* total,
@@ -191,6 +222,11 @@ int exclusive_scan_u32(const uint32_t* src, int kind, int64_t n, uint32_t* out, 
       int rc = fill_u32(reinterpret_cast<uint32_t*>(total), 1, 0u, s);
       if (rc) return rc;
     }
+    return 0;
+  }
+  if (n <= kSmallScan) {
+    scan_small_kernel<<<1, 1024, 0, s>>>(src, kind, n, out, total);
+    TSC_LAUNCH_CHECK("scan_small");
     return 0;
   }
   const int64_t nblk = ceil_div(n, kScanTile);
