@@ -182,10 +182,11 @@ __global__ void __launch_bounds__(kScanThreads) scan_apply_kernel(const uint32_t
   }
 }
 
-// Inputs of up to kSmallScan items are scanned by one workgroup in a single
-// launch (chunks of 1024 x 16 consecutive items, carried across chunks).
+// Inputs of up to kSmallScan items (one chunk of 1024 x 16 consecutive
+// items) are scanned by one workgroup in a single launch; one workgroup is
+// slower than the three-kernel scan beyond that.
 constexpr int kSmallItems = 16;
-constexpr int64_t kSmallScan = 65536;
+constexpr int64_t kSmallScan = 1024 * kSmallItems;
 
 __global__ void __launch_bounds__(1024) scan_small_kernel(const uint32_t* __restrict__ src, int kind,
                                                           int64_t n, uint32_t* __restrict__ out,
