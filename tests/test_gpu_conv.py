@@ -90,6 +90,9 @@ LAYER_CASES = [
     (64, 64, torch.float16), (96, 96, torch.float16), (128, 128, torch.float16),
     (128, 128, torch.bfloat16), (256, 128, torch.float16), (64, 256, torch.bfloat16),
     (160, 192, torch.float16), (64, 64, torch.float32),
+    # fp32 on the matrix cores (v_mfma_f32_32x32x2_f32): every column tile width
+    (32, 32, torch.float32), (128, 128, torch.float32), (64, 96, torch.float32),
+    (96, 64, torch.float32),
 ]
 
 
@@ -102,7 +105,8 @@ def test_subm_layer(c_in, c_out, dtype):
 
 
 @pytest.mark.parametrize("c_in,c_out,dtype", [(16, 32, torch.float32), (32, 64, torch.bfloat16),
-                                              (64, 128, torch.float16), (5, 3, torch.float16)])
+                                              (64, 128, torch.float16), (5, 3, torch.float16),
+                                              (64, 64, torch.float32)])
 @pytest.mark.parametrize("k,s,p", [(3, 2, 1), (2, 2, 0), ((3, 1, 1), (2, 1, 1), 0)])
 def test_strided_layer(c_in, c_out, dtype, k, s, p):
     idx = _tiny(7, (21, 18, 25), 2, 3000)
@@ -158,7 +162,7 @@ def test_one_by_one_layers(dtype):
     assert rel_err(to_np(z.features), ref) <= TOL[dtype]
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("c_in,c_out", [(32, 96), (64, 192), (32, 256), (96, 64), (64, 64)])
 @pytest.mark.parametrize("n", [1500, 6000])
 def test_every_bias_dtype_and_column_tile(c_in, c_out, dtype, n):

@@ -32,16 +32,22 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-enum Path { kValu = 0, kMfma16 = 1 };
+enum Path { kValu = 0, kMfma = 1 };
 
-// 64-channel chunks: a ring of four operand buffers (64 registers each at
-// 64 rows per wave) plus the AGPR accumulators fit one wave per SIMD.
-int pick_ck(int c_in) { return c_in % 64 == 0 ? 64 : 32; }
+// Input-channel chunk of one stage: 64 bytes of every gathered row per lane
+// half (64 channels of f16/bf16, 32 of f32), or half that when the channels
+// do not divide.
+int pick_ck(int dtype, int c_in) {
+  if (dtype == TSC_F32) return 32;
+  return c_in % 64 == 0 ? 64 : 32;
+}
 int pick_bn(int c_out) { return c_out % 128 == 0 ? 128 : (c_out % 64 == 0 ? 64 : 32); }
 
+// MFMA for every dtype when both channel counts are multiples of 32 (the
+// slot table of K <= 64 slots fits LDS); VALU otherwise.
 Path pick_path(int dtype, int c_in, int c_out, int K) {
-  if ((dtype == TSC_F16 || dtype == TSC_BF16) && c_in % 32 == 0 && c_out % 32 == 0 && K <= 64)
-    return kMfma16;
+  if (c_in % 32 == 0 && c_out % 32 == 0 && K <= 64) return kMfma;
+  (void)dtype;
   return kValu;
 }
 
@@ -85,29 +91,33 @@ __global__ void pack_valu_kernel(const void* w, int w_dt, int layout, int K, int
   }
 }
 
-// MFMA layout: [k][chunk][c_out/32][step][lane][8].  At step s of a CK-wide
-// input-channel chunk, lane l supplies B[kk][n] for n = l % 32 and
-// kk = (l / 32) * CK/2 + s*8 + 0..7 — the same channel split the A operand
-// uses, so that each lane's A data is a contiguous CK/2-channel run of a row.
+// MFMA layout: [k][chunk][c_out/32][u][lane][16/sizeof(T)].  Lane l of a
+// 32-column block n supplies column n*32 + l%32, and for lane half h = l/32
+// the channels c*CK + h*CK/2 + u*(16/sizeof(T)) + 0.. of chunk c: the same
+// channel split the A operand uses, so that each lane's A data is a
+// contiguous CK/2-channel (64-byte) run of a row.  An f16/bf16 MFMA step
+// (32x32x16) takes one 16-byte vector per lane; an f32 step (32x32x2) one
+// element of it.
 template <typename T>
 __global__ void pack_mfma_kernel(const void* w, int w_dt, int layout, int K, int c_in, int c_out,
                                  int ck, T* packed) {
-  const int steps = ck / 16;
+  constexpr int VPL = 16 / sizeof(T);  // values per 16-byte vector
+  const int ub = (ck / 2) / VPL;      // vectors per lane per chunk
   const int nbt = c_out / 32;
   const int nch = c_in / ck;
   const int64_t total = (int64_t)K * c_in * c_out;
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x) {
-    const int i = e & 7;
-    const int lane = (e >> 3) & 63;
-    int64_t r = e >> 9;
-    const int s = r % steps;
-    r /= steps;
+    const int i = e % VPL;
+    const int lane = (e / VPL) & 63;
+    int64_t r = e / (VPL * 64);
+    const int u = r % ub;
+    r /= ub;
     const int nb = r % nbt;
     r /= nbt;
     const int c = r % nch;
     const int k = r / nch;
-    const int ci = c * ck + (lane >> 5) * (ck / 2) + s * 8 + i;
+    const int ci = c * ck + (lane >> 5) * (ck / 2) + u * VPL + i;
     const int co = nb * 32 + (lane & 31);
     packed[e] = from_f32<T>(src_weight(w, w_dt, layout, K, c_in, c_out, k, ci, co));
   }
@@ -162,6 +172,12 @@ template <> struct MfmaOp<__hip_bfloat16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
 };
+template <> struct MfmaOp<float> {
+  using V = float;
+  static __device__ __forceinline__ f32x16 run(V a, V b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+};
 
 constexpr int kTileRows = 256;  // 4 waves x 64 rows
 
@@ -171,6 +187,10 @@ constexpr int kTileRows = 256;  // 4 waves x 64 rows
 __device__ __attribute__((aligned(256))) uint4 g_zero_row[16];
 
 template <int N> using Slot = std::integral_constant<int, N>;
+
+// Output rows each wave stages per epilogue pass: 32 rows of up to 256 bytes,
+// else 16, so the staging area stays within 35 KB for two workgroups per CU.
+constexpr int mfma_stage_rows(int row_bytes) { return row_bytes <= 256 ? 32 : 16; }
 
 // One workgroup (4 waves, one per SIMD) per CU; each wave owns 64 rows x BN
 // columns of a 256-row tile.  The work of a tile is a sequence of stages
@@ -188,9 +208,12 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
   using Op = MfmaOp<T>;
   using V = typename Op::V;
   constexpr int RING = 2;                        // operand buffers: this stage and the next
-  constexpr int STEPS = CK / 16;                 // 16-deep MFMA steps per chunk
+  constexpr bool F32 = std::is_same<T, float>::value;
+  constexpr int VPL = 16 / (int)sizeof(T);       // values per 16-byte vector
+  constexpr int UB = (CK / 2) / VPL;             // vectors per lane per row and stage
+  static_assert(UB * VPL * 2 == CK && UB >= 1, "chunk must split into 16-byte runs");
   constexpr int NB = BN / 32;                    // 32-wide column blocks
-  constexpr int SLAB_VECS = BN * CK / 8;         // 16-byte vectors of one weight stage
+  constexpr int SLAB_VECS = BN * CK * (int)sizeof(T) / 16;  // 16-byte vectors of one weight stage
   constexpr int WV = SLAB_VECS >= 256 ? SLAB_VECS / 256 : 1;
   constexpr bool FULL = SLAB_VECS % 256 == 0;
   static_assert(WV <= 4, "weight slab too large for the register stage");
@@ -297,14 +320,14 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[rb][nb][i] = 0.f;
 
-  uint4 ring[RING][2][STEPS];  // gathered operands: this stage and the next
+  uint4 ring[RING][2][UB];  // gathered operands: this stage and the next
   uint4 w0, w1, w2, w3;        // this thread's share of the next weight slab
 
   // Loads are issued whether or not the stage exists (past the last stage they
   // re-read stage 0 or the zero row), keeping the loop body straight-line.
   auto load_w = [&](int k, int c) {
     if (k >= K) k = c = 0;
-    const uint4* src = Wv + (((int64_t)k * nch + c) * nbt_all + (int64_t)nbt * NB) * STEPS * 64 + t;
+    const uint4* src = Wv + (((int64_t)k * nch + c) * nbt_all + (int64_t)nbt * NB) * UB * 64 + t;
     if (FULL || t < SLAB_VECS) w0 = src[0];
     if constexpr (WV > 1) w1 = src[256];
     if constexpr (WV > 2) w2 = src[512];
@@ -330,9 +353,9 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
     const uint4* p1 = j1 >= 0 ? reinterpret_cast<const uint4*>(feat + (int64_t)j1 * c_in + coff)
                               : zero_row;
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
-      ring[S][0][s] = p0[s];
-      ring[S][1][s] = p1[s];
+    for (int u = 0; u < UB; ++u) {
+      ring[S][0][u] = p0[u];
+      ring[S][1][u] = p1[u];
     }
   };
   // Every wave runs every stage of its tile: a stage lasts as long as its
@@ -343,12 +366,28 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
   auto compute = [&](auto slot, const uint4* sw) {
     constexpr int S = decltype(slot)::value;
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) {
+    for (int u = 0; u < UB; ++u) {
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        const V b = __builtin_bit_cast(V, sw[(nb * STEPS + s) * 64 + lane]);
-        acc[0][nb] = Op::run(__builtin_bit_cast(V, ring[S][0][s]), b, acc[0][nb]);
-        acc[1][nb] = Op::run(__builtin_bit_cast(V, ring[S][1][s]), b, acc[1][nb]);
+        const uint4 bv = sw[(nb * UB + u) * 64 + lane];
+        if constexpr (F32) {
+          // four 32x32x2 steps per vector: step i uses element i of A and B
+          const float4 a0 = __builtin_bit_cast(float4, ring[S][0][u]);
+          const float4 a1 = __builtin_bit_cast(float4, ring[S][1][u]);
+          const float4 b4 = __builtin_bit_cast(float4, bv);
+          acc[0][nb] = Op::run(a0.x, b4.x, acc[0][nb]);
+          acc[1][nb] = Op::run(a1.x, b4.x, acc[1][nb]);
+          acc[0][nb] = Op::run(a0.y, b4.y, acc[0][nb]);
+          acc[1][nb] = Op::run(a1.y, b4.y, acc[1][nb]);
+          acc[0][nb] = Op::run(a0.z, b4.z, acc[0][nb]);
+          acc[1][nb] = Op::run(a1.z, b4.z, acc[1][nb]);
+          acc[0][nb] = Op::run(a0.w, b4.w, acc[0][nb]);
+          acc[1][nb] = Op::run(a1.w, b4.w, acc[1][nb]);
+        } else {
+          const V b = __builtin_bit_cast(V, bv);
+          acc[0][nb] = Op::run(__builtin_bit_cast(V, ring[S][0][u]), b, acc[0][nb]);
+          acc[1][nb] = Op::run(__builtin_bit_cast(V, ring[S][1][u]), b, acc[1][nb]);
+        }
       }
     }
   };
@@ -382,34 +421,38 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
   }
 
   // ---- epilogue: + bias, round once, store each output element once.
-  // Each wave transposes its accumulators through LDS, 32 rows at a time, so
+  // Each wave transposes its accumulators through LDS, PR rows at a time, so
   // that lanes write 16-byte pieces of output rows instead of single
   // elements.  32x32 accumulator layout: register i of lane l holds row
   // (i/4)*8 + (l/32)*4 + i%4 and column l%32 of the block.
   constexpr int ROW_BYTES = BN * (int)sizeof(T);
   constexpr int STRIDE = ROW_BYTES + 16;            // padded LDS row
   constexpr int CHUNKS = ROW_BYTES / 16;            // 16-byte pieces per row
-  char* stage = reinterpret_cast<char*>(s_nbr) + wave * 32 * STRIDE;
+  constexpr int PR = mfma_stage_rows(ROW_BYTES);    // rows staged per wave and pass
+  char* stage = reinterpret_cast<char*>(s_nbr) + wave * PR * STRIDE;
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb) {
+  for (int pass = 0; pass < 64 / PR; ++pass) {
     __syncthreads();                                // the staging area is free
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const int cl = nb * 32 + (lane & 31);
-      const float bv = s_bias[cl];
+    for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int row = (i >> 2) * 8 + h * 4 + (i & 3);
-        *reinterpret_cast<T*>(stage + row * STRIDE + cl * (int)sizeof(T)) =
-            from_f32<T>(acc[rb][nb][i] + bv);
+        const int rblk = rb * 32 + (i >> 2) * 8;    // + h*4 + i%4 stays within 8 rows
+        if (rblk / PR != pass) continue;
+        const int row = rblk % PR + h * 4 + (i & 3);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const int cl = nb * 32 + (lane & 31);
+          *reinterpret_cast<T*>(stage + row * STRIDE + cl * (int)sizeof(T)) =
+              from_f32<T>(acc[rb][nb][i] + s_bias[cl]);
+        }
       }
-    }
     __syncthreads();
 #pragma unroll
-    for (int q = 0; q < CHUNKS / 2; ++q) {
+    for (int q = 0; q < PR * CHUNKS / 64; ++q) {
       const int piece = q * 64 + lane;
       const int row = piece / CHUNKS, ch = piece % CHUNKS;
-      const int32_t orow = s_orow[wave * 64 + rb * 32 + row];
+      const int32_t orow = s_orow[wave * 64 + pass * PR + row];
       if (orow >= 0) {
         const uint4 v = *reinterpret_cast<const uint4*>(stage + row * STRIDE + ch * 16);
         *reinterpret_cast<uint4*>(out + (int64_t)orow * c_out + nbt * BN + ch * (16 / (int)sizeof(T))) = v;
@@ -428,7 +471,8 @@ int launch_mfma(const void* feat, int c_in, const void* W, const void* bias, int
   dim3 grid(static_cast<unsigned>(items));
   // dynamic LDS: the tile's slot lists, later reused to stage the output
   const size_t lds_nbr = (size_t)K * kTileRows * sizeof(int32_t);
-  const size_t lds_out = (size_t)(kTileRows / 2) * (BN * sizeof(T) + 16);  // 32 rows per wave
+  const int row_bytes = BN * (int)sizeof(T);
+  const size_t lds_out = (size_t)4 * mfma_stage_rows(row_bytes) * (row_bytes + 16);  // 4 waves
   const size_t lds = lds_nbr > lds_out ? lds_nbr : lds_out;
   conv_mfma_kernel<T, BN, CK><<<grid, 256, lds, s>>>(
       static_cast<const T*>(feat), c_in, static_cast<const T*>(W), bias, bias_dt, nbr, order,
@@ -441,16 +485,20 @@ template <typename T>
 int dispatch_mfma(const void* feat, int c_in, const void* W, const void* bias, int bias_dt,
                   const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
                   int c_out, void* out, hipStream_t s) {
-  const int bn = pick_bn(c_out), ck = pick_ck(c_in);
+  constexpr int dt = std::is_same<T, float>::value ? TSC_F32
+                     : std::is_same<T, __half>::value ? TSC_F16 : TSC_BF16;
+  const int bn = pick_bn(c_out), ck = pick_ck(dt, c_in);
 #define TSC_MFMA_CASE(BN_, CK_)                                                              \
   if (bn == BN_ && ck == CK_)                                                                \
     return launch_mfma<T, BN_, CK_>(feat, c_in, W, bias, bias_dt, nbr, order, nbr_ordered, \
                                     n_out, K, c_out, out, s);
-  TSC_MFMA_CASE(128, 64)
+  if constexpr (!std::is_same<T, float>::value) {
+    TSC_MFMA_CASE(128, 64)
+    TSC_MFMA_CASE(64, 64)
+    TSC_MFMA_CASE(32, 64)
+  }
   TSC_MFMA_CASE(128, 32)
-  TSC_MFMA_CASE(64, 64)
   TSC_MFMA_CASE(64, 32)
-  TSC_MFMA_CASE(32, 64)
   TSC_MFMA_CASE(32, 32)
 #undef TSC_MFMA_CASE
   return set_error(TSC_EUNSUPPORTED, "conv: no MFMA tile for c_in=%d c_out=%d", c_in, c_out);
@@ -495,7 +543,7 @@ using namespace tsc;
 extern "C" int64_t tsc_packed_weight_bytes(int32_t k_vol, int32_t c_in, int32_t c_out,
                                            int32_t dtype) {
   const int64_t elems = (int64_t)k_vol * c_in * c_out;
-  return pick_path(dtype, c_in, c_out, k_vol) == kMfma16 ? elems * 2 : elems * 4;
+  return pick_path(dtype, c_in, c_out, k_vol) == kMfma ? elems * dtype_bytes(dtype) : elems * 4;
 }
 
 extern "C" int tsc_pack_weight(const void* w, int32_t w_dtype, int32_t layout, int32_t k_vol,
@@ -508,9 +556,12 @@ extern "C" int tsc_pack_weight(const void* w, int32_t w_dtype, int32_t layout, i
   TSC_REQUIRE(w && packed, "pack: null pointer");
   const int64_t total = (int64_t)k_vol * c_in * c_out;
   const int grid = static_cast<int>(ceil_div(total, 256) < 2048 ? ceil_div(total, 256) : 2048);
-  if (pick_path(dtype, c_in, c_out, k_vol) == kMfma16) {
-    const int ck = pick_ck(c_in);
-    if (dtype == TSC_F16)
+  if (pick_path(dtype, c_in, c_out, k_vol) == kMfma) {
+    const int ck = pick_ck(dtype, c_in);
+    if (dtype == TSC_F32)
+      pack_mfma_kernel<float><<<grid, 256, 0, s>>>(w, w_dtype, layout, k_vol, c_in, c_out, ck,
+                                                   static_cast<float*>(packed));
+    else if (dtype == TSC_F16)
       pack_mfma_kernel<__half><<<grid, 256, 0, s>>>(w, w_dtype, layout, k_vol, c_in, c_out, ck,
                                                     static_cast<__half*>(packed));
     else
@@ -545,11 +596,14 @@ extern "C" int tsc_conv_forward(const void* feat, int32_t dtype, int64_t n_in, i
     TSC_REQUIRE(nbr != nullptr, "conv: empty input");
   }
   const Path path = pick_path(dtype, c_in, c_out, k_vol);
-  if (path == kMfma16) {
+  if (path == kMfma) {
     TSC_REQUIRE((reinterpret_cast<uintptr_t>(feat) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(packed_w) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(out) & 15) == 0,
                 "conv: feature, weight and output buffers must be 16-byte aligned");
+    if (dtype == TSC_F32)
+      return dispatch_mfma<float>(feat, c_in, packed_w, bias, bias_dtype, nbr, order, nbr_ordered,
+                                  n_out, k_vol, c_out, out, s);
     if (dtype == TSC_F16)
       return dispatch_mfma<__half>(feat, c_in, packed_w, bias, bias_dtype, nbr, order, nbr_ordered,
                                    n_out, k_vol, c_out, out, s);
