@@ -278,19 +278,34 @@ def test_full_size_workloads(name):
         torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("row_bytes", [256, 2048])
-def test_plan_regions_are_mask_sorted_permutations(row_bytes):
-    """The execution order is a permutation of the output rows whose regions
-    (consecutive runs of region_rows rows) are each sorted by slot mask."""
+@pytest.mark.parametrize("row_bytes", [256, 2048, 1 << 17])
+def test_plan_tiles_mask_sorted_heaviest_first(row_bytes):
+    """The execution order is a permutation of the output rows.  Cut into
+    256-row tiles (the convolution's workgroup tiles), each full tile is sorted
+    by slot mask, and inside each region the full tiles come in non-increasing
+    number of slots used by their rows; the partial tile, if any, is last and
+    mask-sorted too.  row_bytes = 2^17 makes regions of 2048 rows."""
     idx = _tiny(15, (40, 40, 40), 2, 6000)
     x = torch.from_numpy(idx).to(DEV)
     data = generate_subm_indice_pairs(x, (40, 40, 40), 2, 3)
     n = len(idx)
     order = data.execution_order(n, x.device, row_bytes).cpu().numpy().astype(np.int64)
     region = data._order_region
+    assert region % 256 == 0
     assert np.array_equal(np.sort(order), np.arange(n))
     nbr = data.neighbour_map(n, x.device).cpu().numpy()
     mask = ((nbr.T >= 0).astype(np.int64) << np.arange(27)).sum(1)[order]
-    for r0 in range(0, n, region):
-        m = mask[r0:r0 + region]
-        assert (np.diff(m) >= 0).all(), f"region at {r0} not sorted by mask"
+    for t0 in range(0, n, 256):
+        m = mask[t0:t0 + 256]
+        assert (np.diff(m) >= 0).all(), f"tile at {t0} not sorted by mask"
+    n_full = n // 256
+    used = np.array([bin(int(np.bitwise_or.reduce(mask[t * 256:(t + 1) * 256]))).count("1")
+                     for t in range(n_full)])
+    per_region = region // 256
+    for r0 in range(0, n_full, per_region):
+        u = used[r0:r0 + per_region]
+        assert (np.diff(u) <= 0).all(), f"tiles of the region at row {r0 * 256} not heaviest first"
+    # the same tiles as a plain mask sort inside regions: each region's multiset of rows holds
+    for r0 in range(0, n_full * 256, region):
+        hi = min(r0 + region, n_full * 256)
+        assert hi - r0 == len(np.unique(order[r0:hi]))

@@ -32,6 +32,9 @@ const char* last_error();
   } while (0)
 
 constexpr int kWave = 64;
+// Output rows per workgroup tile of the MFMA convolution (4 waves x 64 rows);
+// the execution order reorders whole tiles of this size.
+constexpr int kConvTileRows = 256;
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t align_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }

@@ -179,7 +179,7 @@ template <> struct MfmaOp<float> {
   }
 };
 
-constexpr int kTileRows = 256;  // 4 waves x 64 rows
+constexpr int kTileRows = kConvTileRows;  // 4 waves x 64 rows
 
 // Operand source for absent neighbours: lanes whose output row has no input
 // through the current slot read zeros from here instead of branching around
@@ -228,16 +228,18 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
   const int lane = t & 63;
   const int wave = t >> 6;
   const int h = lane >> 5;
-  // XCD-aware placement: workgroups are dispatched round-robin over the 8
-  // XCDs, so give XCD x a contiguous run of (tile, column tile) items; all
-  // column tiles of a row tile, and neighbouring row tiles of the execution
-  // order, then share that XCD's L2.
+  // XCD placement: workgroups are dispatched round-robin over the 8 XCDs, in
+  // grid order.  Row tiles are dealt round-robin too (the execution order puts
+  // the tiles with the most slots first, so every XCD gets an even share of
+  // the heavy ones), and all column tiles of a row tile run one after another
+  // on the same XCD, sharing its L2 for the gathered rows.
   const uint32_t ncol = static_cast<uint32_t>(c_out / BN);
   uint32_t item;  // the launch keeps the grid below 2^31 workgroups
   {
-    const uint32_t nwg = gridDim.x, lin = blockIdx.x;
-    const uint32_t per = nwg / 8, rem = nwg % 8, x = lin % 8;
-    item = x * per + (x < rem ? x : rem) + lin / 8;
+    const uint32_t lin = blockIdx.x;
+    const uint32_t dealt = (gridDim.x / (8 * ncol)) * (8 * ncol);  // whole rounds of 8 row tiles
+    const uint32_t x = lin % 8, j = lin / 8;
+    item = lin < dealt ? ((j / ncol) * 8 + x) * ncol + j % ncol : lin;
   }
   const int64_t tile0 = static_cast<int64_t>(item / ncol) * kTileRows;
   const int nbt = static_cast<int>(item % ncol);

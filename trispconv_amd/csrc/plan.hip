@@ -12,7 +12,11 @@
 // order, cut into regions of `region_rows` consecutive rows (the caller sizes
 // them so one region's input rows fit in cache), and sorted inside each
 // region by their slot-occupancy mask (bit k set when nbr[k][o] >= 0; slots
-// beyond 32 fold onto bit k mod 32), ties kept in Morton order.
+// beyond 32 fold onto bit k mod 32), ties kept in Morton order.  Last, whole
+// 256-row tiles (the convolution's workgroup tiles) are reordered inside each
+// region by the number of slots their rows use, most first, the partial tile
+// staying last: the convolution deals tiles to the XCDs in this order, so
+// the heavy ones start early and the launch does not end on a few of them.
 //
 // Output values never depend on the order: every row's fp32 accumulation
 // sees the same slots in the same ascending order and absent slots add zero.
@@ -127,15 +131,47 @@ __global__ void __launch_bounds__(256) mask_at_pos_kernel(const uint32_t* __rest
   vals[i] = static_cast<uint32_t>(i);
 }
 
+// Sort key of each full tile of the order (one 256-thread block per tile):
+// the tile's region in the high bits, then 32 - (slots in the union of its
+// rows' masks), so tiles with more slots sort first inside a region.
+__global__ void __launch_bounds__(kConvTileRows) tile_key_kernel(
+    const uint32_t* __restrict__ pos, const uint32_t* __restrict__ mask_pos,
+    int64_t tiles_per_region, uint32_t* __restrict__ keys, uint32_t* __restrict__ vals) {
+  __shared__ uint32_t s_or[kConvTileRows / kWave];
+  const int64_t tile = blockIdx.x;
+  uint32_t m = mask_pos[pos[tile * kConvTileRows + threadIdx.x]];
+#pragma unroll
+  for (int off = kWave / 2; off > 0; off >>= 1) m |= __shfl_xor(m, off, kWave);
+  if ((threadIdx.x & (kWave - 1)) == 0) s_or[threadIdx.x / kWave] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t u = 0;
+#pragma unroll
+    for (int w = 0; w < kConvTileRows / kWave; ++w) u |= s_or[w];
+    const uint32_t region = static_cast<uint32_t>(tile / tiles_per_region);
+    keys[tile] = (region << 6) | (32u - static_cast<uint32_t>(__popc(u)));
+    vals[tile] = static_cast<uint32_t>(tile);
+  }
+}
+
 // perm[i] = map column processed at position i; order[i] = its row.
+// Positions inside the first n_tiles full tiles come from tile tile_perm[i/256]
+// (when given); the rest stay where the sorts put them.
 __global__ void __launch_bounds__(256) gather_rows_kernel(const uint32_t* __restrict__ pos,
                                                           const uint32_t* __restrict__ cols,
                                                           const int32_t* __restrict__ cols_row,
-                                                          int64_t n, uint32_t* __restrict__ perm,
+                                                          int64_t n,
+                                                          const uint32_t* __restrict__ tile_perm,
+                                                          int64_t n_tiles,
+                                                          uint32_t* __restrict__ perm,
                                                           int32_t* __restrict__ order) {
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const uint32_t col = cols[pos[i]];
+  const int64_t tile = i / kConvTileRows;
+  const int64_t src = (tile_perm && tile < n_tiles)
+                          ? static_cast<int64_t>(tile_perm[tile]) * kConvTileRows + i % kConvTileRows
+                          : i;
+  const uint32_t col = cols[pos[src]];
   perm[i] = col;
   order[i] = cols_row ? cols_row[col] : static_cast<int32_t>(col);
 }
@@ -347,8 +383,28 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_
     if ((rc = radix_pass(b, nullptr, vi, nullptr, vo, n_out, d, s))) return rc;
     std::swap(vi, vo);
   }
-  gather_rows_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(vi, b.rows, cols_row, n_out, b.keys_b,
-                                                          order);
+  // ---- sort 3: full tiles by (region, slots used, descending), stable.  The
+  // row masks in keys_a are dead: it holds the tile keys, vo the tile ids.
+  const int64_t n_tiles = n_out / kConvTileRows;
+  const uint32_t* tile_perm = nullptr;
+  if (n_tiles > 1) {
+    const int64_t tiles_per_region =
+        region_rows >= kConvTileRows ? region_rows / kConvTileRows : 1;
+    tile_key_kernel<<<static_cast<unsigned>(n_tiles), kConvTileRows, 0, s>>>(
+        vi, b.mask_pos, tiles_per_region, b.keys_a, vo);
+    TSC_LAUNCH_CHECK("plan_tile_key");
+    const int key_bits = bits_for(static_cast<uint64_t>((n_tiles - 1) / tiles_per_region)) + 6;
+    uint32_t *tki = b.keys_a, *tko = b.keys_a + n_tiles, *tvi = vo, *tvo = vo + n_tiles;
+    for (int p = 0; p < (key_bits + 7) / 8; ++p) {
+      const Digits d{kFromKey, 8 * p, tki, nullptr, 1u};
+      if ((rc = radix_pass(b, tki, tvi, tko, tvo, n_tiles, d, s))) return rc;
+      std::swap(tki, tko);
+      std::swap(tvi, tvo);
+    }
+    tile_perm = tvi;
+  }
+  gather_rows_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(vi, b.rows, cols_row, n_out, tile_perm,
+                                                          n_tiles, b.keys_b, order);
   TSC_LAUNCH_CHECK("plan_gather");
   if (nbr_ordered) {
     // int4 accesses need 16-byte aligned rows of the map and of the order

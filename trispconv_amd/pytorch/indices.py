@@ -190,8 +190,10 @@ class IndiceData:
         """Processing order of the output rows for the fused convolution.
 
         Morton order cut into regions whose gathered input rows (``row_bytes``
-        each) fit in half the Infinity Cache, each region sorted by slot mask.
-        Built once per region size and cached; None for small layers.
+        each) fit in half the Infinity Cache, each region sorted by slot mask,
+        then its whole 256-row tiles put in decreasing number of slots used
+        (the partial tile last).  Built once per region size and cached; None
+        for small layers.
         """
         if n_out < _PLAN_MIN_ROWS:
             return None
