@@ -289,6 +289,11 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
   const uint64_t umask =
       (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(umask_v >> 32))) << 32) |
       __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(umask_v));
+  // the slots this wave's own rows use
+  const uint64_t wmask_v = s_mask[wave];
+  const uint64_t wmask =
+      (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(wmask_v >> 32))) << 32) |
+      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(wmask_v));
   const int r0 = wave * 64 + (lane & 31);  // tile rows of this lane's A operands
   const int r1 = r0 + 32;
 
@@ -360,13 +365,15 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
       ring[S][1][u] = p1[u];
     }
   };
-  // Every wave runs every stage of its tile: a stage lasts as long as its
-  // busiest wave anyway (the waves share the weight slab through LDS), and a
-  // body without branches keeps each stage one scheduling region.  Rows
-  // without input through the stage's slot (and bodies past the last stage)
-  // multiply the zero row and add exact zeros.
-  auto compute = [&](auto slot, const uint4* sw) {
+  // Every wave takes part in every stage of its tile (the waves share the
+  // weight slab through LDS), but it issues the stage's MFMAs only when one of
+  // its own rows has an input through the stage's slot: the matrix core then
+  // serves the other workgroup's wave on the same SIMD.  Inside a computed
+  // stage, rows without input through the slot multiply the zero row and add
+  // exact zeros, so skipping a stage leaves every finite result unchanged.
+  auto compute = [&](auto slot, const uint4* sw, int k) {
     constexpr int S = decltype(slot)::value;
+    if (k >= K || !((wmask >> k) & 1)) return;
 #pragma unroll
     for (int u = 0; u < UB; ++u) {
 #pragma unroll
@@ -406,11 +413,16 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
 
   // Two waves per SIMD (two workgroups per CU): while one wave waits for its
   // gathers or at the barrier, the other's MFMAs keep the matrix core busy.
+  // The next stage's loads are issued before this stage's MFMAs, the weights
+  // first (they are waited for before the barrier, the gathered operands only
+  // in the next stage); the scheduling barrier keeps the compiler from sinking
+  // the loads below the MFMAs.
   auto body = [&](auto slot) {
     constexpr int S = decltype(slot)::value;
     load_w(kn, cn);                           // next stage's weights
     load_a(Slot<(S + 1) % RING>{}, kn, cn);   // next stage's operands
-    compute(Slot<S>{}, s_w[S]);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(Slot<S>{}, s_w[S], kc);
     store_w(s_w[(S + 1) % RING]);
     __syncthreads();
     kc = kn;
