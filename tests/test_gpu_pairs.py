@@ -154,6 +154,32 @@ def test_subm_lookup_paths_with_duplicates(shape, what):
     _subm(idx, shape, B, (3, 1, 3), (1, 2, 1), f"{what} path, 3x1x3 dilated")
 
 
+def test_subm_bitmap_every_cell_occupied():
+    """A fully occupied grid whose x extent (37) is not a multiple of 32: every
+    lookup at the x borders, and every row of three cells that straddles two
+    bitmap words, is exercised; repeated rows on top take the duplicate path."""
+    shape, B = (5, 6, 37), 2
+    b, z, y, x = np.meshgrid(np.arange(B), np.arange(shape[0]), np.arange(shape[1]),
+                             np.arange(shape[2]), indexing="ij")
+    idx = np.stack([b, z, y, x], -1).reshape(-1, 4).astype(np.int32)
+    rng = np.random.default_rng(5)
+    idx = idx[rng.permutation(len(idx))]
+    _subm(idx, shape, B, 3, 1, "every cell occupied")
+    _subm(idx, shape, B, 3, (1, 1, 2), "every cell occupied, x dilation 2")
+    dup = np.concatenate([idx, idx[rng.choice(len(idx), 40)]])
+    _subm(dup[rng.permutation(len(dup))], shape, B, 3, 1, "every cell occupied, repeats")
+
+
+def test_subm_bitmap_long_scan():
+    """A bitmap of more than 2048 scan tiles (1024 words each): the tile sums
+    are scanned in a pass of their own before the ranks are applied."""
+    shape, B, n = (300, 512, 512), 1, 200_000
+    words = -(-B * shape[0] * shape[1] * shape[2] // 32)
+    assert -(-words // 1024) > 2048 and words <= 8 * n + (1 << 20)
+    idx = _clustered_with_duplicates(41, shape, B, n, 64, 0)
+    _subm(idx, shape, B, 3, 1, "long bitmap scan")
+
+
 def test_out_of_grid_coordinates_raise():
     idx = torch.tensor([[0, 1, 1, 1], [0, 9, 1, 1]], dtype=torch.int32, device=DEV)
     with pytest.raises(IndexError):

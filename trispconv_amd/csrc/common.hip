@@ -53,39 +53,6 @@ int fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hipStream_t
   return 0;
 }
 
-// ------------------------------------------------------------ block scan --
-// Inclusive scan across a wave with shuffles.
-__device__ __forceinline__ uint32_t wave_inclusive(uint32_t v) {
-  const int l = __lane_id();
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    uint32_t t = __shfl_up(v, d, kWave);
-    if (l >= d) v += t;
-  }
-  return v;
-}
-
-// Exclusive scan across the block (blockDim.x a multiple of 64, <= 1024).
-// Returns the thread's exclusive prefix; *block_total receives the sum.
-__device__ uint32_t block_exclusive(uint32_t v, uint32_t* s_wave, uint32_t* block_total) {
-  const int w = threadIdx.x / kWave;
-  const int nw = blockDim.x / kWave;
-  uint32_t inc = wave_inclusive(v);
-  if (__lane_id() == kWave - 1) s_wave[w] = inc;
-  __syncthreads();
-  if (w == 0) {
-    uint32_t t = __lane_id() < nw ? s_wave[__lane_id()] : 0u;
-    uint32_t ti = wave_inclusive(t);
-    if (__lane_id() < nw) s_wave[__lane_id()] = ti - t;  // exclusive wave offsets
-    if (__lane_id() == nw - 1) s_wave[32] = ti;
-  }
-  __syncthreads();
-  uint32_t res = s_wave[w] + inc - v;
-  *block_total = s_wave[32];
-  __syncthreads();
-  return res;
-}
-
 // ---------------------------------------------------- per-slot block scan --
 __global__ void __launch_bounds__(1024) scan_slot_blocks_kernel(const int32_t* __restrict__ cnt,
                                                                 int32_t* __restrict__ off,

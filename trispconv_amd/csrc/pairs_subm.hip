@@ -25,6 +25,8 @@
 // resolve to the later row, as the reference's table scatter leaves them.
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace tsc {
 namespace {
 
@@ -135,12 +137,32 @@ __global__ void __launch_bounds__(kRows) subm_probe_kernel(const int4* __restric
 }
 
 // ------------------------------------------------------------ bitmap path --
+// One 8-byte entry per 32 cells: x = occupancy bits, y = rank of the word's
+// first cell (occupied cells before it in (b,z,y,x) order), so a lookup is
+// one load.
+
+// Zeroes the bitmap and the counters (one launch for all of them).
+__global__ void __launch_bounds__(256) subm_init_kernel(uint4* __restrict__ wr2, int64_t n_pairs,
+                                                        int32_t* __restrict__ counts, int K,
+                                                        int32_t* __restrict__ n_extra) {
+  const int64_t i0 = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = i0; i < n_pairs; i += stride) wr2[i] = make_uint4(0u, 0u, 0u, 0u);
+  if (blockIdx.x == 0) {
+    for (int k = threadIdx.x; k < K + 2; k += blockDim.x)
+      counts[k] = k == K + 1 ? 1 : 0;  // counts[K + 1] = 1: columns in (b,z,y,x) order
+    if (threadIdx.x == 0) *n_extra = 0;
+  }
+}
+
 // Sets each row's cell bit; rows outside the grid only raise a status flag.
+// Also marks every column unassigned (the rank pass fills them in).
 __global__ void __launch_bounds__(256) subm_mark_kernel(const int4* __restrict__ coords, int64_t n,
-                                                        SubmGeom g, uint32_t* words,
-                                                        int32_t* status) {
+                                                        SubmGeom g, uint2* wr, int32_t* status,
+                                                        int32_t* __restrict__ cols_row) {
   const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (r >= n) return;
+  cols_row[r] = -1;
   const int4 c = coords[r];
   if (!in_grid(g, c.x, c.y, c.z, c.w)) {
     atomicOr(status, (c.x < 0 || c.x >= g.B) ? TSC_FLAG_BATCH_OUT_OF_RANGE
@@ -148,60 +170,141 @@ __global__ void __launch_bounds__(256) subm_mark_kernel(const int4* __restrict__
     return;
   }
   const uint32_t cell = cell_key(g, c.x, c.y, c.z, c.w);
-  atomicOr(&words[cell >> 5], 1u << (cell & 31));
+  atomicOr(&wr[cell >> 5].x, 1u << (cell & 31));
+}
+
+// Exclusive popcount scan of the bitmap words into their y fields.  A tile is
+// 1024 words (256 threads x 4); the reduce pass writes each tile's popcount,
+// the apply pass takes its tile's offset from those (summing them itself when
+// `pre` is null, else from `pre`, their exclusive scan) and writes the ranks.
+constexpr int kBmThreads = 256;
+constexpr int kBmTile = kBmThreads * 4;
+
+__global__ void __launch_bounds__(kBmThreads) bitmap_reduce_kernel(const uint4* __restrict__ wr2,
+                                                                   int64_t nw,
+                                                                   uint32_t* __restrict__ sums) {
+  __shared__ uint32_t s_wave[33];
+  const int64_t p = (blockIdx.x * (int64_t)kBmTile) / 2 + 2 * threadIdx.x;  // entry pairs
+  uint32_t acc = 0;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    if (2 * (p + j) < nw) {
+      const uint4 v = wr2[p + j];  // word pairs past nw are zero padding
+      acc += __popc(v.x) + __popc(v.z);
+    }
+  }
+  uint32_t tot;
+  block_exclusive(acc, s_wave, &tot);
+  if (threadIdx.x == 0) sums[blockIdx.x] = tot;
+}
+
+__global__ void __launch_bounds__(kBmThreads) bitmap_apply_kernel(uint4* __restrict__ wr2, int64_t nw,
+                                                                  const uint32_t* __restrict__ sums,
+                                                                  const uint32_t* __restrict__ pre,
+                                                                  int nsum,
+                                                                  int32_t* __restrict__ n_unique) {
+  __shared__ uint32_t s_wave[33];
+  uint32_t base;
+  if (pre) {
+    base = pre[blockIdx.x];
+  } else {
+    // this tile's offset, and on block 0 the total, from the tile sums
+    const int lim = blockIdx.x == 0 ? nsum : static_cast<int>(blockIdx.x);
+    uint32_t part = 0;
+    for (int i = threadIdx.x; i < lim; i += kBmThreads) part += sums[i];
+    uint32_t tot;
+    block_exclusive(part, s_wave, &tot);
+    base = blockIdx.x == 0 ? 0u : tot;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *n_unique = static_cast<int32_t>(tot);
+  }
+  const int64_t p = (blockIdx.x * (int64_t)kBmTile) / 2 + 2 * threadIdx.x;
+  uint4 v[2];
+  uint32_t c[4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    v[j] = 2 * (p + j) < nw ? wr2[p + j] : make_uint4(0u, 0u, 0u, 0u);
+    c[2 * j] = __popc(v[j].x);
+    c[2 * j + 1] = __popc(v[j].z);
+  }
+  uint32_t tot;
+  uint32_t run = base + block_exclusive(c[0] + c[1] + c[2] + c[3], s_wave, &tot);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    v[j].y = run;
+    run += c[2 * j];
+    v[j].w = run;
+    run += c[2 * j + 1];
+    if (2 * (p + j) < nw) wr2[p + j] = v[j];
+  }
 }
 
 // Rank of an occupied cell: occupied cells before it in (b,z,y,x) order.
-__device__ __forceinline__ uint32_t cell_rank(uint32_t word, uint32_t word_rank, uint32_t cell) {
-  return word_rank + __popc(word & ((1u << (cell & 31)) - 1u));
+__device__ __forceinline__ uint32_t cell_rank(uint2 e, uint32_t cell) {
+  return e.y + __popc(e.x & ((1u << (cell & 31)) - 1u));
 }
 
-// rank_row[rank of the row's cell] = the largest row with that cell.
+// cols_row[rank of the row's cell] = the largest row with that cell.  When
+// every row has a cell of its own (n_unique == n) the ranks are distinct and
+// plain stores do; otherwise repeated cells take the largest row by atomicMax
+// (cols_row starts at -1).
 __global__ void __launch_bounds__(256) subm_rank_kernel(const int4* __restrict__ coords, int64_t n,
-                                                        SubmGeom g,
-                                                        const uint32_t* __restrict__ words,
-                                                        const uint32_t* __restrict__ word_rank,
-                                                        int32_t* rank_row) {
+                                                        SubmGeom g, const uint2* __restrict__ wr,
+                                                        const int32_t* __restrict__ n_unique,
+                                                        int32_t* cols_row) {
   const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (r >= n) return;
+  const bool unique = *n_unique == n;
   const int4 c = coords[r];
   if (!in_grid(g, c.x, c.y, c.z, c.w)) return;
   const uint32_t cell = cell_key(g, c.x, c.y, c.z, c.w);
-  atomicMax(&rank_row[cell_rank(words[cell >> 5], word_rank[cell >> 5], cell)],
-            static_cast<int32_t>(r));
+  const uint32_t rank = cell_rank(wr[cell >> 5], cell);
+  if (unique)
+    cols_row[rank] = static_cast<int32_t>(r);
+  else
+    atomicMax(&cols_row[rank], static_cast<int32_t>(r));
 }
 
 // Columns of repeated coordinates: a row whose cell's last row is another
 // row gets a column after the n_unique cell columns (in no particular order;
-// the values computed for it do not depend on where it sits).
+// the values computed for it do not depend on where it sits).  Nothing to do
+// when every row has a cell of its own.
 __global__ void __launch_bounds__(256) subm_place_kernel(const int4* __restrict__ coords, int64_t n,
-                                                         SubmGeom g,
-                                                         const uint32_t* __restrict__ words,
-                                                         const uint32_t* __restrict__ word_rank,
+                                                         SubmGeom g, const uint2* __restrict__ wr,
                                                          const int32_t* __restrict__ n_unique,
                                                          int32_t* cols_row, int32_t* n_extra) {
   const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (r >= n) return;
+  const int32_t nu = *n_unique;
+  if (nu == n) return;
   const int4 c = coords[r];
   if (!in_grid(g, c.x, c.y, c.z, c.w)) return;
   const uint32_t cell = cell_key(g, c.x, c.y, c.z, c.w);
-  const uint32_t rank = cell_rank(words[cell >> 5], word_rank[cell >> 5], cell);
+  const uint32_t rank = cell_rank(wr[cell >> 5], cell);
   if (cols_row[rank] != static_cast<int32_t>(r)) {
-    const int32_t col = *n_unique + atomicAdd(n_extra, 1);
+    const int32_t col = nu + atomicAdd(n_extra, 1);
     cols_row[col] = static_cast<int32_t>(r);  // col < rows in the grid <= n
+  }
+}
+
+// Per-slot hit counting shared by the probes: per wave by ballot, per block
+// in LDS, then one atomic per block and slot.
+__device__ __forceinline__ void count_hit(int k, bool hit, int32_t* s_cnt, int32_t* counts) {
+  const uint64_t hits = __ballot(hit);
+  if (__lane_id() == 0 && hits) {
+    if (k < 64)
+      atomicAdd(&s_cnt[k], (int)__popcll(hits));
+    else
+      atomicAdd(&counts[k], (int)__popcll(hits));
   }
 }
 
 // One thread per map column (an occupied cell in rank order, or a repeated
 // row after them): the column gets its row's K neighbours.  Eight slots'
-// bitmap and prefix reads are in flight together, then their rank -> row
-// reads.  Hits are counted per slot: per wave by ballot, per block in LDS,
-// then one atomic per block and slot.
+// bitmap reads are in flight together, then their rank -> row reads.
 constexpr int kLook = 8;
 
 __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
-    const int4* __restrict__ coords, int64_t n, int K, SubmGeom g,
-    const uint32_t* __restrict__ words, const uint32_t* __restrict__ word_rank,
+    const int4* __restrict__ coords, int64_t n, int K, SubmGeom g, const uint2* __restrict__ wr,
     const int32_t* __restrict__ cols_row, const int32_t* __restrict__ n_unique,
     const int32_t* __restrict__ n_extra, int32_t* __restrict__ nbr, int32_t* __restrict__ counts) {
   __shared__ int32_t s_cnt[64];
@@ -212,7 +315,8 @@ __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
   const bool live = col < *n_unique + *n_extra;  // the other columns are empty
   const int4 c = live ? coords[cols_row[col]] : make_int4(0, 0, 0, 0);
   for (int k0 = 0; k0 < K; k0 += kLook) {
-    uint32_t cell[kLook], wv[kLook], wr[kLook];
+    uint32_t cell[kLook];
+    uint2 e[kLook];
     bool look[kLook];
 #pragma unroll
     for (int i = 0; i < kLook; ++i) {
@@ -224,15 +328,14 @@ __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
       const int x = c.w + (kx - g.ks.x / 2) * g.dil.x;
       look[i] = live && k < K && in_grid(g, c.x, z, y, x);
       cell[i] = look[i] ? cell_key(g, c.x, z, y, x) : 0u;
-      wv[i] = words[cell[i] >> 5];  // word 0 exists: unconditional reads
-      wr[i] = word_rank[cell[i] >> 5];
+      e[i] = wr[cell[i] >> 5];  // entry 0 exists: unconditional reads
     }
     int32_t jr[kLook];
 #pragma unroll
     for (int i = 0; i < kLook; ++i) {
-      const bool hit = look[i] && ((wv[i] >> (cell[i] & 31)) & 1u);
+      const bool hit = look[i] && ((e[i].x >> (cell[i] & 31)) & 1u);
       // a hit's rank is below n_unique <= n; a miss reads column 0
-      jr[i] = cols_row[hit ? cell_rank(wv[i], wr[i], cell[i]) : 0u];
+      jr[i] = cols_row[hit ? cell_rank(e[i], cell[i]) : 0u];
       if (!hit) jr[i] = -1;
     }
 #pragma unroll
@@ -240,12 +343,73 @@ __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
       const int k = k0 + i;
       if (k >= K) continue;
       if (col < n) nbr[(int64_t)k * n + col] = jr[i];
-      const uint64_t hits = __ballot(jr[i] >= 0);
-      if (__lane_id() == 0 && hits) {
-        if (k < 64)
-          atomicAdd(&s_cnt[k], (int)__popcll(hits));
-        else
-          atomicAdd(&counts[k], (int)__popcll(hits));
+      count_hit(k, jr[i] >= 0, s_cnt, counts);
+    }
+  }
+  __syncthreads();
+  if (t < K && t < 64 && s_cnt[t]) atomicAdd(&counts[t], s_cnt[t]);
+}
+
+// The same for kernels KX cells wide whose x extent (KX - 1) * dil.x + 1 is at
+// most 32 cells: the KX cells of one (kz, ky) row then lie in two consecutive
+// bitmap entries, so a row costs two 8-byte loads instead of KX.  All rows'
+// entries are loaded before any rank -> row read.
+template <int KX>
+__global__ void __launch_bounds__(256) subm_probe_rows_kernel(
+    const int4* __restrict__ coords, int64_t n, int K, SubmGeom g, const uint2* __restrict__ wr,
+    int64_t nw, const int32_t* __restrict__ cols_row, const int32_t* __restrict__ n_unique,
+    const int32_t* __restrict__ n_extra, int32_t* __restrict__ nbr, int32_t* __restrict__ counts) {
+  constexpr int kRowsAtOnce = 9;  // 3x3 rows of a 3x3x3 kernel in one round
+  __shared__ int32_t s_cnt[64];
+  const int t = threadIdx.x;
+  if (t < 64) s_cnt[t] = 0;
+  __syncthreads();
+  const int64_t col = blockIdx.x * (int64_t)blockDim.x + t;
+  const bool live = col < *n_unique + *n_extra;  // the other columns are empty
+  const int4 c = live ? coords[cols_row[col]] : make_int4(0, 0, 0, 0);
+  const int n_rows = g.ks.z * g.ks.y;
+  const int x_lo = c.w - (KX / 2) * g.dil.x;                 // the row's first cell
+  const int x_first = x_lo > 0 ? x_lo : 0;                   // first cell inside the grid
+  for (int q0 = 0; q0 < n_rows; q0 += kRowsAtOnce) {
+    uint32_t base[kRowsAtOnce];
+    bool row_ok[kRowsAtOnce];
+    uint2 e0[kRowsAtOnce], e1[kRowsAtOnce];
+#pragma unroll
+    for (int i = 0; i < kRowsAtOnce; ++i) {
+      const int q = q0 + i;
+      const int kz = q / g.ks.y, ky = q % g.ks.y;
+      const int z = c.y + (kz - g.ks.z / 2) * g.dil.z;
+      const int y = c.z + (ky - g.ks.y / 2) * g.dil.y;
+      row_ok[i] = live && q < n_rows && in_grid(g, c.x, z, y, x_first);
+      base[i] = row_ok[i] ? cell_key(g, c.x, z, y, x_first) : 0u;  // key of x_first
+      const uint32_t w0 = base[i] >> 5;
+      e0[i] = wr[w0];
+      e1[i] = wr[w0 + 1 < nw ? w0 + 1 : w0];
+    }
+    int32_t jr[kRowsAtOnce][KX];
+#pragma unroll
+    for (int i = 0; i < kRowsAtOnce; ++i) {
+#pragma unroll
+      for (int kx = 0; kx < KX; ++kx) {
+        const int x = x_lo + kx * g.dil.x;
+        const bool ok = row_ok[i] && x >= 0 && x < g.shape.x;
+        const uint32_t off = (base[i] & 31u) + static_cast<uint32_t>(x - x_first);  // < 64
+        const uint2 e = off < 32u ? e0[i] : e1[i];
+        const uint32_t b = off & 31u;
+        const bool hit = ok && ((e.x >> b) & 1u);
+        jr[i][kx] = cols_row[hit ? e.y + __popc(e.x & ((1u << b) - 1u)) : 0u];
+        if (!hit) jr[i][kx] = -1;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < kRowsAtOnce; ++i) {
+      const int q = q0 + i;
+      if (q >= n_rows) continue;
+#pragma unroll
+      for (int kx = 0; kx < KX; ++kx) {
+        const int k = q * KX + kx;
+        if (col < n) nbr[(int64_t)k * n + col] = jr[i][kx];
+        count_hit(k, jr[i][kx] >= 0, s_cnt, counts);
       }
     }
   }
@@ -350,9 +514,16 @@ static bool subm_use_bitmap(int64_t n, int64_t cells) {
 
 struct SubmWork {
   unsigned long long* table;
-  uint32_t *words, *word_rank, *scan_scratch;
+  uint2* wr;                            // bitmap entries (word, rank), even count
+  uint32_t *sums, *pre, *scan_scratch;  // bitmap scan: tile sums, their prefixes
   int32_t *n_unique, *n_extra, *blk_cnt, *blk_off;
 };
+
+// Bitmap scans of up to this many tiles let every apply block sum the tile
+// sums before it (one launch less); longer ones scan the sums first.
+constexpr int64_t kBmDirectTiles = 2048;
+
+static int64_t bitmap_words(int64_t cells) { return ceil_div(cells, 32); }
 
 static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, int64_t* used) {
   Carver c(ws);
@@ -360,10 +531,12 @@ static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, int64_t* u
   const int64_t nblk = ceil_div(m, kRows);
   SubmWork w{};
   if (subm_use_bitmap(n, cells)) {
-    const int64_t nw = ceil_div(cells, 32);
-    w.words = c.take<uint32_t>(nw);
-    w.word_rank = c.take<uint32_t>(nw);
-    w.scan_scratch = c.take<uint32_t>(scan_scratch_words(nw));
+    const int64_t nw = bitmap_words(cells);
+    const int64_t nsum = ceil_div(nw, kBmTile);
+    w.wr = c.take<uint2>(2 * ceil_div(nw, 2));
+    w.sums = c.take<uint32_t>(nsum);
+    w.pre = c.take<uint32_t>(nsum);
+    w.scan_scratch = c.take<uint32_t>(scan_scratch_words(nsum));
     w.n_unique = c.take<int32_t>(1);
     w.n_extra = c.take<int32_t>(1);
   } else {
@@ -416,36 +589,53 @@ extern "C" int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_si
               "subm: workspace too small");
   TSC_REQUIRE(counts != nullptr, "subm: counts is null");
 
-  int rc = fill_u32(reinterpret_cast<uint32_t*>(counts), K + 2, 0u, s);
-  if (rc) return rc;
-  if (n == 0) return 0;
+  int rc = 0;
+  if (n == 0) return fill_u32(reinterpret_cast<uint32_t*>(counts), K + 2, 0u, s);
   TSC_REQUIRE(coords && cols_row && nbr && ws, "subm: null pointer");
 
   const int nblk = static_cast<int>(ceil_div(n, kRows));
   const SubmWork w = subm_carve(ws, n, K, cells, nullptr);
   const int4* c4 = reinterpret_cast<const int4*>(coords);
-  if (w.words) {
-    // columns in (b,z,y,x) order: tell the caller
-    if ((rc = fill_u32(reinterpret_cast<uint32_t*>(counts + K + 1), 1, 1u, s))) return rc;
-    const int64_t nw = ceil_div(cells, 32);
+  if (w.wr) {
+    const int64_t nw = bitmap_words(cells);
+    const int64_t n_pairs = ceil_div(nw, 2);
+    const int64_t nsum = ceil_div(nw, kBmTile);
     SubmGeom g{batch_size, shape, ks, dil, 0u};
-    if ((rc = fill_u32(w.words, nw, 0u, s))) return rc;
-    if ((rc = fill_u32(reinterpret_cast<uint32_t*>(w.n_extra), 1, 0u, s))) return rc;
-    subm_mark_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.words, counts + K);
+    uint4* wr2 = reinterpret_cast<uint4*>(w.wr);
+    const int64_t init_blocks = std::min<int64_t>(ceil_div(n_pairs, 256), 4096);
+    subm_init_kernel<<<static_cast<unsigned>(init_blocks > 0 ? init_blocks : 1), 256, 0, s>>>(
+        wr2, n_pairs, counts, K, w.n_extra);
+    TSC_LAUNCH_CHECK("subm_init");
+    subm_mark_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, counts + K, cols_row);
     TSC_LAUNCH_CHECK("subm_mark");
-    if ((rc = exclusive_scan_u32(w.words, 0, nw, w.word_rank, w.n_unique, w.scan_scratch, s)))
-      return rc;
-    if ((rc = fill_u32(reinterpret_cast<uint32_t*>(cols_row), n, 0xffffffffu, s))) return rc;
-    subm_rank_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.words, w.word_rank, cols_row);
+    bitmap_reduce_kernel<<<static_cast<unsigned>(nsum), kBmThreads, 0, s>>>(wr2, nw, w.sums);
+    TSC_LAUNCH_CHECK("subm_bitmap_reduce");
+    const uint32_t* pre = nullptr;
+    if (nsum > kBmDirectTiles) {
+      if ((rc = exclusive_scan_u32(w.sums, 2, nsum, w.pre, w.n_unique, w.scan_scratch, s)))
+        return rc;
+      pre = w.pre;
+    }
+    bitmap_apply_kernel<<<static_cast<unsigned>(nsum), kBmThreads, 0, s>>>(
+        wr2, nw, w.sums, pre, static_cast<int>(std::min<int64_t>(nsum, kBmDirectTiles)),
+        w.n_unique);
+    TSC_LAUNCH_CHECK("subm_bitmap_apply");
+    subm_rank_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, cols_row);
     TSC_LAUNCH_CHECK("subm_rank");
-    subm_place_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.words, w.word_rank, w.n_unique,
-                                                       cols_row, w.n_extra);
+    subm_place_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, cols_row,
+                                                       w.n_extra);
     TSC_LAUNCH_CHECK("subm_place");
-    subm_probe_cols_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, K, g, w.words, w.word_rank,
-                                                            cols_row, w.n_unique, w.n_extra, nbr,
-                                                            counts);
-    TSC_LAUNCH_CHECK("subm_probe_cols");
+    if (ks.x == 3 && 2 * dil.x < 32) {
+      subm_probe_rows_kernel<3><<<ceil_div(n, 256), 256, 0, s>>>(
+          c4, n, K, g, w.wr, nw, cols_row, w.n_unique, w.n_extra, nbr, counts);
+      TSC_LAUNCH_CHECK("subm_probe_rows");
+    } else {
+      subm_probe_cols_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, K, g, w.wr, cols_row,
+                                                              w.n_unique, w.n_extra, nbr, counts);
+      TSC_LAUNCH_CHECK("subm_probe_cols");
+    }
   } else {
+    if ((rc = fill_u32(reinterpret_cast<uint32_t*>(counts), K + 2, 0u, s))) return rc;
     const int64_t cap = subm_capacity(n);
     SubmGeom g{batch_size, shape, ks, dil, static_cast<uint32_t>(cap - 1)};
     if (K > 64 &&
