@@ -5,6 +5,8 @@
     python -m trispconv_amd.profiling calib  <out_dir> --bytes N  [--kernel SUBSTR]
     python -m trispconv_amd.profiling traffic --fetch DIR --write DIR --trace DIR
             --kernel SUBSTR --calib-kernel SUBSTR --calib-bytes N [--algorithmic-bytes B]
+    python -m trispconv_amd.profiling table --fetch DIR --write DIR --trace DIR
+            --kernels SUB1,SUB2,... --calib-kernel SUBSTR --calib-bytes N [--algorithmic-bytes B]
 
 ``out_dir`` is a rocprofv3 ``-d`` directory written with ``--output-format
 csv``.  ``trace`` prints per-kernel call count and average / min / max /
@@ -14,7 +16,8 @@ counter value per byte for a copy kernel of known size (the FETCH_SIZE /
 WRITE_SIZE scale factor); ``traffic`` combines a FETCH_SIZE pass, a WRITE_SIZE
 pass (each holding one copy-like kernel that reads and writes N bytes) and a
 kernel trace into HBM bytes per launch of one kernel, scaled by what the
-counters read for the copy.
+counters read for the copy; ``table`` does the same for each kernel of a
+multi-kernel step (the pair build) and adds up the step.
 """
 from __future__ import annotations
 
@@ -110,11 +113,41 @@ def traffic(fetch_dir: Path, write_dir: Path, trace_dir: Path, kernel: str, cali
         print(f"hbm_gbs_at_avg_duration: {(fetch_b + write_b) / (avg_us * 1e3):.1f}")
 
 
+def _scales(fetch_dir: Path, write_dir: Path, calib_kernel: str, calib_bytes: int):
+    f_c, _ = _pmc(fetch_dir, calib_kernel)["FETCH_SIZE"]
+    w_c, _ = _pmc(write_dir, calib_kernel)["WRITE_SIZE"]
+    return f_c * 1024.0 / calib_bytes, w_c * 1024.0 / calib_bytes
+
+
+def table(fetch_dir: Path, write_dir: Path, trace_dir: Path, kernels, calib_kernel: str,
+          calib_bytes: int, algorithmic: float) -> None:
+    """Per-kernel HBM bytes and rate for the kernels of one step, and the step's
+    totals (kernel time only: launch gaps are not in the sum)."""
+    f_scale, w_scale = _scales(fetch_dir, write_dir, calib_kernel, calib_bytes)
+    print(f"calib: FETCH_SIZE {f_scale:.4f}, WRITE_SIZE {w_scale:.4f} counter KiB per KiB moved "
+          f"({calib_kernel}, {calib_bytes} bytes)")
+    print(f"{'kernel':28s} {'avg_us':>8} {'fetch_MB':>9} {'write_MB':>9} {'GB/s':>8}")
+    tot_us = tot_b = 0.0
+    for k in kernels:
+        f_k = _pmc(fetch_dir, k).get("FETCH_SIZE", (0.0, 0))[0]
+        w_k = _pmc(write_dir, k).get("WRITE_SIZE", (0.0, 0))[0]
+        fb, wb = f_k * 1024.0 / f_scale, w_k * 1024.0 / w_scale
+        us, _ = _avg_duration_us(trace_dir, k)
+        tot_us += us
+        tot_b += fb + wb
+        print(f"{k:28s} {us:8.2f} {fb / 1e6:9.2f} {wb / 1e6:9.2f} {(fb + wb) / (us * 1e3):8.1f}")
+    print(f"{'step (kernels only)':28s} {tot_us:8.2f} {tot_b / 1e6:19.2f} {tot_b / (tot_us * 1e3):8.1f}")
+    if algorithmic:
+        print(f"algorithmic_bytes: {algorithmic:.0f}  -> {algorithmic / (tot_us * 1e3):.1f} GB/s "
+              f"over the kernel time")
+
+
 def main(argv=None) -> None:
     ap = argparse.ArgumentParser()
-    ap.add_argument("mode", choices=["trace", "pmc", "calib", "traffic"])
+    ap.add_argument("mode", choices=["trace", "pmc", "calib", "traffic", "table"])
     ap.add_argument("out_dir", type=Path, nargs="?")
     ap.add_argument("--kernel", default="")
+    ap.add_argument("--kernels", default="")
     ap.add_argument("--bytes", type=int, default=0)
     ap.add_argument("--fetch", type=Path)
     ap.add_argument("--write", type=Path)
@@ -123,7 +156,10 @@ def main(argv=None) -> None:
     ap.add_argument("--calib-bytes", type=int, default=0)
     ap.add_argument("--algorithmic-bytes", type=float, default=0.0)
     a = ap.parse_args(argv)
-    if a.mode == "traffic":
+    if a.mode == "table":
+        table(a.fetch, a.write, a.trace, [k for k in a.kernels.split(",") if k], a.calib_kernel,
+              a.calib_bytes, a.algorithmic_bytes)
+    elif a.mode == "traffic":
         traffic(a.fetch, a.write, a.trace, a.kernel, a.calib_kernel, a.calib_bytes,
                 a.algorithmic_bytes)
     elif a.mode == "trace":
