@@ -1,6 +1,6 @@
 """Benchmark: the 128->128 fp16 SubMConv3d layer over 500k surface voxels.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--encoder]
 
 One step is one forward of the layer over the whole batch, with its indice
 pairs cached under its ``indice_key`` (as a network reuses them), inputs
@@ -12,7 +12,11 @@ they run on.  Prints ONE JSON line:
   cpu_baseline  the CPU oracle (a numpy port of the reference's CPU path)
                 timed on this host on the same workload
 Other workloads (``--workload``) are for exploration; the default is the one
-the headline metric is quoted on.
+the headline metric is quoted on.  ``--encoder`` times a multi-layer
+workload's whole network instead of its first layer: the VoxelNet-style
+encoder as a SparseSequential with an eval-mode BatchNorm1d + ReLU after every
+layer but the last (fused into the conv stores, and unfused for comparison),
+or the strided + inverse pair.
 """
 from __future__ import annotations
 
@@ -48,6 +52,8 @@ def parse():
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run one elementwise negation over this many MiB (a copy-like "
                          "kernel of known size to scale FETCH_SIZE / WRITE_SIZE counters by)")
+    ap.add_argument("--encoder", action="store_true",
+                    help="time the workload's whole network (all layers) instead of layer 0")
     ap.add_argument("--verbose", action="store_true")
     return ap.parse_args()
 
@@ -109,6 +115,9 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     w = workloads.make_workload(args.workload)
+    if args.encoder:
+        encoder_bench(args, w, dev)
+        return
     layer = w.layers[0]
     dt = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}[w.dtype]
     rng = np.random.default_rng(w.seed)
@@ -232,10 +241,7 @@ def main():
                            "frac": pb_bytes / (pair_ms * 1e6) / HBM_PEAK_GBS},
         "plan_ms": plan_ms,
         "conv_kernel_ms": kern_ms,
-        "roofline": {"bound": "mfma", "achieved": tflops, "peak": peak,
-                     "unit": unit, "frac": tflops / peak,
-                     "traffic": None, "algorithmic_bytes": alg_bytes,
-                     "kernel": "conv_mfma_kernel" if elem == 2 else "conv_valu_kernel"},
+        "roofline": roofline(layer, k_vol, tflops, peak, unit, alg_bytes, kern_ms),
     }
     traffic = measured_traffic(w.name, kern_ms)
     if traffic is not None:
@@ -245,6 +251,167 @@ def main():
         result["cpu_baseline"] = cpu_baseline(w, rounded(feats_np, dt), rounded(w_np, dt),
                                               rounded(b_np, dt), layer)
     print(json.dumps(result), flush=True)
+
+
+def build_network(w, dt, dev, rng):
+    """The workload's layers as one SparseSequential.  Each layer but the last
+    is followed by an eval-mode BatchNorm1d (random affine and running
+    statistics) and a ReLU when the workload is the VoxelNet-style encoder."""
+    import torch
+    import torch.nn as nn
+
+    import trispconv.pytorch as spconv
+    from trispconv_amd import workloads
+
+    mods = []
+    bn_relu = w.name.startswith("voxelnet")
+    for i, lay in enumerate(w.layers):
+        if lay["kind"] == "subm":
+            m = spconv.SubMConv3d(lay["c_in"], lay["c_out"], lay["kernel_size"],
+                                  dilation=lay["dilation"], indice_key=lay["indice_key"])
+        elif lay["kind"] == "strided":
+            m = spconv.SparseConv3d(lay["c_in"], lay["c_out"], lay["kernel_size"],
+                                    stride=lay["stride"], padding=lay["padding"],
+                                    dilation=lay["dilation"], indice_key=lay["indice_key"])
+        else:
+            m = spconv.SparseInverseConv3d(lay["c_in"], lay["c_out"], lay["kernel_size"],
+                                           indice_key=lay["indice_key"])
+        wk, bk = workloads.layer_params(rng, lay)
+        with torch.no_grad():
+            m.weight.copy_(torch.from_numpy(wk))
+            m.bias.copy_(torch.from_numpy(bk))
+        mods.append(m)
+        if bn_relu and i + 1 < len(w.layers):
+            bn = nn.BatchNorm1d(lay["c_out"])
+            with torch.no_grad():
+                bn.weight.copy_(torch.from_numpy(rng.uniform(0.5, 1.5, lay["c_out"])))
+                bn.bias.copy_(torch.from_numpy(rng.uniform(-0.2, 0.2, lay["c_out"])))
+                bn.running_mean.copy_(torch.from_numpy(rng.uniform(-0.1, 0.1, lay["c_out"])))
+                bn.running_var.copy_(torch.from_numpy(rng.uniform(0.5, 1.5, lay["c_out"])))
+            mods += [bn, nn.ReLU()]
+    return spconv.SparseSequential(*mods).to(dev).to(dt).eval()
+
+
+def encoder_bench(args, w, dev):
+    """The whole network of a multi-layer workload, three ways: pairs cached
+    with the BatchNorm/ReLU epilogues fused (value), pairs cached unfused, and
+    cold (a fresh tensor, so every layer builds its pairs and plan)."""
+    import torch
+
+    import trispconv.pytorch as spconv
+    from trispconv_amd import workloads
+
+    dt = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}[w.dtype]
+    rng = np.random.default_rng(w.seed)
+    feats = torch.from_numpy(workloads.features(rng, len(w.indices), w.layers[0]["c_in"]))
+    feats = feats.to(dev).to(dt)
+    idx = torch.from_numpy(w.indices).to(dev)
+    net = build_network(w, dt, dev, rng)
+    n_in = len(w.indices)
+    stream = torch.cuda.current_stream(dev)
+
+    def fresh():
+        return spconv.SparseConvTensor(feats, idx, list(w.spatial_shape), w.batch_size)
+
+    warm = fresh()
+
+    def timed(fn, steps, warmup):
+        with torch.no_grad():
+            for _ in range(warmup):
+                y = fn()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                y = fn()
+            torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / steps, y
+
+    net.fuse_epilogues = True
+    fused_ms, y = timed(lambda: net(warm), args.steps, args.warmup)
+    net.fuse_epilogues = False
+    unfused_ms, y_plain = timed(lambda: net(warm), args.steps, max(args.warmup // 4, 3))
+    net.fuse_epilogues = True
+    cold_steps = max(args.steps // 10, 5)
+    cold_ms, _ = timed(lambda: net(fresh()), cold_steps, 3)
+    rel = float((y.features.float() - y_plain.features.float()).abs().max()
+                / y_plain.features.float().abs().max().clamp_min(1e-30))
+
+    # per-layer conv time (pairs cached, fused epilogue), events on the stream
+    per_layer = []
+    flops_total = 0.0
+    with torch.no_grad():
+        x = warm
+        mods = list(net.children())
+        i = 0
+        while i < len(mods):
+            m = mods[i]
+            i += 1
+            if not isinstance(m, spconv.SparseConvolution):
+                continue
+            from trispconv_amd.pytorch.modules import _fusable
+            ep, used = _fusable(mods, i, m, x)
+            out = m.forward_with_epilogue(x, ep)
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            for _ in range(20):  # back to back: the layer's GPU time, launches overlapped
+                out = m.forward_with_epilogue(x, ep)
+            b.record(stream)
+            b.synchronize()
+            if m.inverse:
+                P = int(x.indice_dict[m.indice_key].pair_num.sum())
+            else:
+                P = int(out.indice_dict[m.indice_key].pair_num.sum()) if m.indice_key else 0
+            f = 2.0 * P * m.in_channels * m.out_channels
+            flops_total += f
+            ms = a.elapsed_time(b) / 20
+            per_layer.append({"layer": f"{'inverse' if m.inverse else 'subm' if m.subm else 'strided'}"
+                              f" {tuple(m.kernel_size)} {m.in_channels}->{m.out_channels}",
+                              "rows_out": int(out.features.shape[0]), "pairs": P, "ms": ms,
+                              "tflops": f / (ms * 1e-3) / 1e12,
+                              "epilogue": None if ep is None else
+                              ("bn+relu" if ep.scale is not None and ep.relu else
+                               "bn" if ep.scale is not None else "relu")})
+            x = out
+            i += used
+    result = {
+        "metric": "voxels/sec + effective TFLOP/s per SubMConv3d layer; indice-pair build ms",
+        "value": n_in / (fused_ms * 1e-3),
+        "unit": "voxels/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": fused_ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": DTYPE_TAG[w.dtype],
+        "data": "synthetic (seeded voxels, N(0,1) features, kaiming-uniform KRSC weights, "
+                "random BatchNorm affine and running statistics)",
+        "config": {"workload": f"{w.name} (whole network, {len(w.layers)} conv layers)",
+                   "voxels": n_in, "spatial_shape": list(w.spatial_shape), "batch": w.batch_size},
+        "network_ms_fused": fused_ms,
+        "network_ms_unfused": unfused_ms,
+        "network_ms_cold": cold_ms,
+        "fused_vs_unfused_rel_err": rel,
+        "tflops_effective": flops_total / (fused_ms * 1e-3) / 1e12,
+        "layers": per_layer,
+    }
+    print(json.dumps(result), flush=True)
+
+
+def roofline(layer, k_vol, tflops, peak, unit, alg_bytes, kern_ms):
+    """The conv kernel against its bound: MFMA peak on the matrix-core path
+    (C_in and C_out multiples of 32, K <= 64), else HBM bandwidth (the VALU
+    path serves narrow layers whose arithmetic is small)."""
+    if layer["c_in"] % 32 == 0 and layer["c_out"] % 32 == 0 and k_vol <= 64:
+        return {"bound": "mfma", "achieved": tflops, "peak": peak, "unit": unit,
+                "frac": tflops / peak, "traffic": None, "algorithmic_bytes": alg_bytes,
+                "kernel": "conv_mfma_kernel"}
+    gbs = alg_bytes / (kern_ms * 1e6)
+    return {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": gbs / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes": alg_bytes,
+            "kernel": "conv_valu_kernel"}
 
 
 def measured_traffic(workload: str, kern_ms: float):

@@ -1,0 +1,184 @@
+"""Convolution epilogue (eval-mode BatchNorm1d and ReLU folded into the store).
+
+The fused store computes relu((acc + bias) * scale + shift) in fp32 and rounds
+once; it is checked against the fp64 oracle of the same expression, with the
+tolerances of the convolution tests (max |out - ref| / max |ref|: 1e-5 fp32,
+1e-2 fp16/bf16).  A SparseSequential chain with fusion is checked against the
+same chain run module by module (which rounds the features between the
+layers), and the cases that must not fuse (a BatchNorm1d in training mode,
+modules with hooks) are checked to run unfused.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+
+import trispconv.pytorch as spconv
+from gpu_util import DEV, needs_gpu, oracle_rows, rel_err, rounded, say, to_np
+from oracle import conv as OC
+from oracle import pairs as OP
+from trispconv.pytorch import functional as Fn
+from trispconv.pytorch.indices import generate_subm_indice_pairs
+from trispconv.pytorch.weight import pack_weight
+from trispconv_amd.pytorch import modules as M
+
+pytestmark = [pytest.mark.gpu, needs_gpu]
+
+TOL = {torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 1e-2}
+
+
+def _cloud(seed, shape, n):
+    rng = np.random.default_rng(seed)
+    cells = rng.choice(shape[0] * shape[1] * shape[2], size=n, replace=False)
+    z, r = np.divmod(cells, shape[1] * shape[2])
+    y, x = np.divmod(r, shape[2])
+    return np.stack([np.zeros(n), z, y, x], 1).astype(np.int32)
+
+
+# MFMA shapes (f16, bf16, f32) and VALU shapes (narrow / ragged channels)
+CASES = [(128, 128, torch.float16), (64, 96, torch.bfloat16), (32, 64, torch.float32),
+         (16, 16, torch.float32), (4, 16, torch.float16), (24, 40, torch.bfloat16)]
+
+
+@pytest.mark.parametrize("c_in,c_out,dtype", CASES)
+@pytest.mark.parametrize("affine,relu", [(True, True), (False, True), (True, False)])
+def test_conv_epilogue_against_oracle(c_in, c_out, dtype, affine, relu):
+    shape = (24, 24, 24)
+    idx = _cloud(3, shape, 4000)
+    rng = np.random.default_rng(7)
+    feats = rng.standard_normal((len(idx), c_in)).astype(np.float32)
+    w = (rng.standard_normal((c_out, 3, 3, 3, c_in)) / np.sqrt(27 * c_in)).astype(np.float32)
+    bias = rng.uniform(-0.1, 0.1, c_out).astype(np.float32)
+    scale = rng.uniform(0.5, 2.0, c_out).astype(np.float32) if affine else None
+    shift = rng.uniform(-0.5, 0.5, c_out).astype(np.float32) if affine else None
+    say("epilogue:", c_in, "->", c_out, dtype, "affine", affine, "relu", relu)
+    x = torch.from_numpy(idx).to(DEV)
+    data = generate_subm_indice_pairs(x, shape, 1, 3)
+    wt = torch.from_numpy(w).to(DEV).to(dtype)
+    packed = pack_weight(wt, (3, 3, 3), c_in, c_out, dtype)
+    ep = Fn.Epilogue(torch.from_numpy(scale).to(DEV) if affine else None,
+                     torch.from_numpy(shift).to(DEV) if affine else None, relu)
+    out = Fn.sparse_conv_forward(torch.from_numpy(feats).to(DEV).to(dtype), packed,
+                                 torch.from_numpy(bias).to(DEV).to(dtype), data, len(idx), ep)
+    pr = OP.subm_pairs(idx, shape, 1, 3, 1)
+    w64 = OC.normalize_weight(rounded(w, dtype), (3, 3, 3), c_in, c_out)
+    ref = oracle_rows(rounded(feats, dtype), w64, rounded(bias, dtype), pr.pairs_in,
+                      pr.pairs_out, np.arange(len(idx)))
+    if affine:
+        ref = ref * scale.astype(np.float64) + shift.astype(np.float64)
+    if relu:
+        ref = np.maximum(ref, 0.0)
+    got = to_np(out)
+    err = rel_err(got, ref)
+    say("   rel err", err)
+    assert out.dtype == dtype and np.isfinite(got).all()
+    if relu:
+        assert (got >= 0).all()
+    assert err <= TOL[dtype]
+
+
+def test_epilogue_off_is_bitwise_the_plain_convolution():
+    """No scale and no ReLU: the same bits as the plain entry point."""
+    shape = (20, 20, 20)
+    idx = _cloud(5, shape, 3000)
+    x = torch.from_numpy(idx).to(DEV)
+    data = generate_subm_indice_pairs(x, shape, 1, 3)
+    torch.manual_seed(0)
+    for c_in, c_out, dtype in [(64, 64, torch.float16), (16, 8, torch.float32)]:
+        f = torch.randn(len(idx), c_in, device=DEV).to(dtype)
+        w = (torch.randn(c_out, 3, 3, 3, c_in, device=DEV) * 0.05).to(dtype)
+        b = (torch.randn(c_out, device=DEV) * 0.1).to(dtype)
+        packed = pack_weight(w, (3, 3, 3), c_in, c_out, dtype)
+        a = Fn.sparse_conv_forward(f, packed, b, data, len(idx))
+        # a ReLU-only epilogue equals clamping the plain result (one rounding
+        # of a non-negative or zeroed value)
+        r = Fn.sparse_conv_forward(f, packed, b, data, len(idx), Fn.Epilogue(None, None, True))
+        assert torch.equal(r, torch.clamp_min(a, 0)), (c_in, c_out, dtype)
+        # an identity affine map changes nothing
+        one = torch.ones(c_out, device=DEV)
+        zero = torch.zeros(c_out, device=DEV)
+        i = Fn.sparse_conv_forward(f, packed, b, data, len(idx), Fn.Epilogue(one, zero, False))
+        assert torch.equal(i, a), (c_in, c_out, dtype)
+
+
+def _bn(c, seed):
+    g = torch.Generator().manual_seed(seed)
+    bn = nn.BatchNorm1d(c)
+    with torch.no_grad():
+        bn.weight.copy_(torch.rand(c, generator=g) * 1.5 + 0.25)
+        bn.bias.copy_(torch.randn(c, generator=g) * 0.2)
+        bn.running_mean.copy_(torch.randn(c, generator=g) * 0.1)
+        bn.running_var.copy_(torch.rand(c, generator=g) * 0.5 + 0.5)
+    return bn
+
+
+def _chain(dtype):
+    torch.manual_seed(11)
+    net = spconv.SparseSequential(
+        spconv.SubMConv3d(16, 32, 3, indice_key="s0"), _bn(32, 1), nn.ReLU(),
+        spconv.SparseConv3d(32, 64, 3, stride=2, padding=1), _bn(64, 2), nn.ReLU(inplace=True),
+        spconv.SubMConv3d(64, 64, 3, indice_key="s1"), nn.ReLU(),
+        spconv.SubMConv3d(64, 32, 3, indice_key="s1"), _bn(32, 3),
+        spconv.SubMConv3d(32, 32, 3, indice_key="s1"))
+    return net.to(DEV).to(dtype).eval()
+
+
+def _input(dtype, n=6000, shape=(32, 32, 32)):
+    idx = _cloud(9, shape, n)
+    feats = torch.randn(n, 16, generator=torch.Generator().manual_seed(4))
+    return spconv.SparseConvTensor(feats.to(DEV).to(dtype), torch.from_numpy(idx).to(DEV),
+                                   list(shape), 1)
+
+
+def _record(monkeypatch):
+    seen = []
+    orig = M.SparseConvolution.forward_with_epilogue
+
+    def rec(self, x, ep):
+        seen.append(ep)
+        return orig(self, x, ep)
+
+    monkeypatch.setattr(M.SparseConvolution, "forward_with_epilogue", rec)
+    return seen
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_sequential_fusion_matches_module_by_module(dtype, monkeypatch):
+    net = _chain(dtype)
+    x = _input(dtype)
+    seen = _record(monkeypatch)
+    with torch.no_grad():
+        fused = net(x)
+    kinds = [None if e is None else (e.scale is not None, e.relu) for e in seen]
+    say("epilogues:", kinds)
+    assert kinds == [(True, True), (True, True), (False, True), (True, False), None]
+    net.fuse_epilogues = False
+    seen.clear()
+    with torch.no_grad():
+        plain = net(x)
+    assert all(e is None for e in seen)
+    assert torch.equal(fused.indices, plain.indices)
+    err = rel_err(to_np(fused.features), to_np(plain.features).astype(np.float64))
+    say("   fused vs module by module:", err)
+    # module by module rounds the features between conv, BatchNorm and ReLU
+    assert err <= TOL[dtype] * (1 if dtype == torch.float32 else 2)
+
+
+def test_training_batchnorm_and_hooks_are_not_fused(monkeypatch):
+    dtype = torch.float32
+    net = _chain(dtype)
+    x = _input(dtype)
+    seen = _record(monkeypatch)
+    net._modules["1"].train()  # batch statistics: cannot be folded
+    calls = []
+    net._modules["7"].register_forward_hook(lambda m, i, o: calls.append(1))  # hook on a ReLU
+    with torch.no_grad():
+        fused = net(x)
+    kinds = [None if e is None else (e.scale is not None, e.relu) for e in seen]
+    # conv0: BatchNorm in training mode -> unfused; conv2: its ReLU has a hook -> unfused
+    assert kinds == [None, (True, True), None, (True, False), None], kinds
+    assert calls == [1]
+    net.fuse_epilogues = False
+    with torch.no_grad():
+        plain = net(x)
+    assert rel_err(to_np(fused.features), to_np(plain.features).astype(np.float64)) <= 1e-5

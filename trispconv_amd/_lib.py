@@ -53,9 +53,11 @@ _SIGNATURES = {
     "tsc_pack_weight": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp]),
     "tsc_conv_forward": (ctypes.c_int, [_vp, _i32, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32,
                                         _i64, _i32, _i32, _vp, _vp]),
+    "tsc_conv_forward_ep": (ctypes.c_int, [_vp, _i32, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32,
+                                           _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp]),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lib: Optional[ctypes.CDLL] = None
 

@@ -210,4 +210,4 @@ int exclusive_scan_u32(const uint32_t* src, int kind, int64_t n, uint32_t* out, 
 }  // namespace tsc
 
 extern "C" const char* tsc_last_error(void) { return tsc::last_error(); }
-extern "C" int tsc_abi_version(void) { return 5; }
+extern "C" int tsc_abi_version(void) { return 6; }

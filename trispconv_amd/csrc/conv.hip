@@ -16,11 +16,16 @@
 // bitwise reproducible and independent of the tile order.
 //
 // Two code shapes share that structure:
-//   * mfma: f16/bf16 with C_in, C_out multiples of 32 and K <= 64 —
-//     v_mfma_f32_32x32x16_{f16,bf16}, 4 waves x (64 rows x BN cols) per tile.
-//   * valu: everything else (narrow or ragged channels, fp32) — one output row
-//     per lane and CO columns per thread, weights read with wave-uniform
+//   * mfma: f32/f16/bf16 with C_in, C_out multiples of 32 and K <= 64 —
+//     v_mfma_f32_32x32x16_{f16,bf16} or v_mfma_f32_32x32x2_f32, 4 waves x
+//     (64 rows x BN cols) per tile.
+//   * valu: everything else (narrow or ragged channels, K > 64) — one output
+//     row per lane and CO columns per thread, weights read with wave-uniform
 //     addresses, slots skipped when no lane of the wave needs them.
+//
+// The epilogue adds the bias and, when asked, a per-channel affine map and a
+// ReLU (an eval-mode BatchNorm1d and ReLU following the convolution in a
+// SparseSequential), all in fp32 before the one rounding.
 #include "common.hpp"
 
 #include <type_traits>
@@ -70,6 +75,23 @@ __device__ __forceinline__ float load_bias(const void* p, int dt, int64_t i) {
   const uint32_t bits = wide ? (lo | (hi << 16)) : (dt == TSC_BF16 ? lo << 16 : 0u);
   const float h = __half2float(__ushort_as_half(static_cast<unsigned short>(lo)));
   return dt == TSC_F16 ? h : __uint_as_float(bits);
+}
+
+// What happens to an output element after the slot sum: v = acc + bias[c];
+// with an affine map v = v * scale[c] + shift[c]; with relu v = max(v, 0)
+// (NaN stays NaN); then one rounding.
+struct Epilogue {
+  const void* bias;     // per output channel, bias_dt, or null
+  int bias_dt;
+  const float* scale;   // per output channel, with shift, or null
+  const float* shift;
+  int relu;
+};
+
+__device__ __forceinline__ float finish(float v, float scale, float shift, bool affine, bool relu) {
+  if (affine) v = fmaf(v, scale, shift);
+  if (relu) v = v < 0.f ? 0.f : v;
+  return v;
 }
 
 __device__ __forceinline__ float src_weight(const void* w, int dt, int layout, int K, int c_in,
@@ -126,7 +148,7 @@ __global__ void pack_mfma_kernel(const void* w, int w_dt, int layout, int K, int
 // ---------------------------------------------------------------- VALU --
 template <typename T, int CO>
 __global__ void __launch_bounds__(256) conv_valu_kernel(
-    const T* __restrict__ feat, int c_in, const float* __restrict__ W, const void* bias, int bias_dt,
+    const T* __restrict__ feat, int c_in, const float* __restrict__ W, Epilogue ep,
     const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int nbr_ordered,
     int64_t n_out, int K, int c_out, T* __restrict__ out) {
   const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
@@ -153,8 +175,11 @@ __global__ void __launch_bounds__(256) conv_valu_kernel(
   T* dst = out + o * c_out + co0;
 #pragma unroll
   for (int c = 0; c < CO; ++c) {
-    const float b = bias ? load_bias(bias, bias_dt, co0 + c) : 0.f;
-    dst[c] = from_f32<T>(acc[c] + b);
+    const float b = ep.bias ? load_bias(ep.bias, ep.bias_dt, co0 + c) : 0.f;
+    const bool affine = ep.scale != nullptr;
+    const float sc = affine ? ep.scale[co0 + c] : 1.f;
+    const float sh = affine ? ep.shift[co0 + c] : 0.f;
+    dst[c] = from_f32<T>(finish(acc[c] + b, sc, sh, affine, ep.relu != 0));
   }
 }
 
@@ -202,7 +227,7 @@ constexpr int mfma_stage_rows(int row_bytes) { return row_bytes <= 256 ? 32 : 16
 // four waves share one copy.  fp32 accumulators live in AGPRs.
 template <typename T, int BN, int CK>
 __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
-    const T* __restrict__ feat, int c_in, const T* __restrict__ W, const void* bias, int bias_dt,
+    const T* __restrict__ feat, int c_in, const T* __restrict__ W, Epilogue ep,
     const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int nbr_ordered,
     int64_t n_out, int K, int c_out, T* __restrict__ out) {
   using Op = MfmaOp<T>;
@@ -221,6 +246,8 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
   __shared__ __attribute__((aligned(16))) uint4 s_w[2][SLAB_VECS];
   __shared__ __attribute__((aligned(16))) int32_t s_orow[kTileRows];
   __shared__ float s_bias[BN];        // this column tile's bias in fp32 (0 without one)
+  __shared__ float s_scale[BN];       // its affine epilogue (1 and 0 without one)
+  __shared__ float s_shift[BN];
   __shared__ uint64_t s_mask[4];      // per wave: slots its rows use (K <= 64)
   extern __shared__ int32_t s_nbr[];  // [K][kTileRows]; output staging at the end
 
@@ -255,7 +282,12 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
     // column of the map holding this row: its processing position when the map
     // was permuted into the execution order (contiguous reads), else the row
     const int64_t src_row = orow >= 0 ? (nbr_ordered ? tr : orow) : 0;
-    if (t < BN) s_bias[t] = bias ? load_bias(bias, bias_dt, (int64_t)nbt * BN + t) : 0.f;
+    if (t < BN) {
+      const int64_t col = (int64_t)nbt * BN + t;
+      s_bias[t] = ep.bias ? load_bias(ep.bias, ep.bias_dt, col) : 0.f;
+      s_scale[t] = ep.scale ? ep.scale[col] : 1.f;
+      s_shift[t] = ep.scale ? ep.shift[col] : 0.f;
+    }
     uint64_t m = 0;
     for (int k0 = 0; k0 < K; k0 += 8) {
       int32_t jv[8];
@@ -434,7 +466,10 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
     body(Slot<1>{});
   }
 
-  // ---- epilogue: + bias, round once, store each output element once.
+  // ---- epilogue: + bias (and the affine map and ReLU when asked), round
+  // once, store each output element once.
+  const bool affine = ep.scale != nullptr;
+  const bool relu = ep.relu != 0;
   // Each wave transposes its accumulators through LDS, PR rows at a time, so
   // that lanes write 16-byte pieces of output rows instead of single
   // elements.  32x32 accumulator layout: register i of lane l holds row
@@ -458,7 +493,8 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
         for (int nb = 0; nb < NB; ++nb) {
           const int cl = nb * 32 + (lane & 31);
           *reinterpret_cast<T*>(stage + row * STRIDE + cl * (int)sizeof(T)) =
-              from_f32<T>(acc[rb][nb][i] + s_bias[cl]);
+              from_f32<T>(finish(acc[rb][nb][i] + s_bias[cl], s_scale[cl], s_shift[cl], affine,
+                                 relu));
         }
       }
     __syncthreads();
@@ -476,7 +512,7 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
 }
 
 template <typename T, int BN, int CK>
-int launch_mfma(const void* feat, int c_in, const void* W, const void* bias, int bias_dt,
+int launch_mfma(const void* feat, int c_in, const void* W, const Epilogue& ep,
                 const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
                 int c_out, void* out, hipStream_t s) {
   const int64_t items = ceil_div(n_out, kTileRows) * (c_out / BN);
@@ -489,14 +525,14 @@ int launch_mfma(const void* feat, int c_in, const void* W, const void* bias, int
   const size_t lds_out = (size_t)4 * mfma_stage_rows(row_bytes) * (row_bytes + 16);  // 4 waves
   const size_t lds = lds_nbr > lds_out ? lds_nbr : lds_out;
   conv_mfma_kernel<T, BN, CK><<<grid, 256, lds, s>>>(
-      static_cast<const T*>(feat), c_in, static_cast<const T*>(W), bias, bias_dt, nbr, order,
+      static_cast<const T*>(feat), c_in, static_cast<const T*>(W), ep, nbr, order,
       nbr_ordered, n_out, K, c_out, static_cast<T*>(out));
   TSC_LAUNCH_CHECK("conv_mfma");
   return 0;
 }
 
 template <typename T>
-int dispatch_mfma(const void* feat, int c_in, const void* W, const void* bias, int bias_dt,
+int dispatch_mfma(const void* feat, int c_in, const void* W, const Epilogue& ep,
                   const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
                   int c_out, void* out, hipStream_t s) {
   constexpr int dt = std::is_same<T, float>::value ? TSC_F32
@@ -504,7 +540,7 @@ int dispatch_mfma(const void* feat, int c_in, const void* W, const void* bias, i
   const int bn = pick_bn(c_out), ck = pick_ck(dt, c_in);
 #define TSC_MFMA_CASE(BN_, CK_)                                                              \
   if (bn == BN_ && ck == CK_)                                                                \
-    return launch_mfma<T, BN_, CK_>(feat, c_in, W, bias, bias_dt, nbr, order, nbr_ordered, \
+    return launch_mfma<T, BN_, CK_>(feat, c_in, W, ep, nbr, order, nbr_ordered,          \
                                     n_out, K, c_out, out, s);
   if constexpr (!std::is_same<T, float>::value) {
     TSC_MFMA_CASE(128, 64)
@@ -519,12 +555,12 @@ int dispatch_mfma(const void* feat, int c_in, const void* W, const void* bias, i
 }
 
 template <typename T, int CO>
-int launch_valu(const void* feat, int c_in, const void* W, const void* bias, int bias_dt,
+int launch_valu(const void* feat, int c_in, const void* W, const Epilogue& ep,
                 const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
                 int c_out, void* out, hipStream_t s) {
   dim3 grid(static_cast<unsigned>(ceil_div(n_out, 256)), static_cast<unsigned>(c_out / CO));
   conv_valu_kernel<T, CO><<<grid, 256, 0, s>>>(static_cast<const T*>(feat), c_in,
-                                               static_cast<const float*>(W), bias, bias_dt, nbr,
+                                               static_cast<const float*>(W), ep, nbr,
                                                order, nbr_ordered, n_out, K, c_out,
                                                static_cast<T*>(out));
   TSC_LAUNCH_CHECK("conv_valu");
@@ -532,12 +568,12 @@ int launch_valu(const void* feat, int c_in, const void* W, const void* bias, int
 }
 
 template <typename T>
-int dispatch_valu(const void* feat, int c_in, const void* W, const void* bias, int bias_dt,
+int dispatch_valu(const void* feat, int c_in, const void* W, const Epilogue& ep,
                   const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
                   int c_out, void* out, hipStream_t s) {
 #define TSC_VALU_CASE(CO_)                                                                   \
   if (c_out % CO_ == 0)                                                                      \
-    return launch_valu<T, CO_>(feat, c_in, W, bias, bias_dt, nbr, order, nbr_ordered, n_out, K, \
+    return launch_valu<T, CO_>(feat, c_in, W, ep, nbr, order, nbr_ordered, n_out, K,        \
                                c_out, out, s);
   TSC_VALU_CASE(32)
   TSC_VALU_CASE(16)
@@ -589,14 +625,14 @@ extern "C" int tsc_pack_weight(const void* w, int32_t w_dtype, int32_t layout, i
   return 0;
 }
 
-extern "C" int tsc_conv_forward(const void* feat, int32_t dtype, int64_t n_in, int32_t c_in,
-                                const void* packed_w, const void* bias, int32_t bias_dtype,
-                                const int32_t* nbr, const int32_t* order, int32_t nbr_ordered,
-                                int64_t n_out, int32_t k_vol, int32_t c_out, void* out,
-                                tsc_stream_t stream) {
-  hipStream_t s = static_cast<hipStream_t>(stream);
+static int conv_forward(const void* feat, int32_t dtype, int64_t n_in, int32_t c_in,
+                        const void* packed_w, const Epilogue& ep, const int32_t* nbr,
+                        const int32_t* order, int32_t nbr_ordered, int64_t n_out, int32_t k_vol,
+                        int32_t c_out, void* out, hipStream_t s) {
   TSC_REQUIRE(dtype_ok(dtype), "conv: unsupported dtype %d", dtype);
-  TSC_REQUIRE(!bias || dtype_ok(bias_dtype), "conv: unsupported bias dtype %d", bias_dtype);
+  TSC_REQUIRE(!ep.bias || dtype_ok(ep.bias_dt), "conv: unsupported bias dtype %d", ep.bias_dt);
+  TSC_REQUIRE((ep.scale == nullptr) == (ep.shift == nullptr),
+              "conv: scale and shift come together");
   TSC_REQUIRE(c_in > 0 && c_out > 0 && k_vol > 0, "conv: sizes must be positive");
   TSC_REQUIRE(n_out >= 0 && n_out < (int64_t(1) << 31) && n_in >= 0 && n_in < (int64_t(1) << 31),
               "conv: row counts out of range");
@@ -606,7 +642,7 @@ extern "C" int tsc_conv_forward(const void* feat, int32_t dtype, int64_t n_in, i
   if (n_out == 0) return 0;
   TSC_REQUIRE(packed_w && out && (feat || n_in == 0), "conv: null pointer");
   if (n_in == 0) {
-    // no inputs: every output is the bias alone
+    // no inputs: every output is the epilogue of zero
     TSC_REQUIRE(nbr != nullptr, "conv: empty input");
   }
   const Path path = pick_path(dtype, c_in, c_out, k_vol);
@@ -616,20 +652,41 @@ extern "C" int tsc_conv_forward(const void* feat, int32_t dtype, int64_t n_in, i
                     (reinterpret_cast<uintptr_t>(out) & 15) == 0,
                 "conv: feature, weight and output buffers must be 16-byte aligned");
     if (dtype == TSC_F32)
-      return dispatch_mfma<float>(feat, c_in, packed_w, bias, bias_dtype, nbr, order, nbr_ordered,
-                                  n_out, k_vol, c_out, out, s);
+      return dispatch_mfma<float>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out, k_vol,
+                                  c_out, out, s);
     if (dtype == TSC_F16)
-      return dispatch_mfma<__half>(feat, c_in, packed_w, bias, bias_dtype, nbr, order, nbr_ordered,
-                                   n_out, k_vol, c_out, out, s);
-    return dispatch_mfma<__hip_bfloat16>(feat, c_in, packed_w, bias, bias_dtype, nbr, order,
-                                         nbr_ordered, n_out, k_vol, c_out, out, s);
+      return dispatch_mfma<__half>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out, k_vol,
+                                   c_out, out, s);
+    return dispatch_mfma<__hip_bfloat16>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out,
+                                         k_vol, c_out, out, s);
   }
   if (dtype == TSC_F32)
-    return dispatch_valu<float>(feat, c_in, packed_w, bias, bias_dtype, nbr, order, nbr_ordered,
-                                n_out, k_vol, c_out, out, s);
+    return dispatch_valu<float>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out, k_vol,
+                                c_out, out, s);
   if (dtype == TSC_F16)
-    return dispatch_valu<__half>(feat, c_in, packed_w, bias, bias_dtype, nbr, order, nbr_ordered,
-                                 n_out, k_vol, c_out, out, s);
-  return dispatch_valu<__hip_bfloat16>(feat, c_in, packed_w, bias, bias_dtype, nbr, order,
-                                       nbr_ordered, n_out, k_vol, c_out, out, s);
+    return dispatch_valu<__half>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out, k_vol,
+                                 c_out, out, s);
+  return dispatch_valu<__hip_bfloat16>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out,
+                                       k_vol, c_out, out, s);
+}
+
+extern "C" int tsc_conv_forward(const void* feat, int32_t dtype, int64_t n_in, int32_t c_in,
+                                const void* packed_w, const void* bias, int32_t bias_dtype,
+                                const int32_t* nbr, const int32_t* order, int32_t nbr_ordered,
+                                int64_t n_out, int32_t k_vol, int32_t c_out, void* out,
+                                tsc_stream_t stream) {
+  const Epilogue ep{bias, bias_dtype, nullptr, nullptr, 0};
+  return conv_forward(feat, dtype, n_in, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out, k_vol,
+                      c_out, out, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tsc_conv_forward_ep(const void* feat, int32_t dtype, int64_t n_in, int32_t c_in,
+                                   const void* packed_w, const void* bias, int32_t bias_dtype,
+                                   const float* scale, const float* shift, int32_t relu,
+                                   const int32_t* nbr, const int32_t* order, int32_t nbr_ordered,
+                                   int64_t n_out, int32_t k_vol, int32_t c_out, void* out,
+                                   tsc_stream_t stream) {
+  const Epilogue ep{bias, bias_dtype, scale, shift, relu != 0 ? 1 : 0};
+  return conv_forward(feat, dtype, n_in, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out, k_vol,
+                      c_out, out, static_cast<hipStream_t>(stream));
 }

@@ -9,7 +9,7 @@ Triton kernel become ``tsc_conv_forward``.
 """
 from __future__ import annotations
 
-from typing import Optional, Union
+from typing import NamedTuple, Optional, Union
 
 import torch
 
@@ -18,9 +18,18 @@ from .indices import IndiceData
 from .weight import PackedWeight, pack_weight
 
 
+class Epilogue(NamedTuple):
+    """What follows the convolution inside its store: v = v * scale + shift per
+    output channel (an eval-mode BatchNorm1d, fp32 device tensors, both or
+    neither), then max(v, 0) when ``relu``."""
+    scale: Optional[torch.Tensor]
+    shift: Optional[torch.Tensor]
+    relu: bool
+
+
 def _run(features: torch.Tensor, packed: PackedWeight, bias: Optional[torch.Tensor],
          nbr: Optional[torch.Tensor], order: Optional[torch.Tensor], n_out: int,
-         nbr_ordered: bool = False) -> torch.Tensor:
+         nbr_ordered: bool = False, epilogue: Optional[Epilogue] = None) -> torch.Tensor:
     L.require_gpu(features, "sparse_conv_forward")
     feats = features.contiguous()
     if feats.data_ptr() % 16:
@@ -36,32 +45,51 @@ def _run(features: torch.Tensor, packed: PackedWeight, bias: Optional[torch.Tens
         if b.numel() != packed.c_out:
             raise ValueError(f"bias has {b.numel()} entries, expected {packed.c_out}")
     lib = L.lib()
-    L.check(lib.tsc_conv_forward(
+    b_ptr, b_code = L.ptr(b), (L.dtype_code(b.dtype) if b is not None else 0)
+    if epilogue is None or (epilogue.scale is None and not epilogue.relu):
+        L.check(lib.tsc_conv_forward(
+            feats.data_ptr(), L.dtype_code(feats.dtype), feats.shape[0], packed.c_in,
+            packed.data.data_ptr(), b_ptr, b_code, L.ptr(nbr), L.ptr(order), int(nbr_ordered),
+            n_out, packed.k_vol, packed.c_out, out.data_ptr(), L.stream_of(feats)),
+            "sparse_conv_forward")
+        return out
+    scale, shift = epilogue.scale, epilogue.shift
+    if (scale is None) != (shift is None):
+        raise ValueError("sparse_conv_forward: epilogue scale and shift come together")
+    for t in (scale, shift):
+        if t is not None and (t.dtype != torch.float32 or t.device != feats.device
+                              or t.numel() != packed.c_out or not t.is_contiguous()):
+            raise ValueError("sparse_conv_forward: epilogue scale/shift must be contiguous fp32 "
+                             f"tensors of {packed.c_out} entries on {feats.device}")
+    L.check(lib.tsc_conv_forward_ep(
         feats.data_ptr(), L.dtype_code(feats.dtype), feats.shape[0], packed.c_in,
-        packed.data.data_ptr(), L.ptr(b), L.dtype_code(b.dtype) if b is not None else 0,
+        packed.data.data_ptr(), b_ptr, b_code, L.ptr(scale), L.ptr(shift), int(epilogue.relu),
         L.ptr(nbr), L.ptr(order), int(nbr_ordered), n_out, packed.k_vol, packed.c_out,
-        out.data_ptr(),
-        L.stream_of(feats)), "sparse_conv_forward")
+        out.data_ptr(), L.stream_of(feats)), "sparse_conv_forward")
     return out
 
 
 def sparse_conv_forward(features: torch.Tensor, weight: Union[torch.Tensor, PackedWeight],
                         bias: Optional[torch.Tensor], indice_data: IndiceData,
-                        N_out: int) -> torch.Tensor:
-    """Sparse convolution forward; ``weight`` is (K, C_in, C_out) or a PackedWeight."""
+                        N_out: int, epilogue: Optional[Epilogue] = None) -> torch.Tensor:
+    """Sparse convolution forward; ``weight`` is (K, C_in, C_out) or a PackedWeight.
+
+    ``epilogue`` (not in the reference's signature; the modules pass it for a
+    SparseSequential chain) folds a following eval-mode BatchNorm1d and ReLU
+    into the store."""
     L.require_gpu(features, "sparse_conv_forward")
     if not isinstance(weight, PackedWeight):
         K, c_in, c_out = weight.shape
         weight = pack_weight(weight, (K, 1, 1), c_in, c_out, features.dtype)
     nbr, order, ordered = indice_data.conv_operands(N_out, features.device,
                                                     weight.c_in * features.element_size())
-    return _run(features, weight, bias, nbr, order, N_out, ordered)
+    return _run(features, weight, bias, nbr, order, N_out, ordered, epilogue)
 
 
 def dense_forward(features: torch.Tensor, weight: PackedWeight,
-                  bias: Optional[torch.Tensor]) -> torch.Tensor:
+                  bias: Optional[torch.Tensor], epilogue: Optional[Epilogue] = None) -> torch.Tensor:
     """features @ W[0] (+ bias) through the same kernel with the identity map.
 
     Used by the inverse 1x1x1 path (modules.py:162-173).
     """
-    return _run(features, weight, bias, None, None, features.shape[0])
+    return _run(features, weight, bias, None, None, features.shape[0], False, epilogue)

@@ -9,13 +9,14 @@ storage, version or the feature dtype changes.
 """
 from __future__ import annotations
 
+import weakref
 from collections import OrderedDict
-from typing import Optional, Union
+from typing import List, Optional, Tuple, Union
 
 import torch
 import torch.nn as nn
 
-from .functional import dense_forward, sparse_conv_forward
+from .functional import Epilogue, dense_forward, sparse_conv_forward
 from .indices import (IndiceData, _output_spatial_shape, _to3, generate_inverse_indice_pairs,
                       generate_strided_indice_pairs, generate_subm_indice_pairs)
 from .tensor import SparseConvTensor
@@ -79,11 +80,17 @@ class SparseConvolution(SparseModule):
 
     # ------------------------------------------------------------ forward
     def forward(self, x: SparseConvTensor) -> SparseConvTensor:
+        return self.forward_with_epilogue(x, None)
+
+    def forward_with_epilogue(self, x: SparseConvTensor,
+                              epilogue: Optional[Epilogue]) -> SparseConvTensor:
+        """forward() with the layers that follow it folded into the store
+        (SparseSequential passes an eval-mode BatchNorm1d and a ReLU here)."""
         if self.inverse:
-            return self._forward_inverse(x)
+            return self._forward_inverse(x, epilogue)
         if self.subm:
-            return self._forward_subm(x)
-        return self._forward_strided(x)
+            return self._forward_subm(x, epilogue)
+        return self._forward_strided(x, epilogue)
 
     def _get_or_compute_subm_indice(self, x: SparseConvTensor) -> IndiceData:
         # the cached entry is returned whatever its kind (modules.py:93-94)
@@ -105,23 +112,23 @@ class SparseConvolution(SparseModule):
             x.indice_dict[self.indice_key] = data
         return data
 
-    def _forward_subm(self, x: SparseConvTensor) -> SparseConvTensor:
+    def _forward_subm(self, x: SparseConvTensor, epilogue=None) -> SparseConvTensor:
         data = self._get_or_compute_subm_indice(x)
         n_out = len(data.out_indices)
         out = sparse_conv_forward(x.features, self._packed_weight(x.features.dtype), self.bias,
-                                  data, n_out)
+                                  data, n_out, epilogue)
         return SparseConvTensor(out, data.out_indices, x.spatial_shape, x.batch_size,
                                 indice_dict=x.indice_dict)
 
-    def _forward_strided(self, x: SparseConvTensor) -> SparseConvTensor:
+    def _forward_strided(self, x: SparseConvTensor, epilogue=None) -> SparseConvTensor:
         data = self._get_or_compute_strided_indice(x)
         n_out = len(data.out_indices)
         out = sparse_conv_forward(x.features, self._packed_weight(x.features.dtype), self.bias,
-                                  data, n_out)
+                                  data, n_out, epilogue)
         return SparseConvTensor(out, data.out_indices, list(data.output_spatial_shape),
                                 x.batch_size, indice_dict=x.indice_dict)
 
-    def _forward_inverse(self, x: SparseConvTensor) -> SparseConvTensor:
+    def _forward_inverse(self, x: SparseConvTensor, epilogue=None) -> SparseConvTensor:
         # modules.py:149-156
         if self.indice_key is None:
             raise ValueError("SparseInverseConv3d requires indice_key")
@@ -139,7 +146,7 @@ class SparseConvolution(SparseModule):
                 w0 = self._get_weight()[0:1]
                 packed = pack_weight(w0, (1, 1, 1), self.in_channels, self.out_channels,
                                      x.features.dtype)
-            out = dense_forward(x.features, packed, self.bias)
+            out = dense_forward(x.features, packed, self.bias, epilogue)
             return SparseConvTensor(out, x.indices, x.spatial_shape, x.batch_size,
                                     indice_dict=x.indice_dict)
         inv = fwd._inverse_cache
@@ -147,7 +154,7 @@ class SparseConvolution(SparseModule):
             inv = generate_inverse_indice_pairs(fwd)
             fwd._inverse_cache = inv
         n_out = len(inv.out_indices)
-        out = sparse_conv_forward(x.features, packed, self.bias, inv, n_out)
+        out = sparse_conv_forward(x.features, packed, self.bias, inv, n_out, epilogue)
         return SparseConvTensor(out, inv.out_indices, list(fwd.input_spatial_shape), x.batch_size,
                                 indice_dict=x.indice_dict)
 
@@ -182,8 +189,71 @@ class SparseInverseConv3d(SparseConvolution):
                          indice_key=indice_key, algo=algo)
 
 
+# eval-mode BatchNorm1d -> (scale, shift) in fp32 on the features' device,
+# rebuilt when a parameter or running statistic changes
+_BN_AFFINE: "weakref.WeakKeyDictionary[nn.Module, tuple]" = weakref.WeakKeyDictionary()
+
+
+def _bn_affine(bn: nn.BatchNorm1d, device) -> Tuple[torch.Tensor, torch.Tensor]:
+    """y = (x - mean) / sqrt(var + eps) * gamma + beta as y = x * scale + shift."""
+    parts = [bn.running_mean, bn.running_var, bn.weight, bn.bias]
+    key = (device, bn.eps) + tuple((id(t), t._version) if t is not None else None for t in parts)
+    hit = _BN_AFFINE.get(bn)
+    if hit is not None and hit[0] == key:
+        return hit[1], hit[2]
+    with torch.no_grad():
+        var = bn.running_var.detach().to(device=device, dtype=torch.float32)
+        mean = bn.running_mean.detach().to(device=device, dtype=torch.float32)
+        scale = torch.rsqrt(var + bn.eps)
+        if bn.weight is not None:
+            scale = scale * bn.weight.detach().to(device=device, dtype=torch.float32)
+        shift = -mean * scale
+        if bn.bias is not None:
+            shift = shift + bn.bias.detach().to(device=device, dtype=torch.float32)
+    scale, shift = scale.contiguous(), shift.contiguous()
+    _BN_AFFINE[bn] = (key, scale, shift)
+    return scale, shift
+
+
+def _plain(m: nn.Module) -> bool:
+    return not (m._forward_hooks or m._forward_pre_hooks)
+
+
+def _fusable(mods: List[nn.Module], i: int, conv: SparseConvolution,
+             x: SparseConvTensor) -> Tuple[Optional[Epilogue], int]:
+    """The epilogue that modules i, i+1 (an eval-mode BatchNorm1d over the
+    conv's channels, then a ReLU; either may be missing) amount to, and how
+    many modules it covers."""
+    if not (x.features.is_cuda and _plain(conv)):
+        return None, 0
+    scale = shift = None
+    used = 0
+    if i < len(mods):
+        bn = mods[i]
+        if (type(bn) is nn.BatchNorm1d and not bn.training and bn.track_running_stats
+                and bn.running_mean is not None and bn.num_features == conv.out_channels
+                and _plain(bn)):
+            scale, shift = _bn_affine(bn, x.features.device)
+            used = 1
+    relu = False
+    if i + used < len(mods):
+        r = mods[i + used]
+        if type(r) is nn.ReLU and _plain(r):
+            relu = True
+            used += 1
+    return (Epilogue(scale, shift, relu), used) if used else (None, 0)
+
+
 class SparseSequential(SparseModule):
-    """Sequential container; dense modules act on ``.features`` (modules.py:306-329)."""
+    """Sequential container; dense modules act on ``.features`` (modules.py:306-329).
+
+    On the GPU a convolution followed by an eval-mode BatchNorm1d and/or a
+    ReLU runs them inside its store (one pass over the output instead of
+    three); ``fuse_epilogues = False`` turns that off.  The result equals the
+    module-by-module one up to the rounding of the intermediate features.
+    """
+
+    fuse_epilogues = True
 
     def __init__(self, *args, **kwargs):
         super().__init__()
@@ -197,9 +267,19 @@ class SparseSequential(SparseModule):
             self.add_module(name, module)
 
     def forward(self, x: Union[SparseConvTensor, torch.Tensor]):
-        for module in self.children():
+        mods = list(self.children())
+        i = 0
+        while i < len(mods):
+            module = mods[i]
+            i += 1
             if isinstance(x, SparseConvTensor):
                 if isinstance(module, SparseModule):
+                    if self.fuse_epilogues and isinstance(module, SparseConvolution):
+                        ep, used = _fusable(mods, i, module, x)
+                        if used:
+                            x = module.forward_with_epilogue(x, ep)
+                            i += used
+                            continue
                     x = module(x)
                 else:
                     x = x.replace_feature(module(x.features))
