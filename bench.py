@@ -374,6 +374,30 @@ def encoder_bench(args, w, dev):
                                "bn" if ep.scale is not None else "relu")})
             x = out
             i += used
+    # the BEV handoff: the last tensor to a dense (B, C, D, H, W) volume, here
+    # and with the reference's three torch passes (tensor.py:72-99)
+    def dense_ref():
+        D, H, W = x.spatial_shape
+        grid = torch.zeros((x.batch_size, D, H, W, x.features.shape[1]), dtype=x.features.dtype,
+                           device=dev)
+        i = x.indices.long()
+        grid[i[:, 0], i[:, 1], i[:, 2], i[:, 3]] = x.features
+        return grid.permute(0, 4, 1, 2, 3).contiguous()
+
+    def ms_of(fn, reps=20):
+        fn()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            fn()
+        b.record(stream)
+        b.synchronize()
+        return a.elapsed_time(b) / reps
+
+    dense_ms = ms_of(lambda: x.dense())
+    dense_torch_ms = ms_of(dense_ref)
+    dense_ok = bool(torch.equal(x.dense(), dense_ref()))
     result = {
         "metric": "voxels/sec + effective TFLOP/s per SubMConv3d layer; indice-pair build ms",
         "value": n_in / (fused_ms * 1e-3),
@@ -396,6 +420,8 @@ def encoder_bench(args, w, dev):
         "fused_vs_unfused_rel_err": rel,
         "tflops_effective": flops_total / (fused_ms * 1e-3) / 1e12,
         "layers": per_layer,
+        "dense": {"shape": [x.batch_size, int(x.features.shape[1])] + list(x.spatial_shape),
+                  "ms": dense_ms, "torch_three_pass_ms": dense_torch_ms, "equal": dense_ok},
     }
     print(json.dumps(result), flush=True)
 

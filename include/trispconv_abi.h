@@ -200,6 +200,20 @@ TSC_API int tsc_conv_forward_ep(const void* feat, int32_t dtype, int64_t n_in, i
                                 int64_t n_out, int32_t k_vol, int32_t c_out, void* out,
                                 tsc_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Sparse -> dense.  Replaces SparseConvTensor.dense (trispconv/pytorch/
+ * tensor.py:72-99): writes out, zero-filled, of shape (B, C, D, H, W) when
+ * channels_first != 0 else (B, D, H, W, C), with row r's C features at its
+ * coordinate.  elem_bytes is the feature element size (2 or 4; the values are
+ * copied bit for bit).  A row whose coordinate lies outside [0,B) x [0,D) x
+ * [0,H) x [0,W) is not written and sets *status to 1 (device int32, the
+ * reference's range assertions).  out must be 16-byte aligned.
+ * ------------------------------------------------------------------------ */
+TSC_API int tsc_dense_scatter(const void* feat, int32_t elem_bytes, int64_t n, int32_t c,
+                              const int32_t* coords, int32_t batch_size,
+                              const int32_t spatial[3] /* host */, int32_t channels_first,
+                              void* out, int32_t* status, tsc_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -58,21 +58,12 @@ def test_features_setter_raises():
         x.features = torch.zeros(8, 4)
 
 
-def test_dense_shape_and_values():
+def test_dense_has_no_cpu_path():
+    """dense() runs on the GPU only (tensor.py:72-99 runs in
+    libtrispconv_hip.so); a CPU tensor fails loudly instead of falling back."""
     x = make_sparse(B=2, N=10, C=3, D=4, H=5, W=6)
-    idx = x.indices.clone()
-    idx[:5, 0] = 0
-    idx[5:, 0] = 1
-    x2 = spconv.SparseConvTensor(x.features, idx, [4, 5, 6], 2)
-    d = x2.dense()
-    assert d.shape == (2, 3, 4, 5, 6)
-    assert x2.dense(channels_first=False).shape == (2, 4, 5, 6, 3)
-    i = idx.long()
-    # last duplicate wins; check a row whose coordinate is unique
-    keys = ((i[:, 0] * 4 + i[:, 1]) * 5 + i[:, 2]) * 6 + i[:, 3]
-    uniq = [r for r in range(10) if (keys == keys[r]).sum() == 1]
-    r = uniq[0]
-    assert torch.equal(d[i[r, 0], :, i[r, 1], i[r, 2], i[r, 3]], x.features[r])
+    with pytest.raises(RuntimeError, match="CPU"):
+        x.dense()
 
 
 def test_find_indice_pair():

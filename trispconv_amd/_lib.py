@@ -55,6 +55,8 @@ _SIGNATURES = {
                                         _i64, _i32, _i32, _vp, _vp]),
     "tsc_conv_forward_ep": (ctypes.c_int, [_vp, _i32, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32,
                                            _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp]),
+    "tsc_dense_scatter": (ctypes.c_int, [_vp, _i32, _i64, _i32, _vp, _i32, c_i32p, _i32, _vp,
+                                         _vp, _vp]),
 }
 
 ABI_VERSION = 6

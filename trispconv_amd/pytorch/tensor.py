@@ -64,18 +64,25 @@ class SparseConvTensor:
     def dense(self, channels_first: bool = True) -> torch.Tensor:
         """Scatter into a dense (B, C, D, H, W) tensor, or (B, D, H, W, C).
 
-        Same result as tensor.py:72-99 (coordinates are range-checked first).
+        Same result as tensor.py:72-99, written once in its final layout by
+        tsc_dense_scatter; a coordinate out of range raises AssertionError, as
+        the reference's assertions do.
         """
-        B = self.batch_size
-        D, H, W = self.spatial_shape
+        from .. import _lib as L
         f = self._features
-        idx = self.indices.long()
-        lo = torch.zeros(4, dtype=torch.long, device=idx.device)
-        hi = torch.tensor([B, D, H, W], dtype=torch.long, device=idx.device)
-        if idx.numel():
-            assert bool(((idx >= lo) & (idx < hi)).all()), "coordinate out of range"
-        grid = torch.zeros((B, D, H, W, f.shape[1]), dtype=f.dtype, device=f.device)
-        grid[idx[:, 0], idx[:, 1], idx[:, 2], idx[:, 3]] = f
-        if not channels_first:
-            return grid
-        return grid.permute(0, 4, 1, 2, 3).contiguous()
+        L.require_gpu(f, "SparseConvTensor.dense")
+        B = int(self.batch_size)
+        D, H, W = (int(v) for v in self.spatial_shape)
+        C = f.shape[1]
+        shape = (B, C, D, H, W) if channels_first else (B, D, H, W, C)
+        out = torch.empty(shape, dtype=f.dtype, device=f.device)
+        feats = f.contiguous()
+        coords = self.indices.to(device=f.device, dtype=torch.int32).contiguous()
+        status = torch.empty(1, dtype=torch.int32, device=f.device)
+        L.check(L.lib().tsc_dense_scatter(feats.data_ptr(), feats.element_size(), feats.shape[0],
+                                          C, coords.data_ptr(), B, L.i3((D, H, W)),
+                                          int(bool(channels_first)), out.data_ptr(),
+                                          status.data_ptr(), L.stream_of(feats)),
+                "SparseConvTensor.dense")
+        assert int(status.item()) == 0, "coordinate out of range"
+        return out
