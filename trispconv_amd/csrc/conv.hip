@@ -146,11 +146,22 @@ __global__ void pack_mfma_kernel(const void* w, int w_dt, int layout, int K, int
 }
 
 // ---------------------------------------------------------------- VALU --
-template <typename T, int CO>
+// VB: bytes of one feature load (16 or 8 when every row is a whole number of
+// such vectors and the features are aligned to them, else one element).
+template <int VB> struct VecOf;
+template <> struct VecOf<16> { using type = uint4; };
+template <> struct VecOf<8> { using type = uint2; };
+template <> struct VecOf<4> { using type = uint32_t; };
+template <> struct VecOf<2> { using type = uint16_t; };
+
+template <typename T, int CO, int VB>
 __global__ void __launch_bounds__(256) conv_valu_kernel(
     const T* __restrict__ feat, int c_in, const float* __restrict__ W, Epilogue ep,
     const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int nbr_ordered,
     int64_t n_out, int K, int c_out, T* __restrict__ out) {
+  using Vec = typename VecOf<VB>::type;
+  constexpr int NV = VB / (int)sizeof(T);  // values per load
+  static_assert(NV >= 1 && NV * (int)sizeof(T) == VB, "vector of whole elements");
   const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   const int co0 = blockIdx.y * CO;
   const bool valid = t < n_out;
@@ -162,13 +173,19 @@ __global__ void __launch_bounds__(256) conv_valu_kernel(
     const int64_t col = nbr_ordered ? t : o;  // the map's column of this row
     const int32_t j = valid ? (nbr ? nbr[(int64_t)k * n_out + col] : static_cast<int32_t>(o)) : -1;
     if (__ballot(j >= 0) == 0ull) continue;  // no lane of the wave uses slot k
-    const T* x = feat + (int64_t)(j >= 0 ? j : 0) * c_in;
+    const Vec* x = reinterpret_cast<const Vec*>(feat + (int64_t)(j >= 0 ? j : 0) * c_in);
     const float* wk = W + (int64_t)k * c_in * c_out + co0;
-    for (int ci = 0; ci < c_in; ++ci) {
-      const float xv = j >= 0 ? to_f32<T>(x[ci]) : 0.f;
-      const float* wr = wk + (int64_t)ci * c_out;
+    for (int ci0 = 0; ci0 < c_in; ci0 += NV) {
+      Vec v{};
+      if (j >= 0) v = x[ci0 / NV];
+      const T* vals = reinterpret_cast<const T*>(&v);
 #pragma unroll
-      for (int c = 0; c < CO; ++c) acc[c] = fmaf(xv, wr[c], acc[c]);
+      for (int q = 0; q < NV; ++q) {
+        const float xv = to_f32<T>(vals[q]);
+        const float* wr = wk + (int64_t)(ci0 + q) * c_out;
+#pragma unroll
+        for (int c = 0; c < CO; ++c) acc[c] = fmaf(xv, wr[c], acc[c]);
+      }
     }
   }
   if (!valid) return;
@@ -559,10 +576,20 @@ int launch_valu(const void* feat, int c_in, const void* W, const Epilogue& ep,
                 const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
                 int c_out, void* out, hipStream_t s) {
   dim3 grid(static_cast<unsigned>(ceil_div(n_out, 256)), static_cast<unsigned>(c_out / CO));
-  conv_valu_kernel<T, CO><<<grid, 256, 0, s>>>(static_cast<const T*>(feat), c_in,
-                                               static_cast<const float*>(W), ep, nbr,
-                                               order, nbr_ordered, n_out, K, c_out,
-                                               static_cast<T*>(out));
+  const int row_bytes = c_in * (int)sizeof(T);
+  const uintptr_t a = reinterpret_cast<uintptr_t>(feat);
+#define TSC_VALU_LAUNCH(VB_)                                                                  \
+  conv_valu_kernel<T, CO, VB_><<<grid, 256, 0, s>>>(static_cast<const T*>(feat), c_in,       \
+                                                    static_cast<const float*>(W), ep, nbr,    \
+                                                    order, nbr_ordered, n_out, K, c_out,      \
+                                                    static_cast<T*>(out))
+  if (row_bytes % 16 == 0 && a % 16 == 0)
+    TSC_VALU_LAUNCH(16);
+  else if (row_bytes % 8 == 0 && a % 8 == 0)
+    TSC_VALU_LAUNCH(8);
+  else
+    TSC_VALU_LAUNCH(sizeof(T));
+#undef TSC_VALU_LAUNCH
   TSC_LAUNCH_CHECK("conv_valu");
   return 0;
 }
