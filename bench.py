@@ -428,9 +428,9 @@ def encoder_bench(args, w, dev):
 
 def roofline(layer, k_vol, tflops, peak, unit, alg_bytes, kern_ms):
     """The conv kernel against its bound: MFMA peak on the matrix-core path
-    (C_in and C_out multiples of 32, K <= 64), else HBM bandwidth (the VALU
-    path serves narrow layers whose arithmetic is small)."""
-    if layer["c_in"] % 32 == 0 and layer["c_out"] % 32 == 0 and k_vol <= 64:
+    (C_in a multiple of 16, C_out of 32, K <= 64), else HBM bandwidth (the
+    VALU path serves narrow layers whose arithmetic is small)."""
+    if layer["c_in"] % 16 == 0 and layer["c_out"] % 32 == 0 and k_vol <= 64:
         return {"bound": "mfma", "achieved": tflops, "peak": peak, "unit": unit,
                 "frac": tflops / peak, "traffic": None, "algorithmic_bytes": alg_bytes,
                 "kernel": "conv_mfma_kernel"}

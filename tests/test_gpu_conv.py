@@ -93,6 +93,9 @@ LAYER_CASES = [
     # fp32 on the matrix cores (v_mfma_f32_32x32x2_f32): every column tile width
     (32, 32, torch.float32), (128, 128, torch.float32), (64, 96, torch.float32),
     (96, 64, torch.float32),
+    # C_in an odd multiple of 16: the last 32-channel chunk is half padding
+    (16, 64, torch.float32), (48, 32, torch.bfloat16), (80, 96, torch.float16),
+    (16, 128, torch.bfloat16),
 ]
 
 

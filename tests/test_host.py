@@ -170,6 +170,9 @@ def test_workspace_queries_are_host_only():
     # MFMA-eligible layers pack 2-byte weights, others fp32
     assert lib.tsc_packed_weight_bytes(27, 128, 128, L.F16) == 27 * 128 * 128 * 2
     assert lib.tsc_packed_weight_bytes(27, 16, 16, L.F32) == 27 * 16 * 16 * 4
+    # C_in an odd multiple of 16 packs a 32-channel chunk whose upper half is zero
+    assert lib.tsc_packed_weight_bytes(27, 16, 32, L.F16) == 27 * 32 * 32 * 2
+    assert lib.tsc_packed_weight_bytes(27, 48, 64, L.F32) == 27 * 64 * 64 * 4
 
 
 def test_argument_errors_return_codes_without_gpu():

@@ -41,17 +41,19 @@ enum Path { kValu = 0, kMfma = 1 };
 
 // Input-channel chunk of one stage: 64 bytes of every gathered row per lane
 // half (64 channels of f16/bf16, 32 of f32), or half that when the channels
-// do not divide.
+// do not divide.  With C_in an odd multiple of 16 the last chunk's upper half
+// is padding: those lanes read the zero row and the packed weight holds zeros.
 int pick_ck(int dtype, int c_in) {
   if (dtype == TSC_F32) return 32;
   return c_in % 64 == 0 ? 64 : 32;
 }
 int pick_bn(int c_out) { return c_out % 128 == 0 ? 128 : (c_out % 64 == 0 ? 64 : 32); }
+int64_t mfma_chunks(int c_in, int ck) { return ceil_div(c_in, ck); }
 
-// MFMA for every dtype when both channel counts are multiples of 32 (the
+// MFMA for every dtype when C_in is a multiple of 16 and C_out of 32 (the
 // slot table of K <= 64 slots fits LDS); VALU otherwise.
 Path pick_path(int dtype, int c_in, int c_out, int K) {
-  if (c_in % 32 == 0 && c_out % 32 == 0 && K <= 64) return kMfma;
+  if (c_in % 16 == 0 && c_out % 32 == 0 && K <= 64) return kMfma;
   (void)dtype;
   return kValu;
 }
@@ -126,8 +128,8 @@ __global__ void pack_mfma_kernel(const void* w, int w_dt, int layout, int K, int
   constexpr int VPL = 16 / sizeof(T);  // values per 16-byte vector
   const int ub = (ck / 2) / VPL;      // vectors per lane per chunk
   const int nbt = c_out / 32;
-  const int nch = c_in / ck;
-  const int64_t total = (int64_t)K * c_in * c_out;
+  const int nch = (c_in + ck - 1) / ck;  // the last chunk may be half padding
+  const int64_t total = (int64_t)K * nch * ck * c_out;
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x) {
     const int i = e % VPL;
@@ -141,7 +143,8 @@ __global__ void pack_mfma_kernel(const void* w, int w_dt, int layout, int K, int
     const int k = r / nch;
     const int ci = c * ck + (lane >> 5) * (ck / 2) + u * VPL + i;
     const int co = nb * 32 + (lane & 31);
-    packed[e] = from_f32<T>(src_weight(w, w_dt, layout, K, c_in, c_out, k, ci, co));
+    packed[e] = from_f32<T>(ci < c_in ? src_weight(w, w_dt, layout, K, c_in, c_out, k, ci, co)
+                                      : 0.f);
   }
 }
 
@@ -287,7 +290,7 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
   }
   const int64_t tile0 = static_cast<int64_t>(item / ncol) * kTileRows;
   const int nbt = static_cast<int>(item % ncol);
-  const int nch = c_in / CK;
+  const int nch = (c_in + CK - 1) / CK;  // C_in % 16 == 0: the last chunk may be half padding
 
   // ---- tile set-up: output rows, their slot lists and slot masks.  The map
   // entries are read eight slots at a time, all eight loads in flight before
@@ -404,10 +407,13 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
     const int32_t j0 = live ? e0 : -1;
     const int32_t j1 = live ? e1 : -1;
     const int coff = c * CK + h * (CK / 2);
-    const uint4* p0 = j0 >= 0 ? reinterpret_cast<const uint4*>(feat + (int64_t)j0 * c_in + coff)
-                              : zero_row;
-    const uint4* p1 = j1 >= 0 ? reinterpret_cast<const uint4*>(feat + (int64_t)j1 * c_in + coff)
-                              : zero_row;
+    const bool pad = coff >= c_in;  // the upper half of a half-filled last chunk
+    const uint4* p0 = j0 >= 0 && !pad
+                          ? reinterpret_cast<const uint4*>(feat + (int64_t)j0 * c_in + coff)
+                          : zero_row;
+    const uint4* p1 = j1 >= 0 && !pad
+                          ? reinterpret_cast<const uint4*>(feat + (int64_t)j1 * c_in + coff)
+                          : zero_row;
 #pragma unroll
     for (int u = 0; u < UB; ++u) {
       ring[S][0][u] = p0[u];
@@ -554,7 +560,12 @@ int dispatch_mfma(const void* feat, int c_in, const void* W, const Epilogue& ep,
                   int c_out, void* out, hipStream_t s) {
   constexpr int dt = std::is_same<T, float>::value ? TSC_F32
                      : std::is_same<T, __half>::value ? TSC_F16 : TSC_BF16;
-  const int bn = pick_bn(c_out), ck = pick_ck(dt, c_in);
+  // Narrower column tiles for small layers: below two workgroups per CU,
+  // halve BN (each halving doubles the workgroups; gathers repeat per column
+  // tile, which a small layer can afford).
+  int bn = pick_bn(c_out);
+  const int ck = pick_ck(dt, c_in);
+  while (bn > 32 && ceil_div(n_out, kTileRows) * (c_out / bn) < 512) bn /= 2;
 #define TSC_MFMA_CASE(BN_, CK_)                                                              \
   if (bn == BN_ && ck == CK_)                                                                \
     return launch_mfma<T, BN_, CK_>(feat, c_in, W, ep, nbr, order, nbr_ordered,          \
@@ -619,8 +630,11 @@ using namespace tsc;
 
 extern "C" int64_t tsc_packed_weight_bytes(int32_t k_vol, int32_t c_in, int32_t c_out,
                                            int32_t dtype) {
-  const int64_t elems = (int64_t)k_vol * c_in * c_out;
-  return pick_path(dtype, c_in, c_out, k_vol) == kMfma ? elems * dtype_bytes(dtype) : elems * 4;
+  if (pick_path(dtype, c_in, c_out, k_vol) == kMfma) {
+    const int ck = pick_ck(dtype, c_in);
+    return (int64_t)k_vol * mfma_chunks(c_in, ck) * ck * c_out * dtype_bytes(dtype);
+  }
+  return (int64_t)k_vol * c_in * c_out * 4;
 }
 
 extern "C" int tsc_pack_weight(const void* w, int32_t w_dtype, int32_t layout, int32_t k_vol,
@@ -631,7 +645,7 @@ extern "C" int tsc_pack_weight(const void* w, int32_t w_dtype, int32_t layout, i
   TSC_REQUIRE(layout == 0 || layout == 1, "pack: layout must be 0 (KRSC) or 1 (flat)");
   TSC_REQUIRE(k_vol > 0 && c_in > 0 && c_out > 0, "pack: sizes must be positive");
   TSC_REQUIRE(w && packed, "pack: null pointer");
-  const int64_t total = (int64_t)k_vol * c_in * c_out;
+  const int64_t total = (int64_t)k_vol * (c_in + 32) * c_out;  // covers a padded chunk
   const int grid = static_cast<int>(ceil_div(total, 256) < 2048 ? ceil_div(total, 256) : 2048);
   if (pick_path(dtype, c_in, c_out, k_vol) == kMfma) {
     const int ck = pick_ck(dtype, c_in);
