@@ -207,6 +207,104 @@ int exclusive_scan_u32(const uint32_t* src, int kind, int64_t n, uint32_t* out, 
   return 0;
 }
 
+
+// ------------------------------------------------------ bitmap rank scan --
+// Exclusive popcount scan of the bitmap words into their y fields.  A tile is
+// 1024 words (256 threads x 4); the reduce pass writes each tile's popcount,
+// the apply pass takes its tile's offset from those (summing them itself when
+// `pre` is null, else from `pre`, their exclusive scan) and writes the ranks.
+constexpr int kBmThreads = 256;
+constexpr int kBmTile = kBmThreads * 4;
+
+__global__ void __launch_bounds__(kBmThreads) bitmap_reduce_kernel(const uint4* __restrict__ wr2,
+                                                                   int64_t nw,
+                                                                   uint32_t* __restrict__ sums) {
+  __shared__ uint32_t s_wave[33];
+  const int64_t p = (blockIdx.x * (int64_t)kBmTile) / 2 + 2 * threadIdx.x;  // entry pairs
+  uint32_t acc = 0;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    if (2 * (p + j) < nw) {
+      const uint4 v = wr2[p + j];  // word pairs past nw are zero padding
+      acc += __popc(v.x) + __popc(v.z);
+    }
+  }
+  uint32_t tot;
+  block_exclusive(acc, s_wave, &tot);
+  if (threadIdx.x == 0) sums[blockIdx.x] = tot;
+}
+
+__global__ void __launch_bounds__(kBmThreads) bitmap_apply_kernel(uint4* __restrict__ wr2, int64_t nw,
+                                                                  const uint32_t* __restrict__ sums,
+                                                                  const uint32_t* __restrict__ pre,
+                                                                  int nsum,
+                                                                  int32_t* __restrict__ n_unique) {
+  __shared__ uint32_t s_wave[33];
+  uint32_t base;
+  if (pre) {
+    base = pre[blockIdx.x];
+  } else {
+    // this tile's offset, and on block 0 the total, from the tile sums
+    const int lim = blockIdx.x == 0 ? nsum : static_cast<int>(blockIdx.x);
+    uint32_t part = 0;
+    for (int i = threadIdx.x; i < lim; i += kBmThreads) part += sums[i];
+    uint32_t tot;
+    block_exclusive(part, s_wave, &tot);
+    base = blockIdx.x == 0 ? 0u : tot;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *n_unique = static_cast<int32_t>(tot);
+  }
+  const int64_t p = (blockIdx.x * (int64_t)kBmTile) / 2 + 2 * threadIdx.x;
+  uint4 v[2];
+  uint32_t c[4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    v[j] = 2 * (p + j) < nw ? wr2[p + j] : make_uint4(0u, 0u, 0u, 0u);
+    c[2 * j] = __popc(v[j].x);
+    c[2 * j + 1] = __popc(v[j].z);
+  }
+  uint32_t tot;
+  uint32_t run = base + block_exclusive(c[0] + c[1] + c[2] + c[3], s_wave, &tot);
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    v[j].y = run;
+    run += c[2 * j];
+    v[j].w = run;
+    run += c[2 * j + 1];
+    if (2 * (p + j) < nw) wr2[p + j] = v[j];
+  }
+}
+
+// Bitmap scans of up to this many tiles let every apply block sum the tile
+// sums before it (one launch less); longer ones scan the sums first.
+constexpr int64_t kBmDirectTiles = 2048;
+
+int64_t bitmap_entries(int64_t nw) { return 2 * ceil_div(nw > 0 ? nw : 1, 2); }
+
+int64_t bitmap_scan_scratch_words(int64_t nw) {
+  const int64_t nsum = ceil_div(nw > 0 ? nw : 1, kBmTile);
+  return 2 * nsum + scan_scratch_words(nsum);
+}
+
+int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStream_t s) {
+  const int64_t nsum = ceil_div(nw > 0 ? nw : 1, kBmTile);
+  uint32_t* sums = scratch;
+  uint32_t* pre = scratch + nsum;
+  uint32_t* more = scratch + 2 * nsum;
+  uint4* wr2 = reinterpret_cast<uint4*>(wr);
+  bitmap_reduce_kernel<<<static_cast<unsigned>(nsum), kBmThreads, 0, s>>>(wr2, nw, sums);
+  TSC_LAUNCH_CHECK("bitmap_reduce");
+  const uint32_t* p = nullptr;
+  if (nsum > kBmDirectTiles) {
+    int rc = exclusive_scan_u32(sums, 2, nsum, pre, total, more, s);
+    if (rc) return rc;
+    p = pre;
+  }
+  bitmap_apply_kernel<<<static_cast<unsigned>(nsum), kBmThreads, 0, s>>>(
+      wr2, nw, sums, p, static_cast<int>(nsum < kBmDirectTiles ? nsum : kBmDirectTiles), total);
+  TSC_LAUNCH_CHECK("bitmap_apply");
+  return 0;
+}
+
 }  // namespace tsc
 
 extern "C" const char* tsc_last_error(void) { return tsc::last_error(); }

@@ -191,6 +191,15 @@ int scan_slot_blocks(const int32_t* cnt, int32_t* off, int32_t* totals, int K, i
 // out[i] receives the prefix, *total the sum (device pointer, may be null).
 // Scratch: scan_scratch_words(n) uint32 words.
 int64_t scan_scratch_words(int64_t n);
+
+// Occupancy bitmaps with ranks: one 8-byte entry per 32 cells, x = the cells'
+// bits, y = the number of set bits in all earlier entries (the rank of the
+// entry's first cell), so a rank lookup is one load.  The entry count is
+// rounded up to even (entries are processed in pairs; the pad entry is zero).
+// bitmap_scan fills every y from the x fields and writes the total to *total.
+int64_t bitmap_entries(int64_t nw);
+int64_t bitmap_scan_scratch_words(int64_t nw);
+int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStream_t s);
 int exclusive_scan_u32(const uint32_t* src, int kind, int64_t n, uint32_t* out, int32_t* total,
                        uint32_t* scratch, hipStream_t s);
 

@@ -43,9 +43,57 @@ __device__ __forceinline__ int64_t candidate(const StridedGeom& g, const int4& c
   return ((static_cast<int64_t>(c.x) * g.out.z + oz) * g.out.y + oy) * g.out.x + ox;
 }
 
+// The slots' candidate cells of one input row.  KZ/KY/KX > 0: the kernel
+// shape is known at compile time, each axis's candidate output coordinates
+// are computed once (KZ + KY + KX divisions instead of 3 per slot) and every
+// slot index is a constant; 0: runtime shape, one candidate() per slot.
+template <int KZ, int KY, int KX>
+struct Cands {
+  static constexpr int K = KZ * KY * KX;
+  int oz[KZ], oy[KY], ox[KX];
+  int b;
+  bool ok;
+  __device__ __forceinline__ Cands(const StridedGeom& g, const int4& c, bool valid) {
+    b = c.x;
+    ok = valid;
+#pragma unroll
+    for (int a = 0; a < KZ; ++a) oz[a] = axis(c.y + g.pad.z - a * g.dil.z, g.st.z, g.out.z);
+#pragma unroll
+    for (int a = 0; a < KY; ++a) oy[a] = axis(c.z + g.pad.y - a * g.dil.y, g.st.y, g.out.y);
+#pragma unroll
+    for (int a = 0; a < KX; ++a) ox[a] = axis(c.w + g.pad.x - a * g.dil.x, g.st.x, g.out.x);
+  }
+  static __device__ __forceinline__ int axis(int v, int st, int out) {
+    if (v < 0 || v % st) return -1;
+    const int q = v / st;
+    return q < out ? q : -1;
+  }
+  // slot k = (kz*KY + ky)*KX + kx with k a compile-time constant after unrolling
+  __device__ __forceinline__ int64_t cell(const StridedGeom& g, int k) const {
+    const int kz = k / (KY * KX), ky = (k / KX) % KY, kx = k % KX;
+    if (!ok || oz[kz] < 0 || oy[ky] < 0 || ox[kx] < 0) return -1;
+    return ((static_cast<int64_t>(b) * g.out.z + oz[kz]) * g.out.y + oy[ky]) * g.out.x + ox[kx];
+  }
+};
+
+template <>
+struct Cands<0, 0, 0> {
+  int4 c;
+  bool ok;
+  __device__ __forceinline__ Cands(const StridedGeom&, const int4& c_, bool valid)
+      : c(c_), ok(valid) {}
+  __device__ __forceinline__ int64_t cell(const StridedGeom& g, int k) const {
+    if (!ok) return -1;
+    int kz, ky, kx;
+    slot_to_zyx(k, g.ks, kz, ky, kx);
+    return candidate(g, c, kz, ky, kx);
+  }
+};
+
+template <int KZ, int KY, int KX>
 __global__ void __launch_bounds__(kRows) strided_mark_kernel(const int4* __restrict__ coords,
                                                              int64_t n, int K, StridedGeom g,
-                                                             uint32_t* bitmap,
+                                                             uint2* wr,
                                                              int32_t* __restrict__ blk_cnt,
                                                              int nblk, int32_t* status) {
   __shared__ int32_t s_cnt[kRows / kWave][64];
@@ -53,14 +101,15 @@ __global__ void __launch_bounds__(kRows) strided_mark_kernel(const int4* __restr
   const int w = t / kWave;
   const int64_t i = blockIdx.x * (int64_t)kRows + t;
   const bool valid = i < n;
-  int4 c = valid ? coords[i] : make_int4(-1, 0, 0, 0);
-  bool ok = valid && c.x >= 0 && c.x < g.B;
+  const int4 c = valid ? coords[i] : make_int4(-1, 0, 0, 0);
+  const bool ok = valid && c.x >= 0 && c.x < g.B;
   if (valid && !ok) atomicOr(status, TSC_FLAG_BATCH_OUT_OF_RANGE);
-  for (int k = 0; k < K; ++k) {
-    int kz, ky, kx;
-    slot_to_zyx(k, g.ks, kz, ky, kx);
-    const int64_t cell = ok ? candidate(g, c, kz, ky, kx) : -1;
-    if (cell >= 0) atomicOr(&bitmap[cell >> 5], 1u << (cell & 31));
+  const Cands<KZ, KY, KX> cand(g, c, ok);
+  constexpr int KC = KZ * KY * KX;
+#pragma unroll
+  for (int k = 0; k < (KC ? KC : K); ++k) {
+    const int64_t cell = cand.cell(g, k);
+    if (cell >= 0) atomicOr(&wr[cell >> 5].x, 1u << (cell & 31));
     const uint64_t hits = __ballot(cell >= 0);
     if (__lane_id() == 0) {
       if (k < 64)
@@ -71,24 +120,24 @@ __global__ void __launch_bounds__(kRows) strided_mark_kernel(const int4* __restr
   }
   __syncthreads();
   if (t < K && t < 64) {
-    int s = 0;
+    int sum = 0;
 #pragma unroll
-    for (int ww = 0; ww < kRows / kWave; ++ww) s += s_cnt[ww][t];
-    blk_cnt[(int64_t)t * nblk + blockIdx.x] = s;
+    for (int ww = 0; ww < kRows / kWave; ++ww) sum += s_cnt[ww][t];
+    blk_cnt[(int64_t)t * nblk + blockIdx.x] = sum;
   }
 }
 
-// One thread per bitmap word: decode every set bit, in ascending order, into
-// its (b, z, y, x) row at the word's prefix rank.
-__global__ void __launch_bounds__(256) strided_emit_kernel(const uint32_t* __restrict__ bitmap,
-                                                           const uint32_t* __restrict__ wprefix,
+// One thread per bitmap entry: decode every set bit, in ascending order, into
+// its (b, z, y, x) row at the entry's rank.
+__global__ void __launch_bounds__(256) strided_emit_kernel(const uint2* __restrict__ wr,
                                                            int64_t nwords, StridedGeom g,
                                                            int4* __restrict__ out_coords,
                                                            int64_t n_out) {
   const int64_t wi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (wi >= nwords) return;
-  uint32_t bits = bitmap[wi];
-  uint32_t rank = wprefix[wi];
+  const uint2 e = wr[wi];
+  uint32_t bits = e.x;
+  uint32_t rank = e.y;
   const int64_t plane = (int64_t)g.out.y * g.out.x;
   const int64_t vol = plane * g.out.z;
   while (bits) {
@@ -106,10 +155,13 @@ __global__ void __launch_bounds__(256) strided_emit_kernel(const uint32_t* __res
   }
 }
 
+// Pair lists in ascending input row per slot (block offsets from the per-slot
+// scan, wave offsets from per-wave counts, lanes ranked by ballot) and the
+// output-major map.  Slots are taken 64 at a time (one LDS count row each).
+template <int KZ, int KY, int KX>
 __global__ void __launch_bounds__(kRows) strided_fill_kernel(const int4* __restrict__ coords,
                                                              int64_t n, int K, StridedGeom g,
-                                                             const uint32_t* __restrict__ bitmap,
-                                                             const uint32_t* __restrict__ wprefix,
+                                                             const uint2* __restrict__ wr,
                                                              const int32_t* __restrict__ blk_off,
                                                              int nblk, int64_t cap, int64_t n_out,
                                                              int32_t* __restrict__ nbr,
@@ -120,30 +172,32 @@ __global__ void __launch_bounds__(kRows) strided_fill_kernel(const int4* __restr
   const int w = t / kWave;
   const int64_t i = blockIdx.x * (int64_t)kRows + t;
   const bool valid = i < n;
-  int4 c = valid ? coords[i] : make_int4(-1, 0, 0, 0);
+  const int4 c = valid ? coords[i] : make_int4(-1, 0, 0, 0);
   const bool ok = valid && c.x >= 0 && c.x < g.B;
-  for (int kb = 0; kb < K; kb += 64) {
-    const int kend = (K - kb) < 64 ? (K - kb) : 64;
-    for (int kk = 0; kk < kend; ++kk) {
-      int kz, ky, kx;
-      slot_to_zyx(kb + kk, g.ks, kz, ky, kx);
-      const int64_t cell = ok ? candidate(g, c, kz, ky, kx) : -1;
-      const uint64_t hits = __ballot(cell >= 0);
+  const Cands<KZ, KY, KX> cand(g, c, ok);
+  constexpr int KC = KZ * KY * KX;
+  const int KR = KC ? KC : K;
+  for (int kb = 0; kb < KR; kb += 64) {
+    const int kend = (KR - kb) < 64 ? (KR - kb) : 64;
+#pragma unroll
+    for (int kk = 0; kk < (KC ? (KC < 64 ? KC : 64) : kend); ++kk) {
+      if (kk >= kend) break;
+      const uint64_t hits = __ballot(cand.cell(g, kb + kk) >= 0);
       if (__lane_id() == 0) s_wcnt[w][kk] = __popcll(hits);
     }
     __syncthreads();
-    for (int kk = 0; kk < kend; ++kk) {
+#pragma unroll
+    for (int kk = 0; kk < (KC ? (KC < 64 ? KC : 64) : kend); ++kk) {
+      if (kk >= kend) break;
       const int k = kb + kk;
-      int kz, ky, kx;
-      slot_to_zyx(k, g.ks, kz, ky, kx);
-      const int64_t cell = ok ? candidate(g, c, kz, ky, kx) : -1;
+      const int64_t cell = cand.cell(g, k);
       const uint64_t hits = __ballot(cell >= 0);
       int base = blk_off[(int64_t)k * nblk + blockIdx.x];
       for (int ww = 0; ww < w; ++ww) base += s_wcnt[ww][kk];
       if (cell >= 0) {
-        const int64_t word = cell >> 5;
-        const uint32_t below = bitmap[word] & ((1u << (cell & 31)) - 1u);
-        const int32_t rank = static_cast<int32_t>(wprefix[word] + __popc(below));
+        const uint2 e = wr[cell >> 5];
+        const int32_t rank =
+            static_cast<int32_t>(e.y + __popc(e.x & ((1u << (cell & 31)) - 1u)));
         const int64_t slot_pos = base + rank_in_wave(hits);
         // both bounds hold by construction; the test keeps a bad count from
         // turning into an out-of-bounds write
@@ -171,9 +225,8 @@ Layout layout(int64_t n, int32_t batch, const int32_t* out) {
 }
 
 struct Buffers {
-  uint32_t* bitmap;
-  uint32_t* wprefix;
-  uint32_t* scratch;
+  uint2* wr;       // output-cell bitmap entries (word, rank)
+  uint32_t* scan;  // bitmap scan scratch
   int32_t* blk_cnt;
   int32_t* blk_off;
 };
@@ -181,14 +234,45 @@ struct Buffers {
 Buffers carve(void* ws, const Layout& L, int K, int64_t* used) {
   Carver c(ws);
   Buffers b;
-  b.bitmap = c.take<uint32_t>(L.nwords);
-  b.wprefix = c.take<uint32_t>(L.nwords);
-  b.scratch = c.take<uint32_t>(scan_scratch_words(L.nwords));
+  b.wr = c.take<uint2>(bitmap_entries(L.nwords));
+  b.scan = c.take<uint32_t>(bitmap_scan_scratch_words(L.nwords));
   b.blk_cnt = c.take<int32_t>(L.nblk * K);
   b.blk_off = c.take<int32_t>(L.nblk * K);
   if (used) *used = c.used;
   return b;
 }
+
+// Runs F<KZ, KY, KX> for the common kernel shapes, F<0, 0, 0> otherwise.
+template <template <int, int, int> class F, typename... A>
+int by_shape(const Box& ks, A... a) {
+  if (ks.z == 3 && ks.y == 3 && ks.x == 3) return F<3, 3, 3>::run(a...);
+  if (ks.z == 2 && ks.y == 2 && ks.x == 2) return F<2, 2, 2>::run(a...);
+  if (ks.z == 3 && ks.y == 1 && ks.x == 1) return F<3, 1, 1>::run(a...);
+  if (ks.z == 1 && ks.y == 1 && ks.x == 1) return F<1, 1, 1>::run(a...);
+  return F<0, 0, 0>::run(a...);
+}
+
+template <int KZ, int KY, int KX>
+struct LaunchMark {
+  static int run(const int4* c, int64_t n, int K, StridedGeom g, uint2* wr, int32_t* blk_cnt,
+                 int nblk, int32_t* status, hipStream_t s) {
+    strided_mark_kernel<KZ, KY, KX><<<nblk, kRows, 0, s>>>(c, n, K, g, wr, blk_cnt, nblk, status);
+    TSC_LAUNCH_CHECK("strided_mark");
+    return 0;
+  }
+};
+
+template <int KZ, int KY, int KX>
+struct LaunchFill {
+  static int run(const int4* c, int64_t n, int K, StridedGeom g, const uint2* wr,
+                 const int32_t* blk_off, int nblk, int64_t cap, int64_t n_out, int32_t* nbr,
+                 int32_t* pin, int32_t* pout, hipStream_t s) {
+    strided_fill_kernel<KZ, KY, KX><<<nblk, kRows, 0, s>>>(c, n, K, g, wr, blk_off, nblk, cap,
+                                                           n_out, nbr, pin, pout);
+    TSC_LAUNCH_CHECK("strided_fill");
+    return 0;
+  }
+};
 
 int check_geom(int64_t n, int32_t batch, const int32_t* spatial, const int32_t* ksize,
                const int32_t* stride, const int32_t* padding, const int32_t* dilation,
@@ -244,16 +328,17 @@ extern "C" int tsc_strided_count(const int32_t* coords, int64_t n, int32_t batch
   TSC_REQUIRE(counts != nullptr, "strided: counts is null");
   Buffers b = carve(ws, L, K, nullptr);
   if ((rc = fill_u32(reinterpret_cast<uint32_t*>(counts), K + 2, 0u, s))) return rc;
-  if ((rc = fill_u32(b.bitmap, L.nwords, 0u, s))) return rc;
+  if ((rc = fill_u32(reinterpret_cast<uint32_t*>(b.wr), 2 * bitmap_entries(L.nwords), 0u, s)))
+    return rc;
   if (n == 0) return 0;
   TSC_REQUIRE(coords != nullptr, "strided: coords is null");
   if (K > 64 && (rc = fill_u32(reinterpret_cast<uint32_t*>(b.blk_cnt), L.nblk * K, 0u, s)))
     return rc;
-  strided_mark_kernel<<<L.nblk, kRows, 0, s>>>(reinterpret_cast<const int4*>(coords), n, K, g,
-                                               b.bitmap, b.blk_cnt, (int)L.nblk, counts + K + 1);
-  TSC_LAUNCH_CHECK("strided_mark");
+  if ((rc = by_shape<LaunchMark>(g.ks, reinterpret_cast<const int4*>(coords), n, K, g, b.wr,
+                                 b.blk_cnt, (int)L.nblk, counts + K + 1, s)))
+    return rc;
   if ((rc = scan_slot_blocks(b.blk_cnt, b.blk_off, counts, K, (int)L.nblk, s))) return rc;
-  return exclusive_scan_u32(b.bitmap, 0, L.nwords, b.wprefix, counts + K, b.scratch, s);
+  return bitmap_scan(b.wr, L.nwords, b.scan, counts + K, s);
 }
 
 extern "C" int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_size,
@@ -275,14 +360,12 @@ extern "C" int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_
   if (n == 0 || n_out == 0) return 0;
   TSC_REQUIRE(coords && out_coords && nbr && pairs_in && pairs_out, "strided: null pointer");
   Buffers b = carve(ws, L, K, nullptr);
-  strided_emit_kernel<<<ceil_div(L.nwords, 256), 256, 0, s>>>(b.bitmap, b.wprefix, L.nwords, g,
+  strided_emit_kernel<<<ceil_div(L.nwords, 256), 256, 0, s>>>(b.wr, L.nwords, g,
                                                              reinterpret_cast<int4*>(out_coords),
                                                              n_out);
   TSC_LAUNCH_CHECK("strided_emit");
   if ((rc = fill_u32(reinterpret_cast<uint32_t*>(nbr), n_out * K, 0xffffffffu, s))) return rc;
-  strided_fill_kernel<<<L.nblk, kRows, 0, s>>>(reinterpret_cast<const int4*>(coords), n, K, g,
-                                               b.bitmap, b.wprefix, b.blk_off, (int)L.nblk, n, n_out,
-                                               nbr, pairs_in, pairs_out);
-  TSC_LAUNCH_CHECK("strided_fill");
-  return 0;
+  return by_shape<LaunchFill>(g.ks, reinterpret_cast<const int4*>(coords), n, K, g,
+                              static_cast<const uint2*>(b.wr), static_cast<const int32_t*>(b.blk_off),
+                              (int)L.nblk, n, n_out, nbr, pairs_in, pairs_out, s);
 }

@@ -173,71 +173,6 @@ __global__ void __launch_bounds__(256) subm_mark_kernel(const int4* __restrict__
   atomicOr(&wr[cell >> 5].x, 1u << (cell & 31));
 }
 
-// Exclusive popcount scan of the bitmap words into their y fields.  A tile is
-// 1024 words (256 threads x 4); the reduce pass writes each tile's popcount,
-// the apply pass takes its tile's offset from those (summing them itself when
-// `pre` is null, else from `pre`, their exclusive scan) and writes the ranks.
-constexpr int kBmThreads = 256;
-constexpr int kBmTile = kBmThreads * 4;
-
-__global__ void __launch_bounds__(kBmThreads) bitmap_reduce_kernel(const uint4* __restrict__ wr2,
-                                                                   int64_t nw,
-                                                                   uint32_t* __restrict__ sums) {
-  __shared__ uint32_t s_wave[33];
-  const int64_t p = (blockIdx.x * (int64_t)kBmTile) / 2 + 2 * threadIdx.x;  // entry pairs
-  uint32_t acc = 0;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    if (2 * (p + j) < nw) {
-      const uint4 v = wr2[p + j];  // word pairs past nw are zero padding
-      acc += __popc(v.x) + __popc(v.z);
-    }
-  }
-  uint32_t tot;
-  block_exclusive(acc, s_wave, &tot);
-  if (threadIdx.x == 0) sums[blockIdx.x] = tot;
-}
-
-__global__ void __launch_bounds__(kBmThreads) bitmap_apply_kernel(uint4* __restrict__ wr2, int64_t nw,
-                                                                  const uint32_t* __restrict__ sums,
-                                                                  const uint32_t* __restrict__ pre,
-                                                                  int nsum,
-                                                                  int32_t* __restrict__ n_unique) {
-  __shared__ uint32_t s_wave[33];
-  uint32_t base;
-  if (pre) {
-    base = pre[blockIdx.x];
-  } else {
-    // this tile's offset, and on block 0 the total, from the tile sums
-    const int lim = blockIdx.x == 0 ? nsum : static_cast<int>(blockIdx.x);
-    uint32_t part = 0;
-    for (int i = threadIdx.x; i < lim; i += kBmThreads) part += sums[i];
-    uint32_t tot;
-    block_exclusive(part, s_wave, &tot);
-    base = blockIdx.x == 0 ? 0u : tot;
-    if (blockIdx.x == 0 && threadIdx.x == 0) *n_unique = static_cast<int32_t>(tot);
-  }
-  const int64_t p = (blockIdx.x * (int64_t)kBmTile) / 2 + 2 * threadIdx.x;
-  uint4 v[2];
-  uint32_t c[4];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    v[j] = 2 * (p + j) < nw ? wr2[p + j] : make_uint4(0u, 0u, 0u, 0u);
-    c[2 * j] = __popc(v[j].x);
-    c[2 * j + 1] = __popc(v[j].z);
-  }
-  uint32_t tot;
-  uint32_t run = base + block_exclusive(c[0] + c[1] + c[2] + c[3], s_wave, &tot);
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    v[j].y = run;
-    run += c[2 * j];
-    v[j].w = run;
-    run += c[2 * j + 1];
-    if (2 * (p + j) < nw) wr2[p + j] = v[j];
-  }
-}
-
 // Rank of an occupied cell: occupied cells before it in (b,z,y,x) order.
 __device__ __forceinline__ uint32_t cell_rank(uint2 e, uint32_t cell) {
   return e.y + __popc(e.x & ((1u << (cell & 31)) - 1u));
@@ -514,14 +449,10 @@ static bool subm_use_bitmap(int64_t n, int64_t cells) {
 
 struct SubmWork {
   unsigned long long* table;
-  uint2* wr;                            // bitmap entries (word, rank), even count
-  uint32_t *sums, *pre, *scan_scratch;  // bitmap scan: tile sums, their prefixes
+  uint2* wr;       // bitmap entries (word, rank)
+  uint32_t* scan;  // bitmap scan scratch
   int32_t *n_unique, *n_extra, *blk_cnt, *blk_off;
 };
-
-// Bitmap scans of up to this many tiles let every apply block sum the tile
-// sums before it (one launch less); longer ones scan the sums first.
-constexpr int64_t kBmDirectTiles = 2048;
 
 static int64_t bitmap_words(int64_t cells) { return ceil_div(cells, 32); }
 
@@ -532,11 +463,8 @@ static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, int64_t* u
   SubmWork w{};
   if (subm_use_bitmap(n, cells)) {
     const int64_t nw = bitmap_words(cells);
-    const int64_t nsum = ceil_div(nw, kBmTile);
-    w.wr = c.take<uint2>(2 * ceil_div(nw, 2));
-    w.sums = c.take<uint32_t>(nsum);
-    w.pre = c.take<uint32_t>(nsum);
-    w.scan_scratch = c.take<uint32_t>(scan_scratch_words(nsum));
+    w.wr = c.take<uint2>(bitmap_entries(nw));
+    w.scan = c.take<uint32_t>(bitmap_scan_scratch_words(nw));
     w.n_unique = c.take<int32_t>(1);
     w.n_extra = c.take<int32_t>(1);
   } else {
@@ -599,7 +527,6 @@ extern "C" int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_si
   if (w.wr) {
     const int64_t nw = bitmap_words(cells);
     const int64_t n_pairs = ceil_div(nw, 2);
-    const int64_t nsum = ceil_div(nw, kBmTile);
     SubmGeom g{batch_size, shape, ks, dil, 0u};
     uint4* wr2 = reinterpret_cast<uint4*>(w.wr);
     const int64_t init_blocks = std::min<int64_t>(ceil_div(n_pairs, 256), 4096);
@@ -608,18 +535,7 @@ extern "C" int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_si
     TSC_LAUNCH_CHECK("subm_init");
     subm_mark_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, counts + K, cols_row);
     TSC_LAUNCH_CHECK("subm_mark");
-    bitmap_reduce_kernel<<<static_cast<unsigned>(nsum), kBmThreads, 0, s>>>(wr2, nw, w.sums);
-    TSC_LAUNCH_CHECK("subm_bitmap_reduce");
-    const uint32_t* pre = nullptr;
-    if (nsum > kBmDirectTiles) {
-      if ((rc = exclusive_scan_u32(w.sums, 2, nsum, w.pre, w.n_unique, w.scan_scratch, s)))
-        return rc;
-      pre = w.pre;
-    }
-    bitmap_apply_kernel<<<static_cast<unsigned>(nsum), kBmThreads, 0, s>>>(
-        wr2, nw, w.sums, pre, static_cast<int>(std::min<int64_t>(nsum, kBmDirectTiles)),
-        w.n_unique);
-    TSC_LAUNCH_CHECK("subm_bitmap_apply");
+    if ((rc = bitmap_scan(w.wr, nw, w.scan, w.n_unique, s))) return rc;
     subm_rank_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, cols_row);
     TSC_LAUNCH_CHECK("subm_rank");
     subm_place_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, cols_row,
