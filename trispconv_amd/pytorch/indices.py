@@ -83,6 +83,9 @@ class IndiceData:
         self._map_cols: Optional[torch.Tensor] = None
         self._cols_row: Optional[torch.Tensor] = None
         self._raster = False
+        # the output rows themselves are in (b,z,y,x) order (strided builds
+        # emit the sorted unique output set)
+        self._rows_raster = False
         self._order: Optional[torch.Tensor] = None  # [n_out] int32 execution order
         self._inverse_cache: Optional["IndiceData"] = None
         self._order_region = 0
@@ -94,11 +97,12 @@ class IndiceData:
     def _from_tables(cls, *, out_indices, input_indices, input_spatial_shape, output_spatial_shape,
                      kernel_size, stride, padding, dilation, subm, pin, pout, cnt_dev,
                      pair_num, nbr, batch_size, map_cols=None, cols_row=None,
-                     raster=False) -> "IndiceData":
+                     raster=False, rows_raster=False) -> "IndiceData":
         d = cls(out_indices, None, None, pair_num, input_indices, input_spatial_shape,
                 output_spatial_shape, kernel_size, stride, padding, dilation, subm)
         d._pin, d._pout, d._cnt, d._nbr = pin, pout, cnt_dev, nbr
         d._map_cols, d._cols_row, d._raster = map_cols, cols_row, bool(raster)
+        d._rows_raster = bool(rows_raster)
         d._batch_size = batch_size
         return d
 
@@ -202,7 +206,7 @@ class IndiceData:
             if self._map_cols is not None:  # the builder's columns, maybe in spatial order
                 nbr, cols_row, raster = self._map_cols, self._cols_row, self._raster
             else:
-                nbr, cols_row, raster = self.neighbour_map(n_out, device), None, False
+                nbr, cols_row, raster = self.neighbour_map(n_out, device), None, self._rows_raster
             coords = None if raster else _coords(self.out_indices, "conv plan")
             lib = L.lib()
             ws = L.workspace(lib.tsc_plan_workspace_bytes(n_out, self.K), device)
@@ -328,7 +332,7 @@ def generate_strided_indice_pairs(indices: torch.Tensor, spatial_shape, batch_si
         out_indices=out_coords, input_indices=indices, input_spatial_shape=shape,
         output_spatial_shape=out_shape, kernel_size=ks, stride=st, padding=pd, dilation=dil,
         subm=False, pin=pin, pout=pout, cnt_dev=counts[:K], pair_num=host[:K].long(), nbr=nbr,
-        batch_size=int(batch_size))
+        batch_size=int(batch_size), rows_raster=True)
 
 
 def generate_inverse_indice_pairs(fwd: IndiceData) -> IndiceData:
