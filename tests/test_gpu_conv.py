@@ -17,6 +17,7 @@ from oracle import pairs as OP
 from trispconv.pytorch import functional as Fn
 from trispconv.pytorch.indices import generate_strided_indice_pairs, generate_subm_indice_pairs
 from trispconv_amd import workloads
+from trispconv_amd.pytorch import indices as I
 
 pytestmark = [pytest.mark.gpu, needs_gpu]
 
@@ -168,9 +169,11 @@ def test_one_by_one_layers(dtype):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("c_in,c_out", [(32, 96), (64, 192), (32, 256), (96, 64), (64, 64)])
 @pytest.mark.parametrize("n", [1500, 6000])
-def test_every_bias_dtype_and_column_tile(c_in, c_out, dtype, n):
+def test_every_bias_dtype_and_column_tile(c_in, c_out, dtype, n, monkeypatch):
     """A bias of any dtype on every MFMA tile shape, with several column tiles
-    per row tile, with (n=6000) and without (n=1500) an execution order."""
+    per row tile, with (n=6000) and without (n=1500) an execution order (the
+    size threshold of the order is lowered so that small layers get one)."""
+    monkeypatch.setattr(I, "_PLAN_MIN_BYTES", 0)
     shape = (24, 24, 24)
     idx = _tiny(15, shape, 1, n)
     x = torch.from_numpy(idx).to(DEV)
@@ -197,7 +200,8 @@ def test_every_bias_dtype_and_column_tile(c_in, c_out, dtype, n):
 
 @pytest.mark.parametrize("c_in,c_out,dtype", [(16, 16, torch.float32), (128, 128, torch.float16),
                                               (64, 32, torch.bfloat16)])
-def test_deterministic_and_order_independent(c_in, c_out, dtype):
+def test_deterministic_and_order_independent(c_in, c_out, dtype, monkeypatch):
+    monkeypatch.setattr(I, "_PLAN_MIN_BYTES", 0)  # an execution order even for this small layer
     idx = _tiny(13, (30, 30, 30), 1, 9000)
     x = torch.from_numpy(idx).to(DEV)
     feats = torch.randn(len(idx), c_in, generator=torch.Generator().manual_seed(0)).to(DEV).to(dtype)
@@ -282,12 +286,13 @@ def test_full_size_workloads(name):
 
 
 @pytest.mark.parametrize("row_bytes", [256, 2048, 1 << 17])
-def test_plan_tiles_mask_sorted_heaviest_first(row_bytes):
+def test_plan_tiles_mask_sorted_heaviest_first(row_bytes, monkeypatch):
     """The execution order is a permutation of the output rows.  Cut into
     256-row tiles (the convolution's workgroup tiles), each full tile is sorted
     by slot mask, and inside each region the full tiles come in non-increasing
     number of slots used by their rows; the partial tile, if any, is last and
     mask-sorted too.  row_bytes = 2^17 makes regions of 2048 rows."""
+    monkeypatch.setattr(I, "_PLAN_MIN_BYTES", 0)  # an order even for this small layer
     idx = _tiny(15, (40, 40, 40), 2, 6000)
     x = torch.from_numpy(idx).to(DEV)
     data = generate_subm_indice_pairs(x, (40, 40, 40), 2, 3)
