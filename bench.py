@@ -370,8 +370,8 @@ def encoder_bench(args, w, dev):
                               "rows_out": int(out.features.shape[0]), "pairs": P, "ms": ms,
                               "tflops": f / (ms * 1e-3) / 1e12,
                               "epilogue": None if ep is None else
-                              ("bn+relu" if ep.scale is not None and ep.relu else
-                               "bn" if ep.scale is not None else "relu")})
+                              ("bn+relu" if ep.mean is not None and ep.relu else
+                               "bn" if ep.mean is not None else "relu")})
             x = out
             i += used
     # the BEV handoff: the last tensor to a dense (B, C, D, H, W) volume, here

@@ -187,18 +187,23 @@ TSC_API int tsc_conv_forward(const void* feat, int32_t dtype, int64_t n_in, int3
  * The same convolution with the layers that follow it in a SparseSequential
  * chain (trispconv/pytorch/modules.py:320-329, which runs them as separate
  * torch ops on the features) folded into the store: an eval-mode
- * BatchNorm1d as a per-channel affine map and a ReLU.  After the bias, in
- * fp32: v = v * scale[c] + shift[c] when scale is not NULL (shift must then
- * be given too; both fp32, c_out entries), v = max(v, 0) when relu != 0 (NaN
- * stays NaN), then one rounding to `dtype`.  With scale == shift == NULL and
- * relu == 0 it computes exactly what tsc_conv_forward computes.
+ * BatchNorm1d and a ReLU.  After the bias, in fp32, when bn_mean is not NULL:
+ *   v = v * s + (beta[c] - mean[c] * s),  s = gamma[c] / sqrt(var[c] + eps)
+ * i.e. (v - mean) / sqrt(var + eps) * gamma + beta, read from the running
+ * statistics on every call (nothing is cached, so updated statistics take
+ * effect at once).  bn_mean and bn_var come together; bn_weight (gamma) and
+ * bn_bias (beta) may be NULL for 1 and 0; all four have c_out entries of
+ * bn_dtype.  Then v = max(v, 0) when relu != 0 (NaN stays NaN), then one
+ * rounding to `dtype`.  With bn_mean == NULL and relu == 0 it computes
+ * exactly what tsc_conv_forward computes.
  * ------------------------------------------------------------------------ */
 TSC_API int tsc_conv_forward_ep(const void* feat, int32_t dtype, int64_t n_in, int32_t c_in,
                                 const void* packed_w, const void* bias, int32_t bias_dtype,
-                                const float* scale, const float* shift, int32_t relu,
-                                const int32_t* nbr, const int32_t* order, int32_t nbr_ordered,
-                                int64_t n_out, int32_t k_vol, int32_t c_out, void* out,
-                                tsc_stream_t stream);
+                                const void* bn_mean, const void* bn_var, const void* bn_weight,
+                                const void* bn_bias, int32_t bn_dtype, float bn_eps,
+                                int32_t relu, const int32_t* nbr, const int32_t* order,
+                                int32_t nbr_ordered, int64_t n_out, int32_t k_vol, int32_t c_out,
+                                void* out, tsc_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Sparse -> dense.  Replaces SparseConvTensor.dense (trispconv/pytorch/

@@ -217,6 +217,37 @@ def test_deterministic_and_order_independent(c_in, c_out, dtype, monkeypatch):
     assert torch.equal(a, b) and torch.equal(a, c) and torch.equal(a, d)
 
 
+@pytest.mark.parametrize("c_in,c_out,dtype", [(64, 128, torch.float16), (32, 128, torch.bfloat16),
+                                              (64, 128, torch.float32), (48, 64, torch.float16)])
+def test_every_column_tile_width_gives_the_same_bits(c_in, c_out, dtype, monkeypatch):
+    """The column tile width (32/64/128) only changes the schedule: each output
+    is summed in the same slot and chunk order, so every width returns the same
+    bits, equal to the oracle within tolerance."""
+    idx = _tiny(21, (40, 40, 40), 1, 12000)
+    x = torch.from_numpy(idx).to(DEV)
+    feats = torch.randn(len(idx), c_in, generator=torch.Generator().manual_seed(2)).to(DEV).to(dtype)
+    data = generate_subm_indice_pairs(x, (40, 40, 40), 1, 3)
+    m = _module("subm", c_in, c_out, 3, dtype=dtype, seed=9)
+    pw = m._packed_weight(dtype)
+    outs = {}
+    for tile in ["32", "64"] + (["128"] if c_out % 128 == 0 else []):
+        monkeypatch.setenv("TSC_CONV_TILE", tile)
+        outs[tile] = Fn.sparse_conv_forward(feats, pw, m.bias, data, len(idx))
+    monkeypatch.delenv("TSC_CONV_TILE")
+    first = outs["32"]
+    for tile, o in outs.items():
+        say("tile", tile, c_in, c_out, dtype)
+        assert torch.equal(o, first), tile
+    pr = OP.subm_pairs(idx, (40, 40, 40), 1, 3, 1)
+    w = OC.normalize_weight(to_np(m.weight).astype(np.float64), (3, 3, 3), c_in, c_out)
+    ref = OC.conv_forward(to_np(feats).astype(np.float64), w,
+                          to_np(m.bias).astype(np.float64), pr.pairs_in, pr.pairs_out, len(idx))
+    assert rel_err(to_np(first), ref) <= TOL[dtype]
+    with pytest.raises(ValueError):
+        monkeypatch.setenv("TSC_CONV_TILE", "48")  # not a column tile width
+        Fn.sparse_conv_forward(feats, pw, m.bias, data, len(idx))
+
+
 def test_raw_internal_weight_and_user_built_indice_data():
     """sparse_conv_forward with a (K, C_in, C_out) tensor and hand-made pair lists."""
     idx = _tiny(14, (10, 10, 10), 1, 300)

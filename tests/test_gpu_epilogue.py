@@ -1,12 +1,14 @@
 """Convolution epilogue (eval-mode BatchNorm1d and ReLU folded into the store).
 
-The fused store computes relu((acc + bias) * scale + shift) in fp32 and rounds
-once; it is checked against the fp64 oracle of the same expression, with the
-tolerances of the convolution tests (max |out - ref| / max |ref|: 1e-5 fp32,
-1e-2 fp16/bf16).  A SparseSequential chain with fusion is checked against the
-same chain run module by module (which rounds the features between the
-layers), and the cases that must not fuse (a BatchNorm1d in training mode,
-modules with hooks) are checked to run unfused.
+The fused store computes relu((acc + bias - mean) / sqrt(var + eps) * gamma +
+beta) in fp32 and rounds once; it is checked against the fp64 oracle of the
+same expression, with the tolerances of the convolution tests (max |out - ref|
+/ max |ref|: 1e-5 fp32, 1e-2 fp16/bf16).  A SparseSequential chain with fusion
+is checked against the same chain run module by module (which rounds the
+features between the layers), the cases that must not fuse (a BatchNorm1d in
+training mode, modules with hooks) are checked to run unfused, and changes to
+running statistics and weights between calls (including writes through
+``.data``) are checked to take effect.
 """
 import numpy as np
 import pytest
@@ -40,32 +42,56 @@ CASES = [(128, 128, torch.float16), (64, 96, torch.bfloat16), (32, 64, torch.flo
          (16, 16, torch.float32), (4, 16, torch.float16), (24, 40, torch.bfloat16)]
 
 
+def _bn_tensors(rng, c_out, bn, dtype):
+    """mean, var, gamma, beta as fp32 numpy arrays, the device tensors the
+    kernel gets (gamma/beta None for a statistics-only norm; "mixed" gives
+    fp32 statistics with gamma/beta in the features' dtype) and the values
+    those tensors hold, for the oracle."""
+    mean = rng.uniform(-0.3, 0.3, c_out).astype(np.float32)
+    var = rng.uniform(0.25, 2.0, c_out).astype(np.float32)
+    gamma = rng.uniform(0.5, 2.0, c_out).astype(np.float32)
+    beta = rng.uniform(-0.5, 0.5, c_out).astype(np.float32)
+    stat_dt = torch.float32 if bn == "mixed" else dtype
+    aff_dt = dtype
+    t = [torch.from_numpy(v).to(DEV).to(d) for v, d in
+         ((mean, stat_dt), (var, stat_dt), (gamma, aff_dt), (beta, aff_dt))]
+    if bn == "stats":
+        t[2] = t[3] = None
+    vals = [to_np(x).astype(np.float64) if x is not None else None for x in t]
+    return t, vals
+
+
 @pytest.mark.parametrize("c_in,c_out,dtype", CASES)
-@pytest.mark.parametrize("affine,relu", [(True, True), (False, True), (True, False)])
-def test_conv_epilogue_against_oracle(c_in, c_out, dtype, affine, relu):
+@pytest.mark.parametrize("bn,relu", [("affine", True), (None, True), ("affine", False),
+                                     ("stats", True), ("mixed", False)])
+def test_conv_epilogue_against_oracle(c_in, c_out, dtype, bn, relu):
     shape = (24, 24, 24)
     idx = _cloud(3, shape, 4000)
     rng = np.random.default_rng(7)
     feats = rng.standard_normal((len(idx), c_in)).astype(np.float32)
     w = (rng.standard_normal((c_out, 3, 3, 3, c_in)) / np.sqrt(27 * c_in)).astype(np.float32)
     bias = rng.uniform(-0.1, 0.1, c_out).astype(np.float32)
-    scale = rng.uniform(0.5, 2.0, c_out).astype(np.float32) if affine else None
-    shift = rng.uniform(-0.5, 0.5, c_out).astype(np.float32) if affine else None
-    say("epilogue:", c_in, "->", c_out, dtype, "affine", affine, "relu", relu)
+    eps = 1e-3
+    say("epilogue:", c_in, "->", c_out, dtype, "bn", bn, "relu", relu)
     x = torch.from_numpy(idx).to(DEV)
     data = generate_subm_indice_pairs(x, shape, 1, 3)
     wt = torch.from_numpy(w).to(DEV).to(dtype)
     packed = pack_weight(wt, (3, 3, 3), c_in, c_out, dtype)
-    ep = Fn.Epilogue(torch.from_numpy(scale).to(DEV) if affine else None,
-                     torch.from_numpy(shift).to(DEV) if affine else None, relu)
+    if bn:
+        tens, (mean, var, gamma, beta) = _bn_tensors(rng, c_out, bn, dtype)
+        ep = Fn.Epilogue(*tens, eps, relu)
+    else:
+        ep = Fn.Epilogue(None, None, None, None, 0.0, relu)
     out = Fn.sparse_conv_forward(torch.from_numpy(feats).to(DEV).to(dtype), packed,
                                  torch.from_numpy(bias).to(DEV).to(dtype), data, len(idx), ep)
     pr = OP.subm_pairs(idx, shape, 1, 3, 1)
     w64 = OC.normalize_weight(rounded(w, dtype), (3, 3, 3), c_in, c_out)
     ref = oracle_rows(rounded(feats, dtype), w64, rounded(bias, dtype), pr.pairs_in,
                       pr.pairs_out, np.arange(len(idx)))
-    if affine:
-        ref = ref * scale.astype(np.float64) + shift.astype(np.float64)
+    if bn:
+        ref = (ref - mean) / np.sqrt(var + np.float64(np.float32(eps)))
+        if gamma is not None:
+            ref = ref * gamma + beta
     if relu:
         ref = np.maximum(ref, 0.0)
     got = to_np(out)
@@ -78,7 +104,7 @@ def test_conv_epilogue_against_oracle(c_in, c_out, dtype, affine, relu):
 
 
 def test_epilogue_off_is_bitwise_the_plain_convolution():
-    """No scale and no ReLU: the same bits as the plain entry point."""
+    """No batch norm and no ReLU: the same bits as the plain entry point."""
     shape = (20, 20, 20)
     idx = _cloud(5, shape, 3000)
     x = torch.from_numpy(idx).to(DEV)
@@ -92,13 +118,34 @@ def test_epilogue_off_is_bitwise_the_plain_convolution():
         a = Fn.sparse_conv_forward(f, packed, b, data, len(idx))
         # a ReLU-only epilogue equals clamping the plain result (one rounding
         # of a non-negative or zeroed value)
-        r = Fn.sparse_conv_forward(f, packed, b, data, len(idx), Fn.Epilogue(None, None, True))
+        r = Fn.sparse_conv_forward(f, packed, b, data, len(idx),
+                                   Fn.Epilogue(None, None, None, None, 0.0, True))
         assert torch.equal(r, torch.clamp_min(a, 0)), (c_in, c_out, dtype)
-        # an identity affine map changes nothing
+        # an identity batch norm (mean 0, var 1, eps 0, gamma 1, beta 0) changes nothing
         one = torch.ones(c_out, device=DEV)
         zero = torch.zeros(c_out, device=DEV)
-        i = Fn.sparse_conv_forward(f, packed, b, data, len(idx), Fn.Epilogue(one, zero, False))
+        i = Fn.sparse_conv_forward(f, packed, b, data, len(idx),
+                                   Fn.Epilogue(zero, one, one, zero, 0.0, False))
         assert torch.equal(i, a), (c_in, c_out, dtype)
+
+
+def test_epilogue_argument_errors():
+    shape = (8, 8, 8)
+    idx = _cloud(2, shape, 100)
+    data = generate_subm_indice_pairs(torch.from_numpy(idx).to(DEV), shape, 1, 3)
+    f = torch.randn(len(idx), 16, device=DEV)
+    packed = pack_weight(torch.randn(32, 3, 3, 3, 16, device=DEV), (3, 3, 3), 16, 32,
+                         torch.float32)
+    one = torch.ones(32, device=DEV)
+    with pytest.raises(ValueError):  # mean without var
+        Fn.sparse_conv_forward(f, packed, None, data, len(idx),
+                               Fn.Epilogue(one, None, None, None, 1e-5, False))
+    with pytest.raises(ValueError):  # wrong channel count
+        Fn.sparse_conv_forward(f, packed, None, data, len(idx),
+                               Fn.Epilogue(one[:16], one[:16], None, None, 1e-5, False))
+    with pytest.raises(ValueError):  # affine parameters without statistics
+        Fn.sparse_conv_forward(f, packed, None, data, len(idx),
+                               Fn.Epilogue(None, None, one, one, 1e-5, False))
 
 
 def _bn(c, seed):
@@ -149,7 +196,7 @@ def test_sequential_fusion_matches_module_by_module(dtype, monkeypatch):
     seen = _record(monkeypatch)
     with torch.no_grad():
         fused = net(x)
-    kinds = [None if e is None else (e.scale is not None, e.relu) for e in seen]
+    kinds = [None if e is None else (e.mean is not None, e.relu) for e in seen]
     say("epilogues:", kinds)
     assert kinds == [(True, True), (True, True), (False, True), (True, False), None]
     net.fuse_epilogues = False
@@ -174,7 +221,7 @@ def test_training_batchnorm_and_hooks_are_not_fused(monkeypatch):
     net._modules["7"].register_forward_hook(lambda m, i, o: calls.append(1))  # hook on a ReLU
     with torch.no_grad():
         fused = net(x)
-    kinds = [None if e is None else (e.scale is not None, e.relu) for e in seen]
+    kinds = [None if e is None else (e.mean is not None, e.relu) for e in seen]
     # conv0: BatchNorm in training mode -> unfused; conv2: its ReLU has a hook -> unfused
     assert kinds == [None, (True, True), None, (True, False), None], kinds
     assert calls == [1]
@@ -182,3 +229,46 @@ def test_training_batchnorm_and_hooks_are_not_fused(monkeypatch):
     with torch.no_grad():
         plain = net(x)
     assert rel_err(to_np(fused.features), to_np(plain.features).astype(np.float64)) <= 1e-5
+
+
+def _fresh_plain(net, x):
+    """The chain module by module with every packed weight dropped first."""
+    for m in net.modules():
+        if isinstance(m, M.SparseConvolution):
+            m._packed = m._packed_key = None
+    net.fuse_epilogues = False
+    with torch.no_grad():
+        out = net(x)
+    net.fuse_epilogues = True
+    return out
+
+
+def test_changes_between_calls_take_effect():
+    """Running statistics, BatchNorm parameters and convolution weights changed
+    after a first call (in place, through ``.data``, or by assigning a new
+    parameter) are what the next call uses."""
+    net = _chain(torch.float32)
+    x = _input(torch.float32)
+    with torch.no_grad():
+        first = net(x)
+    conv0, bn1, conv3, bn4 = (net._modules[k] for k in ("0", "1", "3", "4"))
+    bn1.running_mean.data.add_(0.25)       # writes through .data leave the version as is
+    bn1.weight.data.mul_(1.5)
+    with torch.no_grad():
+        bn4.running_var.mul_(2.0)          # in place: a version bump
+    conv0.weight.data.mul_(-1.0)
+    with torch.no_grad():
+        second = net(x)
+    ref = _fresh_plain(net, x)
+    assert not torch.equal(first.features, second.features)
+    assert rel_err(to_np(second.features), to_np(ref.features).astype(np.float64)) <= 1e-5
+    # a plain Parameter assigned in place of the module's own: repacked on every call
+    conv3.weight = nn.Parameter(conv3.weight.detach() * 0.5)
+    with torch.no_grad():
+        third = net(x)
+    conv3.weight.data.mul_(2.0)
+    with torch.no_grad():
+        fourth = net(x)
+    ref = _fresh_plain(net, x)
+    assert not torch.equal(third.features, fourth.features)
+    assert rel_err(to_np(fourth.features), to_np(ref.features).astype(np.float64)) <= 1e-5

@@ -202,3 +202,39 @@ def test_workloads_unique_in_grid(name):
     assert (idx >= 0).all()
     keys = ((idx[:, 0].astype(np.int64) * D + idx[:, 1]) * H + idx[:, 2]) * W + idx[:, 3]
     assert len(np.unique(keys)) == len(keys)
+
+
+# ----------------------------------------------------------- weight tracking
+def test_conv_weight_state_follows_every_kind_of_write():
+    """The packed-weight cache key changes on in-place updates, on writes
+    through ``.data`` (which leave the version counter alone), on
+    load_state_dict and on dtype conversion; a plain Parameter has no key."""
+    import copy
+    import io
+    from trispconv_amd.pytorch.weight import ConvWeight, weight_state
+    m = spconv.SubMConv3d(4, 8, 3)
+    w = m.weight
+    assert type(w) is ConvWeight and isinstance(w, torch.nn.Parameter)
+    k0 = weight_state(w, torch.float16)
+    assert k0 == weight_state(w, torch.float16)        # stable while untouched
+    assert k0 != weight_state(w, torch.float32)        # per compute dtype
+    w.data.copy_(torch.ones_like(w))
+    k1 = weight_state(w, torch.float16)
+    assert k1 != k0 and w._version == 0                # .data write: counted, not versioned
+    with torch.no_grad():
+        w.mul_(2)
+    k2 = weight_state(w, torch.float16)
+    assert k2 != k1
+    m.load_state_dict({"weight": torch.zeros(8, 3, 3, 3, 4), "bias": torch.zeros(8)})
+    assert weight_state(m.weight, torch.float16) != k2 and m.weight is w
+    m.half()
+    assert type(m.weight) is ConvWeight and m.weight.dtype == torch.float16
+    # deepcopy and pickling keep the class (and so the tracking)
+    assert type(copy.deepcopy(m).weight) is ConvWeight
+    buf = io.BytesIO()
+    torch.save(m, buf)
+    buf.seek(0)
+    assert type(torch.load(buf, weights_only=False).weight) is ConvWeight
+    assert repr(w).startswith("Parameter containing:\ntensor(")
+    m.weight = torch.nn.Parameter(torch.zeros(8, 3, 3, 3, 4))
+    assert weight_state(m.weight, torch.float16) is None

@@ -53,13 +53,14 @@ _SIGNATURES = {
     "tsc_pack_weight": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp]),
     "tsc_conv_forward": (ctypes.c_int, [_vp, _i32, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32,
                                         _i64, _i32, _i32, _vp, _vp]),
-    "tsc_conv_forward_ep": (ctypes.c_int, [_vp, _i32, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32,
-                                           _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp]),
+    "tsc_conv_forward_ep": (ctypes.c_int, [_vp, _i32, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp,
+                                           _vp, _i32, ctypes.c_float, _i32, _vp, _vp, _i32, _i64,
+                                           _i32, _i32, _vp, _vp]),
     "tsc_dense_scatter": (ctypes.c_int, [_vp, _i32, _i64, _i32, _vp, _i32, c_i32p, _i32, _vp,
                                          _vp, _vp]),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lib: Optional[ctypes.CDLL] = None
 

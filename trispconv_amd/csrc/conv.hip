@@ -23,11 +23,15 @@
 //     row per lane and CO columns per thread, weights read with wave-uniform
 //     addresses, slots skipped when no lane of the wave needs them.
 //
-// The epilogue adds the bias and, when asked, a per-channel affine map and a
-// ReLU (an eval-mode BatchNorm1d and ReLU following the convolution in a
-// SparseSequential), all in fp32 before the one rounding.
+// The epilogue adds the bias and, when asked, an eval-mode batch norm and a
+// ReLU (a BatchNorm1d and ReLU following the convolution in a
+// SparseSequential), all in fp32 before the one rounding.  The batch norm is
+// read from its running statistics and affine parameters on every launch, so
+// no folded copy of them can go stale.
 #include "common.hpp"
 
+#include <cstdio>
+#include <cstdlib>
 #include <type_traits>
 
 namespace tsc {
@@ -65,11 +69,12 @@ __device__ __forceinline__ float load_any(const void* p, int dt, int64_t i) {
   return __bfloat162float(static_cast<const __hip_bfloat16*>(p)[i]);
 }
 
-// Bias entry i as fp32 without a branch on the dtype: two 16-bit reads that
-// are in bounds for every dtype (the halves of an fp32, or the same 16-bit
-// entry twice), then selects.  A three-way branch here, in the epilogue, once
-// led the compiler to leave the output address undefined on the bf16 arm.
-__device__ __forceinline__ float load_bias(const void* p, int dt, int64_t i) {
+// Entry i of a per-channel parameter (bias, batch-norm statistics) as fp32
+// without a branch on the dtype: two 16-bit reads that are in bounds for every
+// dtype (the halves of an fp32, or the same 16-bit entry twice), then selects.
+// A three-way branch here, in the epilogue, once led the compiler to leave the
+// output address undefined on the bf16 arm.
+__device__ __forceinline__ float load_param(const void* p, int dt, int64_t i) {
   const uint16_t* q = static_cast<const uint16_t*>(p);
   const bool wide = dt == TSC_F32;
   const uint32_t lo = q[wide ? 2 * i : i];
@@ -80,15 +85,34 @@ __device__ __forceinline__ float load_bias(const void* p, int dt, int64_t i) {
 }
 
 // What happens to an output element after the slot sum: v = acc + bias[c];
-// with an affine map v = v * scale[c] + shift[c]; with relu v = max(v, 0)
-// (NaN stays NaN); then one rounding.
+// with a batch norm v = (v - mean[c]) / sqrt(var[c] + eps) * gamma[c] +
+// beta[c]; with relu v = max(v, 0) (NaN stays NaN); then one rounding.
 struct Epilogue {
   const void* bias;     // per output channel, bias_dt, or null
   int bias_dt;
-  const float* scale;   // per output channel, with shift, or null
-  const float* shift;
+  const void* mean;     // batch-norm running mean and variance, or null for none
+  const void* var;
+  const void* gamma;    // its affine weight and bias, each null for 1 and 0
+  const void* beta;
+  int bn_dt;            // dtype of mean, var, gamma and beta
+  float eps;
   int relu;
 };
+
+// The batch norm of channel c as v * sc + sh: sc = gamma / sqrt(var + eps),
+// sh = beta - mean * sc (the linear-plus-constant form torch's CPU batch norm
+// evaluates).  1 and 0 without a batch norm.
+__device__ __forceinline__ void channel_affine(const Epilogue& ep, int64_t c, float& sc,
+                                               float& sh) {
+  sc = 1.f;
+  sh = 0.f;
+  if (!ep.mean) return;
+  float s = 1.f / sqrtf(load_param(ep.var, ep.bn_dt, c) + ep.eps);
+  if (ep.gamma) s *= load_param(ep.gamma, ep.bn_dt, c);
+  const float b = ep.beta ? load_param(ep.beta, ep.bn_dt, c) : 0.f;
+  sc = s;
+  sh = b - load_param(ep.mean, ep.bn_dt, c) * s;
+}
 
 __device__ __forceinline__ float finish(float v, float scale, float shift, bool affine, bool relu) {
   if (affine) v = fmaf(v, scale, shift);
@@ -148,6 +172,11 @@ __global__ void pack_mfma_kernel(const void* w, int w_dt, int layout, int K, int
   }
 }
 
+// Operand source for absent neighbours: lanes whose output row has no input
+// through the current slot read zeros from here instead of branching around
+// their loads (64 bytes per lane are read at most).
+__device__ __attribute__((aligned(256))) uint4 g_zero_row[16];
+
 // ---------------------------------------------------------------- VALU --
 // VB: bytes of one feature load (16 or 8 when every row is a whole number of
 // such vectors and the features are aligned to them, else one element).
@@ -168,26 +197,53 @@ __global__ void __launch_bounds__(256) conv_valu_kernel(
   const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   const int co0 = blockIdx.y * CO;
   const bool valid = t < n_out;
+  __shared__ float s_scale[CO], s_shift[CO];  // the batch norm of this block's columns
+  if (threadIdx.x < CO)
+    channel_affine(ep, co0 + threadIdx.x, s_scale[threadIdx.x], s_shift[threadIdx.x]);
+  __syncthreads();
   const int64_t o = valid ? (order ? order[t] : t) : 0;
   float acc[CO];
 #pragma unroll
   for (int c = 0; c < CO; ++c) acc[c] = 0.f;
-  for (int k = 0; k < K; ++k) {
-    const int64_t col = nbr_ordered ? t : o;  // the map's column of this row
-    const int32_t j = valid ? (nbr ? nbr[(int64_t)k * n_out + col] : static_cast<int32_t>(o)) : -1;
-    if (__ballot(j >= 0) == 0ull) continue;  // no lane of the wave uses slot k
-    const Vec* x = reinterpret_cast<const Vec*>(feat + (int64_t)(j >= 0 ? j : 0) * c_in);
-    const float* wk = W + (int64_t)k * c_in * c_out + co0;
+  // Slots go in groups of G: the group's map entries are loaded together, then
+  // for each NV-channel piece the G gathers are issued before any is used, so
+  // a row waits on about K/G load round trips instead of K.
+  constexpr int G = 9;
+  const int64_t col = nbr_ordered ? t : o;  // the map's column of this row
+  for (int k0 = 0; k0 < K; k0 += G) {
+    int32_t j[G];
+#pragma unroll
+    for (int u = 0; u < G; ++u) {
+      const int k = k0 + u;
+      j[u] = valid && k < K ? (nbr ? nbr[(int64_t)k * n_out + col] : static_cast<int32_t>(o)) : -1;
+    }
+    uint32_t live = 0;  // slots of the group that some lane of the wave uses
+#pragma unroll
+    for (int u = 0; u < G; ++u) live |= (__ballot(j[u] >= 0) != 0ull ? 1u : 0u) << u;
+    if (live == 0) continue;
     for (int ci0 = 0; ci0 < c_in; ci0 += NV) {
-      Vec v{};
-      if (j >= 0) v = x[ci0 / NV];
-      const T* vals = reinterpret_cast<const T*>(&v);
+      Vec v[G];
 #pragma unroll
-      for (int q = 0; q < NV; ++q) {
-        const float xv = to_f32<T>(vals[q]);
-        const float* wr = wk + (int64_t)(ci0 + q) * c_out;
+      for (int u = 0; u < G; ++u) {
+        // one vector load through a selected pointer (a conditional load of
+        // the vector gets split into per-element loads)
+        const Vec* src = j[u] >= 0
+                             ? reinterpret_cast<const Vec*>(feat + (int64_t)j[u] * c_in) + ci0 / NV
+                             : reinterpret_cast<const Vec*>(g_zero_row);
+        v[u] = *src;
+      }
 #pragma unroll
-        for (int c = 0; c < CO; ++c) acc[c] = fmaf(xv, wr[c], acc[c]);
+      for (int u = 0; u < G; ++u) {
+        if (!((live >> u) & 1u)) continue;
+        const float* wk = W + ((int64_t)(k0 + u) * c_in + ci0) * c_out + co0;
+        const T* vals = reinterpret_cast<const T*>(&v[u]);
+#pragma unroll
+        for (int q = 0; q < NV; ++q) {
+          const float xv = to_f32<T>(vals[q]);
+          const float* wr = wk + (int64_t)q * c_out;
+#pragma unroll
+          for (int c = 0; c < CO; ++c) acc[c] = fmaf(xv, wr[c], acc[c]);
+        }
       }
     }
   }
@@ -195,11 +251,9 @@ __global__ void __launch_bounds__(256) conv_valu_kernel(
   T* dst = out + o * c_out + co0;
 #pragma unroll
   for (int c = 0; c < CO; ++c) {
-    const float b = ep.bias ? load_bias(ep.bias, ep.bias_dt, co0 + c) : 0.f;
-    const bool affine = ep.scale != nullptr;
-    const float sc = affine ? ep.scale[co0 + c] : 1.f;
-    const float sh = affine ? ep.shift[co0 + c] : 0.f;
-    dst[c] = from_f32<T>(finish(acc[c] + b, sc, sh, affine, ep.relu != 0));
+    const float b = ep.bias ? load_param(ep.bias, ep.bias_dt, co0 + c) : 0.f;
+    dst[c] = from_f32<T>(finish(acc[c] + b, s_scale[c], s_shift[c], ep.mean != nullptr,
+                                ep.relu != 0));
   }
 }
 
@@ -226,10 +280,6 @@ template <> struct MfmaOp<float> {
 
 constexpr int kTileRows = kConvTileRows;  // 4 waves x 64 rows
 
-// Operand source for absent neighbours: lanes whose output row has no input
-// through the current slot read zeros from here instead of branching around
-// their loads (64 bytes per lane are read at most).
-__device__ __attribute__((aligned(256))) uint4 g_zero_row[16];
 
 template <int N> using Slot = std::integral_constant<int, N>;
 
@@ -304,9 +354,8 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
     const int64_t src_row = orow >= 0 ? (nbr_ordered ? tr : orow) : 0;
     if (t < BN) {
       const int64_t col = (int64_t)nbt * BN + t;
-      s_bias[t] = ep.bias ? load_bias(ep.bias, ep.bias_dt, col) : 0.f;
-      s_scale[t] = ep.scale ? ep.scale[col] : 1.f;
-      s_shift[t] = ep.scale ? ep.shift[col] : 0.f;
+      s_bias[t] = ep.bias ? load_param(ep.bias, ep.bias_dt, col) : 0.f;
+      channel_affine(ep, col, s_scale[t], s_shift[t]);
     }
     uint64_t m = 0;
     for (int k0 = 0; k0 < K; k0 += 8) {
@@ -491,7 +540,7 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
 
   // ---- epilogue: + bias (and the affine map and ReLU when asked), round
   // once, store each output element once.
-  const bool affine = ep.scale != nullptr;
+  const bool affine = ep.mean != nullptr;
   const bool relu = ep.relu != 0;
   // Each wave transposes its accumulators through LDS, PR rows at a time, so
   // that lanes write 16-byte pieces of output rows instead of single
@@ -566,6 +615,16 @@ int dispatch_mfma(const void* feat, int c_in, const void* W, const Epilogue& ep,
   int bn = pick_bn(c_out);
   const int ck = pick_ck(dt, c_in);
   while (bn > 32 && ceil_div(n_out, kTileRows) * (c_out / bn) < 512) bn /= 2;
+  // TSC_CONV_TILE=BN forces the column tile width (for tests that compare the
+  // widths: each sums every output in the same order, so all give the same
+  // bits).
+  if (const char* force = std::getenv("TSC_CONV_TILE")) {
+    int fb = 0;
+    TSC_REQUIRE(std::sscanf(force, "%d", &fb) == 1 && (fb == 32 || fb == 64 || fb == 128) &&
+                    c_out % fb == 0,
+                "conv: TSC_CONV_TILE=%s is not a column tile width for c_out=%d", force, c_out);
+    bn = fb;
+  }
 #define TSC_MFMA_CASE(BN_, CK_)                                                              \
   if (bn == BN_ && ck == CK_)                                                                \
     return launch_mfma<T, BN_, CK_>(feat, c_in, W, ep, nbr, order, nbr_ordered,          \
@@ -672,8 +731,12 @@ static int conv_forward(const void* feat, int32_t dtype, int64_t n_in, int32_t c
                         int32_t c_out, void* out, hipStream_t s) {
   TSC_REQUIRE(dtype_ok(dtype), "conv: unsupported dtype %d", dtype);
   TSC_REQUIRE(!ep.bias || dtype_ok(ep.bias_dt), "conv: unsupported bias dtype %d", ep.bias_dt);
-  TSC_REQUIRE((ep.scale == nullptr) == (ep.shift == nullptr),
-              "conv: scale and shift come together");
+  TSC_REQUIRE((ep.mean == nullptr) == (ep.var == nullptr),
+              "conv: batch-norm mean and variance come together");
+  TSC_REQUIRE(ep.mean || (!ep.gamma && !ep.beta),
+              "conv: batch-norm weight or bias without running statistics");
+  TSC_REQUIRE(!ep.mean || dtype_ok(ep.bn_dt), "conv: unsupported batch-norm dtype %d", ep.bn_dt);
+  TSC_REQUIRE(!ep.mean || ep.eps >= 0.f, "conv: batch-norm eps must be non-negative");
   TSC_REQUIRE(c_in > 0 && c_out > 0 && k_vol > 0, "conv: sizes must be positive");
   TSC_REQUIRE(n_out >= 0 && n_out < (int64_t(1) << 31) && n_in >= 0 && n_in < (int64_t(1) << 31),
               "conv: row counts out of range");
@@ -716,18 +779,20 @@ extern "C" int tsc_conv_forward(const void* feat, int32_t dtype, int64_t n_in, i
                                 const int32_t* nbr, const int32_t* order, int32_t nbr_ordered,
                                 int64_t n_out, int32_t k_vol, int32_t c_out, void* out,
                                 tsc_stream_t stream) {
-  const Epilogue ep{bias, bias_dtype, nullptr, nullptr, 0};
+  const Epilogue ep{bias, bias_dtype, nullptr, nullptr, nullptr, nullptr, 0, 0.f, 0};
   return conv_forward(feat, dtype, n_in, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out, k_vol,
                       c_out, out, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int tsc_conv_forward_ep(const void* feat, int32_t dtype, int64_t n_in, int32_t c_in,
                                    const void* packed_w, const void* bias, int32_t bias_dtype,
-                                   const float* scale, const float* shift, int32_t relu,
-                                   const int32_t* nbr, const int32_t* order, int32_t nbr_ordered,
-                                   int64_t n_out, int32_t k_vol, int32_t c_out, void* out,
-                                   tsc_stream_t stream) {
-  const Epilogue ep{bias, bias_dtype, scale, shift, relu != 0 ? 1 : 0};
+                                   const void* bn_mean, const void* bn_var,
+                                   const void* bn_weight, const void* bn_bias, int32_t bn_dtype,
+                                   float bn_eps, int32_t relu, const int32_t* nbr,
+                                   const int32_t* order, int32_t nbr_ordered, int64_t n_out,
+                                   int32_t k_vol, int32_t c_out, void* out, tsc_stream_t stream) {
+  const Epilogue ep{bias,      bias_dtype, bn_mean, bn_var, bn_weight,
+                    bn_bias,   bn_dtype,   bn_eps,  relu != 0 ? 1 : 0};
   return conv_forward(feat, dtype, n_in, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out, k_vol,
                       c_out, out, static_cast<hipStream_t>(stream));
 }

@@ -19,12 +19,41 @@ from .weight import PackedWeight, pack_weight
 
 
 class Epilogue(NamedTuple):
-    """What follows the convolution inside its store: v = v * scale + shift per
-    output channel (an eval-mode BatchNorm1d, fp32 device tensors, both or
-    neither), then max(v, 0) when ``relu``."""
-    scale: Optional[torch.Tensor]
-    shift: Optional[torch.Tensor]
+    """What follows the convolution inside its store: an eval-mode batch norm
+    v = (v - mean) / sqrt(var + eps) * weight + bias per output channel (mean
+    and var both or neither; weight and bias may be None), then max(v, 0) when
+    ``relu``.  The tensors are read by every launch, so changes to them take
+    effect at once."""
+    mean: Optional[torch.Tensor]
+    var: Optional[torch.Tensor]
+    weight: Optional[torch.Tensor]
+    bias: Optional[torch.Tensor]
+    eps: float
     relu: bool
+
+
+_PARAM_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+
+
+def _bn_operands(ep: Epilogue, c_out: int, device) -> list:
+    """The batch-norm tensors as contiguous tensors of one kernel dtype on
+    ``device`` (None where absent)."""
+    if (ep.mean is None) != (ep.var is None):
+        raise ValueError("sparse_conv_forward: batch-norm mean and var come together")
+    if ep.mean is None:
+        if ep.weight is not None or ep.bias is not None:
+            raise ValueError("sparse_conv_forward: batch-norm weight/bias without statistics")
+        return [None] * 4
+    ts = [t.detach() if t is not None else None for t in (ep.mean, ep.var, ep.weight, ep.bias)]
+    for t in ts:
+        if t is not None and (t.device != device or t.numel() != c_out):
+            raise ValueError("sparse_conv_forward: batch-norm tensors must have "
+                             f"{c_out} entries on {device}")
+    dts = {t.dtype for t in ts if t is not None}
+    dt = dts.pop() if len(dts) == 1 else torch.float32
+    if dt not in _PARAM_DTYPES:
+        dt = torch.float32
+    return [t.to(dt).contiguous() if t is not None else None for t in ts]
 
 
 def _run(features: torch.Tensor, packed: PackedWeight, bias: Optional[torch.Tensor],
@@ -46,26 +75,21 @@ def _run(features: torch.Tensor, packed: PackedWeight, bias: Optional[torch.Tens
             raise ValueError(f"bias has {b.numel()} entries, expected {packed.c_out}")
     lib = L.lib()
     b_ptr, b_code = L.ptr(b), (L.dtype_code(b.dtype) if b is not None else 0)
-    if epilogue is None or (epilogue.scale is None and not epilogue.relu):
+    bn = [None] * 4 if epilogue is None else _bn_operands(epilogue, packed.c_out, feats.device)
+    if bn[0] is None and (epilogue is None or not epilogue.relu):
         L.check(lib.tsc_conv_forward(
             feats.data_ptr(), L.dtype_code(feats.dtype), feats.shape[0], packed.c_in,
             packed.data.data_ptr(), b_ptr, b_code, L.ptr(nbr), L.ptr(order), int(nbr_ordered),
             n_out, packed.k_vol, packed.c_out, out.data_ptr(), L.stream_of(feats)),
             "sparse_conv_forward")
         return out
-    scale, shift = epilogue.scale, epilogue.shift
-    if (scale is None) != (shift is None):
-        raise ValueError("sparse_conv_forward: epilogue scale and shift come together")
-    for t in (scale, shift):
-        if t is not None and (t.dtype != torch.float32 or t.device != feats.device
-                              or t.numel() != packed.c_out or not t.is_contiguous()):
-            raise ValueError("sparse_conv_forward: epilogue scale/shift must be contiguous fp32 "
-                             f"tensors of {packed.c_out} entries on {feats.device}")
+    bn_code = L.dtype_code(bn[0].dtype) if bn[0] is not None else 0
     L.check(lib.tsc_conv_forward_ep(
         feats.data_ptr(), L.dtype_code(feats.dtype), feats.shape[0], packed.c_in,
-        packed.data.data_ptr(), b_ptr, b_code, L.ptr(scale), L.ptr(shift), int(epilogue.relu),
-        L.ptr(nbr), L.ptr(order), int(nbr_ordered), n_out, packed.k_vol, packed.c_out,
-        out.data_ptr(), L.stream_of(feats)), "sparse_conv_forward")
+        packed.data.data_ptr(), b_ptr, b_code, *[L.ptr(t) for t in bn], bn_code,
+        float(epilogue.eps), int(epilogue.relu), L.ptr(nbr), L.ptr(order), int(nbr_ordered),
+        n_out, packed.k_vol, packed.c_out, out.data_ptr(), L.stream_of(feats)),
+        "sparse_conv_forward")
     return out
 
 

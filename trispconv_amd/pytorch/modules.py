@@ -4,12 +4,12 @@ Constructors, parameter layout (KRSC, modules.py:70-75), the subm / strided /
 inverse dispatch (:85-90), ``indice_key`` caching (:92-120), the inverse pair
 swap (:175-221) and its 1x1x1 shortcut (:160-173) behave as in the reference.
 Every tensor operation of the forward pass runs in libtrispconv_hip.so; the
-module only keeps a packed copy of its weight, rebuilt when the parameter's
-storage, version or the feature dtype changes.
+module only keeps a packed copy of its weight, rebuilt when the parameter may
+have changed (its storage, version counter, a use of ``.data``, or the feature
+dtype) — a weight the module cannot track is packed on every call.
 """
 from __future__ import annotations
 
-import weakref
 from collections import OrderedDict
 from typing import List, Optional, Tuple, Union
 
@@ -20,7 +20,7 @@ from .functional import Epilogue, dense_forward, sparse_conv_forward
 from .indices import (IndiceData, _output_spatial_shape, _to3, generate_inverse_indice_pairs,
                       generate_strided_indice_pairs, generate_subm_indice_pairs)
 from .tensor import SparseConvTensor
-from .weight import PackedWeight, normalize_spconv_weight, pack_weight
+from .weight import ConvWeight, PackedWeight, normalize_spconv_weight, pack_weight, weight_state
 
 __all__ = ["SparseModule", "SparseConvolution", "SubMConv3d", "SparseConv3d",
            "SparseInverseConv3d", "SparseSequential"]
@@ -57,7 +57,7 @@ class SparseConvolution(SparseModule):
         kD, kH, kW = self.kernel_size
         K = kD * kH * kW
         # KRSC parameter, kaiming-uniform over the (C_out, K*C_in) view (modules.py:70-75)
-        self.weight = nn.Parameter(torch.empty(out_channels, kD, kH, kW, in_channels))
+        self.weight = ConvWeight(torch.empty(out_channels, kD, kH, kW, in_channels))
         self.bias = nn.Parameter(torch.zeros(out_channels)) if bias else None
         nn.init.kaiming_uniform_(self.weight.data.reshape(out_channels, K * in_channels))
         self._packed: Optional[PackedWeight] = None
@@ -71,11 +71,12 @@ class SparseConvolution(SparseModule):
 
     def _packed_weight(self, dtype: torch.dtype) -> PackedWeight:
         w = self.weight
-        key = (w.data_ptr(), w._version, w.dtype, w.device, dtype)
-        if self._packed is None or self._packed_key != key:
-            self._packed = pack_weight(w, self.kernel_size, self.in_channels, self.out_channels,
-                                       dtype)
-            self._packed_key = key
+        if self._packed is not None and self._packed_key is not None \
+                and self._packed_key == weight_state(w, dtype):
+            return self._packed
+        self._packed = pack_weight(w, self.kernel_size, self.in_channels, self.out_channels,
+                                   dtype)
+        self._packed_key = weight_state(w, dtype)
         return self._packed
 
     # ------------------------------------------------------------ forward
@@ -189,32 +190,6 @@ class SparseInverseConv3d(SparseConvolution):
                          indice_key=indice_key, algo=algo)
 
 
-# eval-mode BatchNorm1d -> (scale, shift) in fp32 on the features' device,
-# rebuilt when a parameter or running statistic changes
-_BN_AFFINE: "weakref.WeakKeyDictionary[nn.Module, tuple]" = weakref.WeakKeyDictionary()
-
-
-def _bn_affine(bn: nn.BatchNorm1d, device) -> Tuple[torch.Tensor, torch.Tensor]:
-    """y = (x - mean) / sqrt(var + eps) * gamma + beta as y = x * scale + shift."""
-    parts = [bn.running_mean, bn.running_var, bn.weight, bn.bias]
-    key = (device, bn.eps) + tuple((id(t), t._version) if t is not None else None for t in parts)
-    hit = _BN_AFFINE.get(bn)
-    if hit is not None and hit[0] == key:
-        return hit[1], hit[2]
-    with torch.no_grad():
-        var = bn.running_var.detach().to(device=device, dtype=torch.float32)
-        mean = bn.running_mean.detach().to(device=device, dtype=torch.float32)
-        scale = torch.rsqrt(var + bn.eps)
-        if bn.weight is not None:
-            scale = scale * bn.weight.detach().to(device=device, dtype=torch.float32)
-        shift = -mean * scale
-        if bn.bias is not None:
-            shift = shift + bn.bias.detach().to(device=device, dtype=torch.float32)
-    scale, shift = scale.contiguous(), shift.contiguous()
-    _BN_AFFINE[bn] = (key, scale, shift)
-    return scale, shift
-
-
 def _plain(m: nn.Module) -> bool:
     return not (m._forward_hooks or m._forward_pre_hooks)
 
@@ -226,22 +201,24 @@ def _fusable(mods: List[nn.Module], i: int, conv: SparseConvolution,
     many modules it covers."""
     if not (x.features.is_cuda and _plain(conv)):
         return None, 0
-    scale = shift = None
+    bn_parts = (None, None, None, None, 0.0)
     used = 0
     if i < len(mods):
         bn = mods[i]
         if (type(bn) is nn.BatchNorm1d and not bn.training and bn.track_running_stats
                 and bn.running_mean is not None and bn.num_features == conv.out_channels
                 and _plain(bn)):
-            scale, shift = _bn_affine(bn, x.features.device)
-            used = 1
+            parts = (bn.running_mean, bn.running_var, bn.weight, bn.bias)
+            if all(t is None or t.device == x.features.device for t in parts):
+                bn_parts = parts + (float(bn.eps),)
+                used = 1
     relu = False
     if i + used < len(mods):
         r = mods[i + used]
         if type(r) is nn.ReLU and _plain(r):
             relu = True
             used += 1
-    return (Epilogue(scale, shift, relu), used) if used else (None, 0)
+    return (Epilogue(*bn_parts, relu), used) if used else (None, 0)
 
 
 class SparseSequential(SparseModule):

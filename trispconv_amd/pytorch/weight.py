@@ -13,9 +13,10 @@ path) in one HIP launch.  ``weight_source`` is the shared shape dispatch.
 """
 from __future__ import annotations
 
-from typing import Tuple
+from typing import Optional, Tuple
 
 import torch
+import torch.nn as nn
 
 from .. import _lib as L
 
@@ -76,3 +77,46 @@ def pack_weight(w: torch.Tensor, kernel_size, in_channels: int, out_channels: in
                                 out_channels, code, data.data_ptr(), L.stream_of(src)),
             "pack_weight")
     return PackedWeight(data, K, in_channels, out_channels, dtype)
+
+
+def _rebuild_conv_weight(data: torch.Tensor, requires_grad: bool) -> "ConvWeight":
+    return ConvWeight(data, requires_grad)
+
+
+class ConvWeight(nn.Parameter):
+    """The convolution modules' KRSC parameter: an ``nn.Parameter`` that
+    counts uses of its ``.data`` attribute.
+
+    A module keeps its weight packed in the kernel's layout and repacks when
+    the parameter may have changed.  In-place updates (optimizer steps,
+    ``load_state_dict``, ``with torch.no_grad(): w.mul_(...)``) bump the
+    tensor's version counter, but a write through ``w.data`` (``w.data.copy_(t)``,
+    as the reference's checkpoint test loads weights) does not.  Every access
+    to ``.data`` therefore counts as a possible write.  Pickling and deepcopy
+    keep the class."""
+
+    @property
+    def data(self):
+        self.__dict__["_data_uses"] = self.__dict__.get("_data_uses", 0) + 1
+        return torch._C.TensorBase.data.__get__(self)
+
+    @data.setter
+    def data(self, value):
+        self.__dict__["_data_uses"] = self.__dict__.get("_data_uses", 0) + 1
+        torch._C.TensorBase.data.__set__(self, value)
+
+    def __reduce_ex__(self, proto):
+        return (_rebuild_conv_weight, (self.detach(), self.requires_grad))
+
+    def __repr__(self):
+        return nn.Parameter.__repr__(nn.Parameter(self.detach(), self.requires_grad))
+
+
+def weight_state(w: torch.Tensor, dtype: torch.dtype) -> Optional[tuple]:
+    """What a packed copy of ``w`` for ``dtype`` stays valid for, or None when
+    that cannot be told (a plain tensor or Parameter, whose ``.data`` writes
+    leave no trace): such a weight is packed on every call."""
+    if type(w) is not ConvWeight:
+        return None
+    return (id(w), w.data_ptr(), w._version, w.__dict__.get("_data_uses", 0), w.dtype,
+            w.device, tuple(w.shape), dtype)
