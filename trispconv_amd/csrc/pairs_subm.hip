@@ -288,21 +288,29 @@ __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
 // The same for kernels KX cells wide whose x extent (KX - 1) * dil.x + 1 is at
 // most 32 cells: the KX cells of one (kz, ky) row then lie in two consecutive
 // bitmap entries, so a row costs two 8-byte loads instead of KX.  All rows'
-// entries are loaded before any rank -> row read.
-template <int KX>
+// entries are loaded before any rank -> row read.  KZ, KY > 0 fix the kernel's
+// other extents at compile time (3x3x3: no division, fully unrolled); 0 reads
+// them from g.  With K <= 64 slots a wave counts its hits with one lane per
+// slot (lane k adds the popcount of slot k's ballot), so counting needs no
+// branch per slot; larger kernels add each ballot to counts from lane 0.
+template <int KX, int KZ, int KY>
 __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
     const int4* __restrict__ coords, int64_t n, int K, SubmGeom g, const uint2* __restrict__ wr,
     int64_t nw, const int32_t* __restrict__ cols_row, const int32_t* __restrict__ n_unique,
     const int32_t* __restrict__ n_extra, int32_t* __restrict__ nbr, int32_t* __restrict__ counts) {
-  constexpr int kRowsAtOnce = 9;  // 3x3 rows of a 3x3x3 kernel in one round
-  __shared__ int32_t s_cnt[64];
+  constexpr bool kStatic = KZ > 0 && KY > 0;
+  constexpr int kRowsAtOnce = kStatic ? KZ * KY : 9;  // rows whose entries load together
+  __shared__ int32_t s_cnt[kRows / kWave][64];
   const int t = threadIdx.x;
-  if (t < 64) s_cnt[t] = 0;
-  __syncthreads();
+  const int lane = t & (kWave - 1);
   const int64_t col = blockIdx.x * (int64_t)blockDim.x + t;
   const bool live = col < *n_unique + *n_extra;  // the other columns are empty
   const int4 c = live ? coords[cols_row[col]] : make_int4(0, 0, 0, 0);
-  const int n_rows = g.ks.z * g.ks.y;
+  const int ksz = kStatic ? KZ : g.ks.z;
+  const int ksy = kStatic ? KY : g.ks.y;
+  const int n_rows = ksz * ksy;
+  const bool lane_counts = (kStatic && KZ * KY * KX <= kWave) || K <= kWave;
+  int32_t my_cnt = 0;  // lane k: the wave's hits through slot k
   const int x_lo = c.w - (KX / 2) * g.dil.x;                 // the row's first cell
   const int x_first = x_lo > 0 ? x_lo : 0;                   // first cell inside the grid
   for (int q0 = 0; q0 < n_rows; q0 += kRowsAtOnce) {
@@ -312,9 +320,9 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
 #pragma unroll
     for (int i = 0; i < kRowsAtOnce; ++i) {
       const int q = q0 + i;
-      const int kz = q / g.ks.y, ky = q % g.ks.y;
-      const int z = c.y + (kz - g.ks.z / 2) * g.dil.z;
-      const int y = c.z + (ky - g.ks.y / 2) * g.dil.y;
+      const int kz = q / ksy, ky = q % ksy;
+      const int z = c.y + (kz - ksz / 2) * g.dil.z;
+      const int y = c.z + (ky - ksy / 2) * g.dil.y;
       row_ok[i] = live && q < n_rows && in_grid(g, c.x, z, y, x_first);
       base[i] = row_ok[i] ? cell_key(g, c.x, z, y, x_first) : 0u;  // key of x_first
       const uint32_t w0 = base[i] >> 5;
@@ -339,17 +347,36 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
 #pragma unroll
     for (int i = 0; i < kRowsAtOnce; ++i) {
       const int q = q0 + i;
-      if (q >= n_rows) continue;
+      if (!kStatic && q >= n_rows) continue;
 #pragma unroll
       for (int kx = 0; kx < KX; ++kx) {
         const int k = q * KX + kx;
-        if (col < n) nbr[(int64_t)k * n + col] = jr[i][kx];
-        count_hit(k, jr[i][kx] >= 0, s_cnt, counts);
+        const uint64_t hits = __ballot(jr[i][kx] >= 0);
+        if (lane_counts)
+          my_cnt += lane == k ? static_cast<int32_t>(__popcll(hits)) : 0;
+        else if (lane == 0 && hits)
+          atomicAdd(&counts[k], static_cast<int32_t>(__popcll(hits)));
+      }
+    }
+    if (col < n) {  // the map stores, under one branch
+#pragma unroll
+      for (int i = 0; i < kRowsAtOnce; ++i) {
+        const int q = q0 + i;
+        if (!kStatic && q >= n_rows) continue;
+#pragma unroll
+        for (int kx = 0; kx < KX; ++kx) nbr[(int64_t)(q * KX + kx) * n + col] = jr[i][kx];
       }
     }
   }
+  if (!lane_counts) return;
+  s_cnt[t / kWave][lane] = my_cnt;
   __syncthreads();
-  if (t < K && t < 64 && s_cnt[t]) atomicAdd(&counts[t], s_cnt[t]);
+  if (t < K) {
+    int32_t sum = 0;
+#pragma unroll
+    for (int w = 0; w < kRows / kWave; ++w) sum += s_cnt[w][t];
+    if (sum) atomicAdd(&counts[t], sum);
+  }
 }
 
 // Row-order hit counts per (slot, block) of a row-major map, for the
@@ -541,8 +568,12 @@ extern "C" int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_si
     subm_place_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, cols_row,
                                                        w.n_extra);
     TSC_LAUNCH_CHECK("subm_place");
-    if (ks.x == 3 && 2 * dil.x < 32) {
-      subm_probe_rows_kernel<3><<<ceil_div(n, 256), 256, 0, s>>>(
+    if (ks.x == 3 && 2 * dil.x < 32 && ks.y == 3 && ks.z == 3) {
+      subm_probe_rows_kernel<3, 3, 3><<<ceil_div(n, 256), 256, 0, s>>>(
+          c4, n, K, g, w.wr, nw, cols_row, w.n_unique, w.n_extra, nbr, counts);
+      TSC_LAUNCH_CHECK("subm_probe_rows");
+    } else if (ks.x == 3 && 2 * dil.x < 32) {
+      subm_probe_rows_kernel<3, 0, 0><<<ceil_div(n, 256), 256, 0, s>>>(
           c4, n, K, g, w.wr, nw, cols_row, w.n_unique, w.n_extra, nbr, counts);
       TSC_LAUNCH_CHECK("subm_probe_rows");
     } else {
