@@ -12,10 +12,11 @@
 // active set is:
 //   * occupancy bitmap (grids of up to about 32 cells per voxel): one bit per
 //     cell, an exclusive popcount scan of its words (each occupied cell's rank
-//     in (b,z,y,x) order) and rank -> row.  Columns are the occupied cells in
-//     rank order (then any earlier rows of repeated coordinates), so a wave's
-//     64 lookups touch neighbouring cells and share cache lines, and its map
-//     writes are contiguous;
+//     in (b,z,y,x) order) and rank -> (row, cell), one 64-bit word per
+//     column.  Columns are the occupied cells in rank order (then any earlier
+//     rows of repeated coordinates), so a wave's 64 lookups touch neighbouring
+//     cells and share cache lines, its map writes are contiguous, and a column
+//     reads its own cell from its word (no gather of its row's coordinates);
 //   * open-addressing hash of 2N..4N 64-bit slots otherwise, probed in row
 //     order (columns are rows).
 // The reference's pair lists are derived from the map only when asked for
@@ -46,6 +47,25 @@ __device__ __forceinline__ bool in_grid(const SubmGeom& g, int b, int z, int y, 
 __device__ __forceinline__ uint32_t cell_key(const SubmGeom& g, int b, int z, int y, int x) {
   return ((static_cast<uint32_t>(b) * g.shape.z + z) * g.shape.y + y) * g.shape.x + x;
 }
+
+// (b, z, y, x) of a cell key.
+__device__ __forceinline__ int4 cell_coords(const SubmGeom& g, uint32_t cell) {
+  const uint32_t x = cell % static_cast<uint32_t>(g.shape.x);
+  cell /= static_cast<uint32_t>(g.shape.x);
+  const uint32_t y = cell % static_cast<uint32_t>(g.shape.y);
+  cell /= static_cast<uint32_t>(g.shape.y);
+  const uint32_t z = cell % static_cast<uint32_t>(g.shape.z);
+  return make_int4(static_cast<int>(cell / static_cast<uint32_t>(g.shape.z)), static_cast<int>(z),
+                   static_cast<int>(y), static_cast<int>(x));
+}
+
+// A map column of the bitmap path as one 64-bit word: (row + 1) << 32 | cell
+// key, 0 while unassigned.  Rows sharing a cell differ only in the high half,
+// so the largest row is the largest word.
+__device__ __forceinline__ unsigned long long col_entry(int64_t row, uint32_t cell) {
+  return (static_cast<unsigned long long>(row + 1) << 32) | cell;
+}
+__device__ __forceinline__ int32_t entry_row(uint2 e) { return static_cast<int32_t>(e.y) - 1; }
 
 __global__ void __launch_bounds__(256) subm_insert_kernel(const int4* __restrict__ coords,
                                                           int64_t n, SubmGeom g,
@@ -159,10 +179,10 @@ __global__ void __launch_bounds__(256) subm_init_kernel(uint4* __restrict__ wr2,
 // Also marks every column unassigned (the rank pass fills them in).
 __global__ void __launch_bounds__(256) subm_mark_kernel(const int4* __restrict__ coords, int64_t n,
                                                         SubmGeom g, uint2* wr, int32_t* status,
-                                                        int32_t* __restrict__ cols_row) {
+                                                        unsigned long long* __restrict__ cols) {
   const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (r >= n) return;
-  cols_row[r] = -1;
+  cols[r] = 0ull;
   const int4 c = coords[r];
   if (!in_grid(g, c.x, c.y, c.z, c.w)) {
     atomicOr(status, (c.x < 0 || c.x >= g.B) ? TSC_FLAG_BATCH_OUT_OF_RANGE
@@ -178,14 +198,14 @@ __device__ __forceinline__ uint32_t cell_rank(uint2 e, uint32_t cell) {
   return e.y + __popc(e.x & ((1u << (cell & 31)) - 1u));
 }
 
-// cols_row[rank of the row's cell] = the largest row with that cell.  When
-// every row has a cell of its own (n_unique == n) the ranks are distinct and
-// plain stores do; otherwise repeated cells take the largest row by atomicMax
-// (cols_row starts at -1).
+// Column (rank of the row's cell) = the largest row with that cell, and the
+// cell.  When every row has a cell of its own (n_unique == n) the ranks are
+// distinct and plain stores do; otherwise repeated cells take the largest row
+// by atomicMax (entries start at 0).
 __global__ void __launch_bounds__(256) subm_rank_kernel(const int4* __restrict__ coords, int64_t n,
                                                         SubmGeom g, const uint2* __restrict__ wr,
                                                         const int32_t* __restrict__ n_unique,
-                                                        int32_t* cols_row) {
+                                                        unsigned long long* cols) {
   const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (r >= n) return;
   const bool unique = *n_unique == n;
@@ -194,9 +214,9 @@ __global__ void __launch_bounds__(256) subm_rank_kernel(const int4* __restrict__
   const uint32_t cell = cell_key(g, c.x, c.y, c.z, c.w);
   const uint32_t rank = cell_rank(wr[cell >> 5], cell);
   if (unique)
-    cols_row[rank] = static_cast<int32_t>(r);
+    cols[rank] = col_entry(r, cell);
   else
-    atomicMax(&cols_row[rank], static_cast<int32_t>(r));
+    atomicMax(&cols[rank], col_entry(r, cell));
 }
 
 // Columns of repeated coordinates: a row whose cell's last row is another
@@ -206,7 +226,8 @@ __global__ void __launch_bounds__(256) subm_rank_kernel(const int4* __restrict__
 __global__ void __launch_bounds__(256) subm_place_kernel(const int4* __restrict__ coords, int64_t n,
                                                          SubmGeom g, const uint2* __restrict__ wr,
                                                          const int32_t* __restrict__ n_unique,
-                                                         int32_t* cols_row, int32_t* n_extra) {
+                                                         unsigned long long* cols,
+                                                         int32_t* n_extra) {
   const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (r >= n) return;
   const int32_t nu = *n_unique;
@@ -215,9 +236,9 @@ __global__ void __launch_bounds__(256) subm_place_kernel(const int4* __restrict_
   if (!in_grid(g, c.x, c.y, c.z, c.w)) return;
   const uint32_t cell = cell_key(g, c.x, c.y, c.z, c.w);
   const uint32_t rank = cell_rank(wr[cell >> 5], cell);
-  if (cols_row[rank] != static_cast<int32_t>(r)) {
+  if (cols[rank] != col_entry(r, cell)) {
     const int32_t col = nu + atomicAdd(n_extra, 1);
-    cols_row[col] = static_cast<int32_t>(r);  // col < rows in the grid <= n
+    cols[col] = col_entry(r, cell);  // col < rows in the grid <= n
   }
 }
 
@@ -239,16 +260,19 @@ __device__ __forceinline__ void count_hit(int k, bool hit, int32_t* s_cnt, int32
 constexpr int kLook = 8;
 
 __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
-    const int4* __restrict__ coords, int64_t n, int K, SubmGeom g, const uint2* __restrict__ wr,
-    const int32_t* __restrict__ cols_row, const int32_t* __restrict__ n_unique,
-    const int32_t* __restrict__ n_extra, int32_t* __restrict__ nbr, int32_t* __restrict__ counts) {
+    int64_t n, int K, SubmGeom g, const uint2* __restrict__ wr,
+    const uint2* __restrict__ cols, const int32_t* __restrict__ n_unique,
+    const int32_t* __restrict__ n_extra, int32_t* __restrict__ cols_row, int32_t* __restrict__ nbr,
+    int32_t* __restrict__ counts) {
   __shared__ int32_t s_cnt[64];
   const int t = threadIdx.x;
   if (t < 64) s_cnt[t] = 0;
   __syncthreads();
   const int64_t col = blockIdx.x * (int64_t)blockDim.x + t;
   const bool live = col < *n_unique + *n_extra;  // the other columns are empty
-  const int4 c = live ? coords[cols_row[col]] : make_int4(0, 0, 0, 0);
+  const uint2 me = live ? cols[col] : make_uint2(0u, 0u);
+  if (col < n) cols_row[col] = entry_row(me);
+  const int4 c = cell_coords(g, me.x);
   for (int k0 = 0; k0 < K; k0 += kLook) {
     uint32_t cell[kLook];
     uint2 e[kLook];
@@ -270,7 +294,7 @@ __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
     for (int i = 0; i < kLook; ++i) {
       const bool hit = look[i] && ((e[i].x >> (cell[i] & 31)) & 1u);
       // a hit's rank is below n_unique <= n; a miss reads column 0
-      jr[i] = cols_row[hit ? cell_rank(e[i], cell[i]) : 0u];
+      jr[i] = entry_row(cols[hit ? cell_rank(e[i], cell[i]) : 0u]);
       if (!hit) jr[i] = -1;
     }
 #pragma unroll
@@ -295,9 +319,9 @@ __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
 // branch per slot; larger kernels add each ballot to counts from lane 0.
 template <int KX, int KZ, int KY>
 __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
-    const int4* __restrict__ coords, int64_t n, int K, SubmGeom g, const uint2* __restrict__ wr,
-    int64_t nw, const int32_t* __restrict__ cols_row, const int32_t* __restrict__ n_unique,
-    const int32_t* __restrict__ n_extra, int32_t* __restrict__ nbr, int32_t* __restrict__ counts) {
+    int64_t n, int K, SubmGeom g, const uint2* __restrict__ wr, int64_t nw, const uint2* __restrict__ cols, const int32_t* __restrict__ n_unique,
+    const int32_t* __restrict__ n_extra, int32_t* __restrict__ cols_row, int32_t* __restrict__ nbr,
+    int32_t* __restrict__ counts) {
   constexpr bool kStatic = KZ > 0 && KY > 0;
   constexpr int kRowsAtOnce = kStatic ? KZ * KY : 9;  // rows whose entries load together
   __shared__ int32_t s_cnt[kRows / kWave][64];
@@ -305,7 +329,9 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
   const int lane = t & (kWave - 1);
   const int64_t col = blockIdx.x * (int64_t)blockDim.x + t;
   const bool live = col < *n_unique + *n_extra;  // the other columns are empty
-  const int4 c = live ? coords[cols_row[col]] : make_int4(0, 0, 0, 0);
+  const uint2 me = live ? cols[col] : make_uint2(0u, 0u);
+  if (col < n) cols_row[col] = entry_row(me);
+  const int4 c = cell_coords(g, me.x);
   const int ksz = kStatic ? KZ : g.ks.z;
   const int ksy = kStatic ? KY : g.ks.y;
   const int n_rows = ksz * ksy;
@@ -340,7 +366,7 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
         const uint2 e = off < 32u ? e0[i] : e1[i];
         const uint32_t b = off & 31u;
         const bool hit = ok && ((e.x >> b) & 1u);
-        jr[i][kx] = cols_row[hit ? e.y + __popc(e.x & ((1u << b) - 1u)) : 0u];
+        jr[i][kx] = entry_row(cols[hit ? e.y + __popc(e.x & ((1u << b) - 1u)) : 0u]);
         if (!hit) jr[i][kx] = -1;
       }
     }
@@ -478,6 +504,7 @@ struct SubmWork {
   unsigned long long* table;
   uint2* wr;       // bitmap entries (word, rank)
   uint32_t* scan;  // bitmap scan scratch
+  unsigned long long* cols;  // map columns as (row + 1, cell) words
   int32_t *n_unique, *n_extra, *blk_cnt, *blk_off;
 };
 
@@ -492,6 +519,7 @@ static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, int64_t* u
     const int64_t nw = bitmap_words(cells);
     w.wr = c.take<uint2>(bitmap_entries(nw));
     w.scan = c.take<uint32_t>(bitmap_scan_scratch_words(nw));
+    w.cols = c.take<unsigned long long>(m);
     w.n_unique = c.take<int32_t>(1);
     w.n_extra = c.take<int32_t>(1);
   } else {
@@ -560,25 +588,26 @@ extern "C" int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_si
     subm_init_kernel<<<static_cast<unsigned>(init_blocks > 0 ? init_blocks : 1), 256, 0, s>>>(
         wr2, n_pairs, counts, K, w.n_extra);
     TSC_LAUNCH_CHECK("subm_init");
-    subm_mark_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, counts + K, cols_row);
+    subm_mark_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, counts + K, w.cols);
     TSC_LAUNCH_CHECK("subm_mark");
     if ((rc = bitmap_scan(w.wr, nw, w.scan, w.n_unique, s))) return rc;
-    subm_rank_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, cols_row);
+    subm_rank_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, w.cols);
     TSC_LAUNCH_CHECK("subm_rank");
-    subm_place_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, cols_row,
+    subm_place_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, w.cols,
                                                        w.n_extra);
     TSC_LAUNCH_CHECK("subm_place");
+    const uint2* cols = reinterpret_cast<const uint2*>(w.cols);
     if (ks.x == 3 && 2 * dil.x < 32 && ks.y == 3 && ks.z == 3) {
       subm_probe_rows_kernel<3, 3, 3><<<ceil_div(n, 256), 256, 0, s>>>(
-          c4, n, K, g, w.wr, nw, cols_row, w.n_unique, w.n_extra, nbr, counts);
+          n, K, g, w.wr, nw, cols, w.n_unique, w.n_extra, cols_row, nbr, counts);
       TSC_LAUNCH_CHECK("subm_probe_rows");
     } else if (ks.x == 3 && 2 * dil.x < 32) {
       subm_probe_rows_kernel<3, 0, 0><<<ceil_div(n, 256), 256, 0, s>>>(
-          c4, n, K, g, w.wr, nw, cols_row, w.n_unique, w.n_extra, nbr, counts);
+          n, K, g, w.wr, nw, cols, w.n_unique, w.n_extra, cols_row, nbr, counts);
       TSC_LAUNCH_CHECK("subm_probe_rows");
     } else {
-      subm_probe_cols_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, K, g, w.wr, cols_row,
-                                                              w.n_unique, w.n_extra, nbr, counts);
+      subm_probe_cols_kernel<<<ceil_div(n, 256), 256, 0, s>>>(n, K, g, w.wr, cols, w.n_unique,
+                                                              w.n_extra, cols_row, nbr, counts);
       TSC_LAUNCH_CHECK("subm_probe_cols");
     }
   } else {
