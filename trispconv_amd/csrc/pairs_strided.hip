@@ -106,10 +106,35 @@ __global__ void __launch_bounds__(kRows) strided_mark_kernel(const int4* __restr
   if (valid && !ok) atomicOr(status, TSC_FLAG_BATCH_OUT_OF_RANGE);
   const Cands<KZ, KY, KX> cand(g, c, ok);
   constexpr int KC = KZ * KY * KX;
+  if constexpr (KC > 0) {
+    // One atomic per bitmap word a (kz, ky) row of candidates touches, not
+    // one per candidate: the row's cells share (b, oz, oy) and their x
+    // positions are a few cells apart, so they fall in one or two words.
+#pragma unroll
+    for (int r = 0; r < KZ * KY; ++r) {
+      int64_t w0 = -1;
+      uint32_t m0 = 0, m1 = 0;
+#pragma unroll
+      for (int kx = 0; kx < KX; ++kx) {
+        const int64_t cell = cand.cell(g, r * KX + kx);
+        if (cell < 0) continue;
+        if (w0 < 0) w0 = cell >> 5;
+        const uint32_t bit = 1u << (cell & 31);
+        if ((cell >> 5) == w0)
+          m0 |= bit;
+        else if ((cell >> 5) == w0 + 1)
+          m1 |= bit;
+        else
+          atomicOr(&wr[cell >> 5].x, bit);
+      }
+      if (m0) atomicOr(&wr[w0].x, m0);
+      if (m1) atomicOr(&wr[w0 + 1].x, m1);
+    }
+  }
 #pragma unroll
   for (int k = 0; k < (KC ? KC : K); ++k) {
     const int64_t cell = cand.cell(g, k);
-    if (cell >= 0) atomicOr(&wr[cell >> 5].x, 1u << (cell & 31));
+    if (KC == 0 && cell >= 0) atomicOr(&wr[cell >> 5].x, 1u << (cell & 31));
     const uint64_t hits = __ballot(cell >= 0);
     if (__lane_id() == 0) {
       if (k < 64)
