@@ -201,6 +201,48 @@ __global__ void __launch_bounds__(kRows) strided_fill_kernel(const int4* __restr
   const bool ok = valid && c.x >= 0 && c.x < g.B;
   const Cands<KZ, KY, KX> cand(g, c, ok);
   constexpr int KC = KZ * KY * KX;
+  if constexpr (KC > 0 && KC <= 64) {
+    // Fixed kernel shape: every slot's bitmap entry is loaded before any is
+    // used (one straight-line batch of loads, no branch per slot), then the
+    // ranks and the stores.
+    int64_t cell[KC];
+    uint2 e[KC];
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+      cell[k] = cand.cell(g, k);
+      const uint64_t hits = __ballot(cell[k] >= 0);
+      if (__lane_id() == 0) s_wcnt[w][k] = __popcll(hits);
+      e[k] = wr[cell[k] >= 0 ? cell[k] >> 5 : 0];  // entry 0 exists
+    }
+    __syncthreads();
+    // s_wcnt[w][k] becomes the block offset of wave w's slot-k pairs
+    if (t < KC) {
+      int run = blk_off[(int64_t)t * nblk + blockIdx.x];
+#pragma unroll
+      for (int ww = 0; ww < kRows / kWave; ++ww) {
+        const int cnt = s_wcnt[ww][t];
+        s_wcnt[ww][t] = run;
+        run += cnt;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+      const uint64_t hits = __ballot(cell[k] >= 0);
+      const int base = s_wcnt[w][k];
+      const int32_t rank =
+          static_cast<int32_t>(e[k].y + __popc(e[k].x & ((1u << (cell[k] & 31)) - 1u)));
+      const int64_t slot_pos = base + rank_in_wave(hits);
+      // both bounds hold by construction; the test keeps a bad count from
+      // turning into an out-of-bounds write
+      if (cell[k] >= 0 && slot_pos < cap && rank < n_out) {
+        pairs_in[(int64_t)k * cap + slot_pos] = static_cast<int32_t>(i);
+        pairs_out[(int64_t)k * cap + slot_pos] = rank;
+        nbr[(int64_t)k * n_out + rank] = static_cast<int32_t>(i);
+      }
+    }
+    return;
+  }
   const int KR = KC ? KC : K;
   for (int kb = 0; kb < KR; kb += 64) {
     const int kend = (KR - kb) < 64 ? (KR - kb) : 64;
