@@ -238,3 +238,31 @@ def test_conv_weight_state_follows_every_kind_of_write():
     assert repr(w).startswith("Parameter containing:\ntensor(")
     m.weight = torch.nn.Parameter(torch.zeros(8, 3, 3, 3, 4))
     assert weight_state(m.weight, torch.float16) is None
+
+
+def test_anigen_shaped_weights_load_and_normalize():
+    """The reference's checkpoint test without the checkpoint
+    (tests/test_anigen_weights.py:43-91): KRSC tensors of the AniGen decoder's
+    shapes load into the modules (through .data, and through load_state_dict)
+    and normalize to (K, C_in, C_out)."""
+    shapes = {"inv3": ((192, 3, 3, 3, 768), (3, 3, 3), 768, 192),
+              "subm3": ((192, 3, 3, 3, 192), (3, 3, 3), 192, 192),
+              "inv1": ((192, 1, 1, 1, 768), (1, 1, 1), 768, 192)}
+    mods = {"inv3": spconv.SparseInverseConv3d(768, 192, 3, bias=False, indice_key="up0"),
+            "subm3": spconv.SubMConv3d(192, 192, 3, bias=False),
+            "inv1": spconv.SparseInverseConv3d(768, 192, 1, bias=False, indice_key="up0_skip")}
+    g = torch.Generator().manual_seed(0)
+    for name, (shape, ks, c_in, c_out) in shapes.items():
+        w = torch.randn(*shape, generator=g)
+        m = mods[name]
+        m.weight.data.copy_(w)
+        assert torch.equal(m.weight, w)
+        W = normalize_spconv_weight(m.weight, ks, c_in, c_out)
+        K = ks[0] * ks[1] * ks[2]
+        assert W.shape == (K, c_in, c_out)
+        m.load_state_dict({"weight": w * 2})
+        assert torch.equal(m.weight, w * 2)
+    # the 1x1x1 fold re-reads the flat KRSC storage as (C_in, C_out)
+    w1 = mods["inv1"].weight
+    assert torch.equal(normalize_spconv_weight(w1, (1, 1, 1), 768, 192)[0],
+                       w1.reshape(-1).view(768, 192))
