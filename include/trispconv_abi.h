@@ -90,8 +90,10 @@ TSC_API int tsc_pairs_from_map(const int32_t* nbr, int64_t n, int32_t k_vol, int
  * (trispconv/pytorch/indices.py:143-259): candidate generation (:177-195),
  * unique(sorted) of output keys (:215-229) and the per-slot split (:235-244).
  * Two phases around the one host read of the counts:
- *   count: counts [K+2]: counts[k] = pairs in slot k, counts[K] = n_out,
- *          counts[K+1] = status flags.
+ *   count: counts [K+3]: counts[k] = pairs in slot k, counts[K] = n_out,
+ *          counts[K+1] = status flags, counts[K+2] = input rows with at
+ *          least one pair (the row count of this layer's inverse, known
+ *          with the same host read).
  *   fill:  out_coords [n_out][4] sorted by (b,z,y,x); nbr [K][n_out];
  *          pairs_in/pairs_out [K][n] (slot k: input rows ascending, output
  *          rank of each).  The workspace must be the one `count` filled.

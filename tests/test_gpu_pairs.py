@@ -53,6 +53,9 @@ def _inverse(got_fwd, exp_fwd, what):
     say("inverse pairs:", what)
     got = generate_inverse_indice_pairs(got_fwd)
     exp = OP.inverse_pairs(exp_fwd)
+    # the forward build counted the inverse's rows (inputs with a pair), so
+    # the inverse needs no host read of its own
+    assert got_fwd._n_in_paired == len(exp.out_indices), f"{what}: paired input rows"
     assert np.array_equal(got.out_indices.cpu().numpy(), exp.out_indices), f"{what}: out_indices"
     _check_lists(got, exp, what)
     return got

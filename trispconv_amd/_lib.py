@@ -60,7 +60,7 @@ _SIGNATURES = {
                                          _vp, _vp]),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lib: Optional[ctypes.CDLL] = None
 

@@ -95,7 +95,8 @@ __global__ void __launch_bounds__(kRows) strided_mark_kernel(const int4* __restr
                                                              int64_t n, int K, StridedGeom g,
                                                              uint2* wr,
                                                              int32_t* __restrict__ blk_cnt,
-                                                             int nblk, int32_t* status) {
+                                                             int nblk, int32_t* status,
+                                                             int32_t* __restrict__ paired) {
   __shared__ int32_t s_cnt[kRows / kWave][64];
   const int t = threadIdx.x;
   const int w = t / kWave;
@@ -131,10 +132,12 @@ __global__ void __launch_bounds__(kRows) strided_mark_kernel(const int4* __restr
       if (m1) atomicOr(&wr[w0 + 1].x, m1);
     }
   }
+  bool any = false;  // this input row has a pair through some slot
 #pragma unroll
   for (int k = 0; k < (KC ? KC : K); ++k) {
     const int64_t cell = cand.cell(g, k);
     if (KC == 0 && cell >= 0) atomicOr(&wr[cell >> 5].x, 1u << (cell & 31));
+    any |= cell >= 0;
     const uint64_t hits = __ballot(cell >= 0);
     if (__lane_id() == 0) {
       if (k < 64)
@@ -143,6 +146,8 @@ __global__ void __launch_bounds__(kRows) strided_mark_kernel(const int4* __restr
         atomicAdd(&blk_cnt[(int64_t)k * nblk + blockIdx.x], (int)__popcll(hits));
     }
   }
+  const uint64_t with_pairs = __ballot(any);
+  if (__lane_id() == 0 && with_pairs) atomicAdd(paired, (int)__popcll(with_pairs));
   __syncthreads();
   if (t < K && t < 64) {
     int sum = 0;
@@ -322,8 +327,9 @@ int by_shape(const Box& ks, A... a) {
 template <int KZ, int KY, int KX>
 struct LaunchMark {
   static int run(const int4* c, int64_t n, int K, StridedGeom g, uint2* wr, int32_t* blk_cnt,
-                 int nblk, int32_t* status, hipStream_t s) {
-    strided_mark_kernel<KZ, KY, KX><<<nblk, kRows, 0, s>>>(c, n, K, g, wr, blk_cnt, nblk, status);
+                 int nblk, int32_t* status, int32_t* paired, hipStream_t s) {
+    strided_mark_kernel<KZ, KY, KX><<<nblk, kRows, 0, s>>>(c, n, K, g, wr, blk_cnt, nblk, status,
+                                                           paired);
     TSC_LAUNCH_CHECK("strided_mark");
     return 0;
   }
@@ -394,7 +400,7 @@ extern "C" int tsc_strided_count(const int32_t* coords, int64_t n, int32_t batch
               (long long)ws_bytes, (long long)need);
   TSC_REQUIRE(counts != nullptr, "strided: counts is null");
   Buffers b = carve(ws, L, K, nullptr);
-  if ((rc = fill_u32(reinterpret_cast<uint32_t*>(counts), K + 2, 0u, s))) return rc;
+  if ((rc = fill_u32(reinterpret_cast<uint32_t*>(counts), K + 3, 0u, s))) return rc;
   if ((rc = fill_u32(reinterpret_cast<uint32_t*>(b.wr), 2 * bitmap_entries(L.nwords), 0u, s)))
     return rc;
   if (n == 0) return 0;
@@ -402,7 +408,7 @@ extern "C" int tsc_strided_count(const int32_t* coords, int64_t n, int32_t batch
   if (K > 64 && (rc = fill_u32(reinterpret_cast<uint32_t*>(b.blk_cnt), L.nblk * K, 0u, s)))
     return rc;
   if ((rc = by_shape<LaunchMark>(g.ks, reinterpret_cast<const int4*>(coords), n, K, g, b.wr,
-                                 b.blk_cnt, (int)L.nblk, counts + K + 1, s)))
+                                 b.blk_cnt, (int)L.nblk, counts + K + 1, counts + K + 2, s)))
     return rc;
   if ((rc = scan_slot_blocks(b.blk_cnt, b.blk_off, counts, K, (int)L.nblk, s))) return rc;
   return bitmap_scan(b.wr, L.nwords, b.scan, counts + K, s);

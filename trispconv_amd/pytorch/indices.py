@@ -97,6 +97,9 @@ class IndiceData:
         self._order_region = 0
         self._nbr_ordered: Optional[torch.Tensor] = None
         self._batch_size: Optional[int] = None
+        # strided builds: input rows with at least one pair, i.e. the row
+        # count of this layer's inverse, read with the build's counts
+        self._n_in_paired: Optional[int] = None
 
     # --------------------------------------------------- construction
     @classmethod
@@ -317,7 +320,7 @@ def generate_strided_indice_pairs(indices: torch.Tensor, spatial_shape, batch_si
         raise ValueError(f"generate_strided_indice_pairs: empty output shape {out_shape}")
     lib = L.lib()
     ws = L.workspace(lib.tsc_strided_workspace_bytes(n, K, int(batch_size), L.i3(out_shape)), dev)
-    counts = torch.empty(K + 2, dtype=torch.int32, device=dev)
+    counts = torch.empty(K + 3, dtype=torch.int32, device=dev)
     geo = (L.i3(shape), L.i3(ks), L.i3(st), L.i3(pd), L.i3(dil), L.i3(out_shape))
     stream = L.stream_of(coords)
     L.check(lib.tsc_strided_count(coords.data_ptr(), n, int(batch_size), *geo, ws.data_ptr(),
@@ -334,11 +337,13 @@ def generate_strided_indice_pairs(indices: torch.Tensor, spatial_shape, batch_si
                                  ws.numel(), n_out, out_coords.data_ptr(), nbr.data_ptr(),
                                  pin.data_ptr(), pout.data_ptr(), stream),
             "generate_strided_indice_pairs")
-    return IndiceData._from_tables(
+    data = IndiceData._from_tables(
         out_indices=out_coords, input_indices=indices, input_spatial_shape=shape,
         output_spatial_shape=out_shape, kernel_size=ks, stride=st, padding=pd, dilation=dil,
         subm=False, pin=pin, pout=pout, cnt_dev=counts[:K], pair_num=host[:K].long(), nbr=nbr,
         batch_size=int(batch_size), rows_raster=True)
+    data._n_in_paired = int(host[K + 2])
+    return data
 
 
 def generate_inverse_indice_pairs(fwd: IndiceData) -> IndiceData:
@@ -362,7 +367,9 @@ def generate_inverse_indice_pairs(fwd: IndiceData) -> IndiceData:
     L.check(lib.tsc_inverse_count(fwd._pin.data_ptr(), fwd._cnt.data_ptr(), K, cap, n_in,
                                   ws.data_ptr(), ws.numel(), counts.data_ptr(), stream),
             "inverse pairs")
-    n_out = int(counts.cpu()[0])
+    # a forward built here counted its paired input rows with its own pair
+    # counts, so the inverse needs no host read of its own
+    n_out = fwd._n_in_paired if fwd._n_in_paired is not None else int(counts.cpu()[0])
     in_coords = _coords(fwd.input_indices, "inverse pairs")
     out_coords = torch.empty((n_out, 4), dtype=torch.int32, device=dev)
     nbr = torch.empty((K, n_out), dtype=torch.int32, device=dev)
