@@ -348,3 +348,32 @@ def test_plan_tiles_mask_sorted_heaviest_first(row_bytes, monkeypatch):
     for r0 in range(0, n_full * 256, region):
         hi = min(r0 + region, n_full * 256)
         assert hi - r0 == len(np.unique(order[r0:hi]))
+
+
+def test_unkeyed_subm_layers_share_one_build(monkeypatch):
+    """Submanifold layers without an indice_key reuse the pairs of their
+    coordinate tensor while it is unchanged; an in-place change rebuilds."""
+    from trispconv_amd.pytorch import modules as M
+    calls = []
+    real = M.generate_subm_indice_pairs
+
+    def counting(*args, **kw):
+        calls.append(args[3:])
+        return real(*args, **kw)
+
+    monkeypatch.setattr(M, "generate_subm_indice_pairs", counting)
+    idx = torch.from_numpy(_tiny(31, (20, 20, 20), 1, 2500)).to(DEV)
+    x = spconv.SparseConvTensor(torch.randn(len(idx), 16, device=DEV), idx, [20, 20, 20], 1)
+    a = _module("subm", 16, 16, 3, seed=1)
+    b = _module("subm", 16, 32, 3, seed=2)
+    c = _module("subm", 32, 32, 3, d=2, seed=3)
+    y = c(b(a(x)))
+    assert len(calls) == 2  # 3x3x3 dilation 1 once, dilation 2 once
+    y2 = c(b(a(x)))
+    assert len(calls) == 2 and torch.equal(y.features, y2.features)
+    idx.add_(0)  # an in-place op: the coordinate tensor may have changed
+    y3 = c(b(a(x)))
+    assert len(calls) == 4 and torch.equal(y.features, y3.features)
+    M._SUBM_PAIRS.clear()
+    fresh = c(b(a(x)))
+    assert torch.equal(y.features, fresh.features)

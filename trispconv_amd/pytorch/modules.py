@@ -15,6 +15,7 @@ from typing import List, Optional, Tuple, Union
 
 import torch
 import torch.nn as nn
+from torch.utils.weak import WeakIdKeyDictionary
 
 from .functional import Epilogue, dense_forward, sparse_conv_forward
 from .indices import (IndiceData, _output_spatial_shape, _to3, generate_inverse_indice_pairs,
@@ -28,6 +29,31 @@ __all__ = ["SparseModule", "SparseConvolution", "SubMConv3d", "SparseConv3d",
 
 class SparseModule(nn.Module):
     """Marker base class: consumes and produces SparseConvTensor (modules.py:20-22)."""
+
+
+# Submanifold pairs per coordinate tensor.  A submanifold layer's output
+# carries its input's coordinate tensor, so every layer of a stage shares one,
+# with or without an indice_key; a build is reused while that tensor is
+# unchanged (same object, storage and version counter) and for the same
+# kernel, dilation, shape and batch size.  The reference rebuilds unkeyed
+# layers every time (modules.py:92-104); the pairs are a function of these
+# inputs, so reuse gives the same results.
+_SUBM_PAIRS = WeakIdKeyDictionary()  # coordinate tensor (by identity) -> {key: IndiceData}
+
+
+def _subm_pairs_of(indices: torch.Tensor, spatial_shape, batch_size: int, kernel_size,
+                   dilation) -> IndiceData:
+    key = (indices.data_ptr(), indices._version, tuple(indices.shape), tuple(spatial_shape),
+           int(batch_size), tuple(kernel_size), tuple(dilation))
+    per = _SUBM_PAIRS.get(indices)
+    if per is not None and key in per:
+        return per[key]
+    data = generate_subm_indice_pairs(indices, spatial_shape, batch_size, kernel_size, dilation)
+    if per is None or any(k[:3] != key[:3] for k in per):
+        per = {}  # the tensor changed since: drop its old builds
+        _SUBM_PAIRS[indices] = per
+    per[key] = data
+    return data
 
 
 class SparseConvolution(SparseModule):
@@ -97,8 +123,8 @@ class SparseConvolution(SparseModule):
         # the cached entry is returned whatever its kind (modules.py:93-94)
         if self.indice_key is not None and self.indice_key in x.indice_dict:
             return x.indice_dict[self.indice_key]
-        data = generate_subm_indice_pairs(x.indices, tuple(x.spatial_shape), x.batch_size,
-                                          self.kernel_size, self.dilation)
+        data = _subm_pairs_of(x.indices, tuple(x.spatial_shape), x.batch_size,
+                              self.kernel_size, self.dilation)
         if self.indice_key is not None:
             x.indice_dict[self.indice_key] = data
         return data
