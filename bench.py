@@ -115,6 +115,12 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     w = workloads.make_workload(args.workload)
+    # The ~170k objects that the imports leave behind would make every full
+    # garbage collection a ~40 ms pause inside the timed loops; freeze them
+    # (the collector then only walks objects made from here on).
+    import gc
+    gc.collect()
+    gc.freeze()
     if args.encoder:
         encoder_bench(args, w, dev)
         return

@@ -69,6 +69,23 @@ TSC_API int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_size,
                            const int32_t dilation[3] /* host */, void* ws, int64_t ws_bytes,
                            int32_t* cols_row, int32_t* nbr, int32_t* counts, tsc_stream_t stream);
 
+/* The same build for rows that are the occupied cells of an existing
+ * occupancy bitmap in rank order: one (word, rank) 8-byte entry per 32 cells
+ * of the batch x spatial grid, row t the cell of rank t, no repeats.  That is
+ * exactly a strided build's output: its coordinates, and its workspace,
+ * which begins with those entries (tsc_strided_count/fill).  So a
+ * submanifold layer after a strided layer (indices.py:67-140 on the output of
+ * :143-259) skips zeroing, marking, scanning and ranking and runs only the
+ * probe.  Writes cols_row[t] = t, nbr [K][n] by row, counts [K+2] as
+ * tsc_subm_pairs (counts[K+1] = 1).  Kernels 3 cells wide in x, dilation
+ * < 16 in x. */
+TSC_API int tsc_subm_pairs_from_bitmap(const int32_t* coords, int64_t n, int32_t batch_size,
+                                       const int32_t spatial[3] /* host */,
+                                       const int32_t ksize[3] /* host */,
+                                       const int32_t dilation[3] /* host */, const void* bitmap,
+                                       int64_t bitmap_entries_n, int32_t* cols_row, int32_t* nbr,
+                                       int32_t* counts, tsc_stream_t stream);
+
 /* ------------------------------------------------------------------------
  * Pair lists from a neighbour map (the reference's IndiceData.pairs_in /
  * pairs_out, indices.py:123-124).
@@ -94,6 +111,9 @@ TSC_API int tsc_pairs_from_map(const int32_t* nbr, int64_t n, int32_t k_vol, int
  *          counts[K+1] = status flags, counts[K+2] = input rows with at
  *          least one pair (the row count of this layer's inverse, known
  *          with the same host read).
+ *   The workspace begins with the output grid's occupancy bitmap, one
+ *   (word, rank) 8-byte entry per 32 cells, ranks = output rows, which
+ *   tsc_subm_pairs_from_bitmap can build on.
  *   fill:  out_coords [n_out][4] sorted by (b,z,y,x); nbr [K][n_out];
  *          pairs_in/pairs_out [K][n] (slot k: input rows ascending, output
  *          rank of each).  The workspace must be the one `count` filled.

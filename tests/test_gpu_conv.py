@@ -374,6 +374,7 @@ def test_unkeyed_subm_layers_share_one_build(monkeypatch):
     idx.add_(0)  # an in-place op: the coordinate tensor may have changed
     y3 = c(b(a(x)))
     assert len(calls) == 4 and torch.equal(y.features, y3.features)
-    M._SUBM_PAIRS.clear()
+    x._pair_cache.clear()
     fresh = c(b(a(x)))
+    assert len(calls) == 6
     assert torch.equal(y.features, fresh.features)

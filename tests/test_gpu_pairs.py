@@ -206,3 +206,40 @@ def test_pairs_full_size_workloads(name):
                         lay["dilation"], name)
         if len(w.layers) > 1 and w.layers[1]["kind"] == "inverse":
             _inverse(g, e, name + "/inverse")
+
+
+@pytest.mark.parametrize("k,d", [(3, 1), (3, 2), ((3, 1, 3), 1), ((1, 3, 3), (2, 1, 1)), (5, 1)])
+def test_subm_on_a_strided_output_probes_its_bitmap(k, d, monkeypatch):
+    """A submanifold build on a strided build's output coordinates runs on the
+    strided build's bitmap (kernels 3 wide in x) and gives the oracle's pairs;
+    other kernels, or coordinates changed since, take the ordinary build."""
+    from trispconv_amd.pytorch import indices as I
+    used = []
+    reallib = I.L.lib()
+    real = reallib.tsc_subm_pairs_from_bitmap
+
+    class Spy:
+        def __getattr__(self, name):
+            fn = getattr(reallib, name)
+            if name == "tsc_subm_pairs_from_bitmap":
+                def wrapped(*a):
+                    used.append(1)
+                    return real(*a)
+                return wrapped
+            return fn
+
+    monkeypatch.setattr(I.L, "lib", lambda spy=Spy(): spy)
+    idx = _tiny(41, (17, 18, 19), 2, 900)
+    fwd = generate_strided_indice_pairs(torch.from_numpy(idx).to(DEV), (17, 18, 19), 2, 3, 2, 1)
+    out = fwd.out_indices
+    shape = tuple(fwd.output_spatial_shape)
+    got = generate_subm_indice_pairs(out, shape, 2, k, d)
+    ks = (k, k, k) if isinstance(k, int) else k
+    assert bool(used) == (ks[2] == 3), (k, d)
+    exp = OP.subm_pairs(out.cpu().numpy(), shape, 2, k, d)
+    _check_lists(got, exp, f"subm on strided output k={k} d={d}")
+    used.clear()
+    out.add_(0)  # in place: no longer known to be the strided build's output
+    again = generate_subm_indice_pairs(out, shape, 2, k, d)
+    assert not used
+    _check_lists(again, exp, f"subm on changed coordinates k={k} d={d}")

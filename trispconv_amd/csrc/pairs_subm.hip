@@ -317,21 +317,35 @@ __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
 // them from g.  With K <= 64 slots a wave counts its hits with one lane per
 // slot (lane k adds the popcount of slot k's ballot), so counting needs no
 // branch per slot; larger kernels add each ballot to counts from lane 0.
-template <int KX, int KZ, int KY>
+//
+// IDENT: the rows themselves are the occupied cells in rank order (row t has
+// rank t, no repeats: a strided build's sorted output and its bitmap), so the
+// columns are the rows, a row's cell comes from rows_coords and a hit's row
+// is its rank.
+template <int KX, int KZ, int KY, bool IDENT>
 __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
-    int64_t n, int K, SubmGeom g, const uint2* __restrict__ wr, int64_t nw, const uint2* __restrict__ cols, const int32_t* __restrict__ n_unique,
-    const int32_t* __restrict__ n_extra, int32_t* __restrict__ cols_row, int32_t* __restrict__ nbr,
-    int32_t* __restrict__ counts) {
+    int64_t n, int K, SubmGeom g, const uint2* __restrict__ wr, int64_t nw,
+    const uint2* __restrict__ cols, const int4* __restrict__ rows_coords,
+    const int32_t* __restrict__ n_unique, const int32_t* __restrict__ n_extra,
+    int32_t* __restrict__ cols_row, int32_t* __restrict__ nbr, int32_t* __restrict__ counts) {
   constexpr bool kStatic = KZ > 0 && KY > 0;
   constexpr int kRowsAtOnce = kStatic ? KZ * KY : 9;  // rows whose entries load together
   __shared__ int32_t s_cnt[kRows / kWave][64];
   const int t = threadIdx.x;
   const int lane = t & (kWave - 1);
   const int64_t col = blockIdx.x * (int64_t)blockDim.x + t;
-  const bool live = col < *n_unique + *n_extra;  // the other columns are empty
-  const uint2 me = live ? cols[col] : make_uint2(0u, 0u);
-  if (col < n) cols_row[col] = entry_row(me);
-  const int4 c = cell_coords(g, me.x);
+  int4 c;
+  bool live;
+  if constexpr (IDENT) {
+    live = col < n;
+    c = live ? rows_coords[col] : make_int4(0, 0, 0, 0);
+    if (live) cols_row[col] = static_cast<int32_t>(col);
+  } else {
+    live = col < *n_unique + *n_extra;  // the other columns are empty
+    const uint2 me = live ? cols[col] : make_uint2(0u, 0u);
+    if (col < n) cols_row[col] = entry_row(me);
+    c = cell_coords(g, me.x);
+  }
   const int ksz = kStatic ? KZ : g.ks.z;
   const int ksy = kStatic ? KY : g.ks.y;
   const int n_rows = ksz * ksy;
@@ -366,7 +380,11 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
         const uint2 e = off < 32u ? e0[i] : e1[i];
         const uint32_t b = off & 31u;
         const bool hit = ok && ((e.x >> b) & 1u);
-        jr[i][kx] = entry_row(cols[hit ? e.y + __popc(e.x & ((1u << b) - 1u)) : 0u]);
+        const uint32_t rank = e.y + __popc(e.x & ((1u << b) - 1u));
+        if constexpr (IDENT)
+          jr[i][kx] = static_cast<int32_t>(rank);
+        else
+          jr[i][kx] = entry_row(cols[hit ? rank : 0u]);
         if (!hit) jr[i][kx] = -1;
       }
     }
@@ -598,12 +616,12 @@ extern "C" int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_si
     TSC_LAUNCH_CHECK("subm_place");
     const uint2* cols = reinterpret_cast<const uint2*>(w.cols);
     if (ks.x == 3 && 2 * dil.x < 32 && ks.y == 3 && ks.z == 3) {
-      subm_probe_rows_kernel<3, 3, 3><<<ceil_div(n, 256), 256, 0, s>>>(
-          n, K, g, w.wr, nw, cols, w.n_unique, w.n_extra, cols_row, nbr, counts);
+      subm_probe_rows_kernel<3, 3, 3, false><<<ceil_div(n, 256), 256, 0, s>>>(
+          n, K, g, w.wr, nw, cols, nullptr, w.n_unique, w.n_extra, cols_row, nbr, counts);
       TSC_LAUNCH_CHECK("subm_probe_rows");
     } else if (ks.x == 3 && 2 * dil.x < 32) {
-      subm_probe_rows_kernel<3, 0, 0><<<ceil_div(n, 256), 256, 0, s>>>(
-          n, K, g, w.wr, nw, cols, w.n_unique, w.n_extra, cols_row, nbr, counts);
+      subm_probe_rows_kernel<3, 0, 0, false><<<ceil_div(n, 256), 256, 0, s>>>(
+          n, K, g, w.wr, nw, cols, nullptr, w.n_unique, w.n_extra, cols_row, nbr, counts);
       TSC_LAUNCH_CHECK("subm_probe_rows");
     } else {
       subm_probe_cols_kernel<<<ceil_div(n, 256), 256, 0, s>>>(n, K, g, w.wr, cols, w.n_unique,
@@ -626,6 +644,50 @@ extern "C" int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_si
     TSC_LAUNCH_CHECK("subm_probe");
     if ((rc = scan_slot_blocks(w.blk_cnt, w.blk_off, counts, K, nblk, s))) return rc;
   }
+  return 0;
+}
+
+extern "C" int tsc_subm_pairs_from_bitmap(const int32_t* coords, int64_t n, int32_t batch_size,
+                                          const int32_t spatial[3], const int32_t ksize[3],
+                                          const int32_t dilation[3], const void* bitmap,
+                                          int64_t bitmap_entries_n, int32_t* cols_row, int32_t* nbr,
+                                          int32_t* counts, tsc_stream_t stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  TSC_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "subm: n=%lld out of range", (long long)n);
+  TSC_REQUIRE(batch_size > 0, "subm: batch_size must be positive");
+  TSC_REQUIRE(spatial && ksize && dilation, "subm: null shape argument");
+  const Box shape = box(spatial), ks = box(ksize), dil = box(dilation);
+  TSC_REQUIRE(shape.z > 0 && shape.y > 0 && shape.x > 0, "subm: spatial shape must be positive");
+  TSC_REQUIRE(ks.z > 0 && ks.y > 0 && dil.z > 0 && dil.y > 0 && dil.x > 0,
+              "subm: kernel size and dilation must be positive");
+  TSC_REQUIRE(ks.x == 3 && 2 * dil.x < 32,
+              "subm: a build on a bitmap needs a kernel 3 cells wide in x with dilation < 16");
+  const int64_t cells = (int64_t)batch_size * shape.z * shape.y * shape.x;
+  TSC_REQUIRE(cells < 0xffffffffll,
+              "subm: batch*D*H*W = %lld cells exceeds the 32-bit cell id range", (long long)cells);
+  const int K = ks.z * ks.y * ks.x;
+  TSC_REQUIRE(K <= 4096, "subm: kernel volume %d too large", K);
+  const int64_t nw = bitmap_words(cells);
+  TSC_REQUIRE(bitmap && bitmap_entries_n >= nw,
+              "subm: bitmap of %lld entries, the grid needs %lld", (long long)bitmap_entries_n,
+              (long long)nw);
+  TSC_REQUIRE(counts != nullptr, "subm: counts is null");
+  // counts[0..K] = 0 (counts[K]: no status flags), counts[K+1] = 1 (rows in
+  // (b,z,y,x) order)
+  subm_init_kernel<<<1, 256, 0, s>>>(nullptr, 0, counts, K, counts + K);
+  TSC_LAUNCH_CHECK("subm_init");
+  if (n == 0) return 0;
+  TSC_REQUIRE(coords && cols_row && nbr, "subm: null pointer");
+  SubmGeom g{batch_size, shape, ks, dil, 0u};
+  const uint2* wr = static_cast<const uint2*>(bitmap);
+  const int4* c4 = reinterpret_cast<const int4*>(coords);
+  if (ks.y == 3 && ks.z == 3)
+    subm_probe_rows_kernel<3, 3, 3, true><<<ceil_div(n, 256), 256, 0, s>>>(
+        n, K, g, wr, nw, nullptr, c4, nullptr, nullptr, cols_row, nbr, counts);
+  else
+    subm_probe_rows_kernel<3, 0, 0, true><<<ceil_div(n, 256), 256, 0, s>>>(
+        n, K, g, wr, nw, nullptr, c4, nullptr, nullptr, cols_row, nbr, counts);
+  TSC_LAUNCH_CHECK("subm_probe_rows");
   return 0;
 }
 

@@ -15,6 +15,7 @@ from __future__ import annotations
 from typing import List, Optional, Sequence, Tuple
 
 import torch
+from torch.utils.weak import WeakIdKeyDictionary
 
 from .. import _lib as L
 
@@ -272,12 +273,51 @@ def _raise_status(status: int, what: str) -> None:
         raise IndexError(f"{what}: coordinate outside the spatial shape")
 
 
+# Output coordinates of strided builds -> (workspace, which begins with the
+# output grid's occupancy bitmap, its 32-cell words, output shape, batch size,
+# the coordinates' version counter).  A submanifold build on exactly those
+# coordinates probes that bitmap instead of building its own.
+_STRIDED_BITMAPS = WeakIdKeyDictionary()
+
+
+def _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil):
+    """The submanifold build on a strided build's output set, through its
+    bitmap, or None when ``indices`` is not such an output (unchanged)."""
+    bm = _STRIDED_BITMAPS.get(indices)
+    if bm is None:
+        return None
+    ws, nwords, out_shape, batch, version = bm
+    if (out_shape != shape or batch != int(batch_size) or version != indices._version
+            or ks[2] != 3 or 2 * dil[2] >= 32):
+        return None
+    K = ks[0] * ks[1] * ks[2]
+    n = coords.shape[0]
+    dev = coords.device
+    cols_row = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
+    map_cols = torch.empty((K, n), dtype=torch.int32, device=dev)
+    counts = torch.empty(K + 2, dtype=torch.int32, device=dev)
+    L.check(L.lib().tsc_subm_pairs_from_bitmap(
+        coords.data_ptr(), n, int(batch_size), L.i3(shape), L.i3(ks), L.i3(dil), ws.data_ptr(),
+        nwords, cols_row.data_ptr(), map_cols.data_ptr(), counts.data_ptr(), L.stream_of(coords)),
+        "generate_subm_indice_pairs")
+    host = counts.cpu()
+    return IndiceData._from_tables(
+        out_indices=indices, input_indices=indices, input_spatial_shape=shape,
+        output_spatial_shape=shape, kernel_size=ks, stride=(1, 1, 1), padding=(0, 0, 0),
+        dilation=dil, subm=True, pin=None, pout=None, cnt_dev=None, pair_num=host[:K].long(),
+        nbr=None, batch_size=int(batch_size), map_cols=map_cols, cols_row=cols_row[:n],
+        raster=True)
+
+
 def generate_subm_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size: int, kernel_size,
                                dilation=1) -> IndiceData:
     """Submanifold pairs: output set == input set (indices.py:67-140)."""
     coords = _coords(indices, "generate_subm_indice_pairs")
     ks, dil = _to3(kernel_size), _to3(dilation)
     shape = tuple(int(v) for v in spatial_shape)
+    on_bitmap = _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil)
+    if on_bitmap is not None:
+        return on_bitmap
     K = ks[0] * ks[1] * ks[2]
     n = coords.shape[0]
     dev = coords.device
@@ -343,6 +383,9 @@ def generate_strided_indice_pairs(indices: torch.Tensor, spatial_shape, batch_si
         subm=False, pin=pin, pout=pout, cnt_dev=counts[:K], pair_num=host[:K].long(), nbr=nbr,
         batch_size=int(batch_size), rows_raster=True)
     data._n_in_paired = int(host[K + 2])
+    cells = int(batch_size) * out_shape[0] * out_shape[1] * out_shape[2]
+    _STRIDED_BITMAPS[out_coords] = (ws, (cells + 31) // 32, tuple(out_shape), int(batch_size),
+                                    out_coords._version)
     return data
 
 

@@ -15,7 +15,6 @@ from typing import List, Optional, Tuple, Union
 
 import torch
 import torch.nn as nn
-from torch.utils.weak import WeakIdKeyDictionary
 
 from .functional import Epilogue, dense_forward, sparse_conv_forward
 from .indices import (IndiceData, _output_spatial_shape, _to3, generate_inverse_indice_pairs,
@@ -37,22 +36,26 @@ class SparseModule(nn.Module):
 # unchanged (same object, storage and version counter) and for the same
 # kernel, dilation, shape and batch size.  The reference rebuilds unkeyed
 # layers every time (modules.py:92-104); the pairs are a function of these
-# inputs, so reuse gives the same results.
-_SUBM_PAIRS = WeakIdKeyDictionary()  # coordinate tensor (by identity) -> {key: IndiceData}
+# inputs, so reuse gives the same results.  The builds live in the tensor's
+# _pair_cache, which its derived tensors share as they share indice_dict, so
+# they go when the network's tensors go.
+def _derived(x: SparseConvTensor, features, indices, spatial_shape) -> SparseConvTensor:
+    """A layer's output: shares x's indice_dict (modules.py:131) and pair cache."""
+    y = SparseConvTensor(features, indices, spatial_shape, x.batch_size,
+                         indice_dict=x.indice_dict)
+    y._pair_cache = x._pair_cache
+    return y
 
 
-def _subm_pairs_of(indices: torch.Tensor, spatial_shape, batch_size: int, kernel_size,
-                   dilation) -> IndiceData:
-    key = (indices.data_ptr(), indices._version, tuple(indices.shape), tuple(spatial_shape),
-           int(batch_size), tuple(kernel_size), tuple(dilation))
-    per = _SUBM_PAIRS.get(indices)
-    if per is not None and key in per:
-        return per[key]
-    data = generate_subm_indice_pairs(indices, spatial_shape, batch_size, kernel_size, dilation)
-    if per is None or any(k[:3] != key[:3] for k in per):
-        per = {}  # the tensor changed since: drop its old builds
-        _SUBM_PAIRS[indices] = per
-    per[key] = data
+def _subm_pairs_of(x: SparseConvTensor, kernel_size, dilation) -> IndiceData:
+    indices = x.indices
+    key = (id(indices), indices.data_ptr(), indices._version, tuple(indices.shape),
+           tuple(x.spatial_shape), int(x.batch_size), tuple(kernel_size), tuple(dilation))
+    data = x._pair_cache.get(key)
+    if data is None or data.out_indices is not indices:
+        data = generate_subm_indice_pairs(indices, tuple(x.spatial_shape), x.batch_size,
+                                          kernel_size, dilation)
+        x._pair_cache[key] = data
     return data
 
 
@@ -123,8 +126,7 @@ class SparseConvolution(SparseModule):
         # the cached entry is returned whatever its kind (modules.py:93-94)
         if self.indice_key is not None and self.indice_key in x.indice_dict:
             return x.indice_dict[self.indice_key]
-        data = _subm_pairs_of(x.indices, tuple(x.spatial_shape), x.batch_size,
-                              self.kernel_size, self.dilation)
+        data = _subm_pairs_of(x, self.kernel_size, self.dilation)
         if self.indice_key is not None:
             x.indice_dict[self.indice_key] = data
         return data
@@ -144,16 +146,14 @@ class SparseConvolution(SparseModule):
         n_out = len(data.out_indices)
         out = sparse_conv_forward(x.features, self._packed_weight(x.features.dtype), self.bias,
                                   data, n_out, epilogue)
-        return SparseConvTensor(out, data.out_indices, x.spatial_shape, x.batch_size,
-                                indice_dict=x.indice_dict)
+        return _derived(x, out, data.out_indices, x.spatial_shape)
 
     def _forward_strided(self, x: SparseConvTensor, epilogue=None) -> SparseConvTensor:
         data = self._get_or_compute_strided_indice(x)
         n_out = len(data.out_indices)
         out = sparse_conv_forward(x.features, self._packed_weight(x.features.dtype), self.bias,
                                   data, n_out, epilogue)
-        return SparseConvTensor(out, data.out_indices, list(data.output_spatial_shape),
-                                x.batch_size, indice_dict=x.indice_dict)
+        return _derived(x, out, data.out_indices, list(data.output_spatial_shape))
 
     def _forward_inverse(self, x: SparseConvTensor, epilogue=None) -> SparseConvTensor:
         # modules.py:149-156
@@ -174,16 +174,14 @@ class SparseConvolution(SparseModule):
                 packed = pack_weight(w0, (1, 1, 1), self.in_channels, self.out_channels,
                                      x.features.dtype)
             out = dense_forward(x.features, packed, self.bias, epilogue)
-            return SparseConvTensor(out, x.indices, x.spatial_shape, x.batch_size,
-                                    indice_dict=x.indice_dict)
+            return _derived(x, out, x.indices, x.spatial_shape)
         inv = fwd._inverse_cache
         if inv is None:
             inv = generate_inverse_indice_pairs(fwd)
             fwd._inverse_cache = inv
         n_out = len(inv.out_indices)
         out = sparse_conv_forward(x.features, packed, self.bias, inv, n_out, epilogue)
-        return SparseConvTensor(out, inv.out_indices, list(fwd.input_spatial_shape), x.batch_size,
-                                indice_dict=x.indice_dict)
+        return _derived(x, out, inv.out_indices, list(fwd.input_spatial_shape))
 
 
 class SubMConv3d(SparseConvolution):

@@ -33,6 +33,9 @@ class SparseConvTensor:
         self.voxel_num = voxel_num
         self.benchmark = benchmark
         self.benchmark_record: dict = {}
+        # submanifold builds by coordinate tensor, shared like indice_dict
+        # (not part of the reference's surface; see modules._subm_pairs_of)
+        self._pair_cache: dict = {}
 
     def __repr__(self) -> str:
         return f"SparseConvTensor[features={self._features.shape}, spatial={self.spatial_shape}]"
@@ -51,6 +54,7 @@ class SparseConvTensor:
         out = SparseConvTensor(features, self.indices, self.spatial_shape, self.batch_size,
                                self.grid, self.voxel_num, self.indice_dict, self.benchmark)
         out.benchmark_record = self.benchmark_record
+        out._pair_cache = self._pair_cache
         return out
 
     def shadow_copy(self) -> "SparseConvTensor":
