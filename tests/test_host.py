@@ -274,3 +274,12 @@ def test_anigen_shaped_weights_load_and_normalize():
     w1 = mods["inv1"].weight
     assert torch.equal(normalize_spconv_weight(w1, (1, 1, 1), 768, 192)[0],
                        w1.reshape(-1).view(768, 192))
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    """Without the built HIP library there is no fallback: the first call that
+    needs it raises and names the build command."""
+    monkeypatch.setattr(L, "_lib", None)
+    monkeypatch.setattr(L, "LIB_PATH", tmp_path / "libtrispconv_hip.so")
+    with pytest.raises(RuntimeError, match="trispconv_amd.build"):
+        L.lib()
