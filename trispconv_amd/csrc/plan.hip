@@ -176,17 +176,23 @@ __global__ void __launch_bounds__(256) gather_rows_kernel(const uint32_t* __rest
   order[i] = cols_row ? cols_row[col] : static_cast<int32_t>(col);
 }
 
-// nbr_ordered[k][t] = nbr[k][perm[t]].  blockIdx.y is the slot: blocks are
-// dispatched x-fastest, so the blocks in flight share one slot's column and
-// its gathered entries stay in cache; four positions per thread.
+// nbr_ordered[k][t] = nbr[k][perm[t]], four positions per thread.  Blocks are
+// dispatched round-robin over the 8 XCDs in launch order; block b runs on XCD
+// b % 8, which takes slots x, x+8, x+16, ... one after another, so each
+// slot's column (and the order) is gathered through one XCD's L2 instead of
+// being fetched by all eight.
 __global__ void __launch_bounds__(256) permute_map_kernel(const int32_t* __restrict__ nbr,
                                                           const uint32_t* __restrict__ order,
-                                                          int64_t n, int vec,
+                                                          int64_t n, int K, int chunks, int vec,
                                                           int32_t* __restrict__ out) {
-  const int64_t t0 = (blockIdx.x * (int64_t)blockDim.x + threadIdx.x) * 4;
+  const int64_t b = blockIdx.x;
+  const int64_t i = b / 8;                 // this XCD's i-th block
+  const int k = static_cast<int>(b % 8 + 8 * (i / chunks));
+  if (k >= K) return;
+  const int64_t t0 = ((i % chunks) * (int64_t)blockDim.x + threadIdx.x) * 4;
   if (t0 >= n) return;
-  const int32_t* col = nbr + (int64_t)blockIdx.y * n;
-  int32_t* dst = out + (int64_t)blockIdx.y * n;
+  const int32_t* col = nbr + (int64_t)k * n;
+  int32_t* dst = out + (int64_t)k * n;
   if (vec && t0 + 4 <= n) {
     const uint4 o = *reinterpret_cast<const uint4*>(order + t0);
     *reinterpret_cast<int4*>(dst + t0) = make_int4(col[o.x], col[o.y], col[o.z], col[o.w]);
@@ -409,8 +415,11 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_
   if (nbr_ordered) {
     // int4 accesses need 16-byte aligned rows of the map and of the order
     const bool vec = (n_out & 3) == 0 && (reinterpret_cast<uintptr_t>(nbr_ordered) & 15) == 0;
-    dim3 grid(static_cast<unsigned>(ceil_div(ceil_div(n_out, 4), 256)), static_cast<unsigned>(k_vol));
-    permute_map_kernel<<<grid, 256, 0, s>>>(nbr, b.keys_b, n_out, vec ? 1 : 0, nbr_ordered);
+    const int64_t chunks = ceil_div(ceil_div(n_out, 4), 256);  // blocks per slot
+    const int64_t blocks = 8 * ceil_div(k_vol, 8) * chunks;
+    TSC_REQUIRE(blocks < (int64_t(1) << 31), "plan: map too large to permute");
+    permute_map_kernel<<<static_cast<unsigned>(blocks), 256, 0, s>>>(
+        nbr, b.keys_b, n_out, k_vol, static_cast<int>(chunks), vec ? 1 : 0, nbr_ordered);
     TSC_LAUNCH_CHECK("plan_permute_map");
   }
   return 0;
