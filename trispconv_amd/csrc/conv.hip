@@ -668,8 +668,14 @@ template <typename T>
 int dispatch_valu(const void* feat, int c_in, const void* W, const Epilogue& ep,
                   const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
                   int c_out, void* out, hipStream_t s) {
+  // Columns per thread: the widest that divides c_out, narrowed for small
+  // layers until there are at least 64k threads (a small layer's time is one
+  // thread's chain of slots; narrower threads shorten it, and the repeated
+  // row loads of the column groups hit in cache).
+  int co_max = 32;
+  while (co_max > 4 && n_out * (c_out / co_max) < 65536) co_max /= 2;
 #define TSC_VALU_CASE(CO_)                                                                   \
-  if (c_out % CO_ == 0)                                                                      \
+  if (CO_ <= co_max && c_out % CO_ == 0)                                                     \
     return launch_valu<T, CO_>(feat, c_in, W, ep, nbr, order, nbr_ordered, n_out, K,        \
                                c_out, out, s);
   TSC_VALU_CASE(32)
