@@ -40,7 +40,11 @@ typedef void* tsc_stream_t; /* hipStream_t */
 enum tsc_status { TSC_OK = 0, TSC_EINVAL = 1, TSC_ERANGE = 2, TSC_EUNSUPPORTED = 3 };
 enum tsc_dtype { TSC_F32 = 0, TSC_F16 = 1, TSC_BF16 = 2 };
 /* bits of the device-side status word written by the builders */
-enum tsc_flags { TSC_FLAG_COORD_OUT_OF_GRID = 1, TSC_FLAG_BATCH_OUT_OF_RANGE = 2 };
+enum tsc_flags {
+  TSC_FLAG_COORD_OUT_OF_GRID = 1,
+  TSC_FLAG_BATCH_OUT_OF_RANGE = 2,
+  TSC_FLAG_ROWS_NOT_BITMAP = 4 /* tsc_subm_pairs_from_bitmap: rows are not the bitmap's cells */
+};
 
 /* Thread-local description of the last non-zero return. */
 TSC_API const char* tsc_last_error(void);
@@ -78,7 +82,9 @@ TSC_API int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_size,
  * :143-259) skips zeroing, marking, scanning and ranking and runs only the
  * probe.  Writes cols_row[t] = t, nbr [K][n] by row, counts [K+2] as
  * tsc_subm_pairs (counts[K+1] = 1).  Kernels 3 cells wide in x, dilation
- * < 16 in x. */
+ * < 16 in x.  A neighbour whose rank is not below n (rows that are not the
+ * bitmap's cells) is left out of the map and sets TSC_FLAG_ROWS_NOT_BITMAP
+ * in counts[K]. */
 TSC_API int tsc_subm_pairs_from_bitmap(const int32_t* coords, int64_t n, int32_t batch_size,
                                        const int32_t spatial[3] /* host */,
                                        const int32_t ksize[3] /* host */,

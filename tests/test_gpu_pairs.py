@@ -243,3 +243,27 @@ def test_subm_on_a_strided_output_probes_its_bitmap(k, d, monkeypatch):
     again = generate_subm_indice_pairs(out, shape, 2, k, d)
     assert not used
     _check_lists(again, exp, f"subm on changed coordinates k={k} d={d}")
+
+
+def test_bitmap_build_flags_rows_that_are_not_its_cells():
+    """Rows that are only part of the bitmap's cells: neighbours ranked past
+    the rows are left out of the map (no entry names a row that does not
+    exist) and the status flag says so."""
+    from trispconv_amd import _lib as L
+    from trispconv_amd.pytorch import indices as I
+    idx = _tiny(43, (17, 18, 19), 1, 900)
+    fwd = generate_strided_indice_pairs(torch.from_numpy(idx).to(DEV), (17, 18, 19), 1, 3, 2, 1)
+    ws, nwords, shape, B, _ = I._STRIDED_BITMAPS[fwd.out_indices]
+    half = fwd.out_indices[: len(fwd.out_indices) // 2].contiguous()
+    n = len(half)
+    cols_row = torch.empty(n, dtype=torch.int32, device=DEV)
+    nbr = torch.empty((27, n), dtype=torch.int32, device=DEV)
+    counts = torch.empty(29, dtype=torch.int32, device=DEV)
+    lib = L.lib()
+    L.check(lib.tsc_subm_pairs_from_bitmap(half.data_ptr(), n, B, L.i3(shape), L.i3((3, 3, 3)),
+                                           L.i3((1, 1, 1)), ws.data_ptr(), nwords,
+                                           cols_row.data_ptr(), nbr.data_ptr(),
+                                           counts.data_ptr(), L.stream_of(half)), "bitmap build")
+    host = counts.cpu()
+    assert int(host[27]) & L.FLAG_ROWS_NOT_BITMAP
+    assert int(nbr.max()) < n

@@ -21,6 +21,7 @@ _DTYPE_CODE = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16}
 
 FLAG_COORD_OUT_OF_GRID = 1
 FLAG_BATCH_OUT_OF_RANGE = 2
+FLAG_ROWS_NOT_BITMAP = 4
 
 c_i32p = ctypes.POINTER(ctypes.c_int32)
 _vp = ctypes.c_void_p

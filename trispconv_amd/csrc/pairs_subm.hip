@@ -381,10 +381,17 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
         const uint32_t b = off & 31u;
         const bool hit = ok && ((e.x >> b) & 1u);
         const uint32_t rank = e.y + __popc(e.x & ((1u << b) - 1u));
-        if constexpr (IDENT)
-          jr[i][kx] = static_cast<int32_t>(rank);
-        else
+        if constexpr (IDENT) {
+          // a rank outside the rows: the rows are not the bitmap's cells
+          if (hit && rank >= static_cast<uint64_t>(n)) {
+            atomicOr(&counts[K], TSC_FLAG_ROWS_NOT_BITMAP);
+            jr[i][kx] = -1;
+          } else {
+            jr[i][kx] = static_cast<int32_t>(rank);
+          }
+        } else {
           jr[i][kx] = entry_row(cols[hit ? rank : 0u]);
+        }
         if (!hit) jr[i][kx] = -1;
       }
     }

@@ -301,6 +301,9 @@ def _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil):
         nwords, cols_row.data_ptr(), map_cols.data_ptr(), counts.data_ptr(), L.stream_of(coords)),
         "generate_subm_indice_pairs")
     host = counts.cpu()
+    if int(host[K]) & L.FLAG_ROWS_NOT_BITMAP:
+        raise RuntimeError("generate_subm_indice_pairs: coordinates are not the rows of the "
+                           "strided build they were registered with")
     return IndiceData._from_tables(
         out_indices=indices, input_indices=indices, input_spatial_shape=shape,
         output_spatial_shape=shape, kernel_size=ks, stride=(1, 1, 1), padding=(0, 0, 0),
