@@ -55,7 +55,7 @@ TSC_API int tsc_abi_version(void);
  * Submanifold pairs.  Replaces generate_subm_indice_pairs
  * (trispconv/pytorch/indices.py:67-140) including its dense lookup table
  * (:54-64), which becomes an occupancy bitmap with per-word ranks (grids of
- * up to about 32 cells per voxel) or an open-addressing hash of 2N..4N slots.
+ * up to about 2048 cells per voxel) or an open-addressing hash of 2N..4N slots.
  * The workspace depends on the grid (batch_size * D * H * W cells).
  *
  * Writes the neighbour map as columns: nbr [K][n], column t belongs to row
@@ -187,6 +187,8 @@ TSC_API int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_t r
  *   layout 1 (flat):  W[k][ci][co] = w[((k*c_in + ci)*c_out + co)]
  *                     (the internal (K, C_in, C_out) layout, and the 1x1x1
  *                      fold quirk, which re-reads KRSC storage this way)
+ * The packed layout and size depend on (k_vol, c_in, c_out, dtype), which
+ * choose the convolution kernel; pack once per such tuple.
  * ------------------------------------------------------------------------ */
 TSC_API int64_t tsc_packed_weight_bytes(int32_t k_vol, int32_t c_in, int32_t c_out, int32_t dtype);
 TSC_API int tsc_pack_weight(const void* w, int32_t w_dtype, int32_t layout, int32_t k_vol, int32_t c_in,
@@ -197,8 +199,10 @@ TSC_API int tsc_pack_weight(const void* w, int32_t w_dtype, int32_t layout, int3
  * sparse_conv_forward (trispconv/pytorch/functional.py:14-51) and the Triton
  * per-slot kernel (triton_kernels.py:16-135).  Output-stationary: each
  * output row accumulates sum_k feat[nbr[k][o]] @ W[k] in fp32 with k
- * ascending, adds bias in fp32 and is rounded once to `dtype`.  No atomics;
- * results are bitwise reproducible and independent of `order`.
+ * ascending (f16/bf16 layers with C_in % 4 == 0 and C_out % 16 == 0 that
+ * are not 32x32-tile shapes sum 32 (slot, channel) products per matrix-core
+ * step instead), adds bias in fp32 and is rounded once to `dtype`.  No
+ * atomics; results are bitwise reproducible and independent of `order`.
  *   nbr == NULL means the identity map with k_vol == 1 (1x1x1 layers).
  *   order == NULL means rows in index order.
  *   nbr_ordered != 0 means nbr is the plan's permuted map (entry (k, t)

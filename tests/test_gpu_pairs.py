@@ -144,15 +144,15 @@ def _clustered_with_duplicates(seed, shape, B, n, box, dups):
 
 
 # The submanifold builder looks cells up in an occupancy bitmap when the grid
-# has at most about 32 cells per voxel (8 words per voxel + 2^20 words), and in
+# has at most about 2048 cells per voxel (64 words per voxel + 2^20 words), and in
 # a hash table otherwise; both must give the same lists, repeated coordinates
 # included.
-@pytest.mark.parametrize("shape,what", [((20, 24, 28), "bitmap"), ((320, 320, 200), "hash")])
+@pytest.mark.parametrize("shape,what", [((20, 24, 28), "bitmap"), ((640, 320, 200), "hash")])
 def test_subm_lookup_paths_with_duplicates(shape, what):
     B, n = 2, 3000
     idx = _clustered_with_duplicates(31, shape, B, n, 16, 300)
     words = -(-B * shape[0] * shape[1] * shape[2] // 32)
-    assert (words <= 8 * len(idx) + (1 << 20)) == (what == "bitmap")
+    assert (words <= 64 * len(idx) + (1 << 20)) == (what == "bitmap")
     _subm(idx, shape, B, 3, 1, f"{what} path")
     _subm(idx, shape, B, (3, 1, 3), (1, 2, 1), f"{what} path, 3x1x3 dilated")
 
@@ -178,7 +178,7 @@ def test_subm_bitmap_long_scan():
     are scanned in a pass of their own before the ranks are applied."""
     shape, B, n = (300, 512, 512), 1, 200_000
     words = -(-B * shape[0] * shape[1] * shape[2] // 32)
-    assert -(-words // 1024) > 2048 and words <= 8 * n + (1 << 20)
+    assert -(-words // 1024) > 2048 and words <= 64 * n + (1 << 20)
     idx = _clustered_with_duplicates(41, shape, B, n, 64, 0)
     _subm(idx, shape, B, 3, 1, "long bitmap scan")
 

@@ -10,7 +10,7 @@
 // the per-slot pair counts.  The reference's dense grid-sized lookup table
 // (:54-64) becomes one of two compact structures, chosen by how dense the
 // active set is:
-//   * occupancy bitmap (grids of up to about 32 cells per voxel): one bit per
+//   * occupancy bitmap (grids of up to about 2048 cells per voxel): one bit per
 //     cell, an exclusive popcount scan of its words (each occupied cell's rank
 //     in (b,z,y,x) order) and rank -> (row, cell), one 64-bit word per
 //     column.  Columns are the occupied cells in rank order (then any earlier
@@ -519,10 +519,14 @@ static int64_t subm_capacity(int64_t n) {
   return cap;
 }
 
-// The bitmap is used when its words number at most 8 per voxel plus 2^20
-// (4 MiB): its zeroing and scan then cost about as much as the hash would.
+// The bitmap is used when its words number at most 64 per voxel plus 2^20.
+// Its zeroing and scan cost about 7 ns per 1000 words and its per-voxel
+// kernels about 0.2 ns per voxel, against about 0.9 ns per voxel for the hash
+// once the table outgrows L2 (240 000 voxels in 4 x 41 x 1600 x 1408 cells:
+// 127 us against 222 us), so the bitmap stays ahead up to about 100 words per
+// voxel.  Its entries then take at most 512 bytes per voxel.
 static bool subm_use_bitmap(int64_t n, int64_t cells) {
-  return ceil_div(cells, 32) <= 8 * n + (int64_t(1) << 20);
+  return ceil_div(cells, 32) <= 64 * n + (int64_t(1) << 20);
 }
 
 struct SubmWork {
