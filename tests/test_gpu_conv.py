@@ -1,9 +1,9 @@
 """Fused convolution on the GPU against the fp64 oracle.
 
 Tolerance (max |out - ref| / max |ref|, oracle in fp64 over the rounded
-inputs and weights): 1e-5 for fp32, 1e-2 for fp16 and bf16.  Covers the VALU
-and MFMA kernels, every MFMA tile shape, ragged and wide channels, 1x1x1
-layers, the five workloads at full size (checked on a random subset of output
+inputs and weights): 1e-5 for fp32, 1e-2 for fp16 and bf16.  Covers the VALU,
+narrow-MFMA and MFMA kernels, every MFMA tile shape, ragged and wide channels,
+1x1x1 layers, the five workloads at full size (checked on a random subset of output
 rows), bitwise determinism and independence from the execution order.
 """
 import numpy as np
@@ -97,6 +97,12 @@ LAYER_CASES = [
     # C_in an odd multiple of 16: the last 32-channel chunk is half padding
     (16, 64, torch.float32), (48, 32, torch.bfloat16), (80, 96, torch.float16),
     (16, 128, torch.bfloat16),
+    # the narrow kernel (f16/bf16, C_in % 4 == 0, C_out % 16 == 0): 8-byte
+    # pieces (C_in % 8 == 4, a piece never straddles two slots), 16-byte
+    # pieces, 16-column tiles that do not pair up, many reduction steps
+    (4, 16, torch.float16), (12, 48, torch.float16), (4, 32, torch.bfloat16),
+    (8, 16, torch.bfloat16), (16, 48, torch.float16), (40, 80, torch.float16),
+    (64, 16, torch.bfloat16),
 ]
 
 
@@ -110,13 +116,36 @@ def test_subm_layer(c_in, c_out, dtype):
 
 @pytest.mark.parametrize("c_in,c_out,dtype", [(16, 32, torch.float32), (32, 64, torch.bfloat16),
                                               (64, 128, torch.float16), (5, 3, torch.float16),
-                                              (64, 64, torch.float32)])
+                                              (64, 64, torch.float32), (4, 16, torch.float16),
+                                              (8, 48, torch.bfloat16)])
 @pytest.mark.parametrize("k,s,p", [(3, 2, 1), (2, 2, 0), ((3, 1, 1), (2, 1, 1), 0)])
 def test_strided_layer(c_in, c_out, dtype, k, s, p):
     idx = _tiny(7, (21, 18, 25), 2, 3000)
     feats = np.random.default_rng(8).standard_normal((len(idx), c_in)).astype(np.float32)
     m = _module("strided", c_in, c_out, k, s, p, dtype=dtype, seed=3)
     _check_layer(m, feats, idx, (21, 18, 25), 2, dtype, what=f"strided {c_in}->{c_out} k{k}")
+
+
+@pytest.mark.parametrize("c_in,c_out,dtype", [(4, 64, torch.float16), (8, 32, torch.bfloat16),
+                                              (12, 64, torch.bfloat16)])
+def test_narrow_layers_with_several_column_tiles_per_wave(c_in, c_out, dtype):
+    """Layers of 150 000 rows: enough workgroups for the narrow kernel to give
+    each wave two or four 16-column tiles.  Checked on 3000 random rows."""
+    shape = (64, 64, 64)
+    idx = _tiny(23, shape, 1, 150_000)
+    feats = np.random.default_rng(24).standard_normal((len(idx), c_in)).astype(np.float32)
+    m = _module("subm", c_in, c_out, 3, dtype=dtype, seed=c_in * c_out)
+    _check_layer(m, feats, idx, shape, 1, dtype, rows=3000, what=f"narrow {c_in}->{c_out}")
+
+
+@pytest.mark.parametrize("c_in,c_out,dtype", [(16, 32, torch.float16), (4, 16, torch.bfloat16)])
+def test_layers_of_more_than_64_slots(c_in, c_out, dtype):
+    """5x5x5 (125 slots): past the 32x32 tile's slot table, so the narrow
+    kernel takes these shapes; its reduction runs over 63 and 16 steps."""
+    idx = _tiny(25, (18, 20, 22), 2, 2500)
+    feats = np.random.default_rng(26).standard_normal((len(idx), c_in)).astype(np.float32)
+    m = _module("subm", c_in, c_out, 5, dtype=dtype, seed=11)
+    _check_layer(m, feats, idx, (18, 20, 22), 2, dtype, what=f"subm 5x5x5 {c_in}->{c_out}")
 
 
 @pytest.mark.parametrize("c_mid,c_out,dtype", [(64, 32, torch.bfloat16), (16, 8, torch.float32),
@@ -199,7 +228,8 @@ def test_every_bias_dtype_and_column_tile(c_in, c_out, dtype, n, monkeypatch):
 
 
 @pytest.mark.parametrize("c_in,c_out,dtype", [(16, 16, torch.float32), (128, 128, torch.float16),
-                                              (64, 32, torch.bfloat16)])
+                                              (64, 32, torch.bfloat16), (4, 16, torch.float16),
+                                              (8, 48, torch.bfloat16)])
 def test_deterministic_and_order_independent(c_in, c_out, dtype, monkeypatch):
     monkeypatch.setattr(I, "_PLAN_MIN_BYTES", 0)  # an execution order even for this small layer
     idx = _tiny(13, (30, 30, 30), 1, 9000)

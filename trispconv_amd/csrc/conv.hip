@@ -15,13 +15,17 @@
 // every output element is a fixed sequence of fp32 operations, so results are
 // bitwise reproducible and independent of the tile order.
 //
-// Two code shapes share that structure:
-//   * mfma: f32/f16/bf16 with C_in, C_out multiples of 32 and K <= 64 —
-//     v_mfma_f32_32x32x16_{f16,bf16} or v_mfma_f32_32x32x2_f32, 4 waves x
+// Three code shapes share that structure:
+//   * mfma: f32/f16/bf16 with C_in a multiple of 16, C_out of 32 and K <= 64
+//     — v_mfma_f32_32x32x16_{f16,bf16} or v_mfma_f32_32x32x2_f32, 4 waves x
 //     (64 rows x BN cols) per tile.
-//   * valu: everything else (narrow or ragged channels, K > 64) — one output
-//     row per lane and CO columns per thread, weights read with wave-uniform
-//     addresses, slots skipped when no lane of the wave needs them.
+//   * narrow: the other f16/bf16 layers with C_in % 4 == 0 and C_out % 16 ==
+//     0 (a LiDAR encoder's 4 -> 16 first layer, 16-wide outputs, K > 64) —
+//     v_mfma_f32_16x16x32 over (slot, channel) pairs, 16 rows per wave.
+//   * valu: everything else (fp32 narrow or ragged channels, odd widths) —
+//     one output row per lane and CO columns per thread, weights read with
+//     wave-uniform addresses, slots skipped when no lane of the wave needs
+//     them.
 //
 // The epilogue adds the bias and, when asked, an eval-mode batch norm and a
 // ReLU (a BatchNorm1d and ReLU following the convolution in a
@@ -41,7 +45,7 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-enum Path { kValu = 0, kMfma = 1 };
+enum Path { kValu = 0, kMfma = 1, kNarrow = 2 };
 
 // Input-channel chunk of one stage: 64 bytes of every gathered row per lane
 // half (64 channels of f16/bf16, 32 of f32), or half that when the channels
@@ -55,12 +59,18 @@ int pick_bn(int c_out) { return c_out % 128 == 0 ? 128 : (c_out % 64 == 0 ? 64 :
 int64_t mfma_chunks(int c_in, int ck) { return ceil_div(c_in, ck); }
 
 // MFMA for every dtype when C_in is a multiple of 16 and C_out of 32 (the
-// slot table of K <= 64 slots fits LDS); VALU otherwise.
+// slot table of K <= 64 slots fits LDS); the narrow MFMA kernel for the other
+// f16/bf16 layers whose channels come in 4-channel pieces and 16-column
+// tiles; VALU otherwise.
 Path pick_path(int dtype, int c_in, int c_out, int K) {
   if (c_in % 16 == 0 && c_out % 32 == 0 && K <= 64) return kMfma;
-  (void)dtype;
+  if (dtype != TSC_F32 && c_in % 4 == 0 && c_out % 16 == 0) return kNarrow;
   return kValu;
 }
+
+// Steps of 32 reduction values (slot, channel) of the narrow kernel; the last
+// is padded with zero weights.
+int64_t narrow_steps(int K, int c_in) { return ceil_div((int64_t)K * c_in, 32); }
 
 // ----------------------------------------------------------- weight pack --
 __device__ __forceinline__ float load_any(const void* p, int dt, int64_t i) {
@@ -176,6 +186,29 @@ __global__ void pack_mfma_kernel(const void* w, int w_dt, int layout, int K, int
 // through the current slot read zeros from here instead of branching around
 // their loads (64 bytes per lane are read at most).
 __device__ __attribute__((aligned(256))) uint4 g_zero_row[16];
+
+// Narrow layout: [step i][c_out/16][lane][8].  Lane l of 16-column tile n
+// supplies column n*16 + l%16 and the reduction values r = 32i + 8(l/16) +
+// 0..7, r = k * C_in + c for slot k and channel c (zero past K * C_in): the
+// values the A operand's lane l gathers for its row.
+template <typename T>
+__global__ void pack_narrow_kernel(const void* w, int w_dt, int layout, int K, int c_in,
+                                   int c_out, int64_t nsteps, T* packed) {
+  const int nt_all = c_out / 16;
+  const int64_t total = nsteps * nt_all * 64 * 8;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int v = e % 8;
+    const int lane = (e / 8) % 64;
+    const int nt = (e / 512) % nt_all;
+    const int64_t i = e / (512 * (int64_t)nt_all);
+    const int64_t r = 32 * i + 8 * (lane / 16) + v;
+    const int k = static_cast<int>(r / c_in);
+    const int ci = static_cast<int>(r % c_in);
+    const int co = nt * 16 + lane % 16;
+    packed[e] = from_f32<T>(k < K ? src_weight(w, w_dt, layout, K, c_in, c_out, k, ci, co) : 0.f);
+  }
+}
 
 // ---------------------------------------------------------------- VALU --
 // VB: bytes of one feature load (16 or 8 when every row is a whole number of
@@ -583,6 +616,167 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
   }
 }
 
+// --------------------------------------------------------- narrow MFMA --
+// f16/bf16 layers with C_in % 4 == 0 and C_out % 16 == 0 that the 32x32 tile
+// does not take.  The reduction runs over r = k * C_in + c (slot k, channel
+// c) in steps of 32 on v_mfma_f32_16x16x32: a wave owns 16 output rows and NT
+// 16-column tiles.  Lane l supplies row l%16's values r = 32i + 8(l/16) ..
+// +7 of step i, gathered straight from the input rows the map names: one
+// 16-byte piece when C_in % 8 == 0, else two 8-byte pieces of four channels
+// each (the zero row for absent neighbours and the padding past K * C_in).
+// A group of steps loads all its map entries, then all its gathers and
+// weight operands, then runs its MFMAs, so a 3x3x3 layer with C_in = 4 (four
+// steps) costs two dependent memory round trips.  Each output is the same
+// sequence of MFMAs whatever the row order, so results are bitwise
+// reproducible and independent of the execution order.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T> struct Mfma16;
+template <> struct Mfma16<__half> {
+  using V = f16x8;
+  static __device__ __forceinline__ f32x4 run(V a, V b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma16<__hip_bfloat16> {
+  using V = bf16x8;
+  static __device__ __forceinline__ f32x4 run(V a, V b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+constexpr int kNarrowRows = 16;  // output rows per wave (the MFMA's M)
+
+__device__ __forceinline__ uint4 join_pieces(const uint4& a, const uint4&) { return a; }
+__device__ __forceinline__ uint4 join_pieces(const uint2& a, const uint2& b) {
+  return make_uint4(a.x, a.y, b.x, b.y);
+}
+
+// Entry i of a per-channel parameter, or dflt where the pointer is null.  The
+// load is issued either way (from the zero row), so a run of these issues
+// back to back instead of one branch and wait at a time.
+__device__ __forceinline__ float param_or(const void* p, int dt, int64_t i, float dflt) {
+  const float v = load_param(p ? p : static_cast<const void*>(g_zero_row), dt, p ? i : 0);
+  return p ? v : dflt;
+}
+
+// PIECE: bytes per gather (16 or 8); NT: 16-column tiles per wave.  A group
+// is SG steps: 8 / NT gathers and 32 / NP weight registers per lane.
+template <typename T, int PIECE, int NT>
+__global__ void __launch_bounds__(256) conv_narrow_kernel(
+    const T* __restrict__ feat, int c_in, const T* __restrict__ W, Epilogue ep,
+    const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int nbr_ordered,
+    int64_t n_out, int K, int c_out, int nsteps, T* __restrict__ out) {
+  using Op = Mfma16<T>;
+  using V = typename Op::V;
+  using Piece = typename VecOf<PIECE>::type;
+  constexpr int NP = 16 / PIECE;  // pieces per lane and step
+  constexpr int SG = 8 / (NP * NT) > 0 ? 8 / (NP * NT) : 1;
+  static_assert(PIECE == 16 || PIECE == 8, "8- or 16-byte pieces");
+  const int lane = threadIdx.x & 63;
+  const uint32_t q = lane >> 4;  // which 8 values of a step this lane supplies
+  const int rl = lane & 15;      // A row, B and D column of this lane
+  const int64_t p0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * kNarrowRows;
+  const int64_t pa = p0 + rl;  // processing position of this lane's A row
+  const bool va = pa < n_out;
+  const int32_t oa = va ? (order ? order[pa] : static_cast<int32_t>(pa)) : 0;
+  const int64_t col = nbr_ordered ? pa : oa;  // its column of the map
+  const int nt_all = c_out / 16;
+  const int nt0 = blockIdx.y * NT;
+  uint64_t zero_addr = reinterpret_cast<uint64_t>(g_zero_row);
+  asm volatile("" : "+s"(zero_addr));
+  // global (not flat) loads for both the gathered rows and the zero row
+  const Piece* zero_piece =
+      (const Piece*)reinterpret_cast<const __attribute__((address_space(1))) Piece*>(zero_addr);
+  const uint4* Wv = reinterpret_cast<const uint4*>(W);
+
+  // the epilogue's per-column parameters: loaded before the main loop (their
+  // latency overlaps the map loads), combined after it
+  float bias[NT], mean[NT], var[NT], gamma[NT], beta[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const int co = (nt0 + n) * 16 + rl;
+    bias[n] = param_or(ep.bias, ep.bias_dt, co, 0.f);
+    mean[n] = param_or(ep.mean, ep.bn_dt, co, 0.f);
+    var[n] = param_or(ep.var, ep.bn_dt, co, 1.f);
+    gamma[n] = param_or(ep.gamma, ep.bn_dt, co, 1.f);
+    beta[n] = param_or(ep.beta, ep.bn_dt, co, 0.f);
+  }
+  // The identity map (1x1x1 layers): its map loads read 0 from the zero row
+  // and its row is added on, so the loop has no branch on which map it reads.
+  const int32_t* map = nbr ? nbr : reinterpret_cast<const int32_t*>(g_zero_row);
+  const int64_t map_mask = nbr ? ~int64_t(0) : 0;
+  const int32_t ident_row = nbr ? 0 : oa;
+
+  f32x4 acc[NT];
+#pragma unroll
+  for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int i0 = 0; i0 < nsteps; i0 += SG) {
+    int32_t j[SG * NP];
+    uint32_t ch[SG * NP];
+#pragma unroll
+    for (int u = 0; u < SG * NP; ++u) {
+      const int i = i0 + u / NP;
+      const uint32_t r = 32u * static_cast<uint32_t>(i) + 8u * q + 4u * static_cast<uint32_t>(u % NP);
+      const uint32_t k = r / static_cast<uint32_t>(c_in);
+      ch[u] = r - k * static_cast<uint32_t>(c_in);
+      const bool live = va && i < nsteps && k < static_cast<uint32_t>(K);
+      // every lane loads (dead ones from slot K-1 of their column), so the
+      // group's map loads issue back to back; dead lanes then use -1
+      const int64_t kk = live ? k : K - 1;
+      const int32_t e = map[(kk * n_out + col) & map_mask];
+      // an OR rather than a select: the load's value is then always used, and
+      // the compiler keeps it unconditional instead of branching around it
+      j[u] = (e + ident_row) | (live ? 0 : -1);
+    }
+    Piece v[SG * NP];
+#pragma unroll
+    for (int u = 0; u < SG * NP; ++u) {
+      const Piece* src = j[u] >= 0
+                             ? reinterpret_cast<const Piece*>(feat + (int64_t)j[u] * c_in + ch[u])
+                             : zero_piece;
+      v[u] = *src;
+    }
+    uint4 b[SG][NT];
+#pragma unroll
+    for (int u = 0; u < SG; ++u)
+#pragma unroll
+      for (int n = 0; n < NT; ++n)
+        b[u][n] = i0 + u < nsteps ? Wv[((int64_t)(i0 + u) * nt_all + nt0 + n) * 64 + lane]
+                                  : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int u = 0; u < SG; ++u) {
+      if (i0 + u >= nsteps) break;
+      const V a = __builtin_bit_cast(V, join_pieces(v[u * NP], v[u * NP + NP - 1]));
+#pragma unroll
+      for (int n = 0; n < NT; ++n) acc[n] = Op::run(a, __builtin_bit_cast(V, b[u][n]), acc[n]);
+    }
+  }
+
+  // D: lane l holds rows 4(l/16) + 0..3 of the wave's 16, column l%16; the
+  // output row of wave row r is lane r's oa
+  int32_t orow[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int r = 4 * static_cast<int>(q) + e;
+    const int32_t o = __shfl(oa, r, kWave);
+    orow[e] = p0 + r < n_out ? o : -1;
+  }
+#pragma unroll
+  for (int n = 0; n < NT; ++n) {
+    const int co = (nt0 + n) * 16 + rl;
+    // the batch norm as v * sc + sh, in the order channel_affine computes it
+    const float sc = gamma[n] * (1.f / sqrtf(var[n] + ep.eps));
+    const float sh = beta[n] - mean[n] * sc;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (orow[e] >= 0)
+        out[(int64_t)orow[e] * c_out + co] = from_f32<T>(
+            finish(acc[n][e] + bias[n], sc, sh, ep.mean != nullptr, ep.relu != 0));
+  }
+}
+
 template <typename T, int BN, int CK>
 int launch_mfma(const void* feat, int c_in, const void* W, const Epilogue& ep,
                 const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
@@ -639,6 +833,49 @@ int dispatch_mfma(const void* feat, int c_in, const void* W, const Epilogue& ep,
   TSC_MFMA_CASE(32, 32)
 #undef TSC_MFMA_CASE
   return set_error(TSC_EUNSUPPORTED, "conv: no MFMA tile for c_in=%d c_out=%d", c_in, c_out);
+}
+
+template <typename T, int PIECE, int NT>
+int launch_narrow(const void* feat, int c_in, const void* W, const Epilogue& ep,
+                  const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
+                  int c_out, void* out, hipStream_t s) {
+  const int64_t nsteps = narrow_steps(K, c_in);
+  TSC_REQUIRE(nsteps < (int64_t(1) << 26), "conv: K * C_in too large");
+  dim3 grid(static_cast<unsigned>(ceil_div(n_out, 4 * kNarrowRows)),
+            static_cast<unsigned>(c_out / 16 / NT));
+  conv_narrow_kernel<T, PIECE, NT><<<grid, 256, 0, s>>>(
+      static_cast<const T*>(feat), c_in, static_cast<const T*>(W), ep, nbr, order, nbr_ordered,
+      n_out, K, c_out, static_cast<int>(nsteps), static_cast<T*>(out));
+  TSC_LAUNCH_CHECK("conv_narrow");
+  return 0;
+}
+
+template <typename T>
+int dispatch_narrow(const void* feat, int c_in, const void* W, const Epilogue& ep,
+                    const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out,
+                    int K, int c_out, void* out, hipStream_t s) {
+  // Column tiles per wave: up to 4, fewer while that leaves under 2048
+  // workgroups (each extra column group re-gathers its rows, from cache).
+  const int nt_all = c_out / 16;
+  const int64_t blocks = ceil_div(n_out, 4 * kNarrowRows);
+  int nt = nt_all % 4 == 0 ? 4 : (nt_all % 2 == 0 ? 2 : 1);
+  while (nt > 1 && blocks * (nt_all / nt) < 2048) nt /= 2;
+  const int piece = c_in % 8 == 0 ? 16 : 8;
+  TSC_REQUIRE((reinterpret_cast<uintptr_t>(feat) & (piece - 1)) == 0 &&
+                  (reinterpret_cast<uintptr_t>(W) & 15) == 0,
+              "conv: features must be %d-byte and weights 16-byte aligned", piece);
+#define TSC_NARROW_CASE(P_, NT_)                                                             \
+  if (piece == P_ && nt == NT_)                                                              \
+    return launch_narrow<T, P_, NT_>(feat, c_in, W, ep, nbr, order, nbr_ordered, n_out, K, \
+                                     c_out, out, s);
+  TSC_NARROW_CASE(16, 1)
+  TSC_NARROW_CASE(16, 2)
+  TSC_NARROW_CASE(16, 4)
+  TSC_NARROW_CASE(8, 1)
+  TSC_NARROW_CASE(8, 2)
+  TSC_NARROW_CASE(8, 4)
+#undef TSC_NARROW_CASE
+  return set_error(TSC_EUNSUPPORTED, "conv: no narrow tile for c_in=%d c_out=%d", c_in, c_out);
 }
 
 template <typename T, int CO>
@@ -699,6 +936,8 @@ extern "C" int64_t tsc_packed_weight_bytes(int32_t k_vol, int32_t c_in, int32_t 
     const int ck = pick_ck(dtype, c_in);
     return (int64_t)k_vol * mfma_chunks(c_in, ck) * ck * c_out * dtype_bytes(dtype);
   }
+  if (pick_path(dtype, c_in, c_out, k_vol) == kNarrow)
+    return narrow_steps(k_vol, c_in) * 32 * c_out * dtype_bytes(dtype);
   return (int64_t)k_vol * c_in * c_out * 4;
 }
 
@@ -710,9 +949,18 @@ extern "C" int tsc_pack_weight(const void* w, int32_t w_dtype, int32_t layout, i
   TSC_REQUIRE(layout == 0 || layout == 1, "pack: layout must be 0 (KRSC) or 1 (flat)");
   TSC_REQUIRE(k_vol > 0 && c_in > 0 && c_out > 0, "pack: sizes must be positive");
   TSC_REQUIRE(w && packed, "pack: null pointer");
-  const int64_t total = (int64_t)k_vol * (c_in + 32) * c_out;  // covers a padded chunk
+  const int64_t total = (int64_t)k_vol * (c_in + 32) * c_out;  // covers a padded chunk or step
   const int grid = static_cast<int>(ceil_div(total, 256) < 2048 ? ceil_div(total, 256) : 2048);
-  if (pick_path(dtype, c_in, c_out, k_vol) == kMfma) {
+  const Path path = pick_path(dtype, c_in, c_out, k_vol);
+  if (path == kNarrow) {
+    const int64_t nsteps = narrow_steps(k_vol, c_in);
+    if (dtype == TSC_F16)
+      pack_narrow_kernel<__half><<<grid, 256, 0, s>>>(w, w_dtype, layout, k_vol, c_in, c_out,
+                                                      nsteps, static_cast<__half*>(packed));
+    else
+      pack_narrow_kernel<__hip_bfloat16><<<grid, 256, 0, s>>>(
+          w, w_dtype, layout, k_vol, c_in, c_out, nsteps, static_cast<__hip_bfloat16*>(packed));
+  } else if (path == kMfma) {
     const int ck = pick_ck(dtype, c_in);
     if (dtype == TSC_F32)
       pack_mfma_kernel<float><<<grid, 256, 0, s>>>(w, w_dtype, layout, k_vol, c_in, c_out, ck,
@@ -769,6 +1017,13 @@ static int conv_forward(const void* feat, int32_t dtype, int64_t n_in, int32_t c
                                    c_out, out, s);
     return dispatch_mfma<__hip_bfloat16>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out,
                                          k_vol, c_out, out, s);
+  }
+  if (path == kNarrow) {
+    if (dtype == TSC_F16)
+      return dispatch_narrow<__half>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out,
+                                     k_vol, c_out, out, s);
+    return dispatch_narrow<__hip_bfloat16>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered,
+                                           n_out, k_vol, c_out, out, s);
   }
   if (dtype == TSC_F32)
     return dispatch_valu<float>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out, k_vol,
