@@ -247,7 +247,7 @@ def main():
                            "frac": pb_bytes / (pair_ms * 1e6) / HBM_PEAK_GBS},
         "plan_ms": plan_ms,
         "conv_kernel_ms": kern_ms,
-        "roofline": roofline(layer, k_vol, tflops, peak, unit, alg_bytes, kern_ms),
+        "roofline": roofline(layer, k_vol, tflops, peak, unit, alg_bytes, kern_ms, w.dtype),
     }
     traffic = measured_traffic(w.name, kern_ms)
     if traffic is not None:
@@ -339,6 +339,13 @@ def encoder_bench(args, w, dev):
     net.fuse_epilogues = True
     cold_steps = max(args.steps // 10, 5)
     cold_ms, _ = timed(lambda: net(fresh()), cold_steps, 3)
+    # the fused forward captured once in a HIP graph and replayed: the GPU's
+    # own time per pass, without the host's launch time
+    graph = torch.cuda.CUDAGraph()
+    with torch.no_grad(), torch.cuda.graph(graph):
+        y_graph = net(warm)
+    graph_ms, _ = timed(graph.replay, args.steps, args.warmup)
+    graph_equal = bool(torch.equal(y_graph.features, y.features))
     rel = float((y.features.float() - y_plain.features.float()).abs().max()
                 / y_plain.features.float().abs().max().clamp_min(1e-30))
 
@@ -423,6 +430,8 @@ def encoder_bench(args, w, dev):
         "network_ms_fused": fused_ms,
         "network_ms_unfused": unfused_ms,
         "network_ms_cold": cold_ms,
+        "network_ms_graph": graph_ms,
+        "graph_equal": graph_equal,
         "fused_vs_unfused_rel_err": rel,
         "tflops_effective": flops_total / (fused_ms * 1e-3) / 1e12,
         "layers": per_layer,
@@ -432,10 +441,11 @@ def encoder_bench(args, w, dev):
     print(json.dumps(result), flush=True)
 
 
-def roofline(layer, k_vol, tflops, peak, unit, alg_bytes, kern_ms):
-    """The conv kernel against its bound: MFMA peak on the matrix-core path
+def roofline(layer, k_vol, tflops, peak, unit, alg_bytes, kern_ms, dtype):
+    """The conv kernel against its bound: MFMA peak on the 32x32-tile path
     (C_in a multiple of 16, C_out of 32, K <= 64), else HBM bandwidth (the
-    VALU path serves narrow layers whose arithmetic is small)."""
+    narrow-MFMA and VALU paths serve narrow layers whose arithmetic is
+    small)."""
     if layer["c_in"] % 16 == 0 and layer["c_out"] % 32 == 0 and k_vol <= 64:
         return {"bound": "mfma", "achieved": tflops, "peak": peak, "unit": unit,
                 "frac": tflops / peak, "traffic": None, "algorithmic_bytes": alg_bytes,
@@ -443,7 +453,8 @@ def roofline(layer, k_vol, tflops, peak, unit, alg_bytes, kern_ms):
     gbs = alg_bytes / (kern_ms * 1e6)
     return {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": gbs / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes": alg_bytes,
-            "kernel": "conv_valu_kernel"}
+            "kernel": "conv_narrow_kernel" if dtype != "float32" and layer["c_in"] % 4 == 0
+            and layer["c_out"] % 16 == 0 else "conv_valu_kernel"}
 
 
 def measured_traffic(workload: str, kern_ms: float):

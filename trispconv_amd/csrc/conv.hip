@@ -312,9 +312,22 @@ template <> struct MfmaOp<float> {
 };
 
 constexpr int kTileRows = kConvTileRows;  // 4 waves x 64 rows
+constexpr int kSplitRows = 64;            // rows of a small-layer tile (its 4 waves split the slots)
 
 
 template <int N> using Slot = std::integral_constant<int, N>;
+
+// XCD placement: workgroups are dispatched round-robin over the 8 XCDs, in
+// grid order.  Row tiles are dealt round-robin too (the execution order puts
+// the tiles with the most slots first, so every XCD gets an even share of the
+// heavy ones), and all column tiles of a row tile run one after another on the
+// same XCD, sharing its L2 for the gathered rows.  Returns the work item
+// (row tile * ncol + column tile) of workgroup lin.
+__device__ __forceinline__ uint32_t dealt_item(uint32_t lin, uint32_t grid, uint32_t ncol) {
+  const uint32_t dealt = (grid / (8 * ncol)) * (8 * ncol);  // whole rounds of 8 row tiles
+  const uint32_t x = lin % 8, j = lin / 8;
+  return lin < dealt ? ((j / ncol) * 8 + x) * ncol + j % ncol : lin;
+}
 
 // Output rows each wave stages per epilogue pass: 32 rows of up to 256 bytes,
 // else 16, so the staging area stays within 35 KB for two workgroups per CU.
@@ -358,19 +371,9 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
   const int lane = t & 63;
   const int wave = t >> 6;
   const int h = lane >> 5;
-  // XCD placement: workgroups are dispatched round-robin over the 8 XCDs, in
-  // grid order.  Row tiles are dealt round-robin too (the execution order puts
-  // the tiles with the most slots first, so every XCD gets an even share of
-  // the heavy ones), and all column tiles of a row tile run one after another
-  // on the same XCD, sharing its L2 for the gathered rows.
   const uint32_t ncol = static_cast<uint32_t>(c_out / BN);
-  uint32_t item;  // the launch keeps the grid below 2^31 workgroups
-  {
-    const uint32_t lin = blockIdx.x;
-    const uint32_t dealt = (gridDim.x / (8 * ncol)) * (8 * ncol);  // whole rounds of 8 row tiles
-    const uint32_t x = lin % 8, j = lin / 8;
-    item = lin < dealt ? ((j / ncol) * 8 + x) * ncol + j % ncol : lin;
-  }
+  // the launch keeps the grid below 2^31 workgroups
+  const uint32_t item = dealt_item(blockIdx.x, gridDim.x, ncol);
   const int64_t tile0 = static_cast<int64_t>(item / ncol) * kTileRows;
   const int nbt = static_cast<int>(item % ncol);
   const int nch = (c_in + CK - 1) / CK;  // C_in % 16 == 0: the last chunk may be half padding
@@ -616,6 +619,251 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
   }
 }
 
+// ------------------------------------------------- small-layer split --
+// Layers too small to give half the CUs a 256-row tile (a LiDAR encoder's
+// deepest layers, ~10k rows).  There the 256-row kernel is bound by one
+// tile's chain of 27 stages per CU.  This kernel takes 64-row tiles and splits
+// the slots over the tile's four waves: wave w takes the slots k with
+// k % 4 == w that some row of the tile uses, and loads its weight operands
+// straight from global memory into registers (no shared slab, no barrier per
+// stage).  The waves' partial sums meet in LDS and are added in wave order,
+// ((p0 + p1) + p2) + p3.  Each row's p_w is its own slots of residue w in
+// ascending order (a slot the row does not use adds exact zeros), so every
+// output is still a fixed sequence of fp32 operations, independent of which
+// rows share its tile.
+template <typename T, int BN, int CK>
+__global__ void __launch_bounds__(256, 2) conv_split_kernel(
+    const T* __restrict__ feat, int c_in, const T* __restrict__ W, Epilogue ep,
+    const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int nbr_ordered,
+    int64_t n_out, int K, int c_out, T* __restrict__ out) {
+  using Op = MfmaOp<T>;
+  using V = typename Op::V;
+  constexpr bool F32 = std::is_same<T, float>::value;
+  constexpr int VPL = 16 / (int)sizeof(T);  // values per 16-byte vector
+  constexpr int UB = (CK / 2) / VPL;        // vectors per lane per row and stage
+  static_assert(UB * VPL * 2 == CK && UB >= 1, "chunk must split into 16-byte runs");
+  constexpr int NB = BN / 32;               // 32-wide column blocks
+  constexpr int SR = kSplitRows;
+  constexpr int PART = 2 * NB * 16 * 64;    // floats of one wave's partial sums
+
+  __shared__ int32_t s_orow[SR];
+  __shared__ float s_bias[BN], s_scale[BN], s_shift[BN];
+  __shared__ uint64_t s_mask[4];
+  extern __shared__ int32_t s_dyn[];  // [K][SR] map entries, then 3 waves' partial sums
+  int32_t* s_nbr = s_dyn;
+  float* s_part = reinterpret_cast<float*>(s_dyn + K * SR);
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int h = lane >> 5;
+  const uint32_t ncol = static_cast<uint32_t>(c_out / BN);
+  const uint32_t item = dealt_item(blockIdx.x, gridDim.x, ncol);
+  const int64_t tile0 = static_cast<int64_t>(item / ncol) * SR;
+  const int nbt = static_cast<int>(item % ncol);
+  const int nch = (c_in + CK - 1) / CK;
+
+  // ---- set-up: wave w reads the map entries of its own slots for the 64
+  // rows, eight slots at a time, all eight loads in flight before any is used
+  {
+    const int64_t tr = tile0 + lane;
+    const int32_t orow = tr < n_out ? (order ? order[tr] : static_cast<int32_t>(tr)) : -1;
+    if (wave == 0) s_orow[lane] = orow;
+    const int64_t src_row = orow >= 0 ? (nbr_ordered ? tr : orow) : 0;
+    if (t < BN) {
+      const int64_t col = (int64_t)nbt * BN + t;
+      s_bias[t] = ep.bias ? load_param(ep.bias, ep.bias_dt, col) : 0.f;
+      channel_affine(ep, col, s_scale[t], s_shift[t]);
+    }
+    uint64_t m = 0;
+    for (int i0 = 0; wave + 4 * i0 < K; i0 += 8) {
+      int32_t jv[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int k = wave + 4 * (i0 + i);
+        const int kk = k < K ? k : K - 1;
+        jv[i] = nbr ? nbr[(int64_t)kk * n_out + src_row]
+                    : static_cast<int32_t>(orow >= 0 ? orow : 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int k = wave + 4 * (i0 + i);
+        const int32_t j = orow >= 0 ? jv[i] : -1;
+        if (k < K) {
+          s_nbr[k * SR + lane] = j;
+          m |= (j >= 0 ? uint64_t(1) : uint64_t(0)) << k;
+        }
+      }
+    }
+    uint32_t lo = static_cast<uint32_t>(m), hi = static_cast<uint32_t>(m >> 32);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      lo |= __shfl_xor(lo, off, kWave);
+      hi |= __shfl_xor(hi, off, kWave);
+    }
+    if (lane == 0) s_mask[wave] = (static_cast<uint64_t>(hi) << 32) | lo;
+  }
+  __syncthreads();
+  // this wave's slots (wave-uniform, scalar registers)
+  const uint64_t mine_v = s_mask[wave];
+  const uint64_t mine =
+      (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(mine_v >> 32))) << 32) |
+      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(mine_v));
+  const int r0 = lane & 31;  // tile rows of this lane's A operands
+  const int r1 = r0 + 32;
+
+  auto advance = [&](int& k, int& c) {
+    const bool done = k >= K;
+    const bool more_c = c + 1 < nch;
+    const uint64_t above = k + 1 < 64 ? mine >> (k + 1) : 0;
+    const int nk = above ? k + 1 + __builtin_ctzll(above) : K;
+    const int k2 = done ? K : (more_c ? k : nk);
+    c = done ? c : (more_c ? c + 1 : 0);
+    k = k2;
+  };
+
+  const uint4* Wv = reinterpret_cast<const uint4*>(W);
+  const int nbt_all = c_out / 32;
+  uint64_t zero_addr = reinterpret_cast<uint64_t>(g_zero_row);
+  asm volatile("" : "+s"(zero_addr));
+  const uint4* zero_row =
+      (const uint4*)reinterpret_cast<const __attribute__((address_space(1))) uint4*>(zero_addr);
+
+  f32x16 acc[2][NB];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[rb][nb][i] = 0.f;
+
+  uint4 ring[2][2][UB];   // gathered operands: this stage and the next
+  uint4 bring[2][NB][UB];  // weight operands: this stage and the next
+
+  // Loads are issued whether or not the stage exists (past the last stage they
+  // re-read stage 0 or the zero row), keeping the loop body straight-line.
+  auto load_b = [&](auto slot, int k, int c) {
+    constexpr int S = decltype(slot)::value;
+    if (k >= K) k = c = 0;
+    const uint4* src = Wv + (((int64_t)k * nch + c) * nbt_all + (int64_t)nbt * NB) * UB * 64 + lane;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int u = 0; u < UB; ++u) bring[S][nb][u] = src[(nb * UB + u) * 64];
+  };
+  auto load_a = [&](auto slot, int k, int c) {
+    constexpr int S = decltype(slot)::value;
+    const bool live = k < K;
+    const int kk = live ? k : K - 1;
+    const int32_t e0 = s_nbr[kk * SR + r0];
+    const int32_t e1 = s_nbr[kk * SR + r1];
+    const int32_t j0 = live ? e0 : -1;
+    const int32_t j1 = live ? e1 : -1;
+    const int coff = c * CK + h * (CK / 2);
+    const bool pad = coff >= c_in;  // the upper half of a half-filled last chunk
+    const uint4* p0 = j0 >= 0 && !pad
+                          ? reinterpret_cast<const uint4*>(feat + (int64_t)j0 * c_in + coff)
+                          : zero_row;
+    const uint4* p1 = j1 >= 0 && !pad
+                          ? reinterpret_cast<const uint4*>(feat + (int64_t)j1 * c_in + coff)
+                          : zero_row;
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+      ring[S][0][u] = p0[u];
+      ring[S][1][u] = p1[u];
+    }
+  };
+  auto compute = [&](auto slot, int k) {
+    constexpr int S = decltype(slot)::value;
+    if (k >= K) return;
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint4 bv = bring[S][nb][u];
+        if constexpr (F32) {
+          const float4 a0 = __builtin_bit_cast(float4, ring[S][0][u]);
+          const float4 a1 = __builtin_bit_cast(float4, ring[S][1][u]);
+          const float4 b4 = __builtin_bit_cast(float4, bv);
+          acc[0][nb] = Op::run(a0.x, b4.x, acc[0][nb]);
+          acc[1][nb] = Op::run(a1.x, b4.x, acc[1][nb]);
+          acc[0][nb] = Op::run(a0.y, b4.y, acc[0][nb]);
+          acc[1][nb] = Op::run(a1.y, b4.y, acc[1][nb]);
+          acc[0][nb] = Op::run(a0.z, b4.z, acc[0][nb]);
+          acc[1][nb] = Op::run(a1.z, b4.z, acc[1][nb]);
+          acc[0][nb] = Op::run(a0.w, b4.w, acc[0][nb]);
+          acc[1][nb] = Op::run(a1.w, b4.w, acc[1][nb]);
+        } else {
+          const V b = __builtin_bit_cast(V, bv);
+          acc[0][nb] = Op::run(__builtin_bit_cast(V, ring[S][0][u]), b, acc[0][nb]);
+          acc[1][nb] = Op::run(__builtin_bit_cast(V, ring[S][1][u]), b, acc[1][nb]);
+        }
+      }
+    }
+  };
+
+  int kc = -1, cc = nch - 1;
+  advance(kc, cc);  // this wave's first slot
+  int kn = kc, cn = cc;
+  advance(kn, cn);
+  load_b(Slot<0>{}, kc, cc);
+  load_a(Slot<0>{}, kc, cc);
+  auto body = [&](auto slot) {
+    constexpr int S = decltype(slot)::value;
+    load_b(Slot<(S + 1) % 2>{}, kn, cn);  // next stage's weights
+    load_a(Slot<(S + 1) % 2>{}, kn, cn);  // and operands
+    __builtin_amdgcn_sched_barrier(0);
+    compute(Slot<S>{}, kc);
+    kc = kn;
+    cc = cn;
+    advance(kn, cn);
+  };
+  while (kc < K) {
+    body(Slot<0>{});
+    body(Slot<1>{});
+  }
+
+  // ---- waves 1-3 hand their partial sums to wave 0, which adds them in wave
+  // order and stores.  32x32 accumulator layout: register i of lane l holds
+  // row (i/4)*8 + (l/32)*4 + i%4 and column l%32 of the block.
+  if (wave > 0) {
+    float* dst = s_part + (wave - 1) * PART;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) dst[((rb * NB + nb) * 16 + i) * 64 + lane] = acc[rb][nb][i];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 0; w < 3; ++w)
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          acc[rb][nb][i] += s_part[w * PART + ((rb * NB + nb) * 16 + i) * 64 + lane];
+  const bool affine = ep.mean != nullptr;
+  const bool relu = ep.relu != 0;
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = rb * 32 + (i >> 2) * 8 + h * 4 + (i & 3);
+      const int32_t orow = s_orow[row];
+      if (orow < 0) continue;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int cl = nb * 32 + (lane & 31);
+        out[(int64_t)orow * c_out + nbt * BN + cl] =
+            from_f32<T>(finish(acc[rb][nb][i] + s_bias[cl], s_scale[cl], s_shift[cl], affine, relu));
+      }
+    }
+}
+
 // --------------------------------------------------------- narrow MFMA --
 // f16/bf16 layers with C_in % 4 == 0 and C_out % 16 == 0 that the 32x32 tile
 // does not take.  The reduction runs over r = k * C_in + c (slot k, channel
@@ -797,6 +1045,23 @@ int launch_mfma(const void* feat, int c_in, const void* W, const Epilogue& ep,
   return 0;
 }
 
+template <typename T, int BN, int CK>
+int launch_split(const void* feat, int c_in, const void* W, const Epilogue& ep,
+                 const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
+                 int c_out, void* out, hipStream_t s) {
+  const int64_t items = ceil_div(n_out, kSplitRows) * (c_out / BN);
+  TSC_REQUIRE(items < (int64_t(1) << 31), "conv: %lld workgroups exceed the grid limit",
+              static_cast<long long>(items));
+  // dynamic LDS: the tile's map entries, then three waves' partial sums
+  const size_t lds = (size_t)K * kSplitRows * sizeof(int32_t) +
+                     (size_t)3 * 2 * (BN / 32) * 16 * 64 * sizeof(float);
+  conv_split_kernel<T, BN, CK><<<dim3(static_cast<unsigned>(items)), 256, lds, s>>>(
+      static_cast<const T*>(feat), c_in, static_cast<const T*>(W), ep, nbr, order,
+      nbr_ordered, n_out, K, c_out, static_cast<T*>(out));
+  TSC_LAUNCH_CHECK("conv_split");
+  return 0;
+}
+
 template <typename T>
 int dispatch_mfma(const void* feat, int c_in, const void* W, const Epilogue& ep,
                   const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
@@ -809,20 +1074,36 @@ int dispatch_mfma(const void* feat, int c_in, const void* W, const Epilogue& ep,
   int bn = pick_bn(c_out);
   const int ck = pick_ck(dt, c_in);
   while (bn > 32 && ceil_div(n_out, kTileRows) * (c_out / bn) < 512) bn /= 2;
-  // TSC_CONV_TILE=BN forces the column tile width (for tests that compare the
-  // widths: each sums every output in the same order, so all give the same
-  // bits).
+  // TSC_CONV_TILE=BN forces the 256-row kernel with that column tile width
+  // (for tests that compare the widths: each sums every output in the same
+  // order, so all give the same bits).
+  bool forced = false;
   if (const char* force = std::getenv("TSC_CONV_TILE")) {
     int fb = 0;
     TSC_REQUIRE(std::sscanf(force, "%d", &fb) == 1 && (fb == 32 || fb == 64 || fb == 128) &&
                     c_out % fb == 0,
                 "conv: TSC_CONV_TILE=%s is not a column tile width for c_out=%d", force, c_out);
     bn = fb;
+    forced = true;
   }
+  // Layers that would leave more than half the CUs without a 256-row
+  // workgroup run on 64-row tiles with the slots split over the waves (the
+  // narrowing above has then always reached 32 columns).  Measured on 64->64
+  // fp16 SubM layers: 9.7k rows (76 workgroups) 28.8 -> 20.0 us, but 32k rows
+  // (252 workgroups) 30.7 -> 38 us, where the four waves' separate weight
+  // loads cost more than the shorter slot chain saves.
+  // Short slot lists (K < 8) gain nothing from splitting.
+  const bool split =
+      !forced && bn == 32 && K >= 8 && ceil_div(n_out, kTileRows) * (c_out / bn) < 128;
 #define TSC_MFMA_CASE(BN_, CK_)                                                              \
-  if (bn == BN_ && ck == CK_)                                                                \
+  if (bn == BN_ && ck == CK_) {                                                              \
+    if constexpr (BN_ == 32)                                                                 \
+      if (split)                                                                             \
+        return launch_split<T, BN_, CK_>(feat, c_in, W, ep, nbr, order, nbr_ordered, n_out,  \
+                                         K, c_out, out, s);                                  \
     return launch_mfma<T, BN_, CK_>(feat, c_in, W, ep, nbr, order, nbr_ordered,          \
-                                    n_out, K, c_out, out, s);
+                                    n_out, K, c_out, out, s);                                \
+  }
   if constexpr (!std::is_same<T, float>::value) {
     TSC_MFMA_CASE(128, 64)
     TSC_MFMA_CASE(64, 64)
