@@ -247,7 +247,7 @@ def main():
                            "frac": pb_bytes / (pair_ms * 1e6) / HBM_PEAK_GBS},
         "plan_ms": plan_ms,
         "conv_kernel_ms": kern_ms,
-        "roofline": roofline(layer, k_vol, tflops, peak, unit, alg_bytes, kern_ms, w.dtype),
+        "roofline": roofline(layer, k_vol, tflops, peak, unit, alg_bytes, kern_ms),
     }
     traffic = measured_traffic(w.name, kern_ms)
     if traffic is not None:
@@ -441,7 +441,7 @@ def encoder_bench(args, w, dev):
     print(json.dumps(result), flush=True)
 
 
-def roofline(layer, k_vol, tflops, peak, unit, alg_bytes, kern_ms, dtype):
+def roofline(layer, k_vol, tflops, peak, unit, alg_bytes, kern_ms):
     """The conv kernel against its bound: MFMA peak on the 32x32-tile path
     (C_in a multiple of 16, C_out of 32, K <= 64), else HBM bandwidth (the
     narrow-MFMA and VALU paths serve narrow layers whose arithmetic is
@@ -453,7 +453,7 @@ def roofline(layer, k_vol, tflops, peak, unit, alg_bytes, kern_ms, dtype):
     gbs = alg_bytes / (kern_ms * 1e6)
     return {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": gbs / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes": alg_bytes,
-            "kernel": "conv_narrow_kernel" if dtype != "float32" and layer["c_in"] % 4 == 0
+            "kernel": "conv_narrow_kernel" if layer["c_in"] % 4 == 0
             and layer["c_out"] % 16 == 0 else "conv_valu_kernel"}
 
 

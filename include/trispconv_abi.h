@@ -199,10 +199,12 @@ TSC_API int tsc_pack_weight(const void* w, int32_t w_dtype, int32_t layout, int3
  * sparse_conv_forward (trispconv/pytorch/functional.py:14-51) and the Triton
  * per-slot kernel (triton_kernels.py:16-135).  Output-stationary: each
  * output row accumulates sum_k feat[nbr[k][o]] @ W[k] in fp32 with k
- * ascending (f16/bf16 layers with C_in % 4 == 0 and C_out % 16 == 0 that
- * are not 32x32-tile shapes sum 32 (slot, channel) products per matrix-core
- * step instead), adds bias in fp32 and is rounded once to `dtype`.  No
- * atomics; results are bitwise reproducible and independent of `order`.
+ * ascending (layers with C_in % 4 == 0 and C_out % 16 == 0 that are not
+ * 32x32-tile shapes sum 16 bytes of (slot, channel) products per lane quad
+ * and matrix-core step instead; the smallest 32x32-tile layers sum the slots
+ * of each residue mod 4 apart, then the four partial sums in order), adds
+ * bias in fp32 and is rounded once to `dtype`.  No atomics; results are
+ * bitwise reproducible and independent of `order`.
  *   nbr == NULL means the identity map with k_vol == 1 (1x1x1 layers).
  *   order == NULL means rows in index order.
  *   nbr_ordered != 0 means nbr is the plan's permuted map (entry (k, t)

@@ -97,12 +97,14 @@ LAYER_CASES = [
     # C_in an odd multiple of 16: the last 32-channel chunk is half padding
     (16, 64, torch.float32), (48, 32, torch.bfloat16), (80, 96, torch.float16),
     (16, 128, torch.bfloat16),
-    # the narrow kernel (f16/bf16, C_in % 4 == 0, C_out % 16 == 0): 8-byte
-    # pieces (C_in % 8 == 4, a piece never straddles two slots), 16-byte
-    # pieces, 16-column tiles that do not pair up, many reduction steps
+    # the narrow kernel (C_in % 4 == 0, C_out % 16 == 0): 8-byte pieces
+    # (f16/bf16 with C_in % 8 == 4, a piece never straddles two slots), 16-byte
+    # pieces, 16-column tiles that do not pair up, many reduction steps, and
+    # f32 on v_mfma_f32_16x16x4_f32
     (4, 16, torch.float16), (12, 48, torch.float16), (4, 32, torch.bfloat16),
     (8, 16, torch.bfloat16), (16, 48, torch.float16), (40, 80, torch.float16),
-    (64, 16, torch.bfloat16),
+    (64, 16, torch.bfloat16), (4, 16, torch.float32), (12, 48, torch.float32),
+    (64, 16, torch.float32),
 ]
 
 
@@ -127,7 +129,7 @@ def test_strided_layer(c_in, c_out, dtype, k, s, p):
 
 
 @pytest.mark.parametrize("c_in,c_out,dtype", [(4, 64, torch.float16), (8, 32, torch.bfloat16),
-                                              (12, 64, torch.bfloat16)])
+                                              (12, 64, torch.bfloat16), (4, 64, torch.float32)])
 def test_narrow_layers_with_several_column_tiles_per_wave(c_in, c_out, dtype):
     """Layers of 150 000 rows: enough workgroups for the narrow kernel to give
     each wave two or four 16-column tiles.  Checked on 3000 random rows."""
@@ -138,10 +140,11 @@ def test_narrow_layers_with_several_column_tiles_per_wave(c_in, c_out, dtype):
     _check_layer(m, feats, idx, shape, 1, dtype, rows=3000, what=f"narrow {c_in}->{c_out}")
 
 
-@pytest.mark.parametrize("c_in,c_out,dtype", [(16, 32, torch.float16), (4, 16, torch.bfloat16)])
+@pytest.mark.parametrize("c_in,c_out,dtype", [(16, 32, torch.float16), (4, 16, torch.bfloat16),
+                                              (8, 16, torch.float32)])
 def test_layers_of_more_than_64_slots(c_in, c_out, dtype):
     """5x5x5 (125 slots): past the 32x32 tile's slot table, so the narrow
-    kernel takes these shapes; its reduction runs over 63 and 16 steps."""
+    kernel takes these shapes; its reduction runs over 63, 16 and 63 steps."""
     idx = _tiny(25, (18, 20, 22), 2, 2500)
     feats = np.random.default_rng(26).standard_normal((len(idx), c_in)).astype(np.float32)
     m = _module("subm", c_in, c_out, 5, dtype=dtype, seed=11)

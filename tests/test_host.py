@@ -173,11 +173,12 @@ def test_workspace_queries_are_host_only():
     # C_in an odd multiple of 16 packs a 32-channel chunk whose upper half is zero
     assert lib.tsc_packed_weight_bytes(27, 16, 32, L.F16) == 27 * 32 * 32 * 2
     assert lib.tsc_packed_weight_bytes(27, 48, 64, L.F32) == 27 * 64 * 64 * 4
-    # narrow f16/bf16 layers pack 32-value reduction steps (27 * 4 -> 4 steps,
-    # the last padded), fp32 ones stay on the VALU layout
+    # narrow layers pack 16-byte reduction steps per lane quad: 32 values for
+    # f16/bf16 (27 * 4 -> 4 steps, the last padded), 16 for f32 (27 * 4 -> 7);
+    # C_in not a multiple of 4 stays on the fp32 VALU layout
     assert lib.tsc_packed_weight_bytes(27, 4, 16, L.F16) == 4 * 32 * 16 * 2
     assert lib.tsc_packed_weight_bytes(125, 16, 32, L.BF16) == 63 * 32 * 32 * 2
-    assert lib.tsc_packed_weight_bytes(27, 4, 16, L.F32) == 27 * 4 * 16 * 4
+    assert lib.tsc_packed_weight_bytes(27, 4, 16, L.F32) == 7 * 16 * 16 * 4
     assert lib.tsc_packed_weight_bytes(27, 3, 16, L.F16) == 27 * 3 * 16 * 4
 
 

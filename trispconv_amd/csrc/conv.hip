@@ -19,10 +19,11 @@
 //   * mfma: f32/f16/bf16 with C_in a multiple of 16, C_out of 32 and K <= 64
 //     — v_mfma_f32_32x32x16_{f16,bf16} or v_mfma_f32_32x32x2_f32, 4 waves x
 //     (64 rows x BN cols) per tile.
-//   * narrow: the other f16/bf16 layers with C_in % 4 == 0 and C_out % 16 ==
-//     0 (a LiDAR encoder's 4 -> 16 first layer, 16-wide outputs, K > 64) —
-//     v_mfma_f32_16x16x32 over (slot, channel) pairs, 16 rows per wave.
-//   * valu: everything else (fp32 narrow or ragged channels, odd widths) —
+//   * narrow: the other layers with C_in % 4 == 0 and C_out % 16 == 0 (a
+//     LiDAR encoder's 4 -> 16 first layer, 16-wide outputs, K > 64) —
+//     v_mfma_f32_16x16x32_{f16,bf16} or v_mfma_f32_16x16x4_f32 over (slot,
+//     channel) pairs, 16 rows per wave.
+//   * valu: everything else (C_in not a multiple of 4 or C_out not of 16) —
 //     one output row per lane and CO columns per thread, weights read with
 //     wave-uniform addresses, slots skipped when no lane of the wave needs
 //     them.
@@ -60,17 +61,20 @@ int64_t mfma_chunks(int c_in, int ck) { return ceil_div(c_in, ck); }
 
 // MFMA for every dtype when C_in is a multiple of 16 and C_out of 32 (the
 // slot table of K <= 64 slots fits LDS); the narrow MFMA kernel for the other
-// f16/bf16 layers whose channels come in 4-channel pieces and 16-column
-// tiles; VALU otherwise.
+// layers whose channels come in 4-channel pieces and 16-column tiles; VALU
+// otherwise.
 Path pick_path(int dtype, int c_in, int c_out, int K) {
   if (c_in % 16 == 0 && c_out % 32 == 0 && K <= 64) return kMfma;
-  if (dtype != TSC_F32 && c_in % 4 == 0 && c_out % 16 == 0) return kNarrow;
+  if (c_in % 4 == 0 && c_out % 16 == 0) return kNarrow;
   return kValu;
 }
 
-// Steps of 32 reduction values (slot, channel) of the narrow kernel; the last
-// is padded with zero weights.
-int64_t narrow_steps(int K, int c_in) { return ceil_div((int64_t)K * c_in, 32); }
+// Steps of the narrow kernel: 16 bytes of reduction values (slot, channel)
+// per lane quad, i.e. 32 values for f16/bf16 and 16 for f32; the last step is
+// padded with zero weights.
+int64_t narrow_steps(int dtype, int K, int c_in) {
+  return ceil_div((int64_t)K * c_in, 4 * (16 / dtype_bytes(dtype)));
+}
 
 // ----------------------------------------------------------- weight pack --
 __device__ __forceinline__ float load_any(const void* p, int dt, int64_t i) {
@@ -187,22 +191,24 @@ __global__ void pack_mfma_kernel(const void* w, int w_dt, int layout, int K, int
 // their loads (64 bytes per lane are read at most).
 __device__ __attribute__((aligned(256))) uint4 g_zero_row[16];
 
-// Narrow layout: [step i][c_out/16][lane][8].  Lane l of 16-column tile n
-// supplies column n*16 + l%16 and the reduction values r = 32i + 8(l/16) +
-// 0..7, r = k * C_in + c for slot k and channel c (zero past K * C_in): the
-// values the A operand's lane l gathers for its row.
+// Narrow layout: [step i][c_out/16][lane][LV], LV = 16 / sizeof(T) values.
+// Lane l of 16-column tile n supplies column n*16 + l%16 and the reduction
+// values r = 4*LV*i + LV*(l/16) + 0..LV-1, r = k * C_in + c for slot k and
+// channel c (zero past K * C_in): the values the A operand's lane l gathers
+// for its row.
 template <typename T>
 __global__ void pack_narrow_kernel(const void* w, int w_dt, int layout, int K, int c_in,
                                    int c_out, int64_t nsteps, T* packed) {
+  constexpr int LV = 16 / (int)sizeof(T);
   const int nt_all = c_out / 16;
-  const int64_t total = nsteps * nt_all * 64 * 8;
+  const int64_t total = nsteps * nt_all * 64 * LV;
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
        e += (int64_t)gridDim.x * blockDim.x) {
-    const int v = e % 8;
-    const int lane = (e / 8) % 64;
-    const int nt = (e / 512) % nt_all;
-    const int64_t i = e / (512 * (int64_t)nt_all);
-    const int64_t r = 32 * i + 8 * (lane / 16) + v;
+    const int v = e % LV;
+    const int lane = (e / LV) % 64;
+    const int nt = (e / (64 * LV)) % nt_all;
+    const int64_t i = e / (64 * LV * (int64_t)nt_all);
+    const int64_t r = 4 * LV * i + LV * (lane / 16) + v;
     const int k = static_cast<int>(r / c_in);
     const int ci = static_cast<int>(r % c_in);
     const int co = nt * 16 + lane % 16;
@@ -865,13 +871,15 @@ __global__ void __launch_bounds__(256, 2) conv_split_kernel(
 }
 
 // --------------------------------------------------------- narrow MFMA --
-// f16/bf16 layers with C_in % 4 == 0 and C_out % 16 == 0 that the 32x32 tile
-// does not take.  The reduction runs over r = k * C_in + c (slot k, channel
-// c) in steps of 32 on v_mfma_f32_16x16x32: a wave owns 16 output rows and NT
-// 16-column tiles.  Lane l supplies row l%16's values r = 32i + 8(l/16) ..
-// +7 of step i, gathered straight from the input rows the map names: one
-// 16-byte piece when C_in % 8 == 0, else two 8-byte pieces of four channels
-// each (the zero row for absent neighbours and the padding past K * C_in).
+// Layers with C_in % 4 == 0 and C_out % 16 == 0 that the 32x32 tile does not
+// take.  The reduction runs over r = k * C_in + c (slot k, channel c) in steps
+// of 4*LV values, LV = 16 / sizeof(T): one v_mfma_f32_16x16x32 for f16/bf16,
+// four v_mfma_f32_16x16x4_f32 for f32.  A wave owns 16 output rows and NT
+// 16-column tiles.  Lane l supplies row l%16's values r = 4*LV*i + LV*(l/16)
+// .. +LV-1 of step i, gathered straight from the input rows the map names: one
+// 16-byte piece, or for f16/bf16 with C_in % 8 == 4 two 8-byte pieces of four
+// channels each (the zero row for absent neighbours and the padding past
+// K * C_in).
 // A group of steps loads all its map entries, then all its gathers and
 // weight operands, then runs its MFMAs, so a 3x3x3 layer with C_in = 4 (four
 // steps) costs two dependent memory round trips.  Each output is the same
@@ -879,17 +887,29 @@ __global__ void __launch_bounds__(256, 2) conv_split_kernel(
 // reproducible and independent of the execution order.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// One step on 16-byte operands per lane: a 16x16x32 MFMA for f16/bf16, four
+// 16x16x4 MFMAs for f32 (MFMA e takes element e of every lane's vectors).
 template <typename T> struct Mfma16;
 template <> struct Mfma16<__half> {
-  using V = f16x8;
-  static __device__ __forceinline__ f32x4 run(V a, V b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  static __device__ __forceinline__ f32x4 step(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
   }
 };
 template <> struct Mfma16<__hip_bfloat16> {
-  using V = bf16x8;
-  static __device__ __forceinline__ f32x4 run(V a, V b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  static __device__ __forceinline__ f32x4 step(uint4 a, uint4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+template <> struct Mfma16<float> {
+  static __device__ __forceinline__ f32x4 step(uint4 a, uint4 b, f32x4 c) {
+    const float4 fa = __builtin_bit_cast(float4, a);
+    const float4 fb = __builtin_bit_cast(float4, b);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(fa.x, fb.x, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(fa.y, fb.y, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(fa.z, fb.z, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(fa.w, fb.w, c, 0, 0, 0);
   }
 };
 
@@ -916,11 +936,12 @@ __global__ void __launch_bounds__(256) conv_narrow_kernel(
     const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int nbr_ordered,
     int64_t n_out, int K, int c_out, int nsteps, T* __restrict__ out) {
   using Op = Mfma16<T>;
-  using V = typename Op::V;
   using Piece = typename VecOf<PIECE>::type;
-  constexpr int NP = 16 / PIECE;  // pieces per lane and step
+  constexpr int LV = 16 / (int)sizeof(T);      // reduction values per lane and step
+  constexpr int VPP = PIECE / (int)sizeof(T);  // values per piece
+  constexpr int NP = 16 / PIECE;               // pieces per lane and step
   constexpr int SG = 8 / (NP * NT) > 0 ? 8 / (NP * NT) : 1;
-  static_assert(PIECE == 16 || PIECE == 8, "8- or 16-byte pieces");
+  static_assert(PIECE == 16 || (PIECE == 8 && sizeof(T) == 2), "8- or 16-byte pieces");
   const int lane = threadIdx.x & 63;
   const uint32_t q = lane >> 4;  // which 8 values of a step this lane supplies
   const int rl = lane & 15;      // A row, B and D column of this lane
@@ -966,7 +987,7 @@ __global__ void __launch_bounds__(256) conv_narrow_kernel(
 #pragma unroll
     for (int u = 0; u < SG * NP; ++u) {
       const int i = i0 + u / NP;
-      const uint32_t r = 32u * static_cast<uint32_t>(i) + 8u * q + 4u * static_cast<uint32_t>(u % NP);
+      const uint32_t r = 4u * LV * static_cast<uint32_t>(i) + LV * q + VPP * static_cast<uint32_t>(u % NP);
       const uint32_t k = r / static_cast<uint32_t>(c_in);
       ch[u] = r - k * static_cast<uint32_t>(c_in);
       const bool live = va && i < nsteps && k < static_cast<uint32_t>(K);
@@ -996,9 +1017,9 @@ __global__ void __launch_bounds__(256) conv_narrow_kernel(
 #pragma unroll
     for (int u = 0; u < SG; ++u) {
       if (i0 + u >= nsteps) break;
-      const V a = __builtin_bit_cast(V, join_pieces(v[u * NP], v[u * NP + NP - 1]));
+      const uint4 a = join_pieces(v[u * NP], v[u * NP + NP - 1]);
 #pragma unroll
-      for (int n = 0; n < NT; ++n) acc[n] = Op::run(a, __builtin_bit_cast(V, b[u][n]), acc[n]);
+      for (int n = 0; n < NT; ++n) acc[n] = Op::step(a, b[u][n], acc[n]);
     }
   }
 
@@ -1120,7 +1141,9 @@ template <typename T, int PIECE, int NT>
 int launch_narrow(const void* feat, int c_in, const void* W, const Epilogue& ep,
                   const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
                   int c_out, void* out, hipStream_t s) {
-  const int64_t nsteps = narrow_steps(K, c_in);
+  constexpr int dt = std::is_same<T, float>::value ? TSC_F32
+                     : std::is_same<T, __half>::value ? TSC_F16 : TSC_BF16;
+  const int64_t nsteps = narrow_steps(dt, K, c_in);
   TSC_REQUIRE(nsteps < (int64_t(1) << 26), "conv: K * C_in too large");
   dim3 grid(static_cast<unsigned>(ceil_div(n_out, 4 * kNarrowRows)),
             static_cast<unsigned>(c_out / 16 / NT));
@@ -1141,7 +1164,7 @@ int dispatch_narrow(const void* feat, int c_in, const void* W, const Epilogue& e
   const int64_t blocks = ceil_div(n_out, 4 * kNarrowRows);
   int nt = nt_all % 4 == 0 ? 4 : (nt_all % 2 == 0 ? 2 : 1);
   while (nt > 1 && blocks * (nt_all / nt) < 2048) nt /= 2;
-  const int piece = c_in % 8 == 0 ? 16 : 8;
+  const int piece = (c_in % 8 == 0 || std::is_same<T, float>::value) ? 16 : 8;
   TSC_REQUIRE((reinterpret_cast<uintptr_t>(feat) & (piece - 1)) == 0 &&
                   (reinterpret_cast<uintptr_t>(W) & 15) == 0,
               "conv: features must be %d-byte and weights 16-byte aligned", piece);
@@ -1152,9 +1175,11 @@ int dispatch_narrow(const void* feat, int c_in, const void* W, const Epilogue& e
   TSC_NARROW_CASE(16, 1)
   TSC_NARROW_CASE(16, 2)
   TSC_NARROW_CASE(16, 4)
-  TSC_NARROW_CASE(8, 1)
-  TSC_NARROW_CASE(8, 2)
-  TSC_NARROW_CASE(8, 4)
+  if constexpr (sizeof(T) == 2) {
+    TSC_NARROW_CASE(8, 1)
+    TSC_NARROW_CASE(8, 2)
+    TSC_NARROW_CASE(8, 4)
+  }
 #undef TSC_NARROW_CASE
   return set_error(TSC_EUNSUPPORTED, "conv: no narrow tile for c_in=%d c_out=%d", c_in, c_out);
 }
@@ -1218,7 +1243,7 @@ extern "C" int64_t tsc_packed_weight_bytes(int32_t k_vol, int32_t c_in, int32_t 
     return (int64_t)k_vol * mfma_chunks(c_in, ck) * ck * c_out * dtype_bytes(dtype);
   }
   if (pick_path(dtype, c_in, c_out, k_vol) == kNarrow)
-    return narrow_steps(k_vol, c_in) * 32 * c_out * dtype_bytes(dtype);
+    return narrow_steps(dtype, k_vol, c_in) * (c_out / 16) * 64 * 16;
   return (int64_t)k_vol * c_in * c_out * 4;
 }
 
@@ -1234,8 +1259,11 @@ extern "C" int tsc_pack_weight(const void* w, int32_t w_dtype, int32_t layout, i
   const int grid = static_cast<int>(ceil_div(total, 256) < 2048 ? ceil_div(total, 256) : 2048);
   const Path path = pick_path(dtype, c_in, c_out, k_vol);
   if (path == kNarrow) {
-    const int64_t nsteps = narrow_steps(k_vol, c_in);
-    if (dtype == TSC_F16)
+    const int64_t nsteps = narrow_steps(dtype, k_vol, c_in);
+    if (dtype == TSC_F32)
+      pack_narrow_kernel<float><<<grid, 256, 0, s>>>(w, w_dtype, layout, k_vol, c_in, c_out,
+                                                     nsteps, static_cast<float*>(packed));
+    else if (dtype == TSC_F16)
       pack_narrow_kernel<__half><<<grid, 256, 0, s>>>(w, w_dtype, layout, k_vol, c_in, c_out,
                                                       nsteps, static_cast<__half*>(packed));
     else
@@ -1300,6 +1328,9 @@ static int conv_forward(const void* feat, int32_t dtype, int64_t n_in, int32_t c
                                          k_vol, c_out, out, s);
   }
   if (path == kNarrow) {
+    if (dtype == TSC_F32)
+      return dispatch_narrow<float>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out,
+                                    k_vol, c_out, out, s);
     if (dtype == TSC_F16)
       return dispatch_narrow<__half>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out,
                                      k_vol, c_out, out, s);
