@@ -108,7 +108,15 @@ def ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+# torch's accessor for the current stream's raw handle: a per-layer call, and
+# cheaper than building a Stream object through torch.cuda.current_stream
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
+    """The caller's current stream on ``t``'s device, as a hipStream_t."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream
 
 

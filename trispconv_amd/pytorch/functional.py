@@ -44,7 +44,7 @@ def _bn_operands(ep: Epilogue, c_out: int, device) -> list:
         if ep.weight is not None or ep.bias is not None:
             raise ValueError("sparse_conv_forward: batch-norm weight/bias without statistics")
         return [None] * 4
-    ts = [t.detach() if t is not None else None for t in (ep.mean, ep.var, ep.weight, ep.bias)]
+    ts = (ep.mean, ep.var, ep.weight, ep.bias)
     for t in ts:
         if t is not None and (t.device != device or t.numel() != c_out):
             raise ValueError("sparse_conv_forward: batch-norm tensors must have "
@@ -53,7 +53,10 @@ def _bn_operands(ep: Epilogue, c_out: int, device) -> list:
     dt = dts.pop() if len(dts) == 1 else torch.float32
     if dt not in _PARAM_DTYPES:
         dt = torch.float32
-    return [t.to(dt).contiguous() if t is not None else None for t in ts]
+    # only their addresses are passed: tensors already in that form go as they are
+    return [None if t is None else
+            t if t.dtype == dt and t.is_contiguous() else t.detach().to(dt).contiguous()
+            for t in ts]
 
 
 def _run(features: torch.Tensor, packed: PackedWeight, bias: Optional[torch.Tensor],
@@ -70,7 +73,8 @@ def _run(features: torch.Tensor, packed: PackedWeight, bias: Optional[torch.Tens
     out = torch.empty((n_out, packed.c_out), dtype=feats.dtype, device=feats.device)
     b = None
     if bias is not None:
-        b = bias.detach().to(feats.device).contiguous()
+        b = bias if bias.device == feats.device and bias.is_contiguous() else \
+            bias.detach().to(feats.device).contiguous()
         if b.numel() != packed.c_out:
             raise ValueError(f"bias has {b.numel()} entries, expected {packed.c_out}")
     lib = L.lib()
