@@ -290,3 +290,25 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch):
     monkeypatch.setattr(L, "LIB_PATH", tmp_path / "libtrispconv_hip.so")
     with pytest.raises(RuntimeError, match="trispconv_amd.build"):
         L.lib()
+
+
+def test_pending_pair_counts_are_read_and_checked_on_first_access():
+    """A submanifold build on a strided layer's bitmap leaves its counts on the
+    device; pair_num reads them on first access and raises if the build
+    flagged rows that are not the bitmap's cells."""
+    from trispconv_amd.pytorch.indices import IndiceData
+
+    def data(counts):
+        d = IndiceData(torch.zeros((1, 4), dtype=torch.int32), None, None, None,
+                       torch.zeros((1, 4), dtype=torch.int32), (4, 4, 4), (4, 4, 4), (3, 1, 1),
+                       (1, 1, 1), (0, 0, 0), (1, 1, 1), True)
+        d._counts_pending = (torch.tensor(counts, dtype=torch.int32), 3)
+        return d
+
+    d = data([3, 0, 5, 0])
+    assert d.pair_num.dtype == torch.int64 and d.pair_num.tolist() == [3, 0, 5]
+    assert d._counts_pending is None
+    d.pair_num = torch.tensor([1, 1, 1])
+    assert d.pair_num.tolist() == [1, 1, 1]
+    with pytest.raises(RuntimeError, match="not the rows"):
+        data([1, 1, 1, L.FLAG_ROWS_NOT_BITMAP]).pair_num

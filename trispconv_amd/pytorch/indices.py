@@ -78,6 +78,9 @@ class IndiceData:
         self.dilation = tuple(dilation)
         self.subm = subm
         self.pair_num = pair_num
+        # a build whose counts stay on the device until pair_num is read:
+        # (counts [K + 1] int32, K); counts[K] holds the build's status flags
+        self._counts_pending: Optional[Tuple[torch.Tensor, int]] = None
         self._pairs_in = pairs_in
         self._pairs_out = pairs_out
         # device tables
@@ -101,6 +104,27 @@ class IndiceData:
         # strided builds: input rows with at least one pair, i.e. the row
         # count of this layer's inverse, read with the build's counts
         self._n_in_paired: Optional[int] = None
+
+    @property
+    def pair_num(self) -> torch.Tensor:
+        """Pairs per slot, a CPU int64 tensor (indices.py:131).  A build that
+        left its counts on the device (a submanifold build on a strided
+        layer's bitmap, which has no coordinates to check) is read here, on
+        first access, so the forward pass does not wait for it."""
+        if self._pair_num is None and self._counts_pending is not None:
+            counts, K = self._counts_pending
+            host = counts.cpu()
+            if int(host[K]) & L.FLAG_ROWS_NOT_BITMAP:
+                raise RuntimeError("generate_subm_indice_pairs: coordinates are not the rows of "
+                                   "the strided build they were registered with")
+            self._pair_num = host[:K].long()
+            self._counts_pending = None
+        return self._pair_num
+
+    @pair_num.setter
+    def pair_num(self, value: torch.Tensor) -> None:
+        self._pair_num = value
+        self._counts_pending = None
 
     # --------------------------------------------------- construction
     @classmethod
@@ -300,16 +324,19 @@ def _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil):
         coords.data_ptr(), n, int(batch_size), L.i3(shape), L.i3(ks), L.i3(dil), ws.data_ptr(),
         nwords, cols_row.data_ptr(), map_cols.data_ptr(), counts.data_ptr(), L.stream_of(coords)),
         "generate_subm_indice_pairs")
-    host = counts.cpu()
-    if int(host[K]) & L.FLAG_ROWS_NOT_BITMAP:
-        raise RuntimeError("generate_subm_indice_pairs: coordinates are not the rows of the "
-                           "strided build they were registered with")
-    return IndiceData._from_tables(
+    # No read-back here: the rows are the registered output set (same tensor,
+    # same version), so there is nothing to validate before the convolution.
+    # The counts and the status flag (rows that are not the bitmap's cells,
+    # whose neighbours the kernel leaves out of the map) are read with
+    # pair_num.
+    d = IndiceData._from_tables(
         out_indices=indices, input_indices=indices, input_spatial_shape=shape,
         output_spatial_shape=shape, kernel_size=ks, stride=(1, 1, 1), padding=(0, 0, 0),
-        dilation=dil, subm=True, pin=None, pout=None, cnt_dev=None, pair_num=host[:K].long(),
+        dilation=dil, subm=True, pin=None, pout=None, cnt_dev=None, pair_num=None,
         nbr=None, batch_size=int(batch_size), map_cols=map_cols, cols_row=cols_row[:n],
         raster=True)
+    d._counts_pending = (counts, K)
+    return d
 
 
 def generate_subm_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size: int, kernel_size,
