@@ -21,12 +21,13 @@
 // Output values never depend on the order: every row's fp32 accumulation
 // sees the same slots in the same ascending order and absent slots add zero.
 //
-// Sorting: stable LSD radix passes with 8-bit digits.  Each pass is a
-// histogram kernel (per-block digit counts, digit-major), one exclusive scan
-// of all counts and a stable scatter in which each wave ranks equal digits
-// with eight ballots.  The first sort orders rows by their Morton code; the
-// second carries Morton positions as values and takes its digits from the
-// mask at that position, then from the region (position / region_rows).
+// Sorting: stable LSD radix passes with 9-bit digits (a 27-slot mask sorts
+// in three passes).  Each pass is a histogram kernel (per-block digit counts,
+// digit-major), one exclusive scan of all counts and a stable scatter in
+// which each wave ranks equal digits with nine ballots.  The first sort
+// orders rows by their Morton code; the second carries Morton positions as
+// values and takes its digits from the mask at that position, then from the
+// region (position / region_rows).
 #include "common.hpp"
 
 #include <utility>
@@ -37,7 +38,8 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kItems = 8;                     // per thread per block
 constexpr int kTile = kThreads * kItems;      // items per block
-constexpr int kRadix = 256;
+constexpr int kDigitBits = 9;
+constexpr int kRadix = 1 << kDigitBits;
 
 // Digit sources of a pass.
 enum DigitSrc { kFromKey = 0, kFromMaskAtValue = 1, kFromRegionOfValue = 2 };
@@ -58,7 +60,7 @@ __device__ __forceinline__ uint32_t digit_of(const Digits& d, int64_t i, uint32_
     k = d.mask_pos[value];
   else
     k = value / d.region_rows;
-  return (k >> d.shift) & 0xffu;
+  return (k >> d.shift) & (kRadix - 1u);
 }
 
 // Spreads the low 10 bits of v to every third bit.
@@ -206,7 +208,7 @@ __global__ void __launch_bounds__(kThreads) radix_hist_kernel(const uint32_t* __
                                                               uint32_t* __restrict__ hist,
                                                               int nblk) {
   __shared__ uint32_t s_h[kRadix];
-  s_h[threadIdx.x] = 0;
+  for (int r = threadIdx.x; r < kRadix; r += kThreads) s_h[r] = 0;
   __syncthreads();
   const int64_t base = blockIdx.x * (int64_t)kTile;
 #pragma unroll
@@ -215,7 +217,7 @@ __global__ void __launch_bounds__(kThreads) radix_hist_kernel(const uint32_t* __
     if (i < n) atomicAdd(&s_h[digit_of(d, i, vals[i])], 1u);
   }
   __syncthreads();
-  hist[(int64_t)threadIdx.x * nblk + blockIdx.x] = s_h[threadIdx.x];
+  for (int r = threadIdx.x; r < kRadix; r += kThreads) hist[(int64_t)r * nblk + blockIdx.x] = s_h[r];
 }
 
 __global__ void __launch_bounds__(kThreads) radix_scatter_kernel(
@@ -226,11 +228,12 @@ __global__ void __launch_bounds__(kThreads) radix_scatter_kernel(
   __shared__ uint32_t s_wc[kThreads / kWave][kRadix];  // this round, per wave, per digit
   const int t = threadIdx.x;
   const int w = t / kWave;
-  s_run[t] = hist_off[(int64_t)t * nblk + blockIdx.x];
+  for (int r = t; r < kRadix; r += kThreads) s_run[r] = hist_off[(int64_t)r * nblk + blockIdx.x];
   const int64_t base = blockIdx.x * (int64_t)kTile;
   for (int j = 0; j < kItems; ++j) {
+    for (int r = t; r < kRadix; r += kThreads)
 #pragma unroll
-    for (int ww = 0; ww < kThreads / kWave; ++ww) s_wc[ww][t] = 0;
+      for (int ww = 0; ww < kThreads / kWave; ++ww) s_wc[ww][r] = 0;
     __syncthreads();
     const int64_t i = base + j * kThreads + t;  // items stay in index order
     const bool valid = i < n;
@@ -240,7 +243,7 @@ __global__ void __launch_bounds__(kThreads) radix_scatter_kernel(
     // lanes of this wave holding the same digit
     uint64_t peers = __ballot(valid);
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
+    for (int b = 0; b < kDigitBits; ++b) {
       const uint64_t ones = __ballot((dg >> b) & 1u);
       peers &= ((dg >> b) & 1u) ? ones : ~ones;
     }
@@ -256,10 +259,12 @@ __global__ void __launch_bounds__(kThreads) radix_scatter_kernel(
       }
     }
     __syncthreads();
-    uint32_t add = 0;
+    for (int r = t; r < kRadix; r += kThreads) {
+      uint32_t add = 0;
 #pragma unroll
-    for (int ww = 0; ww < kThreads / kWave; ++ww) add += s_wc[ww][t];
-    s_run[t] += add;
+      for (int ww = 0; ww < kThreads / kWave; ++ww) add += s_wc[ww][r];
+      s_run[r] += add;
+    }
     __syncthreads();
   }
 }
@@ -357,7 +362,7 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_
     TSC_LAUNCH_CHECK("plan_spatial_key");
     uint32_t *ki = b.keys_a, *ko = b.keys_b, *vi = b.vals_a, *vo = b.vals_b;
     for (int p = 0; p < 4; ++p) {
-      const Digits d{kFromKey, 8 * p, ki, nullptr, 1u};
+      const Digits d{kFromKey, kDigitBits * p, ki, nullptr, 1u};
       uint32_t* vdst = (p == 3) ? b.rows : vo;  // the last pass leaves columns in Morton order
       if ((rc = radix_pass(b, ki, vi, ko, vdst, n_out, d, s))) return rc;
       std::swap(ki, ko);
@@ -378,13 +383,13 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_
   const int mask_bits = k_vol < 32 ? k_vol : 32;
   const int64_t regions = ceil_div(n_out, region_rows);
   const int region_bits = bits_for(static_cast<uint64_t>(regions - 1));
-  for (int p = 0; p < (mask_bits + 7) / 8; ++p) {
-    const Digits d{kFromMaskAtValue, 8 * p, nullptr, b.mask_pos, 1u};
+  for (int p = 0; p < (mask_bits + kDigitBits - 1) / kDigitBits; ++p) {
+    const Digits d{kFromMaskAtValue, kDigitBits * p, nullptr, b.mask_pos, 1u};
     if ((rc = radix_pass(b, nullptr, vi, nullptr, vo, n_out, d, s))) return rc;
     std::swap(vi, vo);
   }
-  for (int p = 0; p < (region_bits + 7) / 8; ++p) {
-    const Digits d{kFromRegionOfValue, 8 * p, nullptr, nullptr,
+  for (int p = 0; p < (region_bits + kDigitBits - 1) / kDigitBits; ++p) {
+    const Digits d{kFromRegionOfValue, kDigitBits * p, nullptr, nullptr,
                    static_cast<uint32_t>(region_rows)};
     if ((rc = radix_pass(b, nullptr, vi, nullptr, vo, n_out, d, s))) return rc;
     std::swap(vi, vo);
@@ -401,8 +406,8 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_
     TSC_LAUNCH_CHECK("plan_tile_key");
     const int key_bits = bits_for(static_cast<uint64_t>((n_tiles - 1) / tiles_per_region)) + 6;
     uint32_t *tki = b.keys_a, *tko = b.keys_a + n_tiles, *tvi = vo, *tvo = vo + n_tiles;
-    for (int p = 0; p < (key_bits + 7) / 8; ++p) {
-      const Digits d{kFromKey, 8 * p, tki, nullptr, 1u};
+    for (int p = 0; p < (key_bits + kDigitBits - 1) / kDigitBits; ++p) {
+      const Digits d{kFromKey, kDigitBits * p, tki, nullptr, 1u};
       if ((rc = radix_pass(b, tki, tvi, tko, tvo, n_tiles, d, s))) return rc;
       std::swap(tki, tko);
       std::swap(tvi, tvo);
