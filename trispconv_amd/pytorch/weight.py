@@ -8,8 +8,8 @@ form is read the same way; the internal layout passes through.
 
 The convolution never materialises that (K, C_in, C_out) tensor:
 ``pack_weight`` reads the module's parameter directly and writes the kernel's
-own layout (fp32 for the VALU path, MFMA operand order for the matrix-core
-path) in one HIP launch.  ``weight_source`` is the shared shape dispatch.
+own layout (fp32 for the VALU path, MFMA B-operand order for the 32x32-tile
+and narrow matrix-core paths) in one HIP launch.  ``weight_source`` is the shared shape dispatch.
 """
 from __future__ import annotations
 
