@@ -2,7 +2,8 @@
 
 Tolerance (max |out - ref| / max |ref|, oracle in fp64 over the rounded
 inputs and weights): 1e-5 for fp32, 1e-2 for fp16 and bf16.  Covers the VALU,
-narrow-MFMA and MFMA kernels, every MFMA tile shape, ragged and wide channels,
+narrow-MFMA, slot-split and 256-row MFMA kernels, every MFMA tile shape,
+ragged and wide channels,
 1x1x1 layers, the five workloads at full size (checked on a random subset of output
 rows), bitwise determinism and independence from the execution order.
 """
@@ -248,6 +249,33 @@ def test_deterministic_and_order_independent(c_in, c_out, dtype, monkeypatch):
     rev = torch.flip(data._order, [0]).contiguous()
     d = Fn._run(feats, pw, m.bias, data.neighbour_map(len(idx), feats.device), rev, len(idx))
     assert torch.equal(a, b) and torch.equal(a, c) and torch.equal(a, d)
+
+
+@pytest.mark.parametrize("c_in,c_out,dtype", [(64, 64, torch.float16), (32, 32, torch.bfloat16),
+                                              (64, 96, torch.float32)])
+def test_slot_split_kernel_matches_the_256_row_kernel(c_in, c_out, dtype, monkeypatch):
+    """A layer small enough for the slot-split kernel (64-row tiles, slots
+    split by residue mod 4 over the waves) against the same layer forced onto
+    the 256-row kernel: both within tolerance of the oracle and of each
+    other (their fp32 sums differ only in association)."""
+    idx = _tiny(27, (24, 24, 24), 1, 4000)
+    x = torch.from_numpy(idx).to(DEV)
+    feats = torch.randn(len(idx), c_in, generator=torch.Generator().manual_seed(3)).to(DEV).to(dtype)
+    data = generate_subm_indice_pairs(x, (24, 24, 24), 1, 3)
+    m = _module("subm", c_in, c_out, 3, dtype=dtype, seed=12)
+    pw = m._packed_weight(dtype)
+    split = Fn.sparse_conv_forward(feats, pw, m.bias, data, len(idx))
+    monkeypatch.setenv("TSC_CONV_TILE", "32")
+    whole = Fn.sparse_conv_forward(feats, pw, m.bias, data, len(idx))
+    monkeypatch.delenv("TSC_CONV_TILE")
+    pr = OP.subm_pairs(idx, (24, 24, 24), 1, 3, 1)
+    w = OC.normalize_weight(to_np(m.weight).astype(np.float64), (3, 3, 3), c_in, c_out)
+    ref = OC.conv_forward(to_np(feats).astype(np.float64), w,
+                          to_np(m.bias).astype(np.float64), pr.pairs_in, pr.pairs_out, len(idx))
+    say("split vs 256-row", c_in, c_out, dtype)
+    assert rel_err(to_np(split), ref) <= TOL[dtype]
+    assert rel_err(to_np(whole), ref) <= TOL[dtype]
+    assert rel_err(to_np(split), to_np(whole).astype(np.float64)) <= TOL[dtype]
 
 
 @pytest.mark.parametrize("c_in,c_out,dtype", [(64, 128, torch.float16), (32, 128, torch.bfloat16),
