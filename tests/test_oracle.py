@@ -238,3 +238,99 @@ def test_oracle_weight_layouts():
     assert OC.normalize_weight(W, (3, 2, 3), 4, 6) is not None
     with pytest.raises(ValueError):
         OC.normalize_weight(rng.normal(size=(5, 5)), 3, 4, 6)
+
+
+# ---------------------------------------------------------------------------
+# the torch restatement of the reference's CPU path (the timed CPU baseline):
+# brute force for pair order, golden fixtures for features and coordinates
+# ---------------------------------------------------------------------------
+from oracle import torch_path as TP  # noqa: E402
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a))
+
+
+@pytest.mark.parametrize("k,d", [(3, 1), (3, 2), (1, 1), ((3, 1, 3), (1, 2, 1)), ((2, 3, 2), 1)])
+def test_torch_path_subm_pairs_brute_force(k, d):
+    shape = (5, 6, 4)
+    idx = _tiny(7, shape, 2, 25)
+    pr = TP.subm_pairs(_t(idx), shape, 2, k, d)
+    pin, pout = brute.subm(idx, shape, OP.to3(k), OP.to3(d))
+    assert [p.tolist() for p in pr.pairs_in] == pin
+    assert [p.tolist() for p in pr.pairs_out] == pout
+    assert pr.pair_num.tolist() == [len(p) for p in pin]
+
+
+@pytest.mark.parametrize("k,s,p,d", [(3, 2, 1, 1), (2, 2, 0, 1), (2, 1, 0, 1), (3, 1, 1, 2),
+                                     ((3, 1, 1), (2, 1, 1), 0, 1), (3, (2, 1, 2), (1, 0, 1), 1)])
+def test_torch_path_strided_and_inverse_brute_force(k, s, p, d):
+    shape = (5, 6, 7)
+    idx = _tiny(11, shape, 2, 20)
+    pr = TP.strided_pairs(_t(idx), shape, 2, k, s, p, d)
+    out_idx, pin, pout, oshape = brute.strided(idx, shape, 2, OP.to3(k), OP.to3(s), OP.to3(p),
+                                               OP.to3(d))
+    assert pr.output_spatial_shape == oshape
+    assert np.array_equal(pr.out_indices.numpy(), out_idx)
+    assert [x.tolist() for x in pr.pairs_in] == pin
+    assert [x.tolist() for x in pr.pairs_out] == pout
+    inv = TP.inverse_pairs(pr)
+    bi_idx, bi_in, bi_out = brute.inverse(idx, pin, pout)
+    assert np.array_equal(inv.out_indices.numpy(), bi_idx)
+    assert [x.tolist() for x in inv.pairs_in] == bi_in
+    assert [x.tolist() for x in inv.pairs_out] == bi_out
+
+
+@pytest.mark.parametrize("name", golden_io.fixture_names())
+def test_torch_path_matches_spconv_golden(name):
+    a, m = golden_io.load(name)
+    k, s, p, d = m["kernel_size"], m["stride"], m["padding"], m["dilation"]
+    bias = None if a.get("bias") is None else _t(a["bias"]).double()
+    cache = {}
+    if m["conv_type"] in ("subm", "strided"):
+        lay = {"kind": m["conv_type"], "kernel_size": OP.to3(k), "stride": OP.to3(s),
+               "padding": OP.to3(p), "dilation": OP.to3(d), "indice_key": None}
+        out, coords, shape, _, _, _ = TP.run_layer(
+            lay, _t(a["features"]).double(), _t(a["indices"]), tuple(m["spatial_shape"]),
+            m["batch_size"], _t(a["weight"]).double(), bias, cache)
+    else:
+        down = {"kind": "strided", "kernel_size": OP.to3(k), "stride": OP.to3(s),
+                "padding": OP.to3(p), "dilation": OP.to3(d), "indice_key": "k"}
+        _, dcoords, dshape, _, _, _ = TP.run_layer(
+            down, _t(a["down_in_features"]).double(), _t(a["down_in_indices"]),
+            tuple(m["down_in_spatial_shape"]), m["batch_size"], _t(a["down_weight"]).double(),
+            None, cache)
+        ref_order = np.argsort(golden_io.encode(a["indices"], dshape), kind="stable")
+        ours_order = np.argsort(golden_io.encode(dcoords.numpy(), dshape), kind="stable")
+        feats = np.empty_like(a["features"])
+        feats[ours_order] = a["features"][ref_order]
+        inv = dict(down, kind="inverse")
+        out, coords, shape, _, _, _ = TP.run_layer(
+            inv, _t(feats).double(), dcoords, dshape, m["batch_size"],
+            _t(a["weight"]).double(), bias, cache)
+    f_sorted, i_sorted = golden_io.sort_by_coord(out.numpy(), coords.numpy(), shape)
+    assert np.array_equal(i_sorted, a["out_indices"])
+    np.testing.assert_allclose(f_sorted, a["out_features"], atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16, torch.bfloat16])
+def test_torch_path_conv_native_dtype_matches_oracle(dt):
+    """The CPU branch keeps the features' dtype (functional.py:46): its result
+    is the fp64 oracle's within that dtype's rounding."""
+    rng = np.random.default_rng(77)
+    shape = (10, 9, 8)
+    idx, feats = _random_sparse(rng, shape, 1, 150, 16)
+    w = rng.uniform(-0.3, 0.3, size=(24, 3, 3, 3, 16))
+    b = rng.uniform(-0.1, 0.1, size=24)
+    fr = _t(feats).to(dt)
+    wr = _t(w).to(dt)
+    br = _t(b).to(dt)
+    lay = {"kind": "subm", "kernel_size": (3, 3, 3), "stride": (1, 1, 1), "padding": (0, 0, 0),
+           "dilation": (1, 1, 1), "indice_key": None}
+    out, _, _, pr, _, _ = TP.run_layer(lay, fr, _t(idx), shape, 1, wr, br, {})
+    assert out.dtype == dt
+    ref, _, _, _ = OC.run_layer("subm", fr.double().numpy(), idx, shape, 1, wr.double().numpy(),
+                                br.double().numpy(), 3)
+    tol = {torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 4e-2}[dt]
+    err = np.abs(out.double().numpy() - ref).max() / np.abs(ref).max()
+    assert err < tol
