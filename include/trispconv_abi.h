@@ -240,6 +240,29 @@ TSC_API int tsc_conv_forward_ep(const void* feat, int32_t dtype, int64_t n_in, i
                                 void* out, tsc_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * tsc_conv_forward with the column tile width chosen by the caller instead
+ * of by the layer's size: column_tile = 32, 64 or 128 (dividing c_out) runs
+ * the 256-row 32x32-tile kernel with that width; 0 chooses as
+ * tsc_conv_forward does.  Every width sums each output in the same order, so
+ * all return the same bits.  No counterpart in the reference (its Triton
+ * path autotunes block sizes, triton_kernels.py:16-30); for tests that
+ * compare the widths.  Any other width, or a layer the 32x32 tile does not
+ * serve, is an argument error.
+ * ------------------------------------------------------------------------ */
+TSC_API int tsc_conv_forward_tile(const void* feat, int32_t dtype, int64_t n_in, int32_t c_in,
+                                  const void* packed_w, const void* bias, int32_t bias_dtype,
+                                  const int32_t* nbr, const int32_t* order, int32_t nbr_ordered,
+                                  int64_t n_out, int32_t k_vol, int32_t c_out,
+                                  int32_t column_tile, void* out, tsc_stream_t stream);
+
+/* Name of the kernel tsc_conv_forward launches for a layer of this shape
+ * ("conv_mfma_kernel", "conv_split_kernel", "conv_narrow_kernel" or
+ * "conv_valu_kernel"; "" for invalid sizes): what a kernel trace lists it
+ * under.  No counterpart in the reference; for profilers and benchmarks. */
+TSC_API const char* tsc_conv_kernel_name(int32_t dtype, int32_t c_in, int32_t c_out,
+                                         int32_t k_vol, int64_t n_out);
+
+/* ------------------------------------------------------------------------
  * Sparse -> dense.  Replaces SparseConvTensor.dense (trispconv/pytorch/
  * tensor.py:72-99): writes out, zero-filled, of shape (B, C, D, H, W) when
  * channels_first != 0 else (B, D, H, W, C), with row r's C features at its

@@ -4,8 +4,8 @@ Tolerance (max |out - ref| / max |ref|, oracle in fp64 over the rounded
 inputs and weights): 1e-5 for fp32, 1e-2 for fp16 and bf16.  Covers the VALU,
 narrow-MFMA, slot-split and 256-row MFMA kernels, every MFMA tile shape,
 ragged and wide channels,
-1x1x1 layers, the five workloads at full size (checked on a random subset of output
-rows), bitwise determinism and independence from the execution order.
+1x1x1 layers, the five workloads at full size (every output row), bitwise
+determinism and independence from the execution order.
 """
 import numpy as np
 import pytest
@@ -18,6 +18,7 @@ from oracle import pairs as OP
 from trispconv.pytorch import functional as Fn
 from trispconv.pytorch.indices import generate_strided_indice_pairs, generate_subm_indice_pairs
 from trispconv_amd import workloads
+from trispconv_amd import _lib as L
 from trispconv_amd.pytorch import indices as I
 
 pytestmark = [pytest.mark.gpu, needs_gpu]
@@ -38,6 +39,19 @@ def _module(kind, c_in, c_out, k, s=1, p=0, d=1, key=None, dtype=torch.float32, 
         with torch.no_grad():
             m.bias.uniform_(-0.1, 0.1)
     return m.to(DEV).to(dtype)
+
+
+def _with_tile(feats, pw, bias, data, n_out, tile):
+    """The layer through tsc_conv_forward_tile: the 256-row 32x32-tile kernel
+    with ``tile`` output columns per workgroup."""
+    nbr, order, ordered = data.conv_operands(n_out, feats.device, pw.c_in * feats.element_size())
+    out = torch.empty((n_out, pw.c_out), dtype=feats.dtype, device=feats.device)
+    L.check(L.lib().tsc_conv_forward_tile(
+        feats.data_ptr(), L.dtype_code(feats.dtype), feats.shape[0], pw.c_in, pw.data.data_ptr(),
+        L.ptr(bias), L.dtype_code(bias.dtype) if bias is not None else 0, L.ptr(nbr),
+        L.ptr(order), int(ordered), n_out, pw.k_vol, pw.c_out, tile, out.data_ptr(),
+        L.stream_of(feats)), "conv tile")
+    return out
 
 
 def _tiny(seed, shape, B, n):
@@ -253,7 +267,7 @@ def test_deterministic_and_order_independent(c_in, c_out, dtype, monkeypatch):
 
 @pytest.mark.parametrize("c_in,c_out,dtype", [(64, 64, torch.float16), (32, 32, torch.bfloat16),
                                               (64, 96, torch.float32)])
-def test_slot_split_kernel_matches_the_256_row_kernel(c_in, c_out, dtype, monkeypatch):
+def test_slot_split_kernel_matches_the_256_row_kernel(c_in, c_out, dtype):
     """A layer small enough for the slot-split kernel (64-row tiles, slots
     split by residue mod 4 over the waves) against the same layer forced onto
     the 256-row kernel: both within tolerance of the oracle and of each
@@ -265,9 +279,9 @@ def test_slot_split_kernel_matches_the_256_row_kernel(c_in, c_out, dtype, monkey
     m = _module("subm", c_in, c_out, 3, dtype=dtype, seed=12)
     pw = m._packed_weight(dtype)
     split = Fn.sparse_conv_forward(feats, pw, m.bias, data, len(idx))
-    monkeypatch.setenv("TSC_CONV_TILE", "32")
-    whole = Fn.sparse_conv_forward(feats, pw, m.bias, data, len(idx))
-    monkeypatch.delenv("TSC_CONV_TILE")
+    assert L.lib().tsc_conv_kernel_name(L.dtype_code(dtype), c_in, c_out, 27,
+                                        len(idx)) == b"conv_split_kernel"
+    whole = _with_tile(feats, pw, m.bias, data, len(idx), 32)
     pr = OP.subm_pairs(idx, (24, 24, 24), 1, 3, 1)
     w = OC.normalize_weight(to_np(m.weight).astype(np.float64), (3, 3, 3), c_in, c_out)
     ref = OC.conv_forward(to_np(feats).astype(np.float64), w,
@@ -280,7 +294,7 @@ def test_slot_split_kernel_matches_the_256_row_kernel(c_in, c_out, dtype, monkey
 
 @pytest.mark.parametrize("c_in,c_out,dtype", [(64, 128, torch.float16), (32, 128, torch.bfloat16),
                                               (64, 128, torch.float32), (48, 64, torch.float16)])
-def test_every_column_tile_width_gives_the_same_bits(c_in, c_out, dtype, monkeypatch):
+def test_every_column_tile_width_gives_the_same_bits(c_in, c_out, dtype):
     """The column tile width (32/64/128) only changes the schedule: each output
     is summed in the same slot and chunk order, so every width returns the same
     bits, equal to the oracle within tolerance."""
@@ -291,11 +305,13 @@ def test_every_column_tile_width_gives_the_same_bits(c_in, c_out, dtype, monkeyp
     m = _module("subm", c_in, c_out, 3, dtype=dtype, seed=9)
     pw = m._packed_weight(dtype)
     outs = {}
-    for tile in ["32", "64"] + (["128"] if c_out % 128 == 0 else []):
-        monkeypatch.setenv("TSC_CONV_TILE", tile)
-        outs[tile] = Fn.sparse_conv_forward(feats, pw, m.bias, data, len(idx))
-    monkeypatch.delenv("TSC_CONV_TILE")
-    first = outs["32"]
+    for tile in [32, 64] + ([128] if c_out % 128 == 0 else []):
+        outs[tile] = _with_tile(feats, pw, m.bias, data, len(idx), tile)
+    if L.lib().tsc_conv_kernel_name(L.dtype_code(dtype), c_in, c_out, 27,
+                                    len(idx)) == b"conv_mfma_kernel":
+        # the layer's own choice is one of these widths
+        outs[0] = Fn.sparse_conv_forward(feats, pw, m.bias, data, len(idx))
+    first = outs[32]
     for tile, o in outs.items():
         say("tile", tile, c_in, c_out, dtype)
         assert torch.equal(o, first), tile
@@ -305,8 +321,7 @@ def test_every_column_tile_width_gives_the_same_bits(c_in, c_out, dtype, monkeyp
                           to_np(m.bias).astype(np.float64), pr.pairs_in, pr.pairs_out, len(idx))
     assert rel_err(to_np(first), ref) <= TOL[dtype]
     with pytest.raises(ValueError):
-        monkeypatch.setenv("TSC_CONV_TILE", "48")  # not a column tile width
-        Fn.sparse_conv_forward(feats, pw, m.bias, data, len(idx))
+        _with_tile(feats, pw, m.bias, data, len(idx), 48)  # not a column tile width
 
 
 def test_raw_internal_weight_and_user_built_indice_data():
@@ -330,7 +345,8 @@ def test_raw_internal_weight_and_user_built_indice_data():
 
 @pytest.mark.parametrize("name", workloads.WORKLOAD_NAMES)
 def test_full_size_workloads(name):
-    """Each workload at full size, layer by layer on the GPU's own layer inputs."""
+    """Each workload at full size, layer by layer on the GPU's own layer inputs,
+    every output row against the oracle."""
     w = workloads.make_workload(name)
     dtype = {"float32": torch.float32, "float16": torch.float16, "bfloat16": torch.bfloat16}[w.dtype]
     rng = np.random.default_rng(w.seed)
@@ -350,17 +366,15 @@ def test_full_size_workloads(name):
                                        prev.padding, prev.dilation)
             inv = OP.inverse_pairs(exp_fwd)
             assert np.array_equal(y.indices.cpu().numpy(), inv.out_indices)
-            sel = np.sort(rng.choice(len(inv.out_indices), size=min(4096, len(inv.out_indices)),
-                                     replace=False))
             wt = OC.normalize_weight(to_np(m.weight).astype(np.float64), m.kernel_size,
                                      m.in_channels, m.out_channels)
-            ref = oracle_rows(rounded(feats, dtype), wt, to_np(m.bias).astype(np.float64),
-                              inv.pairs_in, inv.pairs_out, sel)
-            err = rel_err(to_np(y.features)[sel], ref)
+            ref = OC.conv_forward(rounded(feats, dtype), wt, to_np(m.bias).astype(np.float64),
+                                  inv.pairs_in, inv.pairs_out, len(inv.out_indices))
+            err = rel_err(to_np(y.features), ref)
             say(name, "inverse rel err", err)
             assert err <= TOL[dtype]
         else:
-            y = _check_layer(m, feats, idx, shape, w.batch_size, dtype, rows=4096,
+            y = _check_layer(m, feats, idx, shape, w.batch_size, dtype,
                              what=f"{name} layer {li}")
             if lay["kind"] == "strided" and lay["indice_key"]:
                 key = lay["indice_key"]

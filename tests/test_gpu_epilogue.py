@@ -272,3 +272,89 @@ def test_changes_between_calls_take_effect():
     ref = _fresh_plain(net, x)
     assert not torch.equal(third.features, fourth.features)
     assert rel_err(to_np(fourth.features), to_np(ref.features).astype(np.float64)) <= 1e-5
+
+
+def test_voxelnet_encoder_full_size_fused_against_oracle():
+    """The VoxelNet-style encoder workload at full size (4 x 60k LiDAR-like
+    voxels, fp16) as the SparseSequential a user writes: eleven conv layers,
+    each but the last followed by an eval-mode BatchNorm1d (random affine and
+    running statistics) and a ReLU, fused into the conv stores.  Layer by
+    layer on the GPU's own layer inputs, every output row against the fp64
+    oracle (conv, bias, batch norm and ReLU in fp64) at the fp16 tolerance;
+    output coordinates exact; the whole forward equal to the layer-by-layer
+    chain bit for bit."""
+    from trispconv_amd import workloads
+
+    w = workloads.make_workload("voxelnet_encoder4x60k")
+    dtype = torch.float16
+    rng = np.random.default_rng(w.seed)
+    mods = []
+    for i, lay in enumerate(w.layers):
+        if lay["kind"] == "subm":
+            m = spconv.SubMConv3d(lay["c_in"], lay["c_out"], lay["kernel_size"],
+                                  indice_key=lay["indice_key"])
+        else:
+            m = spconv.SparseConv3d(lay["c_in"], lay["c_out"], lay["kernel_size"],
+                                    stride=lay["stride"], padding=lay["padding"],
+                                    indice_key=lay["indice_key"])
+        wk, bk = workloads.layer_params(rng, lay)
+        with torch.no_grad():
+            m.weight.copy_(torch.from_numpy(wk))
+            m.bias.copy_(torch.from_numpy(bk))
+        mods.append(m)
+        if i + 1 < len(w.layers):
+            bn = nn.BatchNorm1d(lay["c_out"])
+            with torch.no_grad():
+                bn.weight.copy_(torch.from_numpy(rng.uniform(0.5, 1.5, lay["c_out"])))
+                bn.bias.copy_(torch.from_numpy(rng.uniform(-0.2, 0.2, lay["c_out"])))
+                bn.running_mean.copy_(torch.from_numpy(rng.uniform(-0.1, 0.1, lay["c_out"])))
+                bn.running_var.copy_(torch.from_numpy(rng.uniform(0.5, 1.5, lay["c_out"])))
+            mods += [bn, nn.ReLU()]
+    net = spconv.SparseSequential(*mods).to(DEV).to(dtype).eval()
+    feats = torch.from_numpy(workloads.features(rng, len(w.indices), 4)).to(DEV).to(dtype)
+    x0 = spconv.SparseConvTensor(feats, torch.from_numpy(w.indices).to(DEV),
+                                 list(w.spatial_shape), w.batch_size)
+    with torch.no_grad():
+        whole = net(x0)
+    # layer by layer through the same fused path, on a fresh tensor
+    x = spconv.SparseConvTensor(feats, x0.indices, list(w.spatial_shape), w.batch_size)
+    children = list(net.children())
+    oracle_pairs = {}
+    i = 0
+    li = 0
+    with torch.no_grad():
+        while i < len(children):
+            m = children[i]
+            i += 1
+            ep, used = M._fusable(children, i, m, x)
+            y = m.forward_with_epilogue(x, ep)
+            idx = x.indices.cpu().numpy()
+            shape = tuple(x.spatial_shape)
+            key = m.indice_key
+            if key not in oracle_pairs:
+                oracle_pairs[key] = (OP.subm_pairs(idx, shape, w.batch_size, m.kernel_size)
+                                     if m.subm else
+                                     OP.strided_pairs(idx, shape, w.batch_size, m.kernel_size,
+                                                      m.stride, m.padding, m.dilation))
+            pr = oracle_pairs[key]
+            assert np.array_equal(y.indices.cpu().numpy(), pr.out_indices), li
+            wt = OC.normalize_weight(to_np(m.weight).astype(np.float64), m.kernel_size,
+                                     m.in_channels, m.out_channels)
+            ref = OC.conv_forward(to_np(x.features).astype(np.float64), wt,
+                                  to_np(m.bias).astype(np.float64), pr.pairs_in, pr.pairs_out,
+                                  len(pr.out_indices))
+            if used:
+                bn = children[i]
+                mean, var, g, b = (to_np(t).astype(np.float64) for t in
+                                   (bn.running_mean, bn.running_var, bn.weight, bn.bias))
+                ref = (ref - mean) / np.sqrt(var + bn.eps) * g + b
+                ref = np.maximum(ref, 0.0)
+            err = rel_err(to_np(y.features), ref)
+            say(f"encoder layer {li} {m.in_channels}->{m.out_channels}",
+                "bn+relu" if used else "plain", "rows", len(ref), "rel err", err)
+            assert err <= TOL[dtype], li
+            x = y
+            i += used
+            li += 1
+    assert torch.equal(whole.indices, x.indices)
+    assert torch.equal(whole.features, x.features)

@@ -253,7 +253,7 @@ def test_bitmap_build_flags_rows_that_are_not_its_cells():
     from trispconv_amd.pytorch import indices as I
     idx = _tiny(43, (17, 18, 19), 1, 900)
     fwd = generate_strided_indice_pairs(torch.from_numpy(idx).to(DEV), (17, 18, 19), 1, 3, 2, 1)
-    ws, nwords, shape, B, _ = I._STRIDED_BITMAPS[fwd.out_indices]
+    ws, nwords, shape, B = I._STRIDED_BITMAPS[fwd.out_indices][:4]
     half = fwd.out_indices[: len(fwd.out_indices) // 2].contiguous()
     n = len(half)
     cols_row = torch.empty(n, dtype=torch.int32, device=DEV)

@@ -59,11 +59,14 @@ _SIGNATURES = {
     "tsc_conv_forward_ep": (ctypes.c_int, [_vp, _i32, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _vp,
                                            _vp, _i32, ctypes.c_float, _i32, _vp, _vp, _i32, _i64,
                                            _i32, _i32, _vp, _vp]),
+    "tsc_conv_forward_tile": (ctypes.c_int, [_vp, _i32, _i64, _i32, _vp, _vp, _i32, _vp, _vp,
+                                             _i32, _i64, _i32, _i32, _i32, _vp, _vp]),
+    "tsc_conv_kernel_name": (ctypes.c_char_p, [_i32, _i32, _i32, _i32, _i64]),
     "tsc_dense_scatter": (ctypes.c_int, [_vp, _i32, _i64, _i32, _vp, _i32, c_i32p, _i32, _vp,
                                          _vp, _vp]),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lib: Optional[ctypes.CDLL] = None
 

@@ -308,4 +308,4 @@ int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStr
 }  // namespace tsc
 
 extern "C" const char* tsc_last_error(void) { return tsc::last_error(); }
-extern "C" int tsc_abi_version(void) { return 8; }
+extern "C" int tsc_abi_version(void) { return 9; }

@@ -200,6 +200,14 @@ int64_t scan_scratch_words(int64_t n);
 int64_t bitmap_entries(int64_t nw);
 int64_t bitmap_scan_scratch_words(int64_t nw);
 int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStream_t s);
+// The submanifold build (tsc_subm_pairs) on a given workspace.  ws_limit > 0:
+// ws is that many bytes of fixed scratch, the bitmap is used only when it
+// fits and a build that fits in neither way is an argument error; 0: ws is
+// the caller's workspace of ws_bytes, sized by tsc_subm_workspace_bytes.
+int subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size, const int32_t spatial[3],
+                  const int32_t ksize[3], const int32_t dilation[3], void* ws, int64_t ws_bytes,
+                  int64_t ws_limit, int32_t* cols_row, int32_t* nbr, int32_t* counts,
+                  tsc_stream_t stream);
 int exclusive_scan_u32(const uint32_t* src, int kind, int64_t n, uint32_t* out, int32_t* total,
                        uint32_t* scratch, hipStream_t s);
 

@@ -35,8 +35,6 @@
 // no folded copy of them can go stale.
 #include "common.hpp"
 
-#include <cstdio>
-#include <cstdlib>
 #include <type_traits>
 
 namespace tsc {
@@ -1083,43 +1081,46 @@ int launch_split(const void* feat, int c_in, const void* W, const Epilogue& ep,
   return 0;
 }
 
+// Which 32x32-tile kernel runs a layer, and with which column tile width.
+struct MfmaChoice {
+  int bn;      // column tile width
+  int ck;      // input-channel chunk of one stage
+  bool split;  // the 64-row slot-split kernel instead of the 256-row one
+};
+
+// Narrower column tiles for small layers: below two workgroups per CU, halve
+// BN (each halving doubles the workgroups; gathers repeat per column tile,
+// which a small layer can afford).  Layers that would leave more than half
+// the CUs without a 256-row workgroup run on 64-row tiles with the slots
+// split over the waves (the narrowing has then always reached 32 columns).
+// Measured on 64->64 fp16 SubM layers: 9.7k rows (76 workgroups) 28.8 ->
+// 20.0 us, but 32k rows (252 workgroups) 30.7 -> 38 us, where the four waves'
+// separate weight loads cost more than the shorter slot chain saves.  Short
+// slot lists (K < 8) gain nothing from splitting.  column_tile != 0 forces
+// the 256-row kernel with that width (every width sums each output in the
+// same order, so all give the same bits).
+MfmaChoice choose_mfma(int dtype, int c_in, int c_out, int K, int64_t n_out, int column_tile) {
+  MfmaChoice c{pick_bn(c_out), pick_ck(dtype, c_in), false};
+  if (column_tile) {
+    c.bn = column_tile;
+    return c;
+  }
+  while (c.bn > 32 && ceil_div(n_out, kTileRows) * (c_out / c.bn) < 512) c.bn /= 2;
+  c.split = c.bn == 32 && K >= 8 && ceil_div(n_out, kTileRows) * (c_out / c.bn) < 128;
+  return c;
+}
+
 template <typename T>
 int dispatch_mfma(const void* feat, int c_in, const void* W, const Epilogue& ep,
                   const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
-                  int c_out, void* out, hipStream_t s) {
+                  int c_out, int column_tile, void* out, hipStream_t s) {
   constexpr int dt = std::is_same<T, float>::value ? TSC_F32
                      : std::is_same<T, __half>::value ? TSC_F16 : TSC_BF16;
-  // Narrower column tiles for small layers: below two workgroups per CU,
-  // halve BN (each halving doubles the workgroups; gathers repeat per column
-  // tile, which a small layer can afford).
-  int bn = pick_bn(c_out);
-  const int ck = pick_ck(dt, c_in);
-  while (bn > 32 && ceil_div(n_out, kTileRows) * (c_out / bn) < 512) bn /= 2;
-  // TSC_CONV_TILE=BN forces the 256-row kernel with that column tile width
-  // (for tests that compare the widths: each sums every output in the same
-  // order, so all give the same bits).
-  bool forced = false;
-  if (const char* force = std::getenv("TSC_CONV_TILE")) {
-    int fb = 0;
-    TSC_REQUIRE(std::sscanf(force, "%d", &fb) == 1 && (fb == 32 || fb == 64 || fb == 128) &&
-                    c_out % fb == 0,
-                "conv: TSC_CONV_TILE=%s is not a column tile width for c_out=%d", force, c_out);
-    bn = fb;
-    forced = true;
-  }
-  // Layers that would leave more than half the CUs without a 256-row
-  // workgroup run on 64-row tiles with the slots split over the waves (the
-  // narrowing above has then always reached 32 columns).  Measured on 64->64
-  // fp16 SubM layers: 9.7k rows (76 workgroups) 28.8 -> 20.0 us, but 32k rows
-  // (252 workgroups) 30.7 -> 38 us, where the four waves' separate weight
-  // loads cost more than the shorter slot chain saves.
-  // Short slot lists (K < 8) gain nothing from splitting.
-  const bool split =
-      !forced && bn == 32 && K >= 8 && ceil_div(n_out, kTileRows) * (c_out / bn) < 128;
+  const MfmaChoice ch = choose_mfma(dt, c_in, c_out, K, n_out, column_tile);
 #define TSC_MFMA_CASE(BN_, CK_)                                                              \
-  if (bn == BN_ && ck == CK_) {                                                              \
+  if (ch.bn == BN_ && ch.ck == CK_) {                                                        \
     if constexpr (BN_ == 32)                                                                 \
-      if (split)                                                                             \
+      if (ch.split)                                                                          \
         return launch_split<T, BN_, CK_>(feat, c_in, W, ep, nbr, order, nbr_ordered, n_out,  \
                                          K, c_out, out, s);                                  \
     return launch_mfma<T, BN_, CK_>(feat, c_in, W, ep, nbr, order, nbr_ordered,          \
@@ -1291,7 +1292,7 @@ extern "C" int tsc_pack_weight(const void* w, int32_t w_dtype, int32_t layout, i
 static int conv_forward(const void* feat, int32_t dtype, int64_t n_in, int32_t c_in,
                         const void* packed_w, const Epilogue& ep, const int32_t* nbr,
                         const int32_t* order, int32_t nbr_ordered, int64_t n_out, int32_t k_vol,
-                        int32_t c_out, void* out, hipStream_t s) {
+                        int32_t c_out, int32_t column_tile, void* out, hipStream_t s) {
   TSC_REQUIRE(dtype_ok(dtype), "conv: unsupported dtype %d", dtype);
   TSC_REQUIRE(!ep.bias || dtype_ok(ep.bias_dt), "conv: unsupported bias dtype %d", ep.bias_dt);
   TSC_REQUIRE((ep.mean == nullptr) == (ep.var == nullptr),
@@ -1306,13 +1307,18 @@ static int conv_forward(const void* feat, int32_t dtype, int64_t n_in, int32_t c
   TSC_REQUIRE(nbr || k_vol == 1, "conv: identity map needs k_vol == 1");
   TSC_REQUIRE(nbr || n_in >= n_out, "conv: identity map needs n_in >= n_out");
   TSC_REQUIRE(!nbr_ordered || (order && nbr), "conv: an ordered map needs its order");
+  const Path path = pick_path(dtype, c_in, c_out, k_vol);
+  TSC_REQUIRE(column_tile == 0 || (path == kMfma && (column_tile == 32 || column_tile == 64 ||
+                                                     column_tile == 128) &&
+                                   c_out % column_tile == 0),
+              "conv: %d is not a column tile width of this layer (32, 64 or 128 dividing "
+              "c_out=%d, on a 32x32-tile layer)", column_tile, c_out);
   if (n_out == 0) return 0;
   TSC_REQUIRE(packed_w && out && (feat || n_in == 0), "conv: null pointer");
   if (n_in == 0) {
     // no inputs: every output is the epilogue of zero
     TSC_REQUIRE(nbr != nullptr, "conv: empty input");
   }
-  const Path path = pick_path(dtype, c_in, c_out, k_vol);
   if (path == kMfma) {
     TSC_REQUIRE((reinterpret_cast<uintptr_t>(feat) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(packed_w) & 15) == 0 &&
@@ -1320,12 +1326,12 @@ static int conv_forward(const void* feat, int32_t dtype, int64_t n_in, int32_t c
                 "conv: feature, weight and output buffers must be 16-byte aligned");
     if (dtype == TSC_F32)
       return dispatch_mfma<float>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out, k_vol,
-                                  c_out, out, s);
+                                  c_out, column_tile, out, s);
     if (dtype == TSC_F16)
       return dispatch_mfma<__half>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out, k_vol,
-                                   c_out, out, s);
+                                   c_out, column_tile, out, s);
     return dispatch_mfma<__hip_bfloat16>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out,
-                                         k_vol, c_out, out, s);
+                                         k_vol, c_out, column_tile, out, s);
   }
   if (path == kNarrow) {
     if (dtype == TSC_F32)
@@ -1354,7 +1360,7 @@ extern "C" int tsc_conv_forward(const void* feat, int32_t dtype, int64_t n_in, i
                                 tsc_stream_t stream) {
   const Epilogue ep{bias, bias_dtype, nullptr, nullptr, nullptr, nullptr, 0, 0.f, 0};
   return conv_forward(feat, dtype, n_in, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out, k_vol,
-                      c_out, out, static_cast<hipStream_t>(stream));
+                      c_out, 0, out, static_cast<hipStream_t>(stream));
 }
 
 extern "C" int tsc_conv_forward_ep(const void* feat, int32_t dtype, int64_t n_in, int32_t c_in,
@@ -1367,5 +1373,30 @@ extern "C" int tsc_conv_forward_ep(const void* feat, int32_t dtype, int64_t n_in
   const Epilogue ep{bias,      bias_dtype, bn_mean, bn_var, bn_weight,
                     bn_bias,   bn_dtype,   bn_eps,  relu != 0 ? 1 : 0};
   return conv_forward(feat, dtype, n_in, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out, k_vol,
-                      c_out, out, static_cast<hipStream_t>(stream));
+                      c_out, 0, out, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tsc_conv_forward_tile(const void* feat, int32_t dtype, int64_t n_in, int32_t c_in,
+                                     const void* packed_w, const void* bias, int32_t bias_dtype,
+                                     const int32_t* nbr, const int32_t* order,
+                                     int32_t nbr_ordered, int64_t n_out, int32_t k_vol,
+                                     int32_t c_out, int32_t column_tile, void* out,
+                                     tsc_stream_t stream) {
+  const Epilogue ep{bias, bias_dtype, nullptr, nullptr, nullptr, nullptr, 0, 0.f, 0};
+  return conv_forward(feat, dtype, n_in, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out, k_vol,
+                      c_out, column_tile, out, static_cast<hipStream_t>(stream));
+}
+
+extern "C" const char* tsc_conv_kernel_name(int32_t dtype, int32_t c_in, int32_t c_out,
+                                            int32_t k_vol, int64_t n_out) {
+  if (!dtype_ok(dtype) || c_in <= 0 || c_out <= 0 || k_vol <= 0 || n_out < 0) return "";
+  switch (pick_path(dtype, c_in, c_out, k_vol)) {
+    case kMfma:
+      return choose_mfma(dtype, c_in, c_out, k_vol, n_out, 0).split ? "conv_split_kernel"
+                                                                    : "conv_mfma_kernel";
+    case kNarrow:
+      return "conv_narrow_kernel";
+    default:
+      return "conv_valu_kernel";
+  }
 }

@@ -156,6 +156,114 @@ __global__ void __launch_bounds__(kRows) subm_probe_kernel(const int4* __restric
   }
 }
 
+// ------------------------------------------------------ 64-bit cell keys --
+// Grids of 2^32 - 1 cells or more (the reference's int64 keys, indices.py:45-51,
+// work for any grid): an open-addressing table of 64-bit keys with the rows in
+// a parallel int32 array (-1 = none), linear probing from a 64-bit murmur3
+// finaliser.  Repeated coordinates keep the largest row, as the reference's
+// table scatter over rows in order leaves them.
+__device__ __forceinline__ uint64_t cell_key64(const SubmGeom& g, int b, int z, int y, int x) {
+  return ((static_cast<uint64_t>(b) * g.shape.z + z) * g.shape.y + y) * g.shape.x + x;
+}
+
+__device__ __forceinline__ uint32_t hash64(uint64_t k) {
+  k ^= k >> 33;
+  k *= 0xff51afd7ed558ccdull;
+  k ^= k >> 33;
+  k *= 0xc4ceb9fe1a85ec53ull;
+  k ^= k >> 33;
+  return static_cast<uint32_t>(k);
+}
+
+__global__ void __launch_bounds__(256) subm_insert_wide_kernel(const int4* __restrict__ coords,
+                                                               int64_t n, SubmGeom g,
+                                                               unsigned long long* keys,
+                                                               int32_t* vals, int32_t* status) {
+  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  const int4 c = coords[r];  // (b, z, y, x)
+  if (!in_grid(g, c.x, c.y, c.z, c.w)) {
+    atomicOr(status, (c.x < 0 || c.x >= g.B) ? TSC_FLAG_BATCH_OUT_OF_RANGE
+                                              : TSC_FLAG_COORD_OUT_OF_GRID);
+    return;
+  }
+  const unsigned long long key = cell_key64(g, c.x, c.y, c.z, c.w);
+  uint32_t h = hash64(key) & g.mask;
+  while (true) {
+    const unsigned long long old = atomicCAS(&keys[h], static_cast<unsigned long long>(kEmpty), key);
+    if (old == kEmpty || old == key) {
+      atomicMax(&vals[h], static_cast<int32_t>(r));  // later rows win
+      return;
+    }
+    h = (h + 1) & g.mask;
+  }
+}
+
+// One thread per output row; the first probe of every slot of a group is
+// issued before any is inspected, then collisions are followed slot by slot.
+__global__ void __launch_bounds__(kRows) subm_probe_wide_kernel(
+    const int4* __restrict__ coords, int64_t n, int K, SubmGeom g,
+    const unsigned long long* __restrict__ keys, const int32_t* __restrict__ vals,
+    int32_t* __restrict__ nbr, int32_t* __restrict__ blk_cnt, int nblk) {
+  __shared__ int32_t s_cnt[kRows / kWave][64];  // per wave, per slot (slots < 64)
+  const int t = threadIdx.x;
+  const int w = t / kWave;
+  const int64_t r = blockIdx.x * (int64_t)kRows + t;
+  const bool valid = r < n;
+  const int4 c = valid ? coords[r] : make_int4(-1, 0, 0, 0);
+  const bool self_ok = valid && in_grid(g, c.x, c.y, c.z, c.w);
+  for (int kb = 0; kb < K; kb += kGroup) {
+    unsigned long long key[kGroup], kw[kGroup];
+    uint32_t h[kGroup];
+    bool look[kGroup];
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) {
+      const int k = kb + i;
+      int kz, ky, kx;
+      slot_to_zyx(k < K ? k : 0, g.ks, kz, ky, kx);
+      const int z = c.y + (kz - g.ks.z / 2) * g.dil.z;
+      const int y = c.z + (ky - g.ks.y / 2) * g.dil.y;
+      const int x = c.w + (kx - g.ks.x / 2) * g.dil.x;
+      look[i] = self_ok && k < K && in_grid(g, c.x, z, y, x);
+      key[i] = look[i] ? cell_key64(g, c.x, z, y, x) : 0ull;
+      h[i] = hash64(key[i]) & g.mask;
+      kw[i] = keys[h[i]];  // slot h is inside the table: unconditional reads
+    }
+#pragma unroll
+    for (int i = 0; i < kGroup; ++i) {
+      const int k = kb + i;
+      int32_t j = -1;
+      if (look[i]) {
+        while (kw[i] != kEmpty) {
+          if (kw[i] == key[i]) {
+            j = vals[h[i]];
+            break;
+          }
+          h[i] = (h[i] + 1) & g.mask;
+          kw[i] = keys[h[i]];
+        }
+      }
+      if (k < K) {
+        const uint64_t hits = __ballot(j >= 0);
+        if (valid) nbr[(int64_t)k * n + r] = j;
+        if (__lane_id() == 0) {
+          if (k < 64)
+            s_cnt[w][k] = __popcll(hits);
+          else
+            atomicAdd(&blk_cnt[(int64_t)k * nblk + blockIdx.x], (int)__popcll(hits));
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (t < K && t < 64) {
+    int sum = 0;
+#pragma unroll
+    for (int ww = 0; ww < kRows / kWave; ++ww) sum += s_cnt[ww][t];
+    blk_cnt[(int64_t)t * nblk + blockIdx.x] = sum;
+  }
+}
+
 // ------------------------------------------------------------ bitmap path --
 // One 8-byte entry per 32 cells: x = occupancy bits, y = rank of the word's
 // first cell (occupied cells before it in (b,z,y,x) order), so a lookup is
@@ -529,8 +637,13 @@ static bool subm_use_bitmap(int64_t n, int64_t cells) {
   return ceil_div(cells, 32) <= 64 * n + (int64_t(1) << 20);
 }
 
+// Cell keys fit the packed 32-bit hash words and the bitmap's column words
+// below this many cells.
+constexpr int64_t kNarrowCells = 0xffffffffll;
+
 struct SubmWork {
-  unsigned long long* table;
+  unsigned long long* table;  // packed (key << 32 | row) words, or the 64-bit keys
+  int32_t* vals;              // rows of the 64-bit-key table
   uint2* wr;       // bitmap entries (word, rank)
   uint32_t* scan;  // bitmap scan scratch
   unsigned long long* cols;  // map columns as (row + 1, cell) words
@@ -539,12 +652,13 @@ struct SubmWork {
 
 static int64_t bitmap_words(int64_t cells) { return ceil_div(cells, 32); }
 
-static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, int64_t* used) {
+static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, bool bitmap,
+                           int64_t* used) {
   Carver c(ws);
   const int64_t m = n > 0 ? n : 1;
   const int64_t nblk = ceil_div(m, kRows);
   SubmWork w{};
-  if (subm_use_bitmap(n, cells)) {
+  if (bitmap) {
     const int64_t nw = bitmap_words(cells);
     w.wr = c.take<uint2>(bitmap_entries(nw));
     w.scan = c.take<uint32_t>(bitmap_scan_scratch_words(nw));
@@ -553,11 +667,21 @@ static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, int64_t* u
     w.n_extra = c.take<int32_t>(1);
   } else {
     w.table = c.take<unsigned long long>(subm_capacity(m));
+    if (cells >= kNarrowCells) w.vals = c.take<int32_t>(subm_capacity(m));
     w.blk_cnt = c.take<int32_t>(nblk * K);
     w.blk_off = c.take<int32_t>(nblk * K);
   }
   if (used) *used = c.used;
   return w;
+}
+
+// Bitmap or hash: the bitmap while the grid is dense enough (and its cell ids
+// fit 32 bits); with a workspace limit, the hash when only it fits.
+static bool subm_pick_bitmap(int64_t n, int K, int64_t cells, int64_t ws_limit) {
+  if (!(cells < kNarrowCells && subm_use_bitmap(n, cells))) return false;
+  int64_t used = 0;
+  subm_carve(nullptr, n, K, cells, true, &used);
+  return used <= ws_limit;
 }
 
 __global__ void iota_kernel(int32_t* p, int64_t n) {
@@ -572,18 +696,22 @@ using namespace tsc;
 extern "C" int64_t tsc_subm_workspace_bytes(int64_t n, int32_t k_vol, int32_t batch_size,
                                             const int32_t spatial[3]) {
   if (n < 0 || k_vol <= 0 || batch_size <= 0 || !spatial) return -1;
+  if (spatial[0] <= 0 || spatial[1] <= 0 || spatial[2] <= 0 ||
+      (int64_t)batch_size * spatial[0] * spatial[1] > (int64_t(1) << 62) / spatial[2])
+    return -1;
   const int64_t cells = (int64_t)batch_size * spatial[0] * spatial[1] * spatial[2];
-  if (cells <= 0) return -1;
   int64_t used = 0;
-  subm_carve(nullptr, n, k_vol, cells, &used);
+  subm_carve(nullptr, n, k_vol, cells, subm_pick_bitmap(n, k_vol, cells, INT64_MAX), &used);
   return used;
 }
 
-extern "C" int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_size,
-                              const int32_t spatial[3], const int32_t ksize[3],
-                              const int32_t dilation[3], void* ws, int64_t ws_bytes,
-                              int32_t* cols_row, int32_t* nbr, int32_t* counts,
-                              tsc_stream_t stream) {
+// The build on a given workspace.  ws_limit > 0: the workspace is that many
+// bytes of fixed scratch (the bitmap is taken only when it fits, else the
+// hash); 0: the caller's workspace, sized by tsc_subm_workspace_bytes.
+int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
+                      const int32_t spatial[3], const int32_t ksize[3],
+                      const int32_t dilation[3], void* ws, int64_t ws_bytes, int64_t ws_limit,
+                      int32_t* cols_row, int32_t* nbr, int32_t* counts, tsc_stream_t stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   TSC_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "subm: n=%lld out of range", (long long)n);
   TSC_REQUIRE(batch_size > 0, "subm: batch_size must be positive");
@@ -592,13 +720,22 @@ extern "C" int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_si
   TSC_REQUIRE(shape.z > 0 && shape.y > 0 && shape.x > 0, "subm: spatial shape must be positive");
   TSC_REQUIRE(ks.z > 0 && ks.y > 0 && ks.x > 0 && dil.z > 0 && dil.y > 0 && dil.x > 0,
               "subm: kernel size and dilation must be positive");
+  TSC_REQUIRE((int64_t)batch_size * shape.z * shape.y <= (int64_t(1) << 62) / shape.x,
+              "subm: batch*D*H*W exceeds 2^62 cells");
   const int64_t cells = (int64_t)batch_size * shape.z * shape.y * shape.x;
-  TSC_REQUIRE(cells < 0xffffffffll,
-              "subm: batch*D*H*W = %lld cells exceeds the 32-bit cell id range", (long long)cells);
   const int K = ks.z * ks.y * ks.x;
   TSC_REQUIRE(K <= 4096, "subm: kernel volume %d too large", K);
-  TSC_REQUIRE(ws_bytes >= tsc_subm_workspace_bytes(n, K, batch_size, spatial),
-              "subm: workspace too small");
+  const bool bitmap = subm_pick_bitmap(n, K, cells, ws_limit > 0 ? ws_limit : INT64_MAX);
+  int64_t need = 0;
+  subm_carve(nullptr, n, K, cells, bitmap, &need);
+  if (ws_limit > 0)
+    TSC_REQUIRE(need <= ws_limit,
+                "subm: this build needs %lld bytes of scratch, more than the %lld the "
+                "no-allocation entry point holds (n=%lld, %lld cells); use tsc_subm_pairs with "
+                "a workspace", (long long)need, (long long)ws_limit, (long long)n,
+                (long long)cells);
+  else
+    TSC_REQUIRE(ws_bytes >= need, "subm: workspace too small");
   TSC_REQUIRE(counts != nullptr, "subm: counts is null");
 
   int rc = 0;
@@ -606,7 +743,7 @@ extern "C" int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_si
   TSC_REQUIRE(coords && cols_row && nbr && ws, "subm: null pointer");
 
   const int nblk = static_cast<int>(ceil_div(n, kRows));
-  const SubmWork w = subm_carve(ws, n, K, cells, nullptr);
+  const SubmWork w = subm_carve(ws, n, K, cells, bitmap, nullptr);
   const int4* c4 = reinterpret_cast<const int4*>(coords);
   if (w.wr) {
     const int64_t nw = bitmap_words(cells);
@@ -649,13 +786,32 @@ extern "C" int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_si
     if ((rc = fill_u64(w.table, cap, kEmpty, s))) return rc;
     iota_kernel<<<ceil_div(n, 256), 256, 0, s>>>(cols_row, n);
     TSC_LAUNCH_CHECK("subm_iota");
-    subm_insert_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.table, counts + K);
-    TSC_LAUNCH_CHECK("subm_insert");
-    subm_probe_kernel<<<nblk, kRows, 0, s>>>(c4, n, K, g, w.table, nbr, w.blk_cnt, nblk);
-    TSC_LAUNCH_CHECK("subm_probe");
+    if (w.vals) {
+      if ((rc = fill_u32(reinterpret_cast<uint32_t*>(w.vals), cap, 0xffffffffu, s))) return rc;
+      subm_insert_wide_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.table, w.vals,
+                                                               counts + K);
+      TSC_LAUNCH_CHECK("subm_insert_wide");
+      subm_probe_wide_kernel<<<nblk, kRows, 0, s>>>(c4, n, K, g, w.table, w.vals, nbr, w.blk_cnt,
+                                                    nblk);
+      TSC_LAUNCH_CHECK("subm_probe_wide");
+    } else {
+      subm_insert_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.table, counts + K);
+      TSC_LAUNCH_CHECK("subm_insert");
+      subm_probe_kernel<<<nblk, kRows, 0, s>>>(c4, n, K, g, w.table, nbr, w.blk_cnt, nblk);
+      TSC_LAUNCH_CHECK("subm_probe");
+    }
     if ((rc = scan_slot_blocks(w.blk_cnt, w.blk_off, counts, K, nblk, s))) return rc;
   }
   return 0;
+}
+
+extern "C" int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_size,
+                              const int32_t spatial[3], const int32_t ksize[3],
+                              const int32_t dilation[3], void* ws, int64_t ws_bytes,
+                              int32_t* cols_row, int32_t* nbr, int32_t* counts,
+                              tsc_stream_t stream) {
+  return subm_pairs_ws(coords, n, batch_size, spatial, ksize, dilation, ws, ws_bytes, 0, cols_row,
+                       nbr, counts, stream);
 }
 
 extern "C" int tsc_subm_pairs_from_bitmap(const int32_t* coords, int64_t n, int32_t batch_size,
@@ -674,8 +830,9 @@ extern "C" int tsc_subm_pairs_from_bitmap(const int32_t* coords, int64_t n, int3
   TSC_REQUIRE(ks.x == 3 && 2 * dil.x < 32,
               "subm: a build on a bitmap needs a kernel 3 cells wide in x with dilation < 16");
   const int64_t cells = (int64_t)batch_size * shape.z * shape.y * shape.x;
-  TSC_REQUIRE(cells < 0xffffffffll,
-              "subm: batch*D*H*W = %lld cells exceeds the 32-bit cell id range", (long long)cells);
+  TSC_REQUIRE(cells < kNarrowCells,
+              "subm: a build on a bitmap needs fewer than 2^32 - 1 cells (batch*D*H*W = %lld)",
+              (long long)cells);
   const int K = ks.z * ks.y * ks.x;
   TSC_REQUIRE(K <= 4096, "subm: kernel volume %d too large", K);
   const int64_t nw = bitmap_words(cells);

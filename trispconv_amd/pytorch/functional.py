@@ -33,6 +33,32 @@ class Epilogue(NamedTuple):
 
 
 _PARAM_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+_KERNEL_DTYPES = _PARAM_DTYPES
+
+
+def compute_dtype(feat_dtype: torch.dtype, weight_dtype: torch.dtype) -> torch.dtype:
+    """The dtype the kernel computes in.  The reference's GPU branch upcasts
+    fp16/bf16 (and any non-fp32) features and the weight to fp32, sums in
+    fp32 and casts the result back to the features' dtype
+    (functional.py:32-36, :51).  Features whose weight has the same dtype
+    (f32, f16, bf16) run natively: products of f16/bf16 values are exact in
+    the fp32 accumulator, so that is the same arithmetic.  Anything else
+    (float64 features, or a weight of another dtype than the features, whose
+    values the features' dtype may not hold) runs on fp32 copies."""
+    if feat_dtype in _KERNEL_DTYPES and weight_dtype == feat_dtype:
+        return feat_dtype
+    return torch.float32
+
+
+def _epilogue_torch(out: torch.Tensor, ep: Epilogue) -> torch.Tensor:
+    """An epilogue as torch ops on ``out`` (for feature dtypes the kernels do
+    not store): eval batch norm, then ReLU."""
+    if ep.mean is not None:
+        out = torch.nn.functional.batch_norm(out, ep.mean.to(out.dtype), ep.var.to(out.dtype),
+                                             None if ep.weight is None else ep.weight.to(out.dtype),
+                                             None if ep.bias is None else ep.bias.to(out.dtype),
+                                             False, 0.0, ep.eps)
+    return torch.relu(out) if ep.relu else out
 
 
 def _bn_operands(ep: Epilogue, c_out: int, device) -> list:
@@ -62,19 +88,36 @@ def _bn_operands(ep: Epilogue, c_out: int, device) -> list:
 def _run(features: torch.Tensor, packed: PackedWeight, bias: Optional[torch.Tensor],
          nbr: Optional[torch.Tensor], order: Optional[torch.Tensor], n_out: int,
          nbr_ordered: bool = False, epilogue: Optional[Epilogue] = None) -> torch.Tensor:
+    """The fused kernel on features in the packed weight's dtype.  Features
+    of another dtype are cast to it and the result cast back
+    (functional.py:32-36, :51); for a dtype the kernels do not store (float64)
+    the bias and epilogue follow in that dtype, as the reference adds the
+    bias after the cast back (out + bias promotes to it)."""
     L.require_gpu(features, "sparse_conv_forward")
+    orig = features.dtype
+    if orig != packed.dtype:
+        wide = orig not in _KERNEL_DTYPES
+        out = _run(features.to(packed.dtype), packed, None if wide else bias, nbr, order, n_out,
+                   nbr_ordered, None if wide else epilogue).to(orig)
+        if wide:
+            if bias is not None:
+                out = out + bias.to(out.device)
+            if epilogue is not None:
+                out = _epilogue_torch(out, epilogue)
+        return out
     feats = features.contiguous()
     if feats.data_ptr() % 16:
         feats = feats.clone()  # rows are read as 16-byte vectors
-    if feats.dtype != packed.dtype:
-        raise TypeError(f"weight packed for {packed.dtype}, features are {feats.dtype}")
     if feats.shape[1] != packed.c_in:
         raise ValueError(f"features have {feats.shape[1]} channels, weight expects {packed.c_in}")
     out = torch.empty((n_out, packed.c_out), dtype=feats.dtype, device=feats.device)
     b = None
     if bias is not None:
-        b = bias if bias.device == feats.device and bias.is_contiguous() else \
+        b = bias if bias.device == feats.device and bias.is_contiguous() \
+            and bias.dtype in _PARAM_DTYPES else \
             bias.detach().to(feats.device).contiguous()
+        if b.dtype not in _PARAM_DTYPES:
+            b = b.to(torch.float32)
         if b.numel() != packed.c_out:
             raise ValueError(f"bias has {b.numel()} entries, expected {packed.c_out}")
     lib = L.lib()
@@ -108,9 +151,11 @@ def sparse_conv_forward(features: torch.Tensor, weight: Union[torch.Tensor, Pack
     L.require_gpu(features, "sparse_conv_forward")
     if not isinstance(weight, PackedWeight):
         K, c_in, c_out = weight.shape
-        weight = pack_weight(weight, (K, 1, 1), c_in, c_out, features.dtype)
-    nbr, order, ordered = indice_data.conv_operands(N_out, features.device,
-                                                    weight.c_in * features.element_size())
+        weight = pack_weight(weight, (K, 1, 1), c_in, c_out,
+                             compute_dtype(features.dtype, weight.dtype))
+    elem = torch.empty((), dtype=weight.dtype).element_size()
+    nbr, order, ordered = indice_data.conv_operands(N_out, features.device, weight.c_in * elem,
+                                                    n_in=features.shape[0])
     return _run(features, weight, bias, nbr, order, N_out, ordered, epilogue)
 
 

@@ -104,6 +104,9 @@ class IndiceData:
         # strided builds: input rows with at least one pair, i.e. the row
         # count of this layer's inverse, read with the build's counts
         self._n_in_paired: Optional[int] = None
+        # input rows the pairs may name: ids lie in [0, _in_bound) (the
+        # builders' input rows; for user-assigned lists their largest id + 1)
+        self._in_bound: Optional[int] = None
 
     @property
     def pair_num(self) -> torch.Tensor:
@@ -155,6 +158,8 @@ class IndiceData:
 
     @pairs_in.setter
     def pairs_in(self, value: List[torch.Tensor]) -> None:
+        if self._pairs_out is None and (self._pout is not None or self._map_cols is not None):
+            self.pairs_out  # keep the other list: the tables it comes from go
         self._pairs_in = value
         self._drop_tables()
 
@@ -167,6 +172,8 @@ class IndiceData:
 
     @pairs_out.setter
     def pairs_out(self, value: List[torch.Tensor]) -> None:
+        if self._pairs_in is None and (self._pin is not None or self._map_cols is not None):
+            self.pairs_in  # keep the other list: the tables it comes from go
         self._pairs_out = value
         self._drop_tables()
 
@@ -200,10 +207,13 @@ class IndiceData:
         self._raster = False
         self._nbr_ordered = None
         self._inverse_cache = None
+        self._in_bound = None
 
     # --------------------------------------------------- convolution inputs
-    def neighbour_map(self, n_out: int, device) -> torch.Tensor:
-        """[K][n_out] int32: input row feeding output row o through slot k, or -1."""
+    def neighbour_map(self, n_out: int, device, n_in: Optional[int] = None) -> torch.Tensor:
+        """[K][n_out] int32: input row feeding output row o through slot k, or -1.
+        ``n_in``: the rows of the features the map will gather from (checked
+        against user-assigned lists)."""
         if self._nbr is None and self._map_cols is not None:
             if not self._raster:  # the builder's columns are the rows in order
                 self._nbr = self._map_cols
@@ -214,15 +224,85 @@ class IndiceData:
                                                 nbr.data_ptr(), L.stream_of(nbr)), "map to rows")
                 self._nbr = nbr
         if self._nbr is None:
-            # user-built lists: scatter them into a map (each slot maps an
-            # output at most once, as every generator guarantees)
-            K = self.K
-            nbr = torch.full((K, n_out), -1, dtype=torch.int32, device=device)
-            for k, (pi, po) in enumerate(zip(self.pairs_in, self.pairs_out)):
-                if pi.numel():
-                    nbr[k, po.to(device).long()] = pi.to(device).int()
-            self._nbr = nbr
+            self._nbr = self._user_map(n_out, n_in, device)
         return self._nbr
+
+    def _user_lists(self, n_in: Optional[int], n_out: int, device):
+        """The user-assigned pair lists as flat device tensors (slot of each
+        pair, input ids, output ids) and the per-slot sizes, after the checks
+        the reference's own indexing makes: ``features[in_ids]`` and
+        ``out.index_add_(0, out_ids, ...)`` (functional.py:46) raise
+        IndexError for ids outside the rows.  Ids must lie in [0, n_in) and
+        [0, n_out)."""
+        K = self.K
+        pin, pout = self.pairs_in, self.pairs_out
+        if len(pin) != K or len(pout) != K:
+            raise ValueError(f"IndiceData: {len(pin)} pairs_in and {len(pout)} pairs_out lists "
+                             f"for a kernel of {K} slots")
+        sizes = [int(p.numel()) for p in pin]
+        if sizes != [int(p.numel()) for p in pout]:
+            raise ValueError("IndiceData: pairs_in[k] and pairs_out[k] differ in length")
+        total = sum(sizes)
+        if total == 0:
+            e = torch.empty(0, dtype=torch.long, device=device)
+            return e, e, e, sizes
+        cat_in = torch.cat([p.reshape(-1).to(device=device, dtype=torch.long) for p in pin])
+        cat_out = torch.cat([p.reshape(-1).to(device=device, dtype=torch.long) for p in pout])
+        slot = torch.repeat_interleave(torch.arange(K, device=device),
+                                       torch.tensor(sizes, device=device))
+        return slot, cat_in, cat_out, sizes
+
+    @staticmethod
+    def _range_error(lo_in, hi_in, lo_out, hi_out, n_in, n_out, what):
+        if n_in is not None and (lo_in < 0 or hi_in >= n_in):
+            raise IndexError(f"{what}: pairs_in holds ids in [{lo_in}, {hi_in}], outside the "
+                             f"{n_in} input rows")
+        if lo_out < 0 or hi_out >= n_out:
+            raise IndexError(f"{what}: pairs_out holds ids in [{lo_out}, {hi_out}], outside the "
+                             f"{n_out} output rows")
+
+    def _user_map(self, n_out: int, n_in: Optional[int], device) -> torch.Tensor:
+        """[K][n_out] map of user-assigned lists, checked with one host read:
+        ids in range, and no output row twice within a slot (the map holds one
+        input per slot and output, as every generator's lists do)."""
+        K = self.K
+        slot, cat_in, cat_out, sizes = self._user_lists(n_in, n_out, device)
+        nbr = torch.full((K, n_out), -1, dtype=torch.int32, device=device)
+        if not slot.numel():
+            self._in_bound = 0
+            return nbr
+        # scatter with clamped ids, so that the check below reads a map
+        # written in bounds whatever the lists hold
+        hi_in = (n_in if n_in is not None else 1 << 31) - 1
+        nbr[slot, cat_out.clamp(0, max(n_out - 1, 0))] = cat_in.clamp(0, hi_in).int()
+        stats = torch.stack([cat_in.min(), cat_in.max(), cat_out.min(), cat_out.max(),
+                             (nbr >= 0).sum()]).cpu().tolist()
+        self._range_error(*stats[:4], n_in, n_out, "sparse_conv_forward")
+        if stats[4] != len(slot):
+            raise ValueError("sparse_conv_forward: a pairs_out list names one output row twice "
+                             "within a slot; each slot maps an output row at most once")
+        self._in_bound = int(stats[1]) + 1
+        return nbr
+
+    def _tables_from_lists(self, device) -> None:
+        """Padded device tables (and counts) from user-assigned lists, for the
+        inverse remap (modules.py:175-212 reads the forward's lists)."""
+        K = self.K
+        n_in, n_out = len(self.input_indices), len(self.out_indices)
+        slot, cat_in, cat_out, sizes = self._user_lists(n_in, n_out, device)
+        cap = max([n_in, 1] + sizes)
+        pin = torch.full((K, cap), -1, dtype=torch.int32, device=device)
+        pout = torch.full((K, cap), -1, dtype=torch.int32, device=device)
+        if slot.numel():
+            starts = torch.tensor([0] + sizes[:-1], device=device).cumsum(0)
+            pos = torch.arange(len(slot), device=device) - starts[slot]
+            stats = torch.stack([cat_in.min(), cat_in.max(), cat_out.min(),
+                                 cat_out.max()]).cpu().tolist()
+            self._range_error(*stats, n_in, n_out, "SparseInverseConv3d")
+            pin[slot, pos] = cat_in.int()
+            pout[slot, pos] = cat_out.int()
+        self._pin, self._pout = pin, pout
+        self._cnt = torch.tensor(sizes, dtype=torch.int32, device=device)
 
     def execution_order(self, n_out: int, device, row_bytes: int = 256) -> Optional[torch.Tensor]:
         """Processing order of the output rows for the fused convolution.
@@ -254,10 +334,20 @@ class IndiceData:
             self._order, self._order_region, self._nbr_ordered = order, region, nbr_ordered
         return self._order
 
-    def conv_operands(self, n_out: int, device, row_bytes: int = 256):
+    def conv_operands(self, n_out: int, device, row_bytes: int = 256,
+                      n_in: Optional[int] = None):
         """(map, order, ordered) for the fused convolution: the planned order
         and its permuted map; for small layers the builder's own spatial
-        column order when it has one; else the row-major map."""
+        column order when it has one; else the row-major map.  ``n_in``, the
+        feature rows, must cover every input id the pairs name (IndexError,
+        as the reference's ``features[in_ids]``)."""
+        if self._map_cols is None and self._nbr is None:
+            self.neighbour_map(n_out, device, n_in)  # user-assigned lists: checked here
+        if n_in is not None:
+            bound = self._in_bound if self._in_bound is not None else len(self.input_indices)
+            if n_in < bound:
+                raise IndexError(f"sparse_conv_forward: the pairs read input rows up to "
+                                 f"{bound - 1}, the features have {n_in} rows")
         order = self.execution_order(n_out, device, row_bytes)
         if order is not None:
             return self._nbr_ordered, order, True
@@ -299,9 +389,14 @@ def _raise_status(status: int, what: str) -> None:
 
 # Output coordinates of strided builds -> (workspace, which begins with the
 # output grid's occupancy bitmap, its 32-cell words, output shape, batch size,
-# the coordinates' version counter).  A submanifold build on exactly those
+# the coordinates' version counter, their address and storage offset).  A submanifold build on exactly those
 # coordinates probes that bitmap instead of building its own.
 _STRIDED_BITMAPS = WeakIdKeyDictionary()
+
+
+# A submanifold build on a bitmap packs cell ids in 32 bits: grids of this
+# many cells or more take the 64-bit-key hash build instead.
+_NARROW_CELLS = (1 << 32) - 1
 
 
 def _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil):
@@ -310,9 +405,10 @@ def _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil):
     bm = _STRIDED_BITMAPS.get(indices)
     if bm is None:
         return None
-    ws, nwords, out_shape, batch, version = bm
+    ws, nwords, out_shape, batch, version, ptr = bm
     if (out_shape != shape or batch != int(batch_size) or version != indices._version
-            or ks[2] != 3 or 2 * dil[2] >= 32):
+            or ptr != (indices.data_ptr(), indices.storage_offset())
+            or ks[2] != 3 or 2 * dil[2] >= 32 or nwords * 32 >= _NARROW_CELLS):
         return None
     K = ks[0] * ks[1] * ks[2]
     n = coords.shape[0]
@@ -415,7 +511,8 @@ def generate_strided_indice_pairs(indices: torch.Tensor, spatial_shape, batch_si
     data._n_in_paired = int(host[K + 2])
     cells = int(batch_size) * out_shape[0] * out_shape[1] * out_shape[2]
     _STRIDED_BITMAPS[out_coords] = (ws, (cells + 31) // 32, tuple(out_shape), int(batch_size),
-                                    out_coords._version)
+                                    out_coords._version,
+                                    (out_coords.data_ptr(), out_coords.storage_offset()))
     return data
 
 
@@ -427,8 +524,13 @@ def generate_inverse_indice_pairs(fwd: IndiceData) -> IndiceData:
     forward input pairs_in[k]; pair_num is the forward's.
     """
     fwd._ensure_tables()
-    if fwd._pin is None:
-        raise ValueError("inverse pairs need a forward IndiceData built on the GPU")
+    from_lists = fwd._pin is None
+    if from_lists:
+        # lists assigned by the user: the reference remaps whatever lists it
+        # finds (modules.py:175-212); check them and lay them out as tables
+        dev = fwd.input_indices.device
+        L.require_gpu(fwd.input_indices, "SparseInverseConv3d")
+        fwd._tables_from_lists(dev)
     dev = fwd._pin.device
     K = fwd.K
     cap = fwd._pin.shape[1]
@@ -442,7 +544,8 @@ def generate_inverse_indice_pairs(fwd: IndiceData) -> IndiceData:
             "inverse pairs")
     # a forward built here counted its paired input rows with its own pair
     # counts, so the inverse needs no host read of its own
-    n_out = fwd._n_in_paired if fwd._n_in_paired is not None else int(counts.cpu()[0])
+    n_out = fwd._n_in_paired if (fwd._n_in_paired is not None and not from_lists) \
+        else int(counts.cpu()[0])
     in_coords = _coords(fwd.input_indices, "inverse pairs")
     out_coords = torch.empty((n_out, 4), dtype=torch.int32, device=dev)
     nbr = torch.empty((K, n_out), dtype=torch.int32, device=dev)
@@ -451,6 +554,12 @@ def generate_inverse_indice_pairs(fwd: IndiceData) -> IndiceData:
                                  cap, in_coords.data_ptr(), n_in, ws.data_ptr(), ws.numel(), n_out,
                                  out_coords.data_ptr(), nbr.data_ptr(), inv_pout.data_ptr(),
                                  stream), "inverse pairs")
+    if from_lists:
+        # the inverse writes output id_map[pairs_in[k]] through slot k: an
+        # input row listed twice within a slot would need two entries
+        if int((nbr >= 0).sum()) != int(fwd._cnt.sum()):
+            raise ValueError("SparseInverseConv3d: a forward pairs_in list names one input row "
+                             "twice within a slot; each slot maps a row at most once")
     return IndiceData._from_tables(
         out_indices=out_coords, input_indices=fwd.out_indices,
         input_spatial_shape=fwd.output_spatial_shape,

@@ -16,7 +16,7 @@ from typing import List, Optional, Tuple, Union
 import torch
 import torch.nn as nn
 
-from .functional import Epilogue, dense_forward, sparse_conv_forward
+from .functional import Epilogue, compute_dtype, dense_forward, sparse_conv_forward
 from .indices import (IndiceData, _output_spatial_shape, _to3, generate_inverse_indice_pairs,
                       generate_strided_indice_pairs, generate_subm_indice_pairs)
 from .tensor import SparseConvTensor
@@ -98,8 +98,11 @@ class SparseConvolution(SparseModule):
         return normalize_spconv_weight(self.weight, self.kernel_size, self.in_channels,
                                        self.out_channels)
 
-    def _packed_weight(self, dtype: torch.dtype) -> PackedWeight:
+    def _packed_weight(self, feat_dtype: torch.dtype) -> PackedWeight:
+        """The weight packed for features of ``feat_dtype`` (in the dtype the
+        kernel computes those in, see compute_dtype)."""
         w = self.weight
+        dtype = compute_dtype(feat_dtype, w.dtype)
         if self._packed is not None and self._packed_key is not None \
                 and self._packed_key == weight_state(w, dtype):
             return self._packed
@@ -172,7 +175,7 @@ class SparseConvolution(SparseModule):
             if packed.k_vol != 1:
                 w0 = self._get_weight()[0:1]
                 packed = pack_weight(w0, (1, 1, 1), self.in_channels, self.out_channels,
-                                     x.features.dtype)
+                                     packed.dtype)
             out = dense_forward(x.features, packed, self.bias, epilogue)
             return _derived(x, out, x.indices, x.spatial_shape)
         inv = fwd._inverse_cache
@@ -223,7 +226,8 @@ def _fusable(mods: List[nn.Module], i: int, conv: SparseConvolution,
     """The epilogue that modules i, i+1 (an eval-mode BatchNorm1d over the
     conv's channels, then a ReLU; either may be missing) amount to, and how
     many modules it covers."""
-    if not (x.features.is_cuda and _plain(conv)):
+    if not (x.features.is_cuda and _plain(conv)
+            and x.features.dtype in (torch.float32, torch.float16, torch.bfloat16)):
         return None, 0
     bn_parts = (None, None, None, None, 0.0)
     used = 0

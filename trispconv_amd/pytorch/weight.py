@@ -69,6 +69,8 @@ def pack_weight(w: torch.Tensor, kernel_size, in_channels: int, out_channels: in
     layout = weight_source(w, tuple(kernel_size), in_channels, out_channels)
     K = int(kernel_size[0]) * int(kernel_size[1]) * int(kernel_size[2])
     src = w.detach().contiguous()
+    if src.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        src = src.to(torch.float32)  # e.g. a float64 module: the kernels read f32/f16/bf16
     lib = L.lib()
     code = L.dtype_code(dtype)
     nbytes = lib.tsc_packed_weight_bytes(K, in_channels, out_channels, code)
