@@ -73,6 +73,23 @@ TSC_API int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_size,
                            const int32_t dilation[3] /* host */, void* ws, int64_t ws_bytes,
                            int32_t* cols_row, int32_t* nbr, int32_t* counts, tsc_stream_t stream);
 
+/* tsc_subm_pairs without a workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation).  No counterpart in the reference.  The
+ * scratch is a fixed device array of tsc_subm_pairs_noalloc_limit() bytes
+ * (64 MiB) in this library, one copy per GPU held until the process ends;
+ * the bitmap is used only when it fits there, else the hash, and a build
+ * that fits in neither is refused (TSC_EINVAL, nothing launched).  Outputs
+ * are those of tsc_subm_pairs for the same choice of structure.  Calls that
+ * overlap on one GPU (two streams or threads) share the array and race;
+ * calls in stream order do not.  Nothing is allocated. */
+TSC_API int64_t tsc_subm_pairs_noalloc_limit(void);
+TSC_API int tsc_subm_pairs_noalloc(const int32_t* coords, int64_t n, int32_t batch_size,
+                                   const int32_t spatial[3] /* host */,
+                                   const int32_t ksize[3] /* host */,
+                                   const int32_t dilation[3] /* host */, int32_t* cols_row,
+                                   int32_t* nbr, int32_t* counts, tsc_stream_t stream);
+
 /* The same build for rows that are the occupied cells of an existing
  * occupancy bitmap in rank order: one (word, rank) 8-byte entry per 32 cells
  * of the batch x spatial grid, row t the cell of rank t, no repeats.  That is

@@ -35,6 +35,9 @@ _SIGNATURES = {
     "tsc_subm_workspace_bytes": (_i64, [_i64, _i32, _i32, c_i32p]),
     "tsc_subm_pairs": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, _vp, _i64,
                                       _vp, _vp, _vp, _vp]),
+    "tsc_subm_pairs_noalloc_limit": (_i64, []),
+    "tsc_subm_pairs_noalloc": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, _vp, _vp,
+                                              _vp, _vp]),
     "tsc_subm_pairs_from_bitmap": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, _vp,
                                                   _i64, _vp, _vp, _vp, _vp]),
     "tsc_map_to_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _vp, _vp]),
