@@ -293,7 +293,7 @@ def bench_gpu(w, args, dev, mods, feats, idx):
 
             def plan(data=data, n_out=n_out, c_in=m.in_channels, elem=elem):
                 data._order = None
-                return data.execution_order(n_out, dev, c_in * elem)
+                return data.execution_order(n_out, dev, c_in * elem, eager=True)
             planned = plan() is not None
             plan_ms = event_ms(plan, 10) if planned else 0.0
             out = m.forward_with_epilogue(x, ep)

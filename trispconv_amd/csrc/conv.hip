@@ -383,30 +383,31 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
   const int nch = (c_in + CK - 1) / CK;  // C_in % 16 == 0: the last chunk may be half padding
 
   // ---- tile set-up: output rows, their slot lists and slot masks.  The map
-  // entries are read eight slots at a time, all eight loads in flight before
-  // any is used (rows past the end read row 0 and are then discarded).
+  // entries are read 32 slots at a time, all in flight before any is used
+  // (rows past the end read column 0 and are then discarded).  A map permuted
+  // into the execution order is indexed by processing position, so its first
+  // batch goes out before the order lookup: one memory round trip, not two.
   {
     const int64_t tr = tile0 + t;
-    const int32_t orow = tr < n_out ? (order ? order[tr] : static_cast<int32_t>(tr)) : -1;
-    s_orow[t] = orow;
-    // column of the map holding this row: its processing position when the map
-    // was permuted into the execution order (contiguous reads), else the row
-    const int64_t src_row = orow >= 0 ? (nbr_ordered ? tr : orow) : 0;
-    if (t < BN) {
-      const int64_t col = (int64_t)nbt * BN + t;
-      s_bias[t] = ep.bias ? load_param(ep.bias, ep.bias_dt, col) : 0.f;
-      channel_affine(ep, col, s_scale[t], s_shift[t]);
-    }
+    const bool in = tr < n_out;
     uint64_t m = 0;
-    for (int k0 = 0; k0 < K; k0 += 8) {
-      int32_t jv[8];
+    int32_t jv[32];
+    auto issue = [&](int k0, int64_t src_row, int32_t self) {
+      if (nbr) {
+        const int32_t* col = nbr + src_row;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int k = k0 + i < K ? k0 + i : K - 1;
-        jv[i] = nbr ? nbr[(int64_t)k * n_out + src_row] : static_cast<int32_t>(orow >= 0 ? orow : 0);
+        for (int i = 0; i < 32; ++i) {
+          const int k = k0 + i < K ? k0 + i : K - 1;
+          jv[i] = col[(int64_t)k * n_out];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) jv[i] = self;
       }
+    };
+    auto consume = [&](int k0, int32_t orow) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < 32; ++i) {
         const int k = k0 + i;
         const int32_t j = orow >= 0 ? jv[i] : -1;
         if (k < K) {
@@ -414,6 +415,27 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
           m |= (j >= 0 ? uint64_t(1) : uint64_t(0)) << k;
         }
       }
+    };
+    // column of the map holding this row: its processing position when the map
+    // was permuted into the execution order (contiguous reads), else the row
+    int32_t orow;
+    if (nbr && nbr_ordered) {
+      issue(0, in ? tr : 0, 0);
+      orow = in ? (order ? order[tr] : static_cast<int32_t>(tr)) : -1;
+    } else {
+      orow = in ? (order ? order[tr] : static_cast<int32_t>(tr)) : -1;
+      issue(0, orow >= 0 ? orow : 0, orow >= 0 ? orow : 0);
+    }
+    s_orow[t] = orow;
+    if (t < BN) {
+      const int64_t col = (int64_t)nbt * BN + t;
+      s_bias[t] = ep.bias ? load_param(ep.bias, ep.bias_dt, col) : 0.f;
+      channel_affine(ep, col, s_scale[t], s_shift[t]);
+    }
+    consume(0, orow);
+    for (int k0 = 32; k0 < K; k0 += 32) {
+      issue(k0, nbr_ordered ? (in ? tr : 0) : (orow >= 0 ? orow : 0), orow >= 0 ? orow : 0);
+      consume(k0, orow);
     }
     // OR over the wave (two 32-bit halves)
     uint32_t lo = static_cast<uint32_t>(m), hi = static_cast<uint32_t>(m >> 32);
@@ -610,15 +632,22 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
         }
       }
     __syncthreads();
+    // every LDS read of the pass is issued before the first store waits
+    constexpr int NQ = PR * CHUNKS / 64;
+    int32_t orows[NQ];
+    uint4 vals[NQ];
 #pragma unroll
-    for (int q = 0; q < PR * CHUNKS / 64; ++q) {
+    for (int q = 0; q < NQ; ++q) {
       const int piece = q * 64 + lane;
       const int row = piece / CHUNKS, ch = piece % CHUNKS;
-      const int32_t orow = s_orow[wave * 64 + pass * PR + row];
-      if (orow >= 0) {
-        const uint4 v = *reinterpret_cast<const uint4*>(stage + row * STRIDE + ch * 16);
-        *reinterpret_cast<uint4*>(out + (int64_t)orow * c_out + nbt * BN + ch * (16 / (int)sizeof(T))) = v;
-      }
+      orows[q] = s_orow[wave * 64 + pass * PR + row];
+      vals[q] = *reinterpret_cast<const uint4*>(stage + row * STRIDE + ch * 16);
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int ch = (q * 64 + lane) % CHUNKS;
+      if (orows[q] >= 0)
+        *reinterpret_cast<uint4*>(out + (int64_t)orows[q] * c_out + nbt * BN + ch * (16 / (int)sizeof(T))) = vals[q];
     }
   }
 }
@@ -668,29 +697,30 @@ __global__ void __launch_bounds__(256, 2) conv_split_kernel(
   const int nch = (c_in + CK - 1) / CK;
 
   // ---- set-up: wave w reads the map entries of its own slots for the 64
-  // rows, eight slots at a time, all eight loads in flight before any is used
+  // rows, sixteen slots at a time, all in flight before any is used; a map
+  // permuted into the execution order lets the first batch go out before the
+  // order lookup
   {
     const int64_t tr = tile0 + lane;
-    const int32_t orow = tr < n_out ? (order ? order[tr] : static_cast<int32_t>(tr)) : -1;
-    if (wave == 0) s_orow[lane] = orow;
-    const int64_t src_row = orow >= 0 ? (nbr_ordered ? tr : orow) : 0;
-    if (t < BN) {
-      const int64_t col = (int64_t)nbt * BN + t;
-      s_bias[t] = ep.bias ? load_param(ep.bias, ep.bias_dt, col) : 0.f;
-      channel_affine(ep, col, s_scale[t], s_shift[t]);
-    }
+    const bool in = tr < n_out;
     uint64_t m = 0;
-    for (int i0 = 0; wave + 4 * i0 < K; i0 += 8) {
-      int32_t jv[8];
+    int32_t jv[16];
+    auto issue = [&](int i0, int64_t src_row, int32_t self) {
+      if (nbr) {
+        const int32_t* col = nbr + src_row;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int k = wave + 4 * (i0 + i);
-        const int kk = k < K ? k : K - 1;
-        jv[i] = nbr ? nbr[(int64_t)kk * n_out + src_row]
-                    : static_cast<int32_t>(orow >= 0 ? orow : 0);
+        for (int i = 0; i < 16; ++i) {
+          const int k = wave + 4 * (i0 + i);
+          jv[i] = col[(int64_t)(k < K ? k : K - 1) * n_out];
+        }
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) jv[i] = self;
       }
+    };
+    auto consume = [&](int i0, int32_t orow) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
+      for (int i = 0; i < 16; ++i) {
         const int k = wave + 4 * (i0 + i);
         const int32_t j = orow >= 0 ? jv[i] : -1;
         if (k < K) {
@@ -698,6 +728,25 @@ __global__ void __launch_bounds__(256, 2) conv_split_kernel(
           m |= (j >= 0 ? uint64_t(1) : uint64_t(0)) << k;
         }
       }
+    };
+    int32_t orow;
+    if (nbr && nbr_ordered) {
+      issue(0, in ? tr : 0, 0);
+      orow = in ? (order ? order[tr] : static_cast<int32_t>(tr)) : -1;
+    } else {
+      orow = in ? (order ? order[tr] : static_cast<int32_t>(tr)) : -1;
+      issue(0, orow >= 0 ? orow : 0, orow >= 0 ? orow : 0);
+    }
+    if (wave == 0) s_orow[lane] = orow;
+    if (t < BN) {
+      const int64_t col = (int64_t)nbt * BN + t;
+      s_bias[t] = ep.bias ? load_param(ep.bias, ep.bias_dt, col) : 0.f;
+      channel_affine(ep, col, s_scale[t], s_shift[t]);
+    }
+    consume(0, orow);
+    for (int i0 = 16; wave + 4 * i0 < K; i0 += 16) {
+      issue(i0, nbr_ordered ? (in ? tr : 0) : (orow >= 0 ? orow : 0), orow >= 0 ? orow : 0);
+      consume(i0, orow);
     }
     uint32_t lo = static_cast<uint32_t>(m), hi = static_cast<uint32_t>(m >> 32);
 #pragma unroll

@@ -107,6 +107,8 @@ class IndiceData:
         # input rows the pairs may name: ids lie in [0, _in_bound) (the
         # builders' input rows; for user-assigned lists their largest id + 1)
         self._in_bound: Optional[int] = None
+        # convolutions run on these pairs so far without an execution order
+        self._conv_uses = 0
 
     @property
     def pair_num(self) -> torch.Tensor:
@@ -304,7 +306,8 @@ class IndiceData:
         self._pin, self._pout = pin, pout
         self._cnt = torch.tensor(sizes, dtype=torch.int32, device=device)
 
-    def execution_order(self, n_out: int, device, row_bytes: int = 256) -> Optional[torch.Tensor]:
+    def execution_order(self, n_out: int, device, row_bytes: int = 256,
+                        eager: bool = False) -> Optional[torch.Tensor]:
         """Processing order of the output rows for the fused convolution.
 
         Morton order cut into regions whose gathered input rows (``row_bytes``
@@ -312,11 +315,20 @@ class IndiceData:
         then its whole 256-row tiles put in decreasing number of slots used
         (the partial tile last).  Built once per region size and cached; None
         for small layers.
+
+        The order costs about as much as two uses of it save, and it never
+        changes an output bit, so the first convolution over these pairs runs
+        without one and the order is built when the pairs are used again (the
+        next layer with this indice_key, or the next forward); ``eager``
+        builds it at once.
         """
         if n_out < _PLAN_MIN_ROWS or n_out * int(row_bytes) < _PLAN_MIN_BYTES:
             return None
         region = int(min(max(_REGION_BYTES // max(int(row_bytes), 1), 2048), 1 << 30))
         if self._order is None or self._order_region != region:
+            self._conv_uses += 1
+            if self._conv_uses < 2 and not eager:
+                return None
             if self._map_cols is not None:  # the builder's columns, maybe in spatial order
                 nbr, cols_row, raster = self._map_cols, self._cols_row, self._raster
             else:
