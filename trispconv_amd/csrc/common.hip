@@ -234,6 +234,40 @@ __global__ void __launch_bounds__(kBmThreads) bitmap_reduce_kernel(const uint4* 
   if (threadIdx.x == 0) sums[blockIdx.x] = tot;
 }
 
+// The reduce pass for occupancy given as one byte per cell (0 or 1): packs
+// each word's 32 bytes into its bit mask (word x, y zeroed; words past nw,
+// the entry padding, read zero bytes) and sums the tile's popcounts.  Four
+// bytes b0..b3 of a little-endian dword map to the nibble b0 + 2b1 + 4b2 +
+// 8b3 in the top byte of dword * 0x01020408 (no carries reach it).
+__device__ __forceinline__ uint32_t pack_bytes(uint4 a, uint4 b) {
+  auto nib = [](uint32_t v) { return (v * 0x01020408u) >> 24; };
+  return nib(a.x) | nib(a.y) << 4 | nib(a.z) << 8 | nib(a.w) << 12 | nib(b.x) << 16 |
+         nib(b.y) << 20 | nib(b.z) << 24 | nib(b.w) << 28;
+}
+
+__global__ void __launch_bounds__(kBmThreads) bitmap_pack_kernel(const uint4* __restrict__ bytes,
+                                                                 uint4* __restrict__ wr2, int64_t nw,
+                                                                 uint32_t* __restrict__ sums) {
+  __shared__ uint32_t s_wave[33];
+  const int64_t p = (blockIdx.x * (int64_t)kBmTile) / 2 + 2 * threadIdx.x;  // entry pairs
+  uint32_t acc = 0;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    if (2 * (p + j) < nw) {
+      // words 2(p + j) and 2(p + j) + 1: 64 bytes, four 16-byte loads (the
+      // byte map covers whole entry pairs)
+      const uint4* src = bytes + 4 * (p + j);
+      const uint32_t m0 = pack_bytes(src[0], src[1]);
+      const uint32_t m1 = pack_bytes(src[2], src[3]);
+      wr2[p + j] = make_uint4(m0, 0u, m1, 0u);
+      acc += __popc(m0) + __popc(m1);
+    }
+  }
+  uint32_t tot;
+  block_exclusive(acc, s_wave, &tot);
+  if (threadIdx.x == 0) sums[blockIdx.x] = tot;
+}
+
 __global__ void __launch_bounds__(kBmThreads) bitmap_apply_kernel(uint4* __restrict__ wr2, int64_t nw,
                                                                   const uint32_t* __restrict__ sums,
                                                                   const uint32_t* __restrict__ pre,
@@ -285,14 +319,21 @@ int64_t bitmap_scan_scratch_words(int64_t nw) {
   return 2 * nsum + scan_scratch_words(nsum);
 }
 
-int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStream_t s) {
+int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStream_t s,
+                const uint8_t* bytes) {
   const int64_t nsum = ceil_div(nw > 0 ? nw : 1, kBmTile);
   uint32_t* sums = scratch;
   uint32_t* pre = scratch + nsum;
   uint32_t* more = scratch + 2 * nsum;
   uint4* wr2 = reinterpret_cast<uint4*>(wr);
-  bitmap_reduce_kernel<<<static_cast<unsigned>(nsum), kBmThreads, 0, s>>>(wr2, nw, sums);
-  TSC_LAUNCH_CHECK("bitmap_reduce");
+  if (bytes) {
+    bitmap_pack_kernel<<<static_cast<unsigned>(nsum), kBmThreads, 0, s>>>(
+        reinterpret_cast<const uint4*>(bytes), wr2, nw, sums);
+    TSC_LAUNCH_CHECK("bitmap_pack");
+  } else {
+    bitmap_reduce_kernel<<<static_cast<unsigned>(nsum), kBmThreads, 0, s>>>(wr2, nw, sums);
+    TSC_LAUNCH_CHECK("bitmap_reduce");
+  }
   const uint32_t* p = nullptr;
   if (nsum > kBmDirectTiles) {
     int rc = exclusive_scan_u32(sums, 2, nsum, pre, total, more, s);

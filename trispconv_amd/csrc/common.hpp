@@ -199,7 +199,8 @@ int64_t scan_scratch_words(int64_t n);
 // bitmap_scan fills every y from the x fields and writes the total to *total.
 int64_t bitmap_entries(int64_t nw);
 int64_t bitmap_scan_scratch_words(int64_t nw);
-int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStream_t s);
+int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStream_t s,
+                const uint8_t* bytes = nullptr);
 // The submanifold build (tsc_subm_pairs) on a given workspace.  ws_limit > 0:
 // ws is that many bytes of fixed scratch, the bitmap is used only when it
 // fits and a build that fits in neither way is an argument error; 0: ws is

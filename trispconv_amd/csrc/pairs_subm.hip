@@ -12,11 +12,13 @@
 // active set is:
 //   * occupancy bitmap (grids of up to about 2048 cells per voxel): one bit per
 //     cell, an exclusive popcount scan of its words (each occupied cell's rank
-//     in (b,z,y,x) order) and rank -> (row, cell), one 64-bit word per
+//     in (b,z,y,x) order) and rank -> (row + 1, cell), one 8-byte entry per
 //     column.  Columns are the occupied cells in rank order (then any earlier
 //     rows of repeated coordinates), so a wave's 64 lookups touch neighbouring
 //     cells and share cache lines, its map writes are contiguous, and a column
-//     reads its own cell from its word (no gather of its row's coordinates);
+//     reads its own cell from its entry (no gather of its row's coordinates).  Where the grid has at most 64 cells per row the bits are
+//     first marked as one byte per cell with plain stores and packed by the
+//     scan; sparser grids set them with atomics;
 //   * open-addressing hash of 2N..4N 64-bit slots otherwise, probed in row
 //     order (columns are rows).
 // The reference's pair lists are derived from the map only when asked for
@@ -59,13 +61,9 @@ __device__ __forceinline__ int4 cell_coords(const SubmGeom& g, uint32_t cell) {
                    static_cast<int>(y), static_cast<int>(x));
 }
 
-// A map column of the bitmap path as one 64-bit word: (row + 1) << 32 | cell
-// key, 0 while unassigned.  Rows sharing a cell differ only in the high half,
-// so the largest row is the largest word.
-__device__ __forceinline__ unsigned long long col_entry(int64_t row, uint32_t cell) {
-  return (static_cast<unsigned long long>(row + 1) << 32) | cell;
-}
-__device__ __forceinline__ int32_t entry_row(uint2 e) { return static_cast<int32_t>(e.y) - 1; }
+// A map column of the bitmap path is one 8-byte entry: x = its row + 1 (0
+// while unassigned; repeated cells keep the largest row by atomicMax on x)
+// and y = its cell key.
 
 __global__ void __launch_bounds__(256) subm_insert_kernel(const int4* __restrict__ coords,
                                                           int64_t n, SubmGeom g,
@@ -269,7 +267,8 @@ __global__ void __launch_bounds__(kRows) subm_probe_wide_kernel(
 // first cell (occupied cells before it in (b,z,y,x) order), so a lookup is
 // one load.
 
-// Zeroes the bitmap and the counters (one launch for all of them).
+// Zeroes the occupancy marks (bitmap entries or the byte map, as 16-byte
+// units) and the counters, in one launch.
 __global__ void __launch_bounds__(256) subm_init_kernel(uint4* __restrict__ wr2, int64_t n_pairs,
                                                         int32_t* __restrict__ counts, int K,
                                                         int32_t* __restrict__ n_extra) {
@@ -283,14 +282,23 @@ __global__ void __launch_bounds__(256) subm_init_kernel(uint4* __restrict__ wr2,
   }
 }
 
-// Sets each row's cell bit; rows outside the grid only raise a status flag.
-// Also marks every column unassigned (the rank pass fills them in).
+// Marks each row's cell occupied; rows outside the grid only raise a status
+// flag.  Also marks every column unassigned (the rank pass fills them in).
+// BYTES: one byte per cell, set by plain stores (every writer stores 1, so
+// races are harmless); the scan packs the bytes into the bitmap.  Otherwise
+// the cell's bit is set by a device-scope atomicOr, which on this part is
+// carried out beyond the XCD's L2 (the L2s are not coherent with each other):
+// several times the cost of the byte store and the packing pass together,
+// taken only where the byte map would be large (sparse grids).
+template <bool BYTES>
 __global__ void __launch_bounds__(256) subm_mark_kernel(const int4* __restrict__ coords, int64_t n,
-                                                        SubmGeom g, uint2* wr, int32_t* status,
-                                                        unsigned long long* __restrict__ cols) {
+                                                        SubmGeom g, uint2* wr,
+                                                        uint8_t* __restrict__ bytes,
+                                                        int32_t* status,
+                                                        uint2* __restrict__ col) {
   const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (r >= n) return;
-  cols[r] = 0ull;
+  col[r].x = 0u;
   const int4 c = coords[r];
   if (!in_grid(g, c.x, c.y, c.z, c.w)) {
     atomicOr(status, (c.x < 0 || c.x >= g.B) ? TSC_FLAG_BATCH_OUT_OF_RANGE
@@ -298,7 +306,10 @@ __global__ void __launch_bounds__(256) subm_mark_kernel(const int4* __restrict__
     return;
   }
   const uint32_t cell = cell_key(g, c.x, c.y, c.z, c.w);
-  atomicOr(&wr[cell >> 5].x, 1u << (cell & 31));
+  if constexpr (BYTES)
+    bytes[cell] = 1;
+  else
+    atomicOr(&wr[cell >> 5].x, 1u << (cell & 31));
 }
 
 // Rank of an occupied cell: occupied cells before it in (b,z,y,x) order.
@@ -309,11 +320,11 @@ __device__ __forceinline__ uint32_t cell_rank(uint2 e, uint32_t cell) {
 // Column (rank of the row's cell) = the largest row with that cell, and the
 // cell.  When every row has a cell of its own (n_unique == n) the ranks are
 // distinct and plain stores do; otherwise repeated cells take the largest row
-// by atomicMax (entries start at 0).
+// by atomicMax (entries start at 0; every writer stores the same cell).
 __global__ void __launch_bounds__(256) subm_rank_kernel(const int4* __restrict__ coords, int64_t n,
                                                         SubmGeom g, const uint2* __restrict__ wr,
                                                         const int32_t* __restrict__ n_unique,
-                                                        unsigned long long* cols) {
+                                                        uint2* col) {
   const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (r >= n) return;
   const bool unique = *n_unique == n;
@@ -321,10 +332,12 @@ __global__ void __launch_bounds__(256) subm_rank_kernel(const int4* __restrict__
   if (!in_grid(g, c.x, c.y, c.z, c.w)) return;
   const uint32_t cell = cell_key(g, c.x, c.y, c.z, c.w);
   const uint32_t rank = cell_rank(wr[cell >> 5], cell);
-  if (unique)
-    cols[rank] = col_entry(r, cell);
-  else
-    atomicMax(&cols[rank], col_entry(r, cell));
+  if (unique) {
+    col[rank] = make_uint2(static_cast<uint32_t>(r + 1), cell);
+  } else {
+    col[rank].y = cell;
+    atomicMax(&col[rank].x, static_cast<uint32_t>(r + 1));
+  }
 }
 
 // Columns of repeated coordinates: a row whose cell's last row is another
@@ -334,8 +347,7 @@ __global__ void __launch_bounds__(256) subm_rank_kernel(const int4* __restrict__
 __global__ void __launch_bounds__(256) subm_place_kernel(const int4* __restrict__ coords, int64_t n,
                                                          SubmGeom g, const uint2* __restrict__ wr,
                                                          const int32_t* __restrict__ n_unique,
-                                                         unsigned long long* cols,
-                                                         int32_t* n_extra) {
+                                                         uint2* col_e, int32_t* n_extra) {
   const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (r >= n) return;
   const int32_t nu = *n_unique;
@@ -344,9 +356,9 @@ __global__ void __launch_bounds__(256) subm_place_kernel(const int4* __restrict_
   if (!in_grid(g, c.x, c.y, c.z, c.w)) return;
   const uint32_t cell = cell_key(g, c.x, c.y, c.z, c.w);
   const uint32_t rank = cell_rank(wr[cell >> 5], cell);
-  if (cols[rank] != col_entry(r, cell)) {
-    const int32_t col = nu + atomicAdd(n_extra, 1);
-    cols[col] = col_entry(r, cell);  // col < rows in the grid <= n
+  if (col_e[rank].x != static_cast<uint32_t>(r + 1)) {
+    const int32_t c2 = nu + atomicAdd(n_extra, 1);  // < rows in the grid <= n
+    col_e[c2] = make_uint2(static_cast<uint32_t>(r + 1), cell);
   }
 }
 
@@ -369,7 +381,7 @@ constexpr int kLook = 8;
 
 __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
     int64_t n, int K, SubmGeom g, const uint2* __restrict__ wr,
-    const uint2* __restrict__ cols, const int32_t* __restrict__ n_unique,
+    const uint2* __restrict__ col_e, const int32_t* __restrict__ n_unique,
     const int32_t* __restrict__ n_extra, int32_t* __restrict__ cols_row, int32_t* __restrict__ nbr,
     int32_t* __restrict__ counts) {
   __shared__ int32_t s_cnt[64];
@@ -378,9 +390,9 @@ __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
   __syncthreads();
   const int64_t col = blockIdx.x * (int64_t)blockDim.x + t;
   const bool live = col < *n_unique + *n_extra;  // the other columns are empty
-  const uint2 me = live ? cols[col] : make_uint2(0u, 0u);
-  if (col < n) cols_row[col] = entry_row(me);
-  const int4 c = cell_coords(g, me.x);
+  const uint2 me = live ? col_e[col] : make_uint2(0u, 0u);
+  if (col < n) cols_row[col] = static_cast<int32_t>(me.x) - 1;
+  const int4 c = cell_coords(g, me.y);
   for (int k0 = 0; k0 < K; k0 += kLook) {
     uint32_t cell[kLook];
     uint2 e[kLook];
@@ -402,7 +414,7 @@ __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
     for (int i = 0; i < kLook; ++i) {
       const bool hit = look[i] && ((e[i].x >> (cell[i] & 31)) & 1u);
       // a hit's rank is below n_unique <= n; a miss reads column 0
-      jr[i] = entry_row(cols[hit ? cell_rank(e[i], cell[i]) : 0u]);
+      jr[i] = static_cast<int32_t>(col_e[hit ? cell_rank(e[i], cell[i]) : 0u].x) - 1;
       if (!hit) jr[i] = -1;
     }
 #pragma unroll
@@ -430,14 +442,23 @@ __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
 // rank t, no repeats: a strided build's sorted output and its bitmap), so the
 // columns are the rows, a row's cell comes from rows_coords and a hit's row
 // is its rank.
+//
+// With dil.x == 1 the hits of one kernel row are consecutive cells, so their
+// ranks are consecutive too: the columns of a run of up to three hits lie in
+// the four entries from (first rank & ~1), two aligned 16-byte loads, instead
+// of one load per hit.  The column array carries 4 entries of padding for
+// them.  Three kernel rows are processed at a time, which keeps the kernel
+// at eight waves per SIMD.
 template <int KX, int KZ, int KY, bool IDENT>
 __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
     int64_t n, int K, SubmGeom g, const uint2* __restrict__ wr, int64_t nw,
-    const uint2* __restrict__ cols, const int4* __restrict__ rows_coords,
+    const uint2* __restrict__ col_e, const int4* __restrict__ rows_coords,
     const int32_t* __restrict__ n_unique, const int32_t* __restrict__ n_extra,
     int32_t* __restrict__ cols_row, int32_t* __restrict__ nbr, int32_t* __restrict__ counts) {
   constexpr bool kStatic = KZ > 0 && KY > 0;
-  constexpr int kRowsAtOnce = kStatic ? KZ * KY : 9;  // rows whose entries load together
+  constexpr int kRowsAtOnce = kStatic ? KY : 3;  // rows whose entries load together
+  // the fixed-extent path stores whole batches without a row bound
+  static_assert(!kStatic || (KZ * KY) % kRowsAtOnce == 0, "row batches must tile the kernel");
   __shared__ int32_t s_cnt[kRows / kWave][64];
   const int t = threadIdx.x;
   const int lane = t & (kWave - 1);
@@ -450,9 +471,9 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
     if (live) cols_row[col] = static_cast<int32_t>(col);
   } else {
     live = col < *n_unique + *n_extra;  // the other columns are empty
-    const uint2 me = live ? cols[col] : make_uint2(0u, 0u);
-    if (col < n) cols_row[col] = entry_row(me);
-    c = cell_coords(g, me.x);
+    const uint2 me = live ? col_e[col] : make_uint2(0u, 0u);
+    if (col < n) cols_row[col] = static_cast<int32_t>(me.x) - 1;
+    c = cell_coords(g, me.y);
   }
   const int ksz = kStatic ? KZ : g.ks.z;
   const int ksy = kStatic ? KY : g.ks.y;
@@ -478,6 +499,8 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
       e1[i] = wr[w0 + 1 < nw ? w0 + 1 : w0];
     }
     int32_t jr[kRowsAtOnce][KX];
+    bool hit[kRowsAtOnce][KX];
+    uint32_t rank[kRowsAtOnce][KX];
 #pragma unroll
     for (int i = 0; i < kRowsAtOnce; ++i) {
 #pragma unroll
@@ -487,21 +510,59 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
         const uint32_t off = (base[i] & 31u) + static_cast<uint32_t>(x - x_first);  // < 64
         const uint2 e = off < 32u ? e0[i] : e1[i];
         const uint32_t b = off & 31u;
-        const bool hit = ok && ((e.x >> b) & 1u);
-        const uint32_t rank = e.y + __popc(e.x & ((1u << b) - 1u));
-        if constexpr (IDENT) {
-          // a rank outside the rows: the rows are not the bitmap's cells
-          if (hit && rank >= static_cast<uint64_t>(n)) {
-            atomicOr(&counts[K], TSC_FLAG_ROWS_NOT_BITMAP);
-            jr[i][kx] = -1;
-          } else {
-            jr[i][kx] = static_cast<int32_t>(rank);
-          }
-        } else {
-          jr[i][kx] = entry_row(cols[hit ? rank : 0u]);
-        }
-        if (!hit) jr[i][kx] = -1;
+        hit[i][kx] = ok && ((e.x >> b) & 1u);
+        rank[i][kx] = e.y + __popc(e.x & ((1u << b) - 1u));
       }
+    }
+    if constexpr (IDENT) {
+#pragma unroll
+      for (int i = 0; i < kRowsAtOnce; ++i)
+#pragma unroll
+        for (int kx = 0; kx < KX; ++kx) {
+          // a rank outside the rows: the rows are not the bitmap's cells
+          if (hit[i][kx] && rank[i][kx] >= static_cast<uint64_t>(n)) {
+            atomicOr(&counts[K], TSC_FLAG_ROWS_NOT_BITMAP);
+            hit[i][kx] = false;
+          }
+          jr[i][kx] = hit[i][kx] ? static_cast<int32_t>(rank[i][kx]) : -1;
+        }
+    } else if (g.dil.x != 1) {
+      // dilated rows skip cells, so other occupied cells can sit between the
+      // hits: one load per hit
+#pragma unroll
+      for (int i = 0; i < kRowsAtOnce; ++i)
+#pragma unroll
+        for (int kx = 0; kx < KX; ++kx)
+          jr[i][kx] = hit[i][kx] ? static_cast<int32_t>(col_e[rank[i][kx]].x) - 1 : -1;
+    } else {
+      // the row's first hit has the lowest rank; the others follow it
+      static_assert(KX <= 3, "a run of hits must fit four entries");
+      uint4 lo[kRowsAtOnce], hi[kRowsAtOnce];
+      uint32_t at[kRowsAtOnce];
+#pragma unroll
+      for (int i = 0; i < kRowsAtOnce; ++i) {
+        uint32_t first = 0u;
+        bool any = false;
+#pragma unroll
+        for (int kx = KX - 1; kx >= 0; --kx) {
+          first = hit[i][kx] ? rank[i][kx] : first;
+          any = any || hit[i][kx];
+        }
+        at[i] = first & ~1u;  // < n_unique <= n: the window stays in the padded array
+        const uint4* w = reinterpret_cast<const uint4*>(col_e + at[i]);
+        lo[i] = w[0];  // entries at, at + 1
+        // a run of up to three hits from first ends by entry (first & 1) + 2
+        hi[i] = any && (first & 1u) + (KX - 1) >= 2u ? w[1] : make_uint4(0u, 0u, 0u, 0u);
+      }
+#pragma unroll
+      for (int i = 0; i < kRowsAtOnce; ++i)
+#pragma unroll
+        for (int kx = 0; kx < KX; ++kx) {
+          const uint32_t d = rank[i][kx] - at[i];  // 0..3 for a hit
+          const uint4 v = d < 2u ? lo[i] : hi[i];
+          const uint32_t row1 = (d & 1u) ? v.z : v.x;
+          jr[i][kx] = hit[i][kx] ? static_cast<int32_t>(row1) - 1 : -1;
+        }
     }
 #pragma unroll
     for (int i = 0; i < kRowsAtOnce; ++i) {
@@ -645,24 +706,29 @@ struct SubmWork {
   unsigned long long* table;  // packed (key << 32 | row) words, or the 64-bit keys
   int32_t* vals;              // rows of the 64-bit-key table
   uint2* wr;       // bitmap entries (word, rank)
+  uint8_t* bytes;  // byte-per-cell occupancy (byte-marked bitmap builds)
   uint32_t* scan;  // bitmap scan scratch
-  unsigned long long* cols;  // map columns as (row + 1, cell) words
+  uint2* col;      // map columns: (row + 1, cell), 4 entries of padding
   int32_t *n_unique, *n_extra, *blk_cnt, *blk_off;
 };
 
+// How the build finds neighbours: hash table, or occupancy bitmap whose bits
+// are set by atomics or packed from a byte per cell.
+enum SubmMode { kSubmHash = 0, kSubmBitmap = 1, kSubmBytes = 2 };
+
 static int64_t bitmap_words(int64_t cells) { return ceil_div(cells, 32); }
 
-static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, bool bitmap,
-                           int64_t* used) {
+static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, int mode, int64_t* used) {
   Carver c(ws);
   const int64_t m = n > 0 ? n : 1;
   const int64_t nblk = ceil_div(m, kRows);
   SubmWork w{};
-  if (bitmap) {
+  if (mode != kSubmHash) {
     const int64_t nw = bitmap_words(cells);
     w.wr = c.take<uint2>(bitmap_entries(nw));
+    if (mode == kSubmBytes) w.bytes = c.take<uint8_t>(bitmap_entries(nw) * 32);
     w.scan = c.take<uint32_t>(bitmap_scan_scratch_words(nw));
-    w.cols = c.take<unsigned long long>(m);
+    w.col = c.take<uint2>(m + 4);
     w.n_unique = c.take<int32_t>(1);
     w.n_extra = c.take<int32_t>(1);
   } else {
@@ -676,12 +742,17 @@ static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, bool bitma
 }
 
 // Bitmap or hash: the bitmap while the grid is dense enough (and its cell ids
-// fit 32 bits); with a workspace limit, the hash when only it fits.
-static bool subm_pick_bitmap(int64_t n, int K, int64_t cells, int64_t ws_limit) {
-  if (!(cells < kNarrowCells && subm_use_bitmap(n, cells))) return false;
+// fit 32 bits), marked through a byte map while that is at most 64 bytes per
+// row; with a workspace limit, the first of these that fits.
+static int subm_pick_mode(int64_t n, int K, int64_t cells, int64_t ws_limit) {
+  if (!(cells < kNarrowCells && subm_use_bitmap(n, cells))) return kSubmHash;
   int64_t used = 0;
-  subm_carve(nullptr, n, K, cells, true, &used);
-  return used <= ws_limit;
+  if (cells <= 64 * n) {
+    subm_carve(nullptr, n, K, cells, kSubmBytes, &used);
+    if (used <= ws_limit) return kSubmBytes;
+  }
+  subm_carve(nullptr, n, K, cells, kSubmBitmap, &used);
+  return used <= ws_limit ? kSubmBitmap : kSubmHash;
 }
 
 __global__ void iota_kernel(int32_t* p, int64_t n) {
@@ -701,7 +772,7 @@ extern "C" int64_t tsc_subm_workspace_bytes(int64_t n, int32_t k_vol, int32_t ba
     return -1;
   const int64_t cells = (int64_t)batch_size * spatial[0] * spatial[1] * spatial[2];
   int64_t used = 0;
-  subm_carve(nullptr, n, k_vol, cells, subm_pick_bitmap(n, k_vol, cells, INT64_MAX), &used);
+  subm_carve(nullptr, n, k_vol, cells, subm_pick_mode(n, k_vol, cells, INT64_MAX), &used);
   return used;
 }
 
@@ -725,9 +796,9 @@ int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
   const int64_t cells = (int64_t)batch_size * shape.z * shape.y * shape.x;
   const int K = ks.z * ks.y * ks.x;
   TSC_REQUIRE(K <= 4096, "subm: kernel volume %d too large", K);
-  const bool bitmap = subm_pick_bitmap(n, K, cells, ws_limit > 0 ? ws_limit : INT64_MAX);
+  const int mode = subm_pick_mode(n, K, cells, ws_limit > 0 ? ws_limit : INT64_MAX);
   int64_t need = 0;
-  subm_carve(nullptr, n, K, cells, bitmap, &need);
+  subm_carve(nullptr, n, K, cells, mode, &need);
   if (ws_limit > 0)
     TSC_REQUIRE(need <= ws_limit,
                 "subm: this build needs %lld bytes of scratch, more than the %lld the "
@@ -743,36 +814,43 @@ int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
   TSC_REQUIRE(coords && cols_row && nbr && ws, "subm: null pointer");
 
   const int nblk = static_cast<int>(ceil_div(n, kRows));
-  const SubmWork w = subm_carve(ws, n, K, cells, bitmap, nullptr);
+  const SubmWork w = subm_carve(ws, n, K, cells, mode, nullptr);
   const int4* c4 = reinterpret_cast<const int4*>(coords);
   if (w.wr) {
     const int64_t nw = bitmap_words(cells);
-    const int64_t n_pairs = ceil_div(nw, 2);
     SubmGeom g{batch_size, shape, ks, dil, 0u};
-    uint4* wr2 = reinterpret_cast<uint4*>(w.wr);
-    const int64_t init_blocks = std::min<int64_t>(ceil_div(n_pairs, 256), 4096);
+    // zero the marks: the byte map (the scan then writes every bitmap entry)
+    // or the bitmap entries themselves
+    const int64_t units = w.bytes ? bitmap_entries(nw) * 2 : ceil_div(nw, 2);  // 16-byte units
+    uint4* marks = reinterpret_cast<uint4*>(w.bytes ? static_cast<void*>(w.bytes)
+                                                    : static_cast<void*>(w.wr));
+    const int64_t init_blocks = std::min<int64_t>(ceil_div(units, 256), 4096);
     subm_init_kernel<<<static_cast<unsigned>(init_blocks > 0 ? init_blocks : 1), 256, 0, s>>>(
-        wr2, n_pairs, counts, K, w.n_extra);
+        marks, units, counts, K, w.n_extra);
     TSC_LAUNCH_CHECK("subm_init");
-    subm_mark_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, counts + K, w.cols);
+    if (w.bytes)
+      subm_mark_kernel<true><<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.bytes, counts + K,
+                                                              w.col);
+    else
+      subm_mark_kernel<false><<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, nullptr,
+                                                               counts + K, w.col);
     TSC_LAUNCH_CHECK("subm_mark");
-    if ((rc = bitmap_scan(w.wr, nw, w.scan, w.n_unique, s))) return rc;
-    subm_rank_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, w.cols);
+    if ((rc = bitmap_scan(w.wr, nw, w.scan, w.n_unique, s, w.bytes))) return rc;
+    subm_rank_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, w.col);
     TSC_LAUNCH_CHECK("subm_rank");
-    subm_place_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, w.cols,
+    subm_place_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, w.col,
                                                        w.n_extra);
     TSC_LAUNCH_CHECK("subm_place");
-    const uint2* cols = reinterpret_cast<const uint2*>(w.cols);
     if (ks.x == 3 && 2 * dil.x < 32 && ks.y == 3 && ks.z == 3) {
       subm_probe_rows_kernel<3, 3, 3, false><<<ceil_div(n, 256), 256, 0, s>>>(
-          n, K, g, w.wr, nw, cols, nullptr, w.n_unique, w.n_extra, cols_row, nbr, counts);
+          n, K, g, w.wr, nw, w.col, nullptr, w.n_unique, w.n_extra, cols_row, nbr, counts);
       TSC_LAUNCH_CHECK("subm_probe_rows");
     } else if (ks.x == 3 && 2 * dil.x < 32) {
       subm_probe_rows_kernel<3, 0, 0, false><<<ceil_div(n, 256), 256, 0, s>>>(
-          n, K, g, w.wr, nw, cols, nullptr, w.n_unique, w.n_extra, cols_row, nbr, counts);
+          n, K, g, w.wr, nw, w.col, nullptr, w.n_unique, w.n_extra, cols_row, nbr, counts);
       TSC_LAUNCH_CHECK("subm_probe_rows");
     } else {
-      subm_probe_cols_kernel<<<ceil_div(n, 256), 256, 0, s>>>(n, K, g, w.wr, cols, w.n_unique,
+      subm_probe_cols_kernel<<<ceil_div(n, 256), 256, 0, s>>>(n, K, g, w.wr, w.col, w.n_unique,
                                                               w.n_extra, cols_row, nbr, counts);
       TSC_LAUNCH_CHECK("subm_probe_cols");
     }
