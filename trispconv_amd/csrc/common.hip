@@ -57,7 +57,8 @@ int fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hipStream_t
 __global__ void __launch_bounds__(1024) scan_slot_blocks_kernel(const int32_t* __restrict__ cnt,
                                                                 int32_t* __restrict__ off,
                                                                 int32_t* __restrict__ totals,
-                                                                int nblk) {
+                                                                int nblk, int K,
+                                                                int32_t* __restrict__ extra_total) {
   __shared__ uint32_t s_wave[33];
   const int k = blockIdx.x;
   const int32_t* c = cnt + (int64_t)k * nblk;
@@ -71,13 +72,38 @@ __global__ void __launch_bounds__(1024) scan_slot_blocks_kernel(const int32_t* _
     if (i < nblk) o[i] = static_cast<int32_t>(carry + ex);
     carry += tot;
   }
-  if (threadIdx.x == 0) totals[k] = static_cast<int32_t>(carry);
+  if (threadIdx.x == 0) {
+    if (k < K)
+      totals[k] = static_cast<int32_t>(carry);
+    else
+      *extra_total = static_cast<int32_t>(carry);
+  }
 }
 
 int scan_slot_blocks(const int32_t* cnt, int32_t* off, int32_t* totals, int K, int nblk,
-                     hipStream_t s) {
-  scan_slot_blocks_kernel<<<K, 1024, 0, s>>>(cnt, off, totals, nblk);
+                     hipStream_t s, int32_t* extra_total) {
+  scan_slot_blocks_kernel<<<K + (extra_total ? 1 : 0), 1024, 0, s>>>(cnt, off, totals, nblk, K,
+                                                                     extra_total);
   TSC_LAUNCH_CHECK("scan_slot_blocks");
+  return 0;
+}
+
+// One block per slot: totals[k] = sum over blocks of cnt[k][*].
+__global__ void __launch_bounds__(256) sum_slot_blocks_kernel(const int32_t* __restrict__ cnt,
+                                                              int32_t* __restrict__ totals,
+                                                              int nblk) {
+  __shared__ uint32_t s_wave[33];
+  const int32_t* c = cnt + (int64_t)blockIdx.x * nblk;
+  uint32_t acc = 0;
+  for (int i = threadIdx.x; i < nblk; i += blockDim.x) acc += static_cast<uint32_t>(c[i]);
+  uint32_t tot;
+  block_exclusive(acc, s_wave, &tot);
+  if (threadIdx.x == 0) totals[blockIdx.x] = static_cast<int32_t>(tot);
+}
+
+int sum_slot_blocks(const int32_t* cnt, int32_t* totals, int K, int nblk, hipStream_t s) {
+  sum_slot_blocks_kernel<<<K, 256, 0, s>>>(cnt, totals, nblk);
+  TSC_LAUNCH_CHECK("sum_slot_blocks");
   return 0;
 }
 

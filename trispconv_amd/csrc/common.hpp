@@ -182,9 +182,14 @@ int fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s);
 int fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hipStream_t s);
 
 // Per-slot, per-block counts -> exclusive offsets along blocks, plus totals.
-// cnt and off are [K][nblk]; totals[k] receives the sum of slot k.
+// cnt and off are [K][nblk]; totals[k] receives the sum of slot k.  With
+// extra_total, cnt and off hold one more row whose sum goes to *extra_total
+// (a per-block count summed without a contended atomic).
 int scan_slot_blocks(const int32_t* cnt, int32_t* off, int32_t* totals, int K, int nblk,
-                     hipStream_t s);
+                     hipStream_t s, int32_t* extra_total = nullptr);
+
+// Per-slot totals of per-block counts: totals[k] = sum of cnt[k][0..nblk).
+int sum_slot_blocks(const int32_t* cnt, int32_t* totals, int K, int nblk, hipStream_t s);
 
 // Exclusive scan of n uint32 values produced by `kind` from `src`:
 //   kind 0: popcount(src[i])   kind 1: src[i] != 0   kind 2: src[i]

@@ -90,13 +90,20 @@ struct Cands<0, 0, 0> {
   }
 };
 
-template <int KZ, int KY, int KX>
+// Marks every candidate output cell and counts each slot's pairs per block.
+// BYTES: one byte per output cell, set by plain stores (every writer stores
+// 1); the scan packs the bytes into the bitmap.  Otherwise the cells' bits are
+// set with device-scope atomics, which on this part are carried out beyond
+// the XCD's L2: several times the cost of the byte stores plus the packing
+// pass, so they are kept for sparse output grids only.
+template <int KZ, int KY, int KX, bool BYTES>
 __global__ void __launch_bounds__(kRows) strided_mark_kernel(const int4* __restrict__ coords,
                                                              int64_t n, int K, StridedGeom g,
-                                                             uint2* wr,
+                                                             uint2* wr, uint8_t* __restrict__ bytes,
                                                              int32_t* __restrict__ blk_cnt,
                                                              int nblk, int32_t* status,
                                                              int32_t* __restrict__ paired) {
+  // paired: [nblk] per-block counts of rows with a pair
   __shared__ int32_t s_cnt[kRows / kWave][64];
   const int t = threadIdx.x;
   const int w = t / kWave;
@@ -107,7 +114,13 @@ __global__ void __launch_bounds__(kRows) strided_mark_kernel(const int4* __restr
   if (valid && !ok) atomicOr(status, TSC_FLAG_BATCH_OUT_OF_RANGE);
   const Cands<KZ, KY, KX> cand(g, c, ok);
   constexpr int KC = KZ * KY * KX;
-  if constexpr (KC > 0) {
+  if constexpr (BYTES) {
+#pragma unroll
+    for (int k = 0; k < (KC ? KC : K); ++k) {
+      const int64_t cell = cand.cell(g, k);
+      if (cell >= 0) bytes[cell] = 1;
+    }
+  } else if constexpr (KC > 0) {
     // One atomic per bitmap word a (kz, ky) row of candidates touches, not
     // one per candidate: the row's cells share (b, oz, oy) and their x
     // positions are a few cells apart, so they fall in one or two words.
@@ -136,7 +149,7 @@ __global__ void __launch_bounds__(kRows) strided_mark_kernel(const int4* __restr
 #pragma unroll
   for (int k = 0; k < (KC ? KC : K); ++k) {
     const int64_t cell = cand.cell(g, k);
-    if (KC == 0 && cell >= 0) atomicOr(&wr[cell >> 5].x, 1u << (cell & 31));
+    if (!BYTES && KC == 0 && cell >= 0) atomicOr(&wr[cell >> 5].x, 1u << (cell & 31));
     any |= cell >= 0;
     const uint64_t hits = __ballot(cell >= 0);
     if (__lane_id() == 0) {
@@ -146,9 +159,18 @@ __global__ void __launch_bounds__(kRows) strided_mark_kernel(const int4* __restr
         atomicAdd(&blk_cnt[(int64_t)k * nblk + blockIdx.x], (int)__popcll(hits));
     }
   }
+  // rows with some pair: per block into row K of the count table (one
+  // counter bumped by every wave would serialize them all)
   const uint64_t with_pairs = __ballot(any);
-  if (__lane_id() == 0 && with_pairs) atomicAdd(paired, (int)__popcll(with_pairs));
+  __shared__ int32_t s_paired[kRows / kWave];
+  if (__lane_id() == 0) s_paired[w] = static_cast<int32_t>(__popcll(with_pairs));
   __syncthreads();
+  if (t == 0) {
+    int32_t sum = 0;
+#pragma unroll
+    for (int ww = 0; ww < kRows / kWave; ++ww) sum += s_paired[ww];
+    paired[blockIdx.x] = sum;
+  }
   if (t < K && t < 64) {
     int sum = 0;
 #pragma unroll
@@ -167,20 +189,36 @@ __global__ void __launch_bounds__(256) strided_emit_kernel(const uint2* __restri
   if (wi >= nwords) return;
   const uint2 e = wr[wi];
   uint32_t bits = e.x;
+  if (!bits) return;
   uint32_t rank = e.y;
+  // the word's first cell, decomposed once; later cells step along x with
+  // carries into y, z and the batch
   const int64_t plane = (int64_t)g.out.y * g.out.x;
   const int64_t vol = plane * g.out.z;
+  const int64_t cell0 = wi << 5;
+  int bb = static_cast<int>(cell0 / vol);
+  const int64_t rem = cell0 - bb * vol;
+  int z = static_cast<int>(rem / plane);
+  const int64_t r2 = rem - z * plane;
+  int y = static_cast<int>(r2 / g.out.x);
+  int x = static_cast<int>(r2 - (int64_t)y * g.out.x);
+  int at = 0;  // bit index of (bb, z, y, x)
   while (bits) {
     const int b = __ffs(bits) - 1;
     bits &= bits - 1;
-    const int64_t cell = (wi << 5) + b;
-    const int64_t bb = cell / vol;
-    const int64_t rem = cell - bb * vol;
-    const int64_t z = rem / plane;
-    const int64_t r2 = rem - z * plane;
-    const int64_t y = r2 / g.out.x;
-    const int64_t x = r2 - y * g.out.x;
-    if (rank < n_out) out_coords[rank] = make_int4((int)bb, (int)z, (int)y, (int)x);
+    x += b - at;
+    at = b;
+    while (x >= g.out.x) {
+      x -= g.out.x;
+      if (++y == g.out.y) {
+        y = 0;
+        if (++z == g.out.z) {
+          z = 0;
+          ++bb;
+        }
+      }
+    }
+    if (rank < n_out) out_coords[rank] = make_int4(bb, z, y, x);
     ++rank;
   }
 }
@@ -286,18 +324,26 @@ __global__ void __launch_bounds__(kRows) strided_fill_kernel(const int4* __restr
 
 struct Layout {
   int64_t cells, nwords, nblk;
+  bool bytes;  // output cells marked through a byte map
 };
+
+// The byte map costs its size twice (zeroing and packing); the atomics cost
+// about one device-scope atomic per (kz, ky) candidate row.  Bytes win up to
+// a few hundred output cells per input row.
+constexpr int64_t kBytesPerRow = 256;
 
 Layout layout(int64_t n, int32_t batch, const int32_t* out) {
   Layout L;
   L.cells = (int64_t)batch * out[0] * out[1] * out[2];
   L.nwords = ceil_div(L.cells > 0 ? L.cells : 1, 32);
   L.nblk = ceil_div(n > 0 ? n : 1, kRows);
+  L.bytes = n > 0 && L.cells <= kBytesPerRow * n;
   return L;
 }
 
 struct Buffers {
   uint2* wr;       // output-cell bitmap entries (word, rank)
+  uint8_t* bytes;  // byte-per-cell marks (byte-marked builds)
   uint32_t* scan;  // bitmap scan scratch
   int32_t* blk_cnt;
   int32_t* blk_off;
@@ -307,9 +353,10 @@ Buffers carve(void* ws, const Layout& L, int K, int64_t* used) {
   Carver c(ws);
   Buffers b;
   b.wr = c.take<uint2>(bitmap_entries(L.nwords));
+  b.bytes = L.bytes ? c.take<uint8_t>(bitmap_entries(L.nwords) * 32) : nullptr;
   b.scan = c.take<uint32_t>(bitmap_scan_scratch_words(L.nwords));
-  b.blk_cnt = c.take<int32_t>(L.nblk * K);
-  b.blk_off = c.take<int32_t>(L.nblk * K);
+  b.blk_cnt = c.take<int32_t>(L.nblk * (K + 1));  // row K: rows with a pair, per block
+  b.blk_off = c.take<int32_t>(L.nblk * (K + 1));
   if (used) *used = c.used;
   return b;
 }
@@ -326,10 +373,14 @@ int by_shape(const Box& ks, A... a) {
 
 template <int KZ, int KY, int KX>
 struct LaunchMark {
-  static int run(const int4* c, int64_t n, int K, StridedGeom g, uint2* wr, int32_t* blk_cnt,
-                 int nblk, int32_t* status, int32_t* paired, hipStream_t s) {
-    strided_mark_kernel<KZ, KY, KX><<<nblk, kRows, 0, s>>>(c, n, K, g, wr, blk_cnt, nblk, status,
-                                                           paired);
+  static int run(const int4* c, int64_t n, int K, StridedGeom g, uint2* wr, uint8_t* bytes,
+                 int32_t* blk_cnt, int nblk, int32_t* status, int32_t* paired, hipStream_t s) {
+    if (bytes)
+      strided_mark_kernel<KZ, KY, KX, true><<<nblk, kRows, 0, s>>>(c, n, K, g, wr, bytes, blk_cnt,
+                                                                   nblk, status, paired);
+    else
+      strided_mark_kernel<KZ, KY, KX, false><<<nblk, kRows, 0, s>>>(c, n, K, g, wr, nullptr,
+                                                                    blk_cnt, nblk, status, paired);
     TSC_LAUNCH_CHECK("strided_mark");
     return 0;
   }
@@ -401,17 +452,26 @@ extern "C" int tsc_strided_count(const int32_t* coords, int64_t n, int32_t batch
   TSC_REQUIRE(counts != nullptr, "strided: counts is null");
   Buffers b = carve(ws, L, K, nullptr);
   if ((rc = fill_u32(reinterpret_cast<uint32_t*>(counts), K + 3, 0u, s))) return rc;
-  if ((rc = fill_u32(reinterpret_cast<uint32_t*>(b.wr), 2 * bitmap_entries(L.nwords), 0u, s)))
+  // zero the marks: the byte map (the scan then writes every bitmap entry) or
+  // the bitmap entries
+  if (b.bytes) {
+    if ((rc = fill_u32(reinterpret_cast<uint32_t*>(b.bytes), 8 * bitmap_entries(L.nwords), 0u, s)))
+      return rc;
+  } else if ((rc = fill_u32(reinterpret_cast<uint32_t*>(b.wr), 2 * bitmap_entries(L.nwords), 0u,
+                            s))) {
     return rc;
+  }
   if (n == 0) return 0;
   TSC_REQUIRE(coords != nullptr, "strided: coords is null");
   if (K > 64 && (rc = fill_u32(reinterpret_cast<uint32_t*>(b.blk_cnt), L.nblk * K, 0u, s)))
     return rc;
   if ((rc = by_shape<LaunchMark>(g.ks, reinterpret_cast<const int4*>(coords), n, K, g, b.wr,
-                                 b.blk_cnt, (int)L.nblk, counts + K + 1, counts + K + 2, s)))
+                                 b.bytes, b.blk_cnt, (int)L.nblk, counts + K + 1,
+                                 b.blk_cnt + (int64_t)K * L.nblk, s)))
     return rc;
-  if ((rc = scan_slot_blocks(b.blk_cnt, b.blk_off, counts, K, (int)L.nblk, s))) return rc;
-  return bitmap_scan(b.wr, L.nwords, b.scan, counts + K, s);
+  if ((rc = scan_slot_blocks(b.blk_cnt, b.blk_off, counts, K, (int)L.nblk, s, counts + K + 2)))
+    return rc;
+  return bitmap_scan(b.wr, L.nwords, b.scan, counts + K, s, b.bytes);
 }
 
 extern "C" int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_size,

@@ -362,15 +362,25 @@ __global__ void __launch_bounds__(256) subm_place_kernel(const int4* __restrict_
   }
 }
 
-// Per-slot hit counting shared by the probes: per wave by ballot, per block
-// in LDS, then one atomic per block and slot.
-__device__ __forceinline__ void count_hit(int k, bool hit, int32_t* s_cnt, int32_t* counts) {
+// Per-slot hit counts of the probes: per wave by ballot, per block in LDS.
+// With a per-block table (blk_cnt, [K][nblk]) each block stores its counts
+// there and a small kernel sums them; without one (the build on a strided
+// output's bitmap has no workspace) each block adds them to counts.  Slots
+// from 64 on are added per wave into the block's entry (zeroed beforehand)
+// or into counts.
+__device__ __forceinline__ int32_t* slot_counter(int k, int32_t* blk_cnt, int nblk,
+                                                 int32_t* counts) {
+  return blk_cnt ? &blk_cnt[(int64_t)k * nblk + blockIdx.x] : &counts[k];
+}
+
+__device__ __forceinline__ void count_hit(int k, bool hit, int32_t* s_cnt, int32_t* blk_cnt,
+                                          int nblk, int32_t* counts) {
   const uint64_t hits = __ballot(hit);
   if (__lane_id() == 0 && hits) {
     if (k < 64)
       atomicAdd(&s_cnt[k], (int)__popcll(hits));
     else
-      atomicAdd(&counts[k], (int)__popcll(hits));
+      atomicAdd(slot_counter(k, blk_cnt, nblk, counts), (int)__popcll(hits));
   }
 }
 
@@ -383,7 +393,7 @@ __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
     int64_t n, int K, SubmGeom g, const uint2* __restrict__ wr,
     const uint2* __restrict__ col_e, const int32_t* __restrict__ n_unique,
     const int32_t* __restrict__ n_extra, int32_t* __restrict__ cols_row, int32_t* __restrict__ nbr,
-    int32_t* __restrict__ counts) {
+    int32_t* __restrict__ blk_cnt, int nblk, int32_t* __restrict__ counts) {
   __shared__ int32_t s_cnt[64];
   const int t = threadIdx.x;
   if (t < 64) s_cnt[t] = 0;
@@ -422,11 +432,16 @@ __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
       const int k = k0 + i;
       if (k >= K) continue;
       if (col < n) nbr[(int64_t)k * n + col] = jr[i];
-      count_hit(k, jr[i] >= 0, s_cnt, counts);
+      count_hit(k, jr[i] >= 0, s_cnt, blk_cnt, nblk, counts);
     }
   }
   __syncthreads();
-  if (t < K && t < 64 && s_cnt[t]) atomicAdd(&counts[t], s_cnt[t]);
+  if (t < K && t < 64) {
+    if (blk_cnt)
+      blk_cnt[(int64_t)t * nblk + blockIdx.x] = s_cnt[t];
+    else if (s_cnt[t])
+      atomicAdd(&counts[t], s_cnt[t]);
+  }
 }
 
 // The same for kernels KX cells wide whose x extent (KX - 1) * dil.x + 1 is at
@@ -454,7 +469,8 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
     int64_t n, int K, SubmGeom g, const uint2* __restrict__ wr, int64_t nw,
     const uint2* __restrict__ col_e, const int4* __restrict__ rows_coords,
     const int32_t* __restrict__ n_unique, const int32_t* __restrict__ n_extra,
-    int32_t* __restrict__ cols_row, int32_t* __restrict__ nbr, int32_t* __restrict__ counts) {
+    int32_t* __restrict__ cols_row, int32_t* __restrict__ nbr, int32_t* __restrict__ blk_cnt,
+    int nblk, int32_t* __restrict__ counts) {
   constexpr bool kStatic = KZ > 0 && KY > 0;
   constexpr int kRowsAtOnce = kStatic ? KY : 3;  // rows whose entries load together
   // the fixed-extent path stores whole batches without a row bound
@@ -575,7 +591,7 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
         if (lane_counts)
           my_cnt += lane == k ? static_cast<int32_t>(__popcll(hits)) : 0;
         else if (lane == 0 && hits)
-          atomicAdd(&counts[k], static_cast<int32_t>(__popcll(hits)));
+          atomicAdd(slot_counter(k, blk_cnt, nblk, counts), static_cast<int32_t>(__popcll(hits)));
       }
     }
     if (col < n) {  // the map stores, under one branch
@@ -595,7 +611,10 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
     int32_t sum = 0;
 #pragma unroll
     for (int w = 0; w < kRows / kWave; ++w) sum += s_cnt[w][t];
-    if (sum) atomicAdd(&counts[t], sum);
+    if (blk_cnt)
+      blk_cnt[(int64_t)t * nblk + blockIdx.x] = sum;
+    else if (sum)
+      atomicAdd(&counts[t], sum);
   }
 }
 
@@ -731,6 +750,7 @@ static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, int mode, 
     w.col = c.take<uint2>(m + 4);
     w.n_unique = c.take<int32_t>(1);
     w.n_extra = c.take<int32_t>(1);
+    w.blk_cnt = c.take<int32_t>(nblk * K);
   } else {
     w.table = c.take<unsigned long long>(subm_capacity(m));
     if (cells >= kNarrowCells) w.vals = c.take<int32_t>(subm_capacity(m));
@@ -841,19 +861,27 @@ int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
     subm_place_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, w.col,
                                                        w.n_extra);
     TSC_LAUNCH_CHECK("subm_place");
+    // slots from 64 on are added into the per-block table, which starts at 0
+    if (K > 64 &&
+        (rc = fill_u32(reinterpret_cast<uint32_t*>(w.blk_cnt), (int64_t)nblk * K, 0u, s)))
+      return rc;
     if (ks.x == 3 && 2 * dil.x < 32 && ks.y == 3 && ks.z == 3) {
       subm_probe_rows_kernel<3, 3, 3, false><<<ceil_div(n, 256), 256, 0, s>>>(
-          n, K, g, w.wr, nw, w.col, nullptr, w.n_unique, w.n_extra, cols_row, nbr, counts);
+          n, K, g, w.wr, nw, w.col, nullptr, w.n_unique, w.n_extra, cols_row, nbr, w.blk_cnt,
+          nblk, counts);
       TSC_LAUNCH_CHECK("subm_probe_rows");
     } else if (ks.x == 3 && 2 * dil.x < 32) {
       subm_probe_rows_kernel<3, 0, 0, false><<<ceil_div(n, 256), 256, 0, s>>>(
-          n, K, g, w.wr, nw, w.col, nullptr, w.n_unique, w.n_extra, cols_row, nbr, counts);
+          n, K, g, w.wr, nw, w.col, nullptr, w.n_unique, w.n_extra, cols_row, nbr, w.blk_cnt,
+          nblk, counts);
       TSC_LAUNCH_CHECK("subm_probe_rows");
     } else {
       subm_probe_cols_kernel<<<ceil_div(n, 256), 256, 0, s>>>(n, K, g, w.wr, w.col, w.n_unique,
-                                                              w.n_extra, cols_row, nbr, counts);
+                                                              w.n_extra, cols_row, nbr, w.blk_cnt,
+                                                              nblk, counts);
       TSC_LAUNCH_CHECK("subm_probe_cols");
     }
+    if ((rc = sum_slot_blocks(w.blk_cnt, counts, K, nblk, s))) return rc;
   } else {
     if ((rc = fill_u32(reinterpret_cast<uint32_t*>(counts), K + 2, 0u, s))) return rc;
     const int64_t cap = subm_capacity(n);
@@ -929,10 +957,10 @@ extern "C" int tsc_subm_pairs_from_bitmap(const int32_t* coords, int64_t n, int3
   const int4* c4 = reinterpret_cast<const int4*>(coords);
   if (ks.y == 3 && ks.z == 3)
     subm_probe_rows_kernel<3, 3, 3, true><<<ceil_div(n, 256), 256, 0, s>>>(
-        n, K, g, wr, nw, nullptr, c4, nullptr, nullptr, cols_row, nbr, counts);
+        n, K, g, wr, nw, nullptr, c4, nullptr, nullptr, cols_row, nbr, nullptr, 0, counts);
   else
     subm_probe_rows_kernel<3, 0, 0, true><<<ceil_div(n, 256), 256, 0, s>>>(
-        n, K, g, wr, nw, nullptr, c4, nullptr, nullptr, cols_row, nbr, counts);
+        n, K, g, wr, nw, nullptr, c4, nullptr, nullptr, cols_row, nbr, nullptr, 0, counts);
   TSC_LAUNCH_CHECK("subm_probe_rows");
   return 0;
 }
