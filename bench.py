@@ -163,9 +163,10 @@ def measured_traffic(kernel: str, workload: str, kern_ms: float):
     FETCH_SIZE / WRITE_SIZE summary of this workload, or None.
 
     Counters cannot be read inside a timed run, so the figure comes from the
-    profile summary; it is used only while the kernel's average duration in
-    that profile is within 15% of the live measurement (a stale profile of an
-    older kernel is not reported).
+    profile summary; it is used only while the kernel's duration in that
+    profile is within 15% (or 5 us, for kernels of a few microseconds whose
+    back-to-back timing here includes launch gaps) of the live measurement, so
+    a stale profile of an older kernel is not reported.
     """
     path = ROOT / "profiles" / f"{kernel.replace('_kernel', '')}_{workload}_traffic.txt"
     if not path.exists():
@@ -176,11 +177,11 @@ def measured_traffic(kernel: str, workload: str, kern_ms: float):
             k, _, v = line.partition(":")
             vals[k.strip()] = v.strip()
     try:
-        prof_us = float(vals["kernel_avg_us"])
-        nbytes = float(vals["traffic_bytes_per_launch"])
+        prof_us = float(vals["kernel_avg_us"].split()[0])
+        nbytes = float(vals["traffic_bytes_per_launch"].split()[0])
     except (KeyError, ValueError):
         return None
-    if abs(prof_us - kern_ms * 1e3) > 0.15 * prof_us:
+    if abs(prof_us - kern_ms * 1e3) > max(0.15 * prof_us, 5.0):
         return None
     return {"bytes": nbytes, "source": f"profiles/{path.name}"}
 
