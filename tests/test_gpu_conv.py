@@ -293,11 +293,14 @@ def test_slot_split_kernel_matches_the_256_row_kernel(c_in, c_out, dtype):
 
 
 @pytest.mark.parametrize("c_in,c_out,dtype", [(64, 128, torch.float16), (32, 128, torch.bfloat16),
-                                              (64, 128, torch.float32), (48, 64, torch.float16)])
+                                              (64, 128, torch.float32), (48, 64, torch.float16),
+                                              (128, 128, torch.bfloat16)])
 def test_every_column_tile_width_gives_the_same_bits(c_in, c_out, dtype):
     """The column tile width (32/64/128) only changes the schedule: each output
     is summed in the same slot and chunk order, so every width returns the same
-    bits, equal to the oracle within tolerance."""
+    bits, equal to the oracle within tolerance.  The forced widths run the
+    register-gather kernel; the layer's own choice is its direct-to-LDS variant
+    for f16/bf16 with C_in % 64 == 0, which must give those bits too."""
     idx = _tiny(21, (40, 40, 40), 1, 12000)
     x = torch.from_numpy(idx).to(DEV)
     feats = torch.randn(len(idx), c_in, generator=torch.Generator().manual_seed(2)).to(DEV).to(dtype)
@@ -307,10 +310,13 @@ def test_every_column_tile_width_gives_the_same_bits(c_in, c_out, dtype):
     outs = {}
     for tile in [32, 64] + ([128] if c_out % 128 == 0 else []):
         outs[tile] = _with_tile(feats, pw, m.bias, data, len(idx), tile)
-    if L.lib().tsc_conv_kernel_name(L.dtype_code(dtype), c_in, c_out, 27,
-                                    len(idx)) == b"conv_mfma_kernel":
+    name = L.lib().tsc_conv_kernel_name(L.dtype_code(dtype), c_in, c_out, 27, len(idx))
+    if name != b"conv_split_kernel":  # the slot-split kernel sums in another order
+        assert name == (b"conv_dma_kernel" if dtype != torch.float32 and c_in % 64 == 0
+                        else b"conv_mfma_kernel")
         # the layer's own choice is one of these widths
         outs[0] = Fn.sparse_conv_forward(feats, pw, m.bias, data, len(idx))
+    assert (0 in outs) == ((c_in, c_out) != (48, 64))
     first = outs[32]
     for tile, o in outs.items():
         say("tile", tile, c_in, c_out, dtype)
@@ -322,6 +328,49 @@ def test_every_column_tile_width_gives_the_same_bits(c_in, c_out, dtype):
     assert rel_err(to_np(first), ref) <= TOL[dtype]
     with pytest.raises(ValueError):
         _with_tile(feats, pw, m.bias, data, len(idx), 48)  # not a column tile width
+
+
+def _conv_raw(feats, pw, bias, nbr, order, ordered, n_out, tile):
+    """One layer through the C-ABI with explicit map operands: tsc_conv_forward
+    (tile 0: the layer's own kernel choice) or tsc_conv_forward_tile."""
+    out = torch.empty((n_out, pw.c_out), dtype=feats.dtype, device=feats.device)
+    lib = L.lib()
+    args = (feats.data_ptr(), L.dtype_code(feats.dtype), feats.shape[0], pw.c_in, pw.data.data_ptr(),
+            L.ptr(bias), L.dtype_code(bias.dtype), L.ptr(nbr), L.ptr(order), int(ordered), n_out,
+            pw.k_vol, pw.c_out)
+    if tile:
+        L.check(lib.tsc_conv_forward_tile(*args, tile, out.data_ptr(), L.stream_of(feats)), "tile")
+    else:
+        L.check(lib.tsc_conv_forward(*args, out.data_ptr(), L.stream_of(feats)), "conv")
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_dma_kernel_matches_the_register_gather_kernel(dtype):
+    """A 128-column layer of 150k rows: the direct-to-LDS kernel (the layer's
+    own choice) against the register-gather kernel forced to the same width,
+    bit for bit, with the map permuted into the execution order, with the
+    row-major map plus the order, and with the row-major map alone."""
+    idx = _tiny(31, (96, 96, 96), 1, 150000)
+    x = torch.from_numpy(idx).to(DEV)
+    feats = torch.randn(len(idx), 128, generator=torch.Generator().manual_seed(5)).to(DEV).to(dtype)
+    data = generate_subm_indice_pairs(x, (96, 96, 96), 1, 3)
+    m = _module("subm", 128, 128, 3, dtype=dtype, seed=21)
+    pw = m._packed_weight(dtype)
+    n = len(idx)
+    assert L.lib().tsc_conv_kernel_name(L.dtype_code(dtype), 128, 128, 27, n) == b"conv_dma_kernel"
+    order = data.execution_order(n, DEV, 128 * feats.element_size(), eager=True)
+    assert order is not None
+    permuted, order2, ordered = data.conv_operands(n, DEV, 128 * feats.element_size())
+    assert ordered and order2 is order
+    rowmajor = data.neighbour_map(n, DEV)
+    for label, ops in (("permuted map", (permuted, order, 1)), ("row-major map + order", (rowmajor, order, 0)),
+                       ("row-major map", (rowmajor, None, 0))):
+        say("dma vs register gather", dtype, label)
+        dma = _conv_raw(feats, pw, m.bias, *ops, n, 0)
+        reg = _conv_raw(feats, pw, m.bias, *ops, n, 128)
+        assert torch.equal(dma, reg), label
+        assert torch.isfinite(dma.float()).all()
 
 
 def test_raw_internal_weight_and_user_built_indice_data():

@@ -652,6 +652,335 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
   }
 }
 
+// ------------------------------------------------------ LDS DMA variant --
+// The same tile schedule as conv_mfma_kernel, for f16/bf16 layers whose
+// stages are 64 channels (C_in a multiple of 64) and with a neighbour map
+// (K > 1).  Its operands reach LDS through direct-to-LDS loads
+// (global_load_lds_dwordx4: each lane names a global address, the 16 bytes
+// land at M0 + 16 * lane), which changes how the gathered rows pass the
+// vector L1:
+//   - each quad of lanes reads one row's 64 contiguous bytes, which the L1
+//     serves as one access (an MFMA operand layout, 32 rows in 32 lanes,
+//     costs one access per lane);
+//   - the data skips the registers, so no transpose is needed to reach the
+//     operand layout: the MFMA reads its operands from LDS in that layout.
+// The weight slab and the map entries of each stage come the same way, so no
+// load the compiler can see remains in the main loop.  The DMA instructions
+// are issued from inline assembly: the compiler does not know they write LDS
+// and adds no waits for them (given the builtin, it waits for every
+// outstanding DMA before any LDS read).  The kernel waits with explicit
+// s_waitcnt at three points (below).  Nothing else in these kernels reads M0.
+__device__ __attribute__((aligned(16))) int32_t g_no_row[4] = {-1, -1, -1, -1};
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));  // low 32 bits of a shared pointer
+}
+__device__ __forceinline__ void dma_b128(const void* g, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(m0) : "memory");
+}
+__device__ __forceinline__ void dma_b32(const void* g, uint32_t m0) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" : : "v"(g), "s"(m0) : "memory");
+}
+
+// Dynamic LDS of conv_dma_kernel: two weight slabs, each wave's operand rows
+// of one stage (64 rows x 64 channels) and two stages of its map entries.
+template <typename T, int BN>
+constexpr size_t dma_pool_bytes() {
+  return (size_t)2 * BN * 64 * sizeof(T) + (size_t)4 * 64 * 64 * sizeof(T) + (size_t)4 * 2 * 256;
+}
+
+template <typename T, int BN>
+__global__ void __launch_bounds__(256, 2) conv_dma_kernel(
+    const T* __restrict__ feat, int c_in, const T* __restrict__ W, Epilogue ep,
+    const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int nbr_ordered,
+    int64_t n_out, int K, int c_out, T* __restrict__ out) {
+  using Op = MfmaOp<T>;
+  using V = typename Op::V;
+  constexpr int CK = 64;
+  constexpr int UB = 4;                      // 16-byte vectors per lane per row and stage
+  constexpr int NB = BN / 32;
+  constexpr int SLAB_VECS = BN * CK * (int)sizeof(T) / 16;
+  constexpr int WD = SLAB_VECS / 256;        // slab DMA instructions per wave
+  static_assert(SLAB_VECS % 256 == 0, "a slab splits into 1 KB pieces per wave");
+  constexpr int SLAB_BYTES = SLAB_VECS * 16;
+  constexpr int A_BYTES = 64 * CK * (int)sizeof(T);  // one wave's rows of one stage (8 KB)
+  // pool: slabs [2][SLAB_BYTES] | operand rows [4 waves][A_BYTES] |
+  // map entries [4 waves][2][64]; the output staging at the end
+  extern __shared__ __attribute__((aligned(16))) char pool[];
+  __shared__ __attribute__((aligned(16))) int32_t s_orow[kTileRows];
+  __shared__ float s_bias[BN];
+  __shared__ float s_scale[BN];
+  __shared__ float s_shift[BN];
+  __shared__ uint64_t s_mask[4];
+
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int h = lane >> 5;
+  const uint32_t wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t ncol = static_cast<uint32_t>(c_out / BN);
+  const uint32_t item = dealt_item(blockIdx.x, gridDim.x, ncol);
+  const int64_t tile0 = static_cast<int64_t>(item / ncol) * kTileRows;
+  const int nbt = static_cast<int>(item % ncol);
+  const int nch = c_in / CK;
+
+  // ---- tile set-up: output rows and slot masks (the entries themselves are
+  // loaded again stage by stage), as in conv_mfma_kernel
+  {
+    const int64_t tr = tile0 + t;
+    const bool in = tr < n_out;
+    uint64_t m = 0;
+    int32_t jv[32];
+    auto issue = [&](int k0, int64_t src_row) {
+      const int32_t* col = nbr + src_row;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const int k = k0 + i < K ? k0 + i : K - 1;
+        jv[i] = col[(int64_t)k * n_out];
+      }
+    };
+    auto consume = [&](int k0, int32_t orow) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const int k = k0 + i;
+        if (k < K && orow >= 0 && jv[i] >= 0) m |= uint64_t(1) << k;
+      }
+    };
+    int32_t orow;
+    if (nbr_ordered) {
+      issue(0, in ? tr : 0);
+      orow = in ? (order ? order[tr] : static_cast<int32_t>(tr)) : -1;
+    } else {
+      orow = in ? (order ? order[tr] : static_cast<int32_t>(tr)) : -1;
+      issue(0, orow >= 0 ? orow : 0);
+    }
+    s_orow[t] = orow;
+    if (t < BN) {
+      const int64_t col = (int64_t)nbt * BN + t;
+      s_bias[t] = ep.bias ? load_param(ep.bias, ep.bias_dt, col) : 0.f;
+      channel_affine(ep, col, s_scale[t], s_shift[t]);
+    }
+    consume(0, orow);
+    for (int k0 = 32; k0 < K; k0 += 32) {
+      issue(k0, nbr_ordered ? (in ? tr : 0) : (orow >= 0 ? orow : 0));
+      consume(k0, orow);
+    }
+    uint32_t lo = static_cast<uint32_t>(m), hi = static_cast<uint32_t>(m >> 32);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+      lo |= __shfl_xor(lo, off, kWave);
+      hi |= __shfl_xor(hi, off, kWave);
+    }
+    if (lane == 0) s_mask[wave] = (static_cast<uint64_t>(hi) << 32) | lo;
+  }
+  __syncthreads();
+  const uint64_t umask_v = s_mask[0] | s_mask[1] | s_mask[2] | s_mask[3];
+  const uint64_t umask =
+      (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(umask_v >> 32))) << 32) |
+      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(umask_v));
+  const uint64_t wmask_v = s_mask[wave];
+  const uint64_t wmask =
+      (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(wmask_v >> 32))) << 32) |
+      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(wmask_v));
+
+  auto advance = [&](int& k, int& c) {
+    const bool done = k >= K;
+    const bool more_c = c + 1 < nch;
+    const uint64_t above = k + 1 < 64 ? umask >> (k + 1) : 0;
+    const int nk = above ? k + 1 + __builtin_ctzll(above) : K;
+    const int k2 = done ? K : (more_c ? k : nk);
+    c = done ? c : (more_c ? c + 1 : 0);
+    k = k2;
+  };
+  auto uses = [&](int k) { return k < K && ((wmask >> k) & 1); };  // this wave computes slot k
+
+  const uint4* Wv = reinterpret_cast<const uint4*>(W);
+  const int nbt_all = c_out / 32;
+  uint64_t zero_addr = reinterpret_cast<uint64_t>(g_zero_row);
+  asm volatile("" : "+s"(zero_addr));
+  const char* zero_row = reinterpret_cast<const char*>(zero_addr);
+  uint64_t none_addr = reinterpret_cast<uint64_t>(g_no_row);
+  asm volatile("" : "+s"(none_addr));
+  const int32_t* no_row = reinterpret_cast<const int32_t*>(none_addr);
+
+  // LDS offsets for M0 (wave-uniform) and the same places as pointers
+  const uint32_t w_lds = lds_offset(pool);                                   // slab P: + P * SLAB_BYTES
+  const uint32_t a_lds = w_lds + 2 * SLAB_BYTES + wave_u * A_BYTES;
+  const uint32_t e_lds = w_lds + 2 * SLAB_BYTES + 4 * A_BYTES + wave_u * 512;  // entries P: + P * 256
+  const uint4* s_w = reinterpret_cast<const uint4*>(pool);
+  const char* s_a = pool + 2 * SLAB_BYTES + wave * A_BYTES;
+  const int32_t* s_e = reinterpret_cast<const int32_t*>(pool + 2 * SLAB_BYTES + 4 * A_BYTES + wave * 512);
+
+  // Map entries: lane l loads the entry of its wave's row l.  Operand rows:
+  // DMA instruction 2g + hh covers rows 16g..16g+15 of the wave and channel
+  // half hh; the quad of lanes 4q..4q+3 reads row 16g + q, lane 4q + j its
+  // 16-byte piece j ^ (q >> 2), which lands in LDS at (4q + j) * 16 of the
+  // instruction's 1 KB.  So piece p of row 16g + q sits at (4q + (p ^ (q >>
+  // 2))) * 16, and the MFMA's reads (lanes 0..15: rows q = 0..15, one piece)
+  // hit sixteen different 16-byte bank groups.
+  const int32_t orow_l = s_orow[wave * 64 + lane];
+  const int64_t col_l = nbr_ordered ? tile0 + wave * 64 + lane : (int64_t)orow_l;
+  const int q = lane >> 2;
+  const int piece = (lane & 3) ^ (q >> 2);
+
+  auto dma_slab = [&](int P, int k, int c) {  // the slab of stage (k, c) into buffer P
+    const uint4* src = Wv + (((int64_t)k * nch + c) * nbt_all + (int64_t)nbt * NB) * UB * 64 + t;
+#pragma unroll
+    for (int m = 0; m < WD; ++m)
+      dma_b128(src + m * 256, w_lds + P * SLAB_BYTES + (m * 256 + wave_u * 64) * 16);
+  };
+  auto dma_entries = [&](int P, int k) {  // slot k's entries of the wave's rows into buffer P
+    dma_b32(orow_l >= 0 ? nbr + (int64_t)k * n_out + col_l : no_row, e_lds + P * 256);
+  };
+  auto dma_rows = [&](int P, int c) {  // chunk c of the rows named by entry buffer P
+    int32_t j[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) j[g] = s_e[P * 64 + 16 * g + q];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const char* src =
+            j[g] >= 0 ? reinterpret_cast<const char*>(feat + (int64_t)j[g] * c_in + c * CK + hh * 32) + piece * 16
+                      : zero_row + piece * 16;
+        dma_b128(src, a_lds + (2 * g + hh) * 1024);
+      }
+  };
+  auto wait_vm0 = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
+  auto wait_vm8 = [] { asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); };  // all but 8 youngest
+  auto wait_lgkm0 = [] { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); };
+  const int qr = lane & 15;
+  auto a_read = [&](int rb, int u) {  // operand u of row block rb (rows rb*32 + lane%32)
+    const int g = rb * 2 + ((lane & 31) >> 4);
+    return *reinterpret_cast<const uint4*>(s_a + (2 * g + h) * 1024 + (4 * qr + (u ^ (qr >> 2))) * 16);
+  };
+
+  f32x16 acc[2][NB];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc[rb][nb][i] = 0.f;
+
+  // stages s (kc, cc), s + 1 (kn, cn) and s + 2 (kp, cp)
+  int kc = -1, cc = nch - 1;
+  advance(kc, cc);
+  int kn = kc, cn = cc;
+  advance(kn, cn);
+  int kp = kn, cp = cn;
+  advance(kp, cp);
+  if (kc < K) {
+    dma_entries(0, kc);
+    dma_slab(0, kc, cc);
+  }
+  if (kn < K) dma_entries(1, kn);
+  wait_vm0();
+  if (uses(kc)) dma_rows(0, cc);
+  wait_vm0();
+  __syncthreads();
+
+  // Stage s (slab and entry buffers S = s % 2), with the three waits:
+  //  1. vmcnt(0): this wave's rows of s have landed (issued in stage s - 1);
+  //  2. the slab of s + 1 and the entries of s + 2 go out; the rows of s and
+  //     the entries of s + 1 are read; lgkmcnt(0): the reads are done, so the
+  //     rows of s + 1 may overwrite the wave's one operand buffer;
+  //  3. MFMAs of s; vmcnt(8) (or 0 when no rows went out): the slab and the
+  //     entries have landed, the 8 row loads of s + 1 may still be in flight;
+  //     the barrier then publishes the slab to every wave.
+  auto body = [&](auto slot) {
+    constexpr int S = decltype(slot)::value;
+    wait_vm0();
+    if (kn < K) dma_slab(S ^ 1, kn, cn);
+    if (kp < K) dma_entries(S, kp);
+    const bool cur = uses(kc);
+    uint4 a[2][UB];
+    if (cur) {
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int u = 0; u < UB; ++u) a[rb][u] = a_read(rb, u);
+    }
+    wait_lgkm0();
+    const bool nxt = uses(kn);
+    if (nxt) dma_rows(S ^ 1, cn);
+    if (cur) {
+      const uint4* sw = s_w + S * SLAB_VECS;
+#pragma unroll
+      for (int u = 0; u < UB; ++u) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const V b = __builtin_bit_cast(V, sw[(nb * UB + u) * 64 + lane]);
+          acc[0][nb] = Op::run(__builtin_bit_cast(V, a[0][u]), b, acc[0][nb]);
+          acc[1][nb] = Op::run(__builtin_bit_cast(V, a[1][u]), b, acc[1][nb]);
+        }
+      }
+    }
+    if (nxt)
+      wait_vm8();
+    else
+      wait_vm0();
+    __syncthreads();
+    kc = kn;
+    cc = cn;
+    kn = kp;
+    cn = cp;
+    advance(kp, cp);
+  };
+  while (kc < K) {
+    body(Slot<0>{});
+    body(Slot<1>{});
+  }
+  wait_vm0();
+  __syncthreads();
+
+  // ---- epilogue, as in conv_mfma_kernel, staged in the pool
+  const bool affine = ep.mean != nullptr;
+  const bool relu = ep.relu != 0;
+  constexpr int ROW_BYTES = BN * (int)sizeof(T);
+  constexpr int STRIDE = ROW_BYTES + 16;
+  constexpr int CHUNKS = ROW_BYTES / 16;
+  constexpr int PR = mfma_stage_rows(ROW_BYTES);
+  static_assert((size_t)4 * PR * STRIDE <= dma_pool_bytes<T, BN>(), "staging exceeds the pool");
+  char* stage = pool + wave * PR * STRIDE;
+#pragma unroll
+  for (int pass = 0; pass < 64 / PR; ++pass) {
+    __syncthreads();
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int rblk = rb * 32 + (i >> 2) * 8;
+        if (rblk / PR != pass) continue;
+        const int row = rblk % PR + h * 4 + (i & 3);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const int cl = nb * 32 + (lane & 31);
+          *reinterpret_cast<T*>(stage + row * STRIDE + cl * (int)sizeof(T)) =
+              from_f32<T>(finish(acc[rb][nb][i] + s_bias[cl], s_scale[cl], s_shift[cl], affine,
+                                 relu));
+        }
+      }
+    __syncthreads();
+    constexpr int NQ = PR * CHUNKS / 64;
+    int32_t orows[NQ];
+    uint4 vals[NQ];
+#pragma unroll
+    for (int qq = 0; qq < NQ; ++qq) {
+      const int pc = qq * 64 + lane;
+      const int row = pc / CHUNKS, ch = pc % CHUNKS;
+      orows[qq] = s_orow[wave * 64 + pass * PR + row];
+      vals[qq] = *reinterpret_cast<const uint4*>(stage + row * STRIDE + ch * 16);
+    }
+#pragma unroll
+    for (int qq = 0; qq < NQ; ++qq) {
+      const int ch = (qq * 64 + lane) % CHUNKS;
+      if (orows[qq] >= 0)
+        *reinterpret_cast<uint4*>(out + (int64_t)orows[qq] * c_out + nbt * BN + ch * (16 / (int)sizeof(T))) = vals[qq];
+    }
+  }
+}
+
 // ------------------------------------------------- small-layer split --
 // Layers too small to give half the CUs a 256-row tile (a LiDAR encoder's
 // deepest layers, ~10k rows).  There the 256-row kernel is bound by one
@@ -1113,6 +1442,28 @@ int launch_mfma(const void* feat, int c_in, const void* W, const Epilogue& ep,
   return 0;
 }
 
+template <typename T, int BN>
+int launch_dma(const void* feat, int c_in, const void* W, const Epilogue& ep,
+               const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
+               int c_out, void* out, hipStream_t s) {
+  const int64_t items = ceil_div(n_out, kTileRows) * (c_out / BN);
+  TSC_REQUIRE(items < (int64_t(1) << 31), "conv: %lld workgroups exceed the grid limit",
+              static_cast<long long>(items));
+  TSC_REQUIRE(nbr != nullptr && c_in % 64 == 0, "conv: the DMA kernel needs a map and C_in %% 64 == 0");
+  constexpr size_t pool = dma_pool_bytes<T, BN>();
+  // more than 64 KB of dynamic LDS for the larger tiles: raise the limit once
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&conv_dma_kernel<T, BN>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(pool));
+  if (attr != hipSuccess)
+    return set_error(-static_cast<int>(attr), "conv_dma: %s", hipGetErrorString(attr));
+  conv_dma_kernel<T, BN><<<dim3(static_cast<unsigned>(items)), 256, pool, s>>>(
+      static_cast<const T*>(feat), c_in, static_cast<const T*>(W), ep, nbr, order, nbr_ordered,
+      n_out, K, c_out, static_cast<T*>(out));
+  TSC_LAUNCH_CHECK("conv_dma");
+  return 0;
+}
+
 template <typename T, int BN, int CK>
 int launch_split(const void* feat, int c_in, const void* W, const Epilogue& ep,
                  const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
@@ -1135,6 +1486,7 @@ struct MfmaChoice {
   int bn;      // column tile width
   int ck;      // input-channel chunk of one stage
   bool split;  // the 64-row slot-split kernel instead of the 256-row one
+  bool dma;    // the 256-row kernel's direct-to-LDS variant
 };
 
 // Narrower column tiles for small layers: below two workgroups per CU, halve
@@ -1147,15 +1499,18 @@ struct MfmaChoice {
 // separate weight loads cost more than the shorter slot chain saves.  Short
 // slot lists (K < 8) gain nothing from splitting.  column_tile != 0 forces
 // the 256-row kernel with that width (every width sums each output in the
-// same order, so all give the same bits).
+// same order, so all give the same bits), always on the register-gather
+// kernel.  The 256-row kernel's direct-to-LDS variant serves f16/bf16 layers
+// with 64-channel stages and a map (K > 1); it sums in the same order too.
 MfmaChoice choose_mfma(int dtype, int c_in, int c_out, int K, int64_t n_out, int column_tile) {
-  MfmaChoice c{pick_bn(c_out), pick_ck(dtype, c_in), false};
+  MfmaChoice c{pick_bn(c_out), pick_ck(dtype, c_in), false, false};
   if (column_tile) {
     c.bn = column_tile;
     return c;
   }
   while (c.bn > 32 && ceil_div(n_out, kTileRows) * (c_out / c.bn) < 512) c.bn /= 2;
   c.split = c.bn == 32 && K >= 8 && ceil_div(n_out, kTileRows) * (c_out / c.bn) < 128;
+  c.dma = !c.split && dtype != TSC_F32 && c.ck == 64 && c_in % 64 == 0 && K > 1;
   return c;
 }
 
@@ -1172,6 +1527,10 @@ int dispatch_mfma(const void* feat, int c_in, const void* W, const Epilogue& ep,
       if (ch.split)                                                                          \
         return launch_split<T, BN_, CK_>(feat, c_in, W, ep, nbr, order, nbr_ordered, n_out,  \
                                          K, c_out, out, s);                                  \
+    if constexpr (CK_ == 64 && !std::is_same<T, float>::value)                               \
+      if (ch.dma)                                                                            \
+        return launch_dma<T, BN_>(feat, c_in, W, ep, nbr, order, nbr_ordered, n_out, K,      \
+                                  c_out, out, s);                                            \
     return launch_mfma<T, BN_, CK_>(feat, c_in, W, ep, nbr, order, nbr_ordered,          \
                                     n_out, K, c_out, out, s);                                \
   }
@@ -1440,9 +1799,10 @@ extern "C" const char* tsc_conv_kernel_name(int32_t dtype, int32_t c_in, int32_t
                                             int32_t k_vol, int64_t n_out) {
   if (!dtype_ok(dtype) || c_in <= 0 || c_out <= 0 || k_vol <= 0 || n_out < 0) return "";
   switch (pick_path(dtype, c_in, c_out, k_vol)) {
-    case kMfma:
-      return choose_mfma(dtype, c_in, c_out, k_vol, n_out, 0).split ? "conv_split_kernel"
-                                                                    : "conv_mfma_kernel";
+    case kMfma: {
+      const MfmaChoice ch = choose_mfma(dtype, c_in, c_out, k_vol, n_out, 0);
+      return ch.split ? "conv_split_kernel" : ch.dma ? "conv_dma_kernel" : "conv_mfma_kernel";
+    }
     case kNarrow:
       return "conv_narrow_kernel";
     default:
