@@ -259,9 +259,10 @@ TSC_API int tsc_conv_forward_ep(const void* feat, int32_t dtype, int64_t n_in, i
 /* ------------------------------------------------------------------------
  * tsc_conv_forward with the column tile width chosen by the caller instead
  * of by the layer's size: column_tile = 32, 64 or 128 (dividing c_out) runs
- * the 256-row 32x32-tile kernel with that width; 0 chooses as
- * tsc_conv_forward does.  Every width sums each output in the same order, so
- * all return the same bits.  No counterpart in the reference (its Triton
+ * the 256-row 32x32-tile kernel with that width, always its register-gather
+ * form; 0 chooses as tsc_conv_forward does (which may pick the direct-to-LDS
+ * form of the same kernel).  Every width and both forms sum each output in
+ * the same order, so all return the same bits.  No counterpart in the reference (its Triton
  * path autotunes block sizes, triton_kernels.py:16-30); for tests that
  * compare the widths.  Any other width, or a layer the 32x32 tile does not
  * serve, is an argument error.
@@ -273,9 +274,9 @@ TSC_API int tsc_conv_forward_tile(const void* feat, int32_t dtype, int64_t n_in,
                                   int32_t column_tile, void* out, tsc_stream_t stream);
 
 /* Name of the kernel tsc_conv_forward launches for a layer of this shape
- * ("conv_mfma_kernel", "conv_split_kernel", "conv_narrow_kernel" or
- * "conv_valu_kernel"; "" for invalid sizes): what a kernel trace lists it
- * under.  No counterpart in the reference; for profilers and benchmarks. */
+ * ("conv_mfma_kernel", "conv_dma_kernel", "conv_split_kernel",
+ * "conv_narrow_kernel" or "conv_valu_kernel"; "" for invalid sizes): what a
+ * kernel trace lists it under.  No counterpart in the reference; for profilers and benchmarks. */
 TSC_API const char* tsc_conv_kernel_name(int32_t dtype, int32_t c_in, int32_t c_out,
                                          int32_t k_vol, int64_t n_out);
 
