@@ -300,7 +300,8 @@ def test_every_column_tile_width_gives_the_same_bits(c_in, c_out, dtype):
     is summed in the same slot and chunk order, so every width returns the same
     bits, equal to the oracle within tolerance.  The forced widths run the
     register-gather kernel; the layer's own choice is its direct-to-LDS variant
-    for f16/bf16 with C_in % 64 == 0, which must give those bits too."""
+    when a stage is 128 bytes of each row (f16/bf16 with C_in % 64 == 0, f32
+    with C_in % 32 == 0), which must give those bits too."""
     idx = _tiny(21, (40, 40, 40), 1, 12000)
     x = torch.from_numpy(idx).to(DEV)
     feats = torch.randn(len(idx), c_in, generator=torch.Generator().manual_seed(2)).to(DEV).to(dtype)
@@ -312,8 +313,8 @@ def test_every_column_tile_width_gives_the_same_bits(c_in, c_out, dtype):
         outs[tile] = _with_tile(feats, pw, m.bias, data, len(idx), tile)
     name = L.lib().tsc_conv_kernel_name(L.dtype_code(dtype), c_in, c_out, 27, len(idx))
     if name != b"conv_split_kernel":  # the slot-split kernel sums in another order
-        assert name == (b"conv_dma_kernel" if dtype != torch.float32 and c_in % 64 == 0
-                        else b"conv_mfma_kernel")
+        stage_bytes_fit = c_in % (32 if dtype == torch.float32 else 64) == 0
+        assert name == (b"conv_dma_kernel" if stage_bytes_fit else b"conv_mfma_kernel")
         # the layer's own choice is one of these widths
         outs[0] = Fn.sparse_conv_forward(feats, pw, m.bias, data, len(idx))
     assert (0 in outs) == ((c_in, c_out) != (48, 64))
@@ -345,7 +346,7 @@ def _conv_raw(feats, pw, bias, nbr, order, ordered, n_out, tile):
     return out
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 def test_dma_kernel_matches_the_register_gather_kernel(dtype):
     """A 128-column layer of 150k rows: the direct-to-LDS kernel (the layer's
     own choice) against the register-gather kernel forced to the same width,

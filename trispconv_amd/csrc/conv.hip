@@ -653,9 +653,9 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
 }
 
 // ------------------------------------------------------ LDS DMA variant --
-// The same tile schedule as conv_mfma_kernel, for f16/bf16 layers whose
-// stages are 64 channels (C_in a multiple of 64) and with a neighbour map
-// (K > 1).  Its operands reach LDS through direct-to-LDS loads
+// The same tile schedule as conv_mfma_kernel, for layers whose stages are
+// 128 bytes of every row (64 channels of f16/bf16 with C_in a multiple of 64,
+// 32 of f32 with C_in a multiple of 32) and with a neighbour map (K > 1).  Its operands reach LDS through direct-to-LDS loads
 // (global_load_lds_dwordx4: each lane names a global address, the 16 bytes
 // land at M0 + 16 * lane), which changes how the gathered rows pass the
 // vector L1:
@@ -683,10 +683,10 @@ __device__ __forceinline__ void dma_b32(const void* g, uint32_t m0) {
 }
 
 // Dynamic LDS of conv_dma_kernel: two weight slabs, each wave's operand rows
-// of one stage (64 rows x 64 channels) and two stages of its map entries.
+// of one stage (64 rows x 128 bytes) and two stages of its map entries.
 template <typename T, int BN>
 constexpr size_t dma_pool_bytes() {
-  return (size_t)2 * BN * 64 * sizeof(T) + (size_t)4 * 64 * 64 * sizeof(T) + (size_t)4 * 2 * 256;
+  return (size_t)2 * BN * 128 + (size_t)4 * 64 * 128 + (size_t)4 * 2 * 256;
 }
 
 template <typename T, int BN>
@@ -696,7 +696,8 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
     int64_t n_out, int K, int c_out, T* __restrict__ out) {
   using Op = MfmaOp<T>;
   using V = typename Op::V;
-  constexpr int CK = 64;
+  constexpr bool F32 = std::is_same<T, float>::value;
+  constexpr int CK = 128 / (int)sizeof(T);   // channels of a stage: 128 bytes of each row
   constexpr int UB = 4;                      // 16-byte vectors per lane per row and stage
   constexpr int NB = BN / 32;
   constexpr int SLAB_VECS = BN * CK * (int)sizeof(T) / 16;
@@ -704,6 +705,8 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
   static_assert(SLAB_VECS % 256 == 0, "a slab splits into 1 KB pieces per wave");
   constexpr int SLAB_BYTES = SLAB_VECS * 16;
   constexpr int A_BYTES = 64 * CK * (int)sizeof(T);  // one wave's rows of one stage (8 KB)
+  static_assert(A_BYTES == 8192 && (size_t)2 * SLAB_BYTES + 4 * A_BYTES + 2048 == dma_pool_bytes<T, BN>(),
+                "pool layout");
   // pool: slabs [2][SLAB_BYTES] | operand rows [4 waves][A_BYTES] |
   // map entries [4 waves][2][64]; the output staging at the end
   extern __shared__ __attribute__((aligned(16))) char pool[];
@@ -841,7 +844,7 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const char* src =
-            j[g] >= 0 ? reinterpret_cast<const char*>(feat + (int64_t)j[g] * c_in + c * CK + hh * 32) + piece * 16
+            j[g] >= 0 ? reinterpret_cast<const char*>(feat + (int64_t)j[g] * c_in + c * CK + hh * (CK / 2)) + piece * 16
                       : zero_row + piece * 16;
         dma_b128(src, a_lds + (2 * g + hh) * 1024);
       }
@@ -910,9 +913,25 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
       for (int u = 0; u < UB; ++u) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-          const V b = __builtin_bit_cast(V, sw[(nb * UB + u) * 64 + lane]);
-          acc[0][nb] = Op::run(__builtin_bit_cast(V, a[0][u]), b, acc[0][nb]);
-          acc[1][nb] = Op::run(__builtin_bit_cast(V, a[1][u]), b, acc[1][nb]);
+          const uint4 bv = sw[(nb * UB + u) * 64 + lane];
+          if constexpr (F32) {
+            // four 32x32x2 steps per vector: step i uses element i of A and B
+            const float4 a0 = __builtin_bit_cast(float4, a[0][u]);
+            const float4 a1 = __builtin_bit_cast(float4, a[1][u]);
+            const float4 b4 = __builtin_bit_cast(float4, bv);
+            acc[0][nb] = Op::run(a0.x, b4.x, acc[0][nb]);
+            acc[1][nb] = Op::run(a1.x, b4.x, acc[1][nb]);
+            acc[0][nb] = Op::run(a0.y, b4.y, acc[0][nb]);
+            acc[1][nb] = Op::run(a1.y, b4.y, acc[1][nb]);
+            acc[0][nb] = Op::run(a0.z, b4.z, acc[0][nb]);
+            acc[1][nb] = Op::run(a1.z, b4.z, acc[1][nb]);
+            acc[0][nb] = Op::run(a0.w, b4.w, acc[0][nb]);
+            acc[1][nb] = Op::run(a1.w, b4.w, acc[1][nb]);
+          } else {
+            const V b = __builtin_bit_cast(V, bv);
+            acc[0][nb] = Op::run(__builtin_bit_cast(V, a[0][u]), b, acc[0][nb]);
+            acc[1][nb] = Op::run(__builtin_bit_cast(V, a[1][u]), b, acc[1][nb]);
+          }
         }
       }
     }
@@ -1449,7 +1468,9 @@ int launch_dma(const void* feat, int c_in, const void* W, const Epilogue& ep,
   const int64_t items = ceil_div(n_out, kTileRows) * (c_out / BN);
   TSC_REQUIRE(items < (int64_t(1) << 31), "conv: %lld workgroups exceed the grid limit",
               static_cast<long long>(items));
-  TSC_REQUIRE(nbr != nullptr && c_in % 64 == 0, "conv: the DMA kernel needs a map and C_in %% 64 == 0");
+  constexpr int CK = 128 / (int)sizeof(T);
+  TSC_REQUIRE(nbr != nullptr && c_in % CK == 0, "conv: the DMA kernel needs a map and C_in %% %d == 0",
+              CK);
   constexpr size_t pool = dma_pool_bytes<T, BN>();
   // more than 64 KB of dynamic LDS for the larger tiles: raise the limit once
   static const hipError_t attr = hipFuncSetAttribute(
@@ -1500,8 +1521,9 @@ struct MfmaChoice {
 // slot lists (K < 8) gain nothing from splitting.  column_tile != 0 forces
 // the 256-row kernel with that width (every width sums each output in the
 // same order, so all give the same bits), always on the register-gather
-// kernel.  The 256-row kernel's direct-to-LDS variant serves f16/bf16 layers
-// with 64-channel stages and a map (K > 1); it sums in the same order too.
+// kernel.  The 256-row kernel's direct-to-LDS variant serves layers whose
+// stages are 128 bytes of each row (f16/bf16 with C_in % 64 == 0, f32 with
+// C_in % 32 == 0) and that have a map (K > 1); it sums in the same order too.
 MfmaChoice choose_mfma(int dtype, int c_in, int c_out, int K, int64_t n_out, int column_tile) {
   MfmaChoice c{pick_bn(c_out), pick_ck(dtype, c_in), false, false};
   if (column_tile) {
@@ -1510,7 +1532,7 @@ MfmaChoice choose_mfma(int dtype, int c_in, int c_out, int K, int64_t n_out, int
   }
   while (c.bn > 32 && ceil_div(n_out, kTileRows) * (c_out / c.bn) < 512) c.bn /= 2;
   c.split = c.bn == 32 && K >= 8 && ceil_div(n_out, kTileRows) * (c_out / c.bn) < 128;
-  c.dma = !c.split && dtype != TSC_F32 && c.ck == 64 && c_in % 64 == 0 && K > 1;
+  c.dma = !c.split && K > 1 && c.ck * dtype_bytes(dtype) == 128 && c_in % c.ck == 0;
   return c;
 }
 
@@ -1527,7 +1549,7 @@ int dispatch_mfma(const void* feat, int c_in, const void* W, const Epilogue& ep,
       if (ch.split)                                                                          \
         return launch_split<T, BN_, CK_>(feat, c_in, W, ep, nbr, order, nbr_ordered, n_out,  \
                                          K, c_out, out, s);                                  \
-    if constexpr (CK_ == 64 && !std::is_same<T, float>::value)                               \
+    if constexpr (CK_ * sizeof(T) == 128)                                                    \
       if (ch.dma)                                                                            \
         return launch_dma<T, BN_>(feat, c_in, W, ep, nbr, order, nbr_ordered, n_out, K,      \
                                   c_out, out, s);                                            \
