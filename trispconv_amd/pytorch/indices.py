@@ -392,6 +392,11 @@ def _coords(indices: torch.Tensor, what: str) -> torch.Tensor:
     return coords
 
 
+def _align64(count: int) -> int:
+    """count rounded up to a multiple of 64 int32 elements (256 bytes)."""
+    return (int(count) + 63) // 64 * 64
+
+
 def _raise_status(status: int, what: str) -> None:
     if status & L.FLAG_BATCH_OUT_OF_RANGE:
         raise IndexError(f"{what}: batch index outside [0, batch_size)")
@@ -465,23 +470,31 @@ def generate_subm_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size:
         raise ValueError(f"generate_subm_indice_pairs: invalid batch size {batch_size} or "
                          f"spatial shape {shape}")
     ws = L.workspace(ws_bytes, dev)
-    # the map by columns (in (b,z,y,x) order when the bitmap path runs); the
-    # reference's pair lists are derived from it on first access
-    cols_row = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
-    map_cols = torch.empty((K, n), dtype=torch.int32, device=dev)
-    counts = torch.empty(K + 2, dtype=torch.int32, device=dev)
+    # The map by columns (in (b,z,y,x) order when the bitmap path runs; the
+    # reference's pair lists are derived from it on first access), the column
+    # -> row table and the counts: one allocation, 256-byte aligned views.
+    n_al = _align64(max(n, 1))
+    tables = torch.empty(n_al + _align64(K * n) + K + 2, dtype=torch.int32, device=dev)
+    cols_row = tables[:n]
+    map_cols = tables[n_al:n_al + K * n].view(K, n)
+    counts = tables[n_al + _align64(K * n):][:K + 2]
     L.check(lib.tsc_subm_pairs(coords.data_ptr(), n, int(batch_size), L.i3(shape), L.i3(ks),
                                L.i3(dil), ws.data_ptr(), ws.numel(), cols_row.data_ptr(),
                                map_cols.data_ptr(), counts.data_ptr(), L.stream_of(coords)),
             "generate_subm_indice_pairs")
-    host = counts.cpu()
-    _raise_status(int(host[K]), "generate_subm_indice_pairs")
-    return IndiceData._from_tables(
+    # the result object is made while the kernels run; the counts and the
+    # status flags are read after
+    d = IndiceData._from_tables(
         out_indices=indices, input_indices=indices, input_spatial_shape=spatial_shape,
         output_spatial_shape=spatial_shape, kernel_size=ks, stride=(1, 1, 1),
         padding=(0, 0, 0), dilation=dil, subm=True, pin=None, pout=None, cnt_dev=None,
-        pair_num=host[:K].long(), nbr=None, batch_size=int(batch_size), map_cols=map_cols,
-        cols_row=cols_row[:n], raster=bool(host[K + 1]))
+        pair_num=None, nbr=None, batch_size=int(batch_size), map_cols=map_cols,
+        cols_row=cols_row)
+    host = counts.cpu()
+    _raise_status(int(host[K]), "generate_subm_indice_pairs")
+    d.pair_num = host[:K].long()
+    d._raster = bool(host[K + 1])
+    return d
 
 
 def generate_strided_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size: int,
@@ -507,10 +520,16 @@ def generate_strided_indice_pairs(indices: torch.Tensor, spatial_shape, batch_si
     host = counts.cpu()
     _raise_status(int(host[K + 1]), "generate_strided_indice_pairs")
     n_out = int(host[K])
+    # the output coordinates (the next tensor's indices, with their own
+    # storage and version counter); the map and the two pair tables in one
+    # allocation, 256-byte aligned views
     out_coords = torch.empty((n_out, 4), dtype=torch.int32, device=dev)
-    nbr = torch.empty((K, n_out), dtype=torch.int32, device=dev)
-    pin = torch.empty((K, n), dtype=torch.int32, device=dev)
-    pout = torch.empty((K, n), dtype=torch.int32, device=dev)
+    o_pin = _align64(K * n_out)
+    o_pout = o_pin + _align64(K * n)
+    tables = torch.empty(max(o_pout + K * n, 1), dtype=torch.int32, device=dev)
+    nbr = tables[:K * n_out].view(K, n_out)
+    pin = tables[o_pin:o_pin + K * n].view(K, n)
+    pout = tables[o_pout:o_pout + K * n].view(K, n)
     L.check(lib.tsc_strided_fill(coords.data_ptr(), n, int(batch_size), *geo, ws.data_ptr(),
                                  ws.numel(), n_out, out_coords.data_ptr(), nbr.data_ptr(),
                                  pin.data_ptr(), pout.data_ptr(), stream),
