@@ -18,8 +18,10 @@ them), inputs already resident in HBM:
 
 Prints ONE JSON line.  Its top-level fields are the headline layer's
 (``value`` = voxels/s = N_in / step time); ``configs`` holds every workload:
-voxels/s, effective TFLOP/s, per-layer conv kernel durations (HIP events on
-the stream the kernels run on), pair-build times with their fraction of HBM
+voxels/s, effective TFLOP/s, per-layer conv times (HIP events on the stream
+the kernels run on, between the layers of the network run in order; each
+includes the few microseconds its event adds, so a network's layer times sum
+to more than its step), pair-build times with their fraction of HBM
 bandwidth, the dominant conv kernel against its roofline (fp16/bf16/fp32 MFMA
 peak or HBM, whichever its arithmetic intensity makes the bound), and the
 reference's CPU path timed on this host (``cpu_baseline``).
@@ -262,6 +264,7 @@ def bench_gpu(w, args, dev, mods, feats, idx):
 
     # ---- per layer: pair build, plan, conv kernel (pairs cached, epilogue fused)
     layers = []
+    seq = []  # (module, fused epilogue) of each layer, in order
     mods_list = list(net.children())
     with torch.no_grad():
         x = warm
@@ -298,7 +301,7 @@ def bench_gpu(w, args, dev, mods, feats, idx):
             planned = plan() is not None
             plan_ms = event_ms(plan, 10) if planned else 0.0
             out = m.forward_with_epilogue(x, ep)
-            conv_ms = back_to_back_ms(lambda m=m, x=x, ep=ep: m.forward_with_epilogue(x, ep), 20)
+            seq.append((m, ep))
             flops = 2.0 * P * m.in_channels * m.out_channels
             kname = L.lib().tsc_conv_kernel_name(L.dtype_code(x.features.dtype), m.in_channels,
                                                  m.out_channels, k_vol, n_out).decode()
@@ -311,7 +314,7 @@ def bench_gpu(w, args, dev, mods, feats, idx):
             layers.append({
                 "layer": f"{kind} {tuple(m.kernel_size)} {m.in_channels}->{m.out_channels}",
                 "rows_in": len(x.indices), "rows_out": n_out, "pairs": P,
-                "conv_ms": conv_ms, "tflops": flops / (conv_ms * 1e-3) / 1e12,
+                "conv_ms": None, "tflops": None,  # set below, from the layer sequence
                 "pair_build_ms": pair_ms,
                 "pair_build_hbm": {"algorithmic_bytes": int(pb), "gbs": pb / (pair_ms * 1e6),
                                    "frac": pb / (pair_ms * 1e6) / HBM_PEAK_GBS},
@@ -319,10 +322,32 @@ def bench_gpu(w, args, dev, mods, feats, idx):
                 "epilogue": None if ep is None else
                 ("bn+relu" if ep.mean is not None and ep.relu else
                  "bn" if ep.mean is not None else "relu"),
-                "roofline": roofline(flops, alg, conv_ms, w.dtype, kname, w.name),
+                "roofline": {"flops": flops, "algorithmic_bytes": alg, "kernel": kname},
             })
             x = out
             i += used
+
+    # ---- per-layer conv times as the step runs them: the layers in order,
+    # each on the previous one's output, with events between them (median
+    # over 20 passes).  Timing a layer alone, back to back on one input,
+    # gives other cache states than the network and can differ by a third.
+    reps = 20
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(seq) + 1)] for _ in range(reps)]
+    with torch.no_grad():
+        for r in range(reps):
+            y = warm
+            evs[r][0].record(stream)
+            for j, (m, ep) in enumerate(seq):
+                y = m.forward_with_epilogue(y, ep)
+                evs[r][j + 1].record(stream)
+        torch.cuda.synchronize()
+    for j, lay in enumerate(layers):
+        conv_ms = float(np.median([evs[r][j].elapsed_time(evs[r][j + 1]) for r in range(reps)]))
+        rf = lay["roofline"]
+        lay["conv_ms"] = conv_ms
+        lay["tflops"] = rf["flops"] / (conv_ms * 1e-3) / 1e12
+        lay["roofline"] = roofline(rf["flops"], rf["algorithmic_bytes"], conv_ms, w.dtype,
+                                   rf["kernel"], w.name)
 
     # ---- the timed step: the whole network with cached pairs.  For a
     # one-layer workload the step is one kernel launch, so the events around
