@@ -135,10 +135,11 @@ def conv_alg_bytes(n_in, n_out, c_in, c_out, k_vol, elem, planned):
             + (n_out * 4 if planned else 0) + k_vol * c_in * c_out * elem)
 
 
-def roofline(flops, alg_bytes, kern_ms, dtype, kernel, workload):
-    """The conv kernel against its bound: MFMA peak when its arithmetic
-    intensity (flops per algorithmic byte) reaches the ridge point of the
-    dtype's peak over 8 TB/s, else HBM bandwidth; both fractions are given."""
+def roofline(flops, alg_bytes, kern_ms, dtype, kernel, workload, layer, rows_out):
+    """The conv kernel of one layer against its bound: MFMA peak when its
+    arithmetic intensity (flops per algorithmic byte) reaches the ridge point
+    of the dtype's peak over 8 TB/s, else HBM bandwidth; both fractions are
+    given."""
     peak = PEAK_TFLOPS[dtype]
     ridge = peak * 1e12 / (HBM_PEAK_GBS * 1e9)
     tflops = flops / (kern_ms * 1e-3) / 1e12
@@ -152,29 +153,33 @@ def roofline(flops, alg_bytes, kern_ms, dtype, kernel, workload):
          "traffic": None,
          "algorithmic_bytes": int(alg_bytes), "flops": flops,
          "mfma_frac": tflops / peak, "hbm_frac": gbs / HBM_PEAK_GBS,
-         "kernel": kernel, "kernel_ms": kern_ms}
-    t = measured_traffic(kernel, workload, kern_ms)
+         "kernel": kernel, "kernel_ms": kern_ms, "layer": layer, "rows_out": rows_out}
+    t = measured_traffic(kernel, workload, kern_ms, f"{layer}, {rows_out} output rows")
     if t is not None:
         r["traffic"] = t["bytes"]
         r["traffic_source"] = t["source"]
     return r
 
 
-def measured_traffic(kernel: str, workload: str, kern_ms: float):
+def measured_traffic(kernel: str, workload: str, kern_ms: float, layer_tag: str):
     """HBM bytes per launch of a conv kernel from the committed rocprofv3
     FETCH_SIZE / WRITE_SIZE summary of this workload, or None.
 
     Counters cannot be read inside a timed run, so the figure comes from the
-    profile summary; it is used only while the kernel's duration in that
-    profile is within 15% (or 5 us, for kernels of a few microseconds whose
-    back-to-back timing here includes launch gaps) of the live measurement, so
-    a stale profile of an older kernel is not reported.
+    profile summary.  It is used only for the layer the summary names (layer
+    and output rows, in its first line) and only while the kernel's duration
+    in that profile is within 15% (or 5 us, for kernels of a few
+    microseconds whose timing here includes launch gaps) of the live
+    measurement, so a stale profile of an older kernel is not reported.
     """
     path = ROOT / "profiles" / f"{kernel.replace('_kernel', '')}_{workload}_traffic.txt"
     if not path.exists():
         return None
+    text = path.read_text().splitlines()
+    if not text or not text[0].endswith(f"layer {layer_tag}"):
+        return None
     vals = {}
-    for line in path.read_text().splitlines():
+    for line in text:
         if ":" in line and not line.startswith("#"):
             k, _, v = line.partition(":")
             vals[k.strip()] = v.strip()
@@ -347,7 +352,7 @@ def bench_gpu(w, args, dev, mods, feats, idx):
         lay["conv_ms"] = conv_ms
         lay["tflops"] = rf["flops"] / (conv_ms * 1e-3) / 1e12
         lay["roofline"] = roofline(rf["flops"], rf["algorithmic_bytes"], conv_ms, w.dtype,
-                                   rf["kernel"], w.name)
+                                   rf["kernel"], w.name, lay["layer"], lay["rows_out"])
 
     # ---- the timed step: the whole network with cached pairs.  For a
     # one-layer workload the step is one kernel launch, so the events around
@@ -374,7 +379,8 @@ def bench_gpu(w, args, dev, mods, feats, idx):
         lay["tflops"] = 2.0 * lay["pairs"] * convs[0].in_channels * convs[0].out_channels \
             / (gpu_step_ms * 1e-3) / 1e12
         lay["roofline"] = roofline(lay["roofline"]["flops"], lay["roofline"]["algorithmic_bytes"],
-                                   gpu_step_ms, w.dtype, lay["roofline"]["kernel"], w.name)
+                                   gpu_step_ms, w.dtype, lay["roofline"]["kernel"], w.name,
+                                   lay["layer"], lay["rows_out"])
     res = {"step_ms": step_ms, "gpu_step_ms": gpu_step_ms, "network_ms_cold": cold_ms,
            "layers": layers, "y": y}
     if len(layers) > 1:
