@@ -2,6 +2,9 @@
 #include "common.hpp"
 
 #include <cstdarg>
+#include <mutex>
+#include <utility>
+#include <vector>
 
 namespace tsc {
 
@@ -37,6 +40,24 @@ __global__ void fill_u64_kernel(unsigned long long* p, int64_t n, unsigned long 
 static int fill_grid(int64_t n) {
   int64_t g = ceil_div(n, 256);
   return static_cast<int>(g < 4096 ? (g < 1 ? 1 : g) : 4096);
+}
+
+// Dynamic LDS limits are a per-device attribute of a kernel: each (kernel,
+// device) pair is raised once, on the first launch on that device.
+int allow_dynamic_lds(const void* kernel, int bytes) {
+  static std::mutex mu;
+  static std::vector<std::pair<const void*, int>> done;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(-static_cast<int>(e), "hipGetDevice: %s", hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(mu);
+  for (const auto& d : done)
+    if (d.first == kernel && d.second == dev) return 0;
+  e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e != hipSuccess)
+    return set_error(-static_cast<int>(e), "dynamic LDS of %d bytes: %s", bytes, hipGetErrorString(e));
+  done.emplace_back(kernel, dev);
+  return 0;
 }
 
 int fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s) {

@@ -179,6 +179,9 @@ __device__ __forceinline__ uint32_t block_exclusive(uint32_t v, uint32_t* s_wave
 __global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v);
 __global__ void fill_u64_kernel(unsigned long long* p, int64_t n, unsigned long long v);
 int fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s);
+// Raises kernel's dynamic LDS limit to bytes on the current device (once per
+// kernel and device); 0 or an error code.
+int allow_dynamic_lds(const void* kernel, int bytes);
 int fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hipStream_t s);
 
 // Per-slot, per-block counts -> exclusive offsets along blocks, plus totals.

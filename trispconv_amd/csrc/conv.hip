@@ -1472,12 +1472,10 @@ int launch_dma(const void* feat, int c_in, const void* W, const Epilogue& ep,
   TSC_REQUIRE(nbr != nullptr && c_in % CK == 0, "conv: the DMA kernel needs a map and C_in %% %d == 0",
               CK);
   constexpr size_t pool = dma_pool_bytes<T, BN>();
-  // more than 64 KB of dynamic LDS for the larger tiles: raise the limit once
-  static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&conv_dma_kernel<T, BN>),
-      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(pool));
-  if (attr != hipSuccess)
-    return set_error(-static_cast<int>(attr), "conv_dma: %s", hipGetErrorString(attr));
+  // more than 64 KB of dynamic LDS for the larger tiles
+  if (int rc = allow_dynamic_lds(reinterpret_cast<const void*>(&conv_dma_kernel<T, BN>),
+                                 static_cast<int>(pool)))
+    return rc;
   conv_dma_kernel<T, BN><<<dim3(static_cast<unsigned>(items)), 256, pool, s>>>(
       static_cast<const T*>(feat), c_in, static_cast<const T*>(W), ep, nbr, order, nbr_ordered,
       n_out, K, c_out, static_cast<T*>(out));
