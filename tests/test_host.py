@@ -312,3 +312,44 @@ def test_pending_pair_counts_are_read_and_checked_on_first_access():
     assert d.pair_num.tolist() == [1, 1, 1]
     with pytest.raises(RuntimeError, match="not the rows"):
         data([1, 1, 1, L.FLAG_ROWS_NOT_BITMAP]).pair_num
+
+
+# Instructions that read M0 implicitly on gfx9-family targets, besides the
+# direct-to-LDS loads themselves.
+_M0_READERS = re.compile(r"\b(s_movrel|v_movrel|s_sendmsg|ds_gws|v_interp|ds_\w*addtid)\w*|"
+                         r"\bbuffer_load\w*\b.*\blds\b")
+
+
+@pytest.mark.skipif(not Path("/opt/rocm/bin/hipcc").exists(), reason="needs ROCm's hipcc")
+def test_dma_kernels_own_m0(tmp_path):
+    """conv_dma_kernel sets M0 in inline assembly right before each
+    direct-to-LDS load, without telling the compiler; that is sound only while
+    nothing else in those kernels uses M0.  The gfx950 assembly of every
+    instantiation, built with the library's own flags, must show each
+    global_load_lds right after its own M0 write and no other M0 user."""
+    import subprocess
+
+    from trispconv_amd import build as B
+    asm = tmp_path / "conv.s"
+    cmd = [B.hipcc(), *B.HIPCC_FLAGS, "--cuda-device-only", "-S", str(B.CSRC / "conv.hip"),
+           "-o", str(asm)]
+    res = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    assert res.returncode == 0, res.stderr[-2000:]
+    text = asm.read_text()
+    names = re.findall(r"^(_Z\S*conv_dma_kernel\S*):", text, re.M)
+    assert len(names) >= 6, "expected the f16, bf16 and f32 instantiations"
+    for name in names:
+        body = text[text.index(name + ":"):]
+        body = body[:body.index("s_endpgm")]
+        lines = [ln.split(";")[0].strip() for ln in body.splitlines()]
+        lines = [ln for ln in lines if ln and not ln.startswith((".", "#"))]
+        n_dma = 0
+        for i, ln in enumerate(lines):
+            assert not _M0_READERS.search(ln), (name, ln)
+            if ln.startswith("global_load_lds"):
+                n_dma += 1
+                assert lines[i - 1].startswith("s_mov_b32 m0,"), (name, lines[i - 1], ln)
+            elif re.search(r"\bm0\b", ln):
+                assert ln.startswith("s_mov_b32 m0,") and lines[i + 1].startswith("global_load_lds"), \
+                    (name, ln)
+        assert n_dma > 0, name
