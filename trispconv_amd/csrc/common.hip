@@ -42,6 +42,26 @@ static int fill_grid(int64_t n) {
   return static_cast<int>(g < 4096 ? (g < 1 ? 1 : g) : 4096);
 }
 
+// Two fills in one launch: the first g1 blocks fill (p1, n1), the rest (p2, n2).
+__global__ void fill2_u32_kernel(uint32_t* p1, int64_t n1, uint32_t v1, int g1, uint32_t* p2,
+                                 int64_t n2, uint32_t v2) {
+  const bool first = static_cast<int>(blockIdx.x) < g1;
+  uint32_t* p = first ? p1 : p2;
+  const int64_t n = first ? n1 : n2;
+  const uint32_t v = first ? v1 : v2;
+  const int64_t b = first ? blockIdx.x : blockIdx.x - g1;
+  const int64_t nb = first ? g1 : gridDim.x - g1;
+  for (int64_t i = b * blockDim.x + threadIdx.x; i < n; i += nb * blockDim.x) p[i] = v;
+}
+
+int fill2_u32(uint32_t* p1, int64_t n1, uint32_t v1, uint32_t* p2, int64_t n2, uint32_t v2,
+              hipStream_t s) {
+  const int g1 = fill_grid(n1), g2 = fill_grid(n2);
+  fill2_u32_kernel<<<g1 + g2, 256, 0, s>>>(p1, n1, v1, g1, p2, n2, v2);
+  TSC_LAUNCH_CHECK("fill2_u32");
+  return 0;
+}
+
 // Dynamic LDS limits are a per-device attribute of a kernel: each (kernel,
 // device) pair is raised once, on the first launch on that device.
 int allow_dynamic_lds(const void* kernel, int bytes) {
@@ -75,13 +95,14 @@ int fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hipStream_t
 }
 
 // ---------------------------------------------------- per-slot block scan --
-__global__ void __launch_bounds__(1024) scan_slot_blocks_kernel(const int32_t* __restrict__ cnt,
-                                                                int32_t* __restrict__ off,
-                                                                int32_t* __restrict__ totals,
-                                                                int nblk, int K,
-                                                                int32_t* __restrict__ extra_total) {
-  __shared__ uint32_t s_wave[33];
-  const int k = blockIdx.x;
+// Slot k's exclusive scan along blocks, by one thread block of any size that
+// is a multiple of 64.
+__device__ void slot_scan_block(const SlotScan& a, int k, uint32_t* s_wave) {
+  const int nblk = a.nblk, K = a.K;
+  const int32_t* cnt = a.cnt;
+  int32_t* off = a.off;
+  int32_t* totals = a.totals;
+  int32_t* extra_total = a.extra_total;
   const int32_t* c = cnt + (int64_t)k * nblk;
   int32_t* o = off + (int64_t)k * nblk;
   uint32_t carry = 0;
@@ -101,10 +122,15 @@ __global__ void __launch_bounds__(1024) scan_slot_blocks_kernel(const int32_t* _
   }
 }
 
+__global__ void __launch_bounds__(1024) scan_slot_blocks_kernel(SlotScan a) {
+  __shared__ uint32_t s_wave[33];
+  slot_scan_block(a, blockIdx.x, s_wave);
+}
+
 int scan_slot_blocks(const int32_t* cnt, int32_t* off, int32_t* totals, int K, int nblk,
                      hipStream_t s, int32_t* extra_total) {
-  scan_slot_blocks_kernel<<<K + (extra_total ? 1 : 0), 1024, 0, s>>>(cnt, off, totals, nblk, K,
-                                                                     extra_total);
+  const SlotScan a{cnt, off, totals, K, nblk, extra_total};
+  scan_slot_blocks_kernel<<<a.blocks(), 1024, 0, s>>>(a);
   TSC_LAUNCH_CHECK("scan_slot_blocks");
   return 0;
 }
@@ -265,8 +291,13 @@ constexpr int kBmTile = kBmThreads * 4;
 
 __global__ void __launch_bounds__(kBmThreads) bitmap_reduce_kernel(const uint4* __restrict__ wr2,
                                                                    int64_t nw,
-                                                                   uint32_t* __restrict__ sums) {
+                                                                   uint32_t* __restrict__ sums,
+                                                                   int nsum, SlotScan scan) {
   __shared__ uint32_t s_wave[33];
+  if (static_cast<int>(blockIdx.x) >= nsum) {  // blocks past the tiles: a slot scan riding along
+    slot_scan_block(scan, blockIdx.x - nsum, s_wave);
+    return;
+  }
   const int64_t p = (blockIdx.x * (int64_t)kBmTile) / 2 + 2 * threadIdx.x;  // entry pairs
   uint32_t acc = 0;
 #pragma unroll
@@ -294,8 +325,13 @@ __device__ __forceinline__ uint32_t pack_bytes(uint4 a, uint4 b) {
 
 __global__ void __launch_bounds__(kBmThreads) bitmap_pack_kernel(const uint4* __restrict__ bytes,
                                                                  uint4* __restrict__ wr2, int64_t nw,
-                                                                 uint32_t* __restrict__ sums) {
+                                                                 uint32_t* __restrict__ sums,
+                                                                 int nsum, SlotScan scan) {
   __shared__ uint32_t s_wave[33];
+  if (static_cast<int>(blockIdx.x) >= nsum) {  // blocks past the tiles: a slot scan riding along
+    slot_scan_block(scan, blockIdx.x - nsum, s_wave);
+    return;
+  }
   const int64_t p = (blockIdx.x * (int64_t)kBmTile) / 2 + 2 * threadIdx.x;  // entry pairs
   uint32_t acc = 0;
 #pragma unroll
@@ -367,18 +403,21 @@ int64_t bitmap_scan_scratch_words(int64_t nw) {
 }
 
 int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStream_t s,
-                const uint8_t* bytes) {
+                const uint8_t* bytes, const SlotScan* scan) {
   const int64_t nsum = ceil_div(nw > 0 ? nw : 1, kBmTile);
   uint32_t* sums = scratch;
   uint32_t* pre = scratch + nsum;
   uint32_t* more = scratch + 2 * nsum;
   uint4* wr2 = reinterpret_cast<uint4*>(wr);
+  const SlotScan none{nullptr, nullptr, nullptr, 0, 0, nullptr};
+  const SlotScan& sc = scan ? *scan : none;
+  const unsigned grid = static_cast<unsigned>(nsum + sc.blocks());
   if (bytes) {
-    bitmap_pack_kernel<<<static_cast<unsigned>(nsum), kBmThreads, 0, s>>>(
-        reinterpret_cast<const uint4*>(bytes), wr2, nw, sums);
+    bitmap_pack_kernel<<<grid, kBmThreads, 0, s>>>(reinterpret_cast<const uint4*>(bytes), wr2, nw,
+                                                   sums, static_cast<int>(nsum), sc);
     TSC_LAUNCH_CHECK("bitmap_pack");
   } else {
-    bitmap_reduce_kernel<<<static_cast<unsigned>(nsum), kBmThreads, 0, s>>>(wr2, nw, sums);
+    bitmap_reduce_kernel<<<grid, kBmThreads, 0, s>>>(wr2, nw, sums, static_cast<int>(nsum), sc);
     TSC_LAUNCH_CHECK("bitmap_reduce");
   }
   const uint32_t* p = nullptr;

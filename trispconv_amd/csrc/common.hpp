@@ -179,10 +179,25 @@ __device__ __forceinline__ uint32_t block_exclusive(uint32_t v, uint32_t* s_wave
 __global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t v);
 __global__ void fill_u64_kernel(unsigned long long* p, int64_t n, unsigned long long v);
 int fill_u32(uint32_t* p, int64_t n, uint32_t v, hipStream_t s);
+// Two fills in one launch.
+int fill2_u32(uint32_t* p1, int64_t n1, uint32_t v1, uint32_t* p2, int64_t n2, uint32_t v2,
+              hipStream_t s);
 // Raises kernel's dynamic LDS limit to bytes on the current device (once per
 // kernel and device); 0 or an error code.
 int allow_dynamic_lds(const void* kernel, int bytes);
 int fill_u64(unsigned long long* p, int64_t n, unsigned long long v, hipStream_t s);
+
+// Per-slot, per-block counts -> exclusive offsets along blocks, plus totals:
+// cnt and off are [K][nblk]; totals[k] receives the sum of slot k.  With
+// extra_total, cnt and off hold one more row whose sum goes to *extra_total.
+struct SlotScan {
+  const int32_t* cnt;
+  int32_t* off;
+  int32_t* totals;
+  int K, nblk;
+  int32_t* extra_total;
+  __host__ __device__ int blocks() const { return cnt ? K + (extra_total ? 1 : 0) : 0; }
+};
 
 // Per-slot, per-block counts -> exclusive offsets along blocks, plus totals.
 // cnt and off are [K][nblk]; totals[k] receives the sum of slot k.  With
@@ -207,8 +222,10 @@ int64_t scan_scratch_words(int64_t n);
 // bitmap_scan fills every y from the x fields and writes the total to *total.
 int64_t bitmap_entries(int64_t nw);
 int64_t bitmap_scan_scratch_words(int64_t nw);
+// With scan, that slot scan (scan_slot_blocks) runs in the same launch as
+// the first pass.
 int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStream_t s,
-                const uint8_t* bytes = nullptr);
+                const uint8_t* bytes = nullptr, const SlotScan* scan = nullptr);
 // The submanifold build (tsc_subm_pairs) on a given workspace.  ws_limit > 0:
 // ws is that many bytes of fixed scratch, the bitmap is used only when it
 // fits and a build that fits in neither way is an argument error; 0: ws is

@@ -17,6 +17,8 @@
 // wave-ballot scheme as the submanifold builder.
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace tsc {
 namespace {
 
@@ -181,10 +183,20 @@ __global__ void __launch_bounds__(kRows) strided_mark_kernel(const int4* __restr
 
 // One thread per bitmap entry: decode every set bit, in ascending order, into
 // its (b, z, y, x) row at the entry's rank.
+// Blocks from emit_blocks on instead fill the map with -1 (one launch for both).
 __global__ void __launch_bounds__(256) strided_emit_kernel(const uint2* __restrict__ wr,
                                                            int64_t nwords, StridedGeom g,
                                                            int4* __restrict__ out_coords,
-                                                           int64_t n_out) {
+                                                           int64_t n_out, int emit_blocks,
+                                                           uint32_t* __restrict__ map,
+                                                           int64_t map_words) {
+  if (static_cast<int>(blockIdx.x) >= emit_blocks) {
+    const int64_t nb = gridDim.x - emit_blocks;
+    for (int64_t i = (blockIdx.x - emit_blocks) * (int64_t)blockDim.x + threadIdx.x; i < map_words;
+         i += nb * blockDim.x)
+      map[i] = 0xffffffffu;
+    return;
+  }
   const int64_t wi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (wi >= nwords) return;
   const uint2 e = wr[wi];
@@ -451,16 +463,13 @@ extern "C" int tsc_strided_count(const int32_t* coords, int64_t n, int32_t batch
               (long long)ws_bytes, (long long)need);
   TSC_REQUIRE(counts != nullptr, "strided: counts is null");
   Buffers b = carve(ws, L, K, nullptr);
-  if ((rc = fill_u32(reinterpret_cast<uint32_t*>(counts), K + 3, 0u, s))) return rc;
-  // zero the marks: the byte map (the scan then writes every bitmap entry) or
-  // the bitmap entries
-  if (b.bytes) {
-    if ((rc = fill_u32(reinterpret_cast<uint32_t*>(b.bytes), 8 * bitmap_entries(L.nwords), 0u, s)))
-      return rc;
-  } else if ((rc = fill_u32(reinterpret_cast<uint32_t*>(b.wr), 2 * bitmap_entries(L.nwords), 0u,
-                            s))) {
+  // zero the counters and the marks (the byte map, which the scan turns into
+  // every bitmap entry, or the bitmap entries), in one launch
+  uint32_t* marks = reinterpret_cast<uint32_t*>(b.bytes ? static_cast<void*>(b.bytes)
+                                                        : static_cast<void*>(b.wr));
+  const int64_t mark_words = (b.bytes ? 8 : 2) * bitmap_entries(L.nwords);
+  if ((rc = fill2_u32(reinterpret_cast<uint32_t*>(counts), K + 3, 0u, marks, mark_words, 0u, s)))
     return rc;
-  }
   if (n == 0) return 0;
   TSC_REQUIRE(coords != nullptr, "strided: coords is null");
   if (K > 64 && (rc = fill_u32(reinterpret_cast<uint32_t*>(b.blk_cnt), L.nblk * K, 0u, s)))
@@ -469,9 +478,9 @@ extern "C" int tsc_strided_count(const int32_t* coords, int64_t n, int32_t batch
                                  b.bytes, b.blk_cnt, (int)L.nblk, counts + K + 1,
                                  b.blk_cnt + (int64_t)K * L.nblk, s)))
     return rc;
-  if ((rc = scan_slot_blocks(b.blk_cnt, b.blk_off, counts, K, (int)L.nblk, s, counts + K + 2)))
-    return rc;
-  return bitmap_scan(b.wr, L.nwords, b.scan, counts + K, s, b.bytes);
+  // the per-slot scan of the block counts rides in the bitmap scan's first launch
+  const SlotScan slots{b.blk_cnt, b.blk_off, counts, K, (int)L.nblk, counts + K + 2};
+  return bitmap_scan(b.wr, L.nwords, b.scan, counts + K, s, b.bytes, &slots);
 }
 
 extern "C" int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_size,
@@ -493,11 +502,14 @@ extern "C" int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_
   if (n == 0 || n_out == 0) return 0;
   TSC_REQUIRE(coords && out_coords && nbr && pairs_in && pairs_out, "strided: null pointer");
   Buffers b = carve(ws, L, K, nullptr);
-  strided_emit_kernel<<<ceil_div(L.nwords, 256), 256, 0, s>>>(b.wr, L.nwords, g,
-                                                             reinterpret_cast<int4*>(out_coords),
-                                                             n_out);
+  // the output coordinates, and the map's -1 fill, in one launch
+  const int emit_blocks = static_cast<int>(ceil_div(L.nwords, 256));
+  const int64_t map_words = n_out * K;
+  const int fill_blocks = static_cast<int>(std::min<int64_t>(std::max<int64_t>(ceil_div(map_words, 256), 1), 4096));
+  strided_emit_kernel<<<emit_blocks + fill_blocks, 256, 0, s>>>(
+      b.wr, L.nwords, g, reinterpret_cast<int4*>(out_coords), n_out, emit_blocks,
+      reinterpret_cast<uint32_t*>(nbr), map_words);
   TSC_LAUNCH_CHECK("strided_emit");
-  if ((rc = fill_u32(reinterpret_cast<uint32_t*>(nbr), n_out * K, 0xffffffffu, s))) return rc;
   return by_shape<LaunchFill>(g.ks, reinterpret_cast<const int4*>(coords), n, K, g,
                               static_cast<const uint2*>(b.wr), static_cast<const int32_t*>(b.blk_off),
                               (int)L.nblk, n, n_out, nbr, pairs_in, pairs_out, s);
