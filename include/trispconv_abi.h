@@ -92,7 +92,8 @@ TSC_API int tsc_subm_pairs_noalloc(const int32_t* coords, int64_t n, int32_t bat
 
 /* The same build for rows that are the occupied cells of an existing
  * occupancy bitmap in rank order: one (word, rank) 8-byte entry per 32 cells
- * of the batch x spatial grid, row t the cell of rank t, no repeats.  That is
+ * of the batch x spatial grid (the rank is read only for words with a set
+ * bit), row t the cell of rank t, no repeats.  That is
  * exactly a strided build's output: its coordinates, and its workspace,
  * which begins with those entries (tsc_strided_count/fill).  So a
  * submanifold layer after a strided layer (indices.py:67-140 on the output of

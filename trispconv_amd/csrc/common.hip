@@ -381,13 +381,16 @@ __global__ void __launch_bounds__(kBmThreads) bitmap_apply_kernel(uint4* __restr
   }
   uint32_t tot;
   uint32_t run = base + block_exclusive(c[0] + c[1] + c[2] + c[3], s_wave, &tot);
+  // a rank is only looked up for a set bit, so pairs of empty words keep
+  // theirs unwritten (on sparse grids nearly every pair: the pass then mostly
+  // reads)
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     v[j].y = run;
     run += c[2 * j];
     v[j].w = run;
     run += c[2 * j + 1];
-    if (2 * (p + j) < nw) wr2[p + j] = v[j];
+    if (2 * (p + j) < nw && (v[j].x | v[j].z)) wr2[p + j] = v[j];
   }
 }
 

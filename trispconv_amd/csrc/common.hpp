@@ -219,7 +219,9 @@ int64_t scan_scratch_words(int64_t n);
 // bits, y = the number of set bits in all earlier entries (the rank of the
 // entry's first cell), so a rank lookup is one load.  The entry count is
 // rounded up to even (entries are processed in pairs; the pad entry is zero).
-// bitmap_scan fills every y from the x fields and writes the total to *total.
+// bitmap_scan fills y from the x fields wherever a pair of entries has a set
+// bit (a rank is only looked up for a set bit; other y are left as they were)
+// and writes the total to *total.
 int64_t bitmap_entries(int64_t nw);
 int64_t bitmap_scan_scratch_words(int64_t nw);
 // With scan, that slot scan (scan_slot_blocks) runs in the same launch as
