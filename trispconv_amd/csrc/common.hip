@@ -222,33 +222,42 @@ __global__ void __launch_bounds__(kScanThreads) scan_apply_kernel(const uint32_t
   }
 }
 
-// Inputs of up to kSmallScan items (one chunk of 1024 x 16 consecutive
-// items) are scanned by one workgroup in a single launch; one workgroup is
-// slower than the three-kernel scan beyond that.
-constexpr int kSmallItems = 16;
+// Inputs of up to kSmallScan items (one chunk of 1024 x 12 consecutive
+// items, 48 KB of LDS) are scanned by one workgroup in a single launch; one
+// workgroup is slower than the three-kernel scan beyond that.
+constexpr int kSmallItems = 12;
 constexpr int64_t kSmallScan = 1024 * kSmallItems;
 
 __global__ void __launch_bounds__(1024) scan_small_kernel(const uint32_t* __restrict__ src, int kind,
                                                           int64_t n, uint32_t* __restrict__ out,
                                                           int32_t* __restrict__ total) {
+  // A chunk goes through LDS both ways, so global reads and writes are
+  // coalesced while each thread scans 16 consecutive values.
+  __shared__ uint32_t s_val[1024 * kSmallItems];
   __shared__ uint32_t s_wave[33];
   uint32_t carry = 0;
   for (int64_t base = 0; base < n; base += 1024 * kSmallItems) {
-    const int64_t b0 = base + threadIdx.x * (int64_t)kSmallItems;
+    const int m = static_cast<int>(n - base < 1024 * kSmallItems ? n - base : 1024 * kSmallItems);
+    for (int i = threadIdx.x; i < m; i += 1024) s_val[i] = scan_value(src, kind, base + i);
+    __syncthreads();
+    const int b0 = threadIdx.x * kSmallItems;
     uint32_t v[kSmallItems];
     uint32_t acc = 0;
 #pragma unroll
     for (int j = 0; j < kSmallItems; ++j) {
-      v[j] = b0 + j < n ? scan_value(src, kind, b0 + j) : 0u;
+      v[j] = b0 + j < m ? s_val[b0 + j] : 0u;
       acc += v[j];
     }
     uint32_t tot;
     uint32_t run = carry + block_exclusive(acc, s_wave, &tot);
 #pragma unroll
     for (int j = 0; j < kSmallItems; ++j) {
-      if (b0 + j < n) out[b0 + j] = run;
+      if (b0 + j < m) s_val[b0 + j] = run;
       run += v[j];
     }
+    __syncthreads();
+    for (int i = threadIdx.x; i < m; i += 1024) out[base + i] = s_val[i];
+    __syncthreads();
     carry += tot;
   }
   if (threadIdx.x == 0 && total) *total = static_cast<int32_t>(carry);
