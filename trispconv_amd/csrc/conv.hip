@@ -655,7 +655,10 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
 // ------------------------------------------------------ LDS DMA variant --
 // The same tile schedule as conv_mfma_kernel, for layers whose stages are
 // 128 bytes of every row (64 channels of f16/bf16 with C_in a multiple of 64,
-// 32 of f32 with C_in a multiple of 32) and with a neighbour map (K > 1).  Its operands reach LDS through direct-to-LDS loads
+// 32 of f32 with C_in a multiple of 32) and with a neighbour map (K > 1).
+// A wave computes RB blocks of 32 rows: 64 rows (256-row tiles) on large
+// layers, 32 (128-row tiles) on layers whose time is one heavy tile's chain
+// of stages rather than the sum of all tiles' work.  Its operands reach LDS through direct-to-LDS loads
 // (global_load_lds_dwordx4: each lane names a global address, the 16 bytes
 // land at M0 + 16 * lane), which changes how the gathered rows pass the
 // vector L1:
@@ -683,13 +686,13 @@ __device__ __forceinline__ void dma_b32(const void* g, uint32_t m0) {
 }
 
 // Dynamic LDS of conv_dma_kernel: two weight slabs, each wave's operand rows
-// of one stage (64 rows x 128 bytes) and two stages of its map entries.
-template <typename T, int BN>
+// of one stage (32 * RB rows x 128 bytes) and two stages of its map entries.
+template <typename T, int BN, int RB>
 constexpr size_t dma_pool_bytes() {
-  return (size_t)2 * BN * 128 + (size_t)4 * 64 * 128 + (size_t)4 * 2 * 256;
+  return (size_t)2 * BN * 128 + (size_t)4 * 32 * RB * 128 + (size_t)4 * 2 * 256;
 }
 
-template <typename T, int BN>
+template <typename T, int BN, int RB>
 __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
     const T* __restrict__ feat, int c_in, const T* __restrict__ W, Epilogue ep,
     const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int nbr_ordered,
@@ -704,13 +707,16 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
   constexpr int WD = SLAB_VECS / 256;        // slab DMA instructions per wave
   static_assert(SLAB_VECS % 256 == 0, "a slab splits into 1 KB pieces per wave");
   constexpr int SLAB_BYTES = SLAB_VECS * 16;
-  constexpr int A_BYTES = 64 * CK * (int)sizeof(T);  // one wave's rows of one stage (8 KB)
-  static_assert(A_BYTES == 8192 && (size_t)2 * SLAB_BYTES + 4 * A_BYTES + 2048 == dma_pool_bytes<T, BN>(),
+  constexpr int WR = 32 * RB;                // rows of a wave: RB blocks of 32
+  constexpr int TR = 4 * WR;                 // rows of a tile
+  constexpr int A_BYTES = WR * CK * (int)sizeof(T);  // one wave's rows of one stage (4 or 8 KB)
+  static_assert(RB == 1 || RB == 2, "one or two 32-row blocks per wave");
+  static_assert(A_BYTES == 4096 * RB && (size_t)2 * SLAB_BYTES + 4 * A_BYTES + 2048 == dma_pool_bytes<T, BN, RB>(),
                 "pool layout");
   // pool: slabs [2][SLAB_BYTES] | operand rows [4 waves][A_BYTES] |
   // map entries [4 waves][2][64]; the output staging at the end
   extern __shared__ __attribute__((aligned(16))) char pool[];
-  __shared__ __attribute__((aligned(16))) int32_t s_orow[kTileRows];
+  __shared__ __attribute__((aligned(16))) int32_t s_orow[TR];
   __shared__ float s_bias[BN];
   __shared__ float s_scale[BN];
   __shared__ float s_shift[BN];
@@ -723,15 +729,16 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
   const uint32_t wave_u = __builtin_amdgcn_readfirstlane(wave);
   const uint32_t ncol = static_cast<uint32_t>(c_out / BN);
   const uint32_t item = dealt_item(blockIdx.x, gridDim.x, ncol);
-  const int64_t tile0 = static_cast<int64_t>(item / ncol) * kTileRows;
+  const int64_t tile0 = static_cast<int64_t>(item / ncol) * TR;
   const int nbt = static_cast<int>(item % ncol);
   const int nch = c_in / CK;
 
   // ---- tile set-up: output rows and slot masks (the entries themselves are
-  // loaded again stage by stage), as in conv_mfma_kernel
+  // loaded again stage by stage), as in conv_mfma_kernel; thread t < TR
+  // takes tile row t, which wave t / WR computes
   {
     const int64_t tr = tile0 + t;
-    const bool in = tr < n_out;
+    const bool in = t < TR && tr < n_out;
     uint64_t m = 0;
     int32_t jv[32];
     auto issue = [&](int k0, int64_t src_row) {
@@ -757,7 +764,7 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
       orow = in ? (order ? order[tr] : static_cast<int32_t>(tr)) : -1;
       issue(0, orow >= 0 ? orow : 0);
     }
-    s_orow[t] = orow;
+    if (t < TR) s_orow[t] = orow;
     if (t < BN) {
       const int64_t col = (int64_t)nbt * BN + t;
       s_bias[t] = ep.bias ? load_param(ep.bias, ep.bias_dt, col) : 0.f;
@@ -770,11 +777,11 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
     }
     uint32_t lo = static_cast<uint32_t>(m), hi = static_cast<uint32_t>(m >> 32);
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
+    for (int off = WR / 2; off > 0; off >>= 1) {
       lo |= __shfl_xor(lo, off, kWave);
       hi |= __shfl_xor(hi, off, kWave);
     }
-    if (lane == 0) s_mask[wave] = (static_cast<uint64_t>(hi) << 32) | lo;
+    if (t < TR && t % WR == 0) s_mask[t / WR] = (static_cast<uint64_t>(hi) << 32) | lo;
   }
   __syncthreads();
   const uint64_t umask_v = s_mask[0] | s_mask[1] | s_mask[2] | s_mask[3];
@@ -814,15 +821,16 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
   const char* s_a = pool + 2 * SLAB_BYTES + wave * A_BYTES;
   const int32_t* s_e = reinterpret_cast<const int32_t*>(pool + 2 * SLAB_BYTES + 4 * A_BYTES + wave * 512);
 
-  // Map entries: lane l loads the entry of its wave's row l.  Operand rows:
+  // Map entries: lane l < WR loads the entry of its wave's row l (lanes
+  // past WR load -1 from the no-row array).  Operand rows:
   // DMA instruction 2g + hh covers rows 16g..16g+15 of the wave and channel
   // half hh; the quad of lanes 4q..4q+3 reads row 16g + q, lane 4q + j its
   // 16-byte piece j ^ (q >> 2), which lands in LDS at (4q + j) * 16 of the
   // instruction's 1 KB.  So piece p of row 16g + q sits at (4q + (p ^ (q >>
   // 2))) * 16, and the MFMA's reads (lanes 0..15: rows q = 0..15, one piece)
   // hit sixteen different 16-byte bank groups.
-  const int32_t orow_l = s_orow[wave * 64 + lane];
-  const int64_t col_l = nbr_ordered ? tile0 + wave * 64 + lane : (int64_t)orow_l;
+  const int32_t orow_l = lane < WR ? s_orow[wave * WR + lane] : -1;
+  const int64_t col_l = nbr_ordered ? tile0 + wave * WR + lane : (int64_t)orow_l;
   const int q = lane >> 2;
   const int piece = (lane & 3) ^ (q >> 2);
 
@@ -836,11 +844,11 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
     dma_b32(orow_l >= 0 ? nbr + (int64_t)k * n_out + col_l : no_row, e_lds + P * 256);
   };
   auto dma_rows = [&](int P, int c) {  // chunk c of the rows named by entry buffer P
-    int32_t j[4];
+    int32_t j[2 * RB];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) j[g] = s_e[P * 64 + 16 * g + q];
+    for (int g = 0; g < 2 * RB; ++g) j[g] = s_e[P * 64 + 16 * g + q];
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
+    for (int g = 0; g < 2 * RB; ++g)
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const char* src =
@@ -850,7 +858,12 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
       }
   };
   auto wait_vm0 = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
-  auto wait_vm8 = [] { asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); };  // all but 8 youngest
+  auto wait_rows = [] {  // all but the 4 * RB youngest: the row DMAs of the next stage
+    if constexpr (RB == 2)
+      asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+  };
   auto wait_lgkm0 = [] { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); };
   const int qr = lane & 15;
   auto a_read = [&](int rb, int u) {  // operand u of row block rb (rows rb*32 + lane%32)
@@ -858,9 +871,9 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
     return *reinterpret_cast<const uint4*>(s_a + (2 * g + h) * 1024 + (4 * qr + (u ^ (qr >> 2))) * 16);
   };
 
-  f32x16 acc[2][NB];
+  f32x16 acc[RB][NB];
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
+  for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
@@ -888,19 +901,19 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
   //  2. the slab of s + 1 and the entries of s + 2 go out; the rows of s and
   //     the entries of s + 1 are read; lgkmcnt(0): the reads are done, so the
   //     rows of s + 1 may overwrite the wave's one operand buffer;
-  //  3. MFMAs of s; vmcnt(8) (or 0 when no rows went out): the slab and the
-  //     entries have landed, the 8 row loads of s + 1 may still be in flight;
-  //     the barrier then publishes the slab to every wave.
+  //  3. MFMAs of s; vmcnt(4 * RB) (or 0 when no rows went out): the slab and
+  //     the entries have landed, the 4 * RB row loads of s + 1 may still be in
+  //     flight; the barrier then publishes the slab to every wave.
   auto body = [&](auto slot) {
     constexpr int S = decltype(slot)::value;
     wait_vm0();
     if (kn < K) dma_slab(S ^ 1, kn, cn);
     if (kp < K) dma_entries(S, kp);
     const bool cur = uses(kc);
-    uint4 a[2][UB];
+    uint4 a[RB][UB];
     if (cur) {
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
+      for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int u = 0; u < UB; ++u) a[rb][u] = a_read(rb, u);
     }
@@ -915,28 +928,28 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
         for (int nb = 0; nb < NB; ++nb) {
           const uint4 bv = sw[(nb * UB + u) * 64 + lane];
           if constexpr (F32) {
-            // four 32x32x2 steps per vector: step i uses element i of A and B
-            const float4 a0 = __builtin_bit_cast(float4, a[0][u]);
-            const float4 a1 = __builtin_bit_cast(float4, a[1][u]);
+            // four 32x32x2 steps per vector: step e uses element e of A and B
             const float4 b4 = __builtin_bit_cast(float4, bv);
-            acc[0][nb] = Op::run(a0.x, b4.x, acc[0][nb]);
-            acc[1][nb] = Op::run(a1.x, b4.x, acc[1][nb]);
-            acc[0][nb] = Op::run(a0.y, b4.y, acc[0][nb]);
-            acc[1][nb] = Op::run(a1.y, b4.y, acc[1][nb]);
-            acc[0][nb] = Op::run(a0.z, b4.z, acc[0][nb]);
-            acc[1][nb] = Op::run(a1.z, b4.z, acc[1][nb]);
-            acc[0][nb] = Op::run(a0.w, b4.w, acc[0][nb]);
-            acc[1][nb] = Op::run(a1.w, b4.w, acc[1][nb]);
+            const float bs[4] = {b4.x, b4.y, b4.z, b4.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+              for (int rb = 0; rb < RB; ++rb) {
+                const float4 a4 = __builtin_bit_cast(float4, a[rb][u]);
+                const float as[4] = {a4.x, a4.y, a4.z, a4.w};
+                acc[rb][nb] = Op::run(as[e], bs[e], acc[rb][nb]);
+              }
           } else {
             const V b = __builtin_bit_cast(V, bv);
-            acc[0][nb] = Op::run(__builtin_bit_cast(V, a[0][u]), b, acc[0][nb]);
-            acc[1][nb] = Op::run(__builtin_bit_cast(V, a[1][u]), b, acc[1][nb]);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+              acc[rb][nb] = Op::run(__builtin_bit_cast(V, a[rb][u]), b, acc[rb][nb]);
           }
         }
       }
     }
     if (nxt)
-      wait_vm8();
+      wait_rows();
     else
       wait_vm0();
     __syncthreads();
@@ -960,13 +973,14 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
   constexpr int STRIDE = ROW_BYTES + 16;
   constexpr int CHUNKS = ROW_BYTES / 16;
   constexpr int PR = mfma_stage_rows(ROW_BYTES);
-  static_assert((size_t)4 * PR * STRIDE <= dma_pool_bytes<T, BN>(), "staging exceeds the pool");
+  static_assert((size_t)4 * PR * STRIDE <= dma_pool_bytes<T, BN, RB>(), "staging exceeds the pool");
+  static_assert(WR % PR == 0, "whole passes");
   char* stage = pool + wave * PR * STRIDE;
 #pragma unroll
-  for (int pass = 0; pass < 64 / PR; ++pass) {
+  for (int pass = 0; pass < WR / PR; ++pass) {
     __syncthreads();
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+    for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int rblk = rb * 32 + (i >> 2) * 8;
@@ -988,7 +1002,7 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
     for (int qq = 0; qq < NQ; ++qq) {
       const int pc = qq * 64 + lane;
       const int row = pc / CHUNKS, ch = pc % CHUNKS;
-      orows[qq] = s_orow[wave * 64 + pass * PR + row];
+      orows[qq] = s_orow[wave * WR + pass * PR + row];
       vals[qq] = *reinterpret_cast<const uint4*>(stage + row * STRIDE + ch * 16);
     }
 #pragma unroll
@@ -1461,22 +1475,22 @@ int launch_mfma(const void* feat, int c_in, const void* W, const Epilogue& ep,
   return 0;
 }
 
-template <typename T, int BN>
+template <typename T, int BN, int RB>
 int launch_dma(const void* feat, int c_in, const void* W, const Epilogue& ep,
                const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
                int c_out, void* out, hipStream_t s) {
-  const int64_t items = ceil_div(n_out, kTileRows) * (c_out / BN);
+  const int64_t items = ceil_div(n_out, 128 * RB) * (c_out / BN);
   TSC_REQUIRE(items < (int64_t(1) << 31), "conv: %lld workgroups exceed the grid limit",
               static_cast<long long>(items));
   constexpr int CK = 128 / (int)sizeof(T);
   TSC_REQUIRE(nbr != nullptr && c_in % CK == 0, "conv: the DMA kernel needs a map and C_in %% %d == 0",
               CK);
-  constexpr size_t pool = dma_pool_bytes<T, BN>();
+  constexpr size_t pool = dma_pool_bytes<T, BN, RB>();
   // more than 64 KB of dynamic LDS for the larger tiles
-  if (int rc = allow_dynamic_lds(reinterpret_cast<const void*>(&conv_dma_kernel<T, BN>),
+  if (int rc = allow_dynamic_lds(reinterpret_cast<const void*>(&conv_dma_kernel<T, BN, RB>),
                                  static_cast<int>(pool)))
     return rc;
-  conv_dma_kernel<T, BN><<<dim3(static_cast<unsigned>(items)), 256, pool, s>>>(
+  conv_dma_kernel<T, BN, RB><<<dim3(static_cast<unsigned>(items)), 256, pool, s>>>(
       static_cast<const T*>(feat), c_in, static_cast<const T*>(W), ep, nbr, order, nbr_ordered,
       n_out, K, c_out, static_cast<T*>(out));
   TSC_LAUNCH_CHECK("conv_dma");
@@ -1506,7 +1520,19 @@ struct MfmaChoice {
   int ck;      // input-channel chunk of one stage
   bool split;  // the 64-row slot-split kernel instead of the 256-row one
   bool dma;    // the 256-row kernel's direct-to-LDS variant
+  int rb;      // its 32-row blocks per wave (tiles of 128 * rb rows)
 };
+
+// Layers with fewer 256-row tiles than this run the direct-to-LDS kernel on
+// 128-row tiles (32 rows per wave).  On such layers the kernel lasts as long
+// as its heaviest tiles' chain of stages (27 slots x the channel chunks, each
+// stage's MFMAs shared by the waves on a SIMD); halving a wave's rows halves
+// the MFMAs of each stage and, with the smaller LDS pool, lets up to four
+// workgroups share a CU.  Measured: the 166k-row 64->64 fp32 strided layer
+// (651 tiles) 182 -> 140-152 us, the 32k-row 64->64 fp16 layers 31.4 -> 30.1
+// us; the 500k-row 128->128 fp16 layer (1954 tiles) is slower that way, 327
+// -> 339 us, where two 64-row waves share each weight slab read from LDS.
+constexpr int64_t kShortTiles = 1024;
 
 // Narrower column tiles for small layers: below two workgroups per CU, halve
 // BN (each halving doubles the workgroups; gathers repeat per column tile,
@@ -1523,7 +1549,7 @@ struct MfmaChoice {
 // stages are 128 bytes of each row (f16/bf16 with C_in % 64 == 0, f32 with
 // C_in % 32 == 0) and that have a map (K > 1); it sums in the same order too.
 MfmaChoice choose_mfma(int dtype, int c_in, int c_out, int K, int64_t n_out, int column_tile) {
-  MfmaChoice c{pick_bn(c_out), pick_ck(dtype, c_in), false, false};
+  MfmaChoice c{pick_bn(c_out), pick_ck(dtype, c_in), false, false, 2};
   if (column_tile) {
     c.bn = column_tile;
     return c;
@@ -1531,6 +1557,7 @@ MfmaChoice choose_mfma(int dtype, int c_in, int c_out, int K, int64_t n_out, int
   while (c.bn > 32 && ceil_div(n_out, kTileRows) * (c_out / c.bn) < 512) c.bn /= 2;
   c.split = c.bn == 32 && K >= 8 && ceil_div(n_out, kTileRows) * (c_out / c.bn) < 128;
   c.dma = !c.split && K > 1 && c.ck * dtype_bytes(dtype) == 128 && c_in % c.ck == 0;
+  if (c.dma && ceil_div(n_out, kTileRows) * (c_out / c.bn) < kShortTiles) c.rb = 1;
   return c;
 }
 
@@ -1549,8 +1576,10 @@ int dispatch_mfma(const void* feat, int c_in, const void* W, const Epilogue& ep,
                                          K, c_out, out, s);                                  \
     if constexpr (CK_ * sizeof(T) == 128)                                                    \
       if (ch.dma)                                                                            \
-        return launch_dma<T, BN_>(feat, c_in, W, ep, nbr, order, nbr_ordered, n_out, K,      \
-                                  c_out, out, s);                                            \
+        return ch.rb == 1 ? launch_dma<T, BN_, 1>(feat, c_in, W, ep, nbr, order, nbr_ordered,  \
+                                                  n_out, K, c_out, out, s)                   \
+                          : launch_dma<T, BN_, 2>(feat, c_in, W, ep, nbr, order, nbr_ordered,  \
+                                                  n_out, K, c_out, out, s);                  \
     return launch_mfma<T, BN_, CK_>(feat, c_in, W, ep, nbr, order, nbr_ordered,          \
                                     n_out, K, c_out, out, s);                                \
   }
