@@ -346,15 +346,17 @@ def _conv_raw(feats, pw, bias, nbr, order, ordered, n_out, tile):
     return out
 
 
-@pytest.mark.parametrize("rows,grid", [(150000, 96), (300000, 128)])
+@pytest.mark.parametrize("rows,grid", [(50000, 64), (150000, 96), (300000, 128)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
-def test_dma_kernel_matches_the_register_gather_kernel(dtype, rows, grid):
+def test_dma_kernel_matches_the_register_gather_kernel(dtype, rows, grid, monkeypatch):
     """A 128-column layer: the direct-to-LDS kernel (the layer's own choice)
     against the register-gather kernel forced to the same width, bit for bit,
     with the map permuted into the execution order, with the row-major map
     plus the order, and with the row-major map alone.  150k rows (586 tiles
     of 256 rows) take its 32-rows-per-wave form, 300k rows (1172 tiles) its
-    64-rows-per-wave form."""
+    64-rows-per-wave form; 50k rows (196 tiles) narrow the column tile to
+    32."""
+    monkeypatch.setattr(I, "_PLAN_MIN_BYTES", 0)  # an execution order at every size
     idx = _tiny(31, (grid, grid, grid), 1, rows)
     x = torch.from_numpy(idx).to(DEV)
     feats = torch.randn(len(idx), 128, generator=torch.Generator().manual_seed(5)).to(DEV).to(dtype)
