@@ -296,6 +296,10 @@ def bench_gpu(w, args, dev, mods, feats, idx):
                 fwd = x.indice_dict[m.indice_key]
                 build = lambda fwd=fwd: generate_inverse_indice_pairs(fwd)  # noqa: E731
             pair_ms = event_ms(build, 10)
+            # the same build with pair_num read on the host (a submanifold
+            # build returns once its coordinates are checked and leaves the
+            # counts on the device until they are read)
+            counts_ms = event_ms(lambda build=build: build().pair_num, 10)
             data = build()
             n_out = len(data.out_indices)
             P = int(data.pair_num.sum())
@@ -321,6 +325,7 @@ def bench_gpu(w, args, dev, mods, feats, idx):
                 "rows_in": len(x.indices), "rows_out": n_out, "pairs": P,
                 "conv_ms": None, "tflops": None,  # set below, from the layer sequence
                 "pair_build_ms": pair_ms,
+                "pair_build_with_counts_ms": counts_ms,
                 "pair_build_hbm": {"algorithmic_bytes": int(pb), "gbs": pb / (pair_ms * 1e6),
                                    "frac": pb / (pair_ms * 1e6) / HBM_PEAK_GBS},
                 "plan_ms": plan_ms,
@@ -548,6 +553,7 @@ def bench_workload(name, args, dev):
         "voxels_per_s": n_in / (g["step_ms"] * 1e-3),
         "tflops_effective": flops / (g["step_ms"] * 1e-3) / 1e12,
         "pair_build_ms": sum(lay["pair_build_ms"] for lay in layers),
+        "pair_build_with_counts_ms": sum(lay["pair_build_with_counts_ms"] for lay in layers),
         "plan_ms": sum(lay["plan_ms"] for lay in layers),
         "network_ms_cold": g["network_ms_cold"],
         "voxels_per_s_cold": n_in / (g["network_ms_cold"] * 1e-3),
@@ -627,6 +633,7 @@ def main():
                    "pairs": head["pairs"]},
         "tflops_effective": head["tflops_effective"],
         "pair_build_ms": head["pair_build_ms"],
+        "pair_build_with_counts_ms": head["pair_build_with_counts_ms"],
         "pair_build_hbm": head.get("pair_build_hbm"),
         "plan_ms": head["plan_ms"],
         "conv_kernel_ms": head["roofline"]["kernel_ms"],

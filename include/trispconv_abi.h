@@ -73,6 +73,37 @@ TSC_API int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_size,
                            const int32_t dilation[3] /* host */, void* ws, int64_t ws_bytes,
                            int32_t* cols_row, int32_t* nbr, int32_t* counts, tsc_stream_t stream);
 
+/* tsc_subm_pairs with the reference's synchronous coordinate check, but no
+ * wait for the map.  The same launches and map; the call returns once the
+ * kernel that checks the coordinates has finished (the rest of the build is
+ * still queued on the stream) and reports result[0] = the status flags
+ * (TSC_FLAG_* bits, 0 when every row is in the grid) and result[1] = 1 when
+ * the columns are in (b,z,y,x) order.  The per-slot pair counts are not
+ * summed: the probe's per-(slot, block) counts go to slot_blocks
+ * (tsc_subm_slot_blocks_len(n, K) int32), and tsc_subm_counts turns them
+ * into counts[0..K) when the caller wants them; counts[K] and counts[K+1]
+ * are written as by tsc_subm_pairs.  Replaces the host read the reference's
+ * build makes before it returns (pair_num is a CPU tensor, indices.py:131; a
+ * coordinate outside the grid raises there) with a wait on the check alone.
+ * It blocks the calling thread until then (spinning on a word of pinned host
+ * memory, one per host thread and device, allocated on first use), so it is
+ * not for code under graph capture: use tsc_subm_pairs there. */
+TSC_API int64_t tsc_subm_slot_blocks_len(int64_t n, int32_t k_vol);
+TSC_API int tsc_subm_pairs_checked(const int32_t* coords, int64_t n, int32_t batch_size,
+                                   const int32_t spatial[3] /* host */,
+                                   const int32_t ksize[3] /* host */,
+                                   const int32_t dilation[3] /* host */, void* ws,
+                                   int64_t ws_bytes, int32_t* cols_row, int32_t* nbr,
+                                   int32_t* counts, int32_t* slot_blocks,
+                                   int32_t result[2] /* host */, tsc_stream_t stream);
+/* counts[k] = sum of slot_blocks[k][*] for the n rows of a
+ * tsc_subm_pairs_checked build (pair_num, indices.py:131), on the build's
+ * stream.  counts_host (may be null): counts[0..K+2) are also copied there
+ * and the call waits for the stream. */
+TSC_API int tsc_subm_counts(const int32_t* slot_blocks, int64_t n, int32_t k_vol,
+                            int32_t* counts, int32_t* counts_host /* host */,
+                            tsc_stream_t stream);
+
 /* tsc_subm_pairs without a workspace, for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid allocation).  No counterpart in the reference.  The

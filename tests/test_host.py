@@ -302,7 +302,7 @@ def test_pending_pair_counts_are_read_and_checked_on_first_access():
         d = IndiceData(torch.zeros((1, 4), dtype=torch.int32), None, None, None,
                        torch.zeros((1, 4), dtype=torch.int32), (4, 4, 4), (4, 4, 4), (3, 1, 1),
                        (1, 1, 1), (0, 0, 0), (1, 1, 1), True)
-        d._counts_pending = (torch.tensor(counts, dtype=torch.int32), 3)
+        d._counts_pending = (torch.tensor(counts, dtype=torch.int32), 3, None)
         return d
 
     d = data([3, 0, 5, 0])

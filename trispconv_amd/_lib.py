@@ -35,6 +35,10 @@ _SIGNATURES = {
     "tsc_subm_workspace_bytes": (_i64, [_i64, _i32, _i32, c_i32p]),
     "tsc_subm_pairs": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, _vp, _i64,
                                       _vp, _vp, _vp, _vp]),
+    "tsc_subm_slot_blocks_len": (_i64, [_i64, _i32]),
+    "tsc_subm_pairs_checked": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, _vp, _i64,
+                                              _vp, _vp, _vp, _vp, c_i32p, _vp]),
+    "tsc_subm_counts": (ctypes.c_int, [_vp, _i64, _i32, _vp, c_i32p, _vp]),
     "tsc_subm_pairs_noalloc_limit": (_i64, []),
     "tsc_subm_pairs_noalloc": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, _vp, _vp,
                                               _vp, _vp]),
@@ -69,7 +73,7 @@ _SIGNATURES = {
                                          _vp, _vp]),
 }
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _lib: Optional[ctypes.CDLL] = None
 

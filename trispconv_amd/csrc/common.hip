@@ -301,8 +301,10 @@ constexpr int kBmTile = kBmThreads * 4;
 __global__ void __launch_bounds__(kBmThreads) bitmap_reduce_kernel(const uint4* __restrict__ wr2,
                                                                    int64_t nw,
                                                                    uint32_t* __restrict__ sums,
-                                                                   int nsum, SlotScan scan) {
+                                                                   int nsum, SlotScan scan,
+                                                                   int32_t* started) {
   __shared__ uint32_t s_wave[33];
+  signal_started(started);
   if (static_cast<int>(blockIdx.x) >= nsum) {  // blocks past the tiles: a slot scan riding along
     slot_scan_block(scan, blockIdx.x - nsum, s_wave);
     return;
@@ -335,8 +337,10 @@ __device__ __forceinline__ uint32_t pack_bytes(uint4 a, uint4 b) {
 __global__ void __launch_bounds__(kBmThreads) bitmap_pack_kernel(const uint4* __restrict__ bytes,
                                                                  uint4* __restrict__ wr2, int64_t nw,
                                                                  uint32_t* __restrict__ sums,
-                                                                 int nsum, SlotScan scan) {
+                                                                 int nsum, SlotScan scan,
+                                                                 int32_t* started) {
   __shared__ uint32_t s_wave[33];
+  signal_started(started);
   if (static_cast<int>(blockIdx.x) >= nsum) {  // blocks past the tiles: a slot scan riding along
     slot_scan_block(scan, blockIdx.x - nsum, s_wave);
     return;
@@ -415,7 +419,7 @@ int64_t bitmap_scan_scratch_words(int64_t nw) {
 }
 
 int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStream_t s,
-                const uint8_t* bytes, const SlotScan* scan) {
+                const uint8_t* bytes, const SlotScan* scan, int32_t* started) {
   const int64_t nsum = ceil_div(nw > 0 ? nw : 1, kBmTile);
   uint32_t* sums = scratch;
   uint32_t* pre = scratch + nsum;
@@ -426,10 +430,11 @@ int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStr
   const unsigned grid = static_cast<unsigned>(nsum + sc.blocks());
   if (bytes) {
     bitmap_pack_kernel<<<grid, kBmThreads, 0, s>>>(reinterpret_cast<const uint4*>(bytes), wr2, nw,
-                                                   sums, static_cast<int>(nsum), sc);
+                                                   sums, static_cast<int>(nsum), sc, started);
     TSC_LAUNCH_CHECK("bitmap_pack");
   } else {
-    bitmap_reduce_kernel<<<grid, kBmThreads, 0, s>>>(wr2, nw, sums, static_cast<int>(nsum), sc);
+    bitmap_reduce_kernel<<<grid, kBmThreads, 0, s>>>(wr2, nw, sums, static_cast<int>(nsum), sc,
+                                                     started);
     TSC_LAUNCH_CHECK("bitmap_reduce");
   }
   const uint32_t* p = nullptr;
@@ -444,7 +449,61 @@ int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStr
   return 0;
 }
 
+// --------------------------------------------------- host status words --
+namespace {
+constexpr int kMaxStatusDevices = 64;
+thread_local HostStatus t_status[kMaxStatusDevices] = {};
+}  // namespace
+
+int host_status(HostStatus* out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess)
+    return set_error(-static_cast<int>(e), "host_status: hipGetDevice: %s", hipGetErrorString(e));
+  TSC_REQUIRE(dev >= 0 && dev < kMaxStatusDevices, "host_status: device %d beyond %d devices",
+              dev, kMaxStatusDevices);
+  HostStatus& h = t_status[dev];
+  if (!h.host) {
+    void* p = nullptr;
+    e = hipHostMalloc(&p, kHostWords * sizeof(int32_t), hipHostMallocMapped | hipHostMallocCoherent);
+    if (e != hipSuccess)
+      return set_error(-static_cast<int>(e), "host_status: hipHostMalloc: %s",
+                       hipGetErrorString(e));
+    void* d = nullptr;
+    e = hipHostGetDevicePointer(&d, p, 0);
+    if (e != hipSuccess) {
+      (void)hipHostFree(p);
+      return set_error(-static_cast<int>(e), "host_status: hipHostGetDevicePointer: %s",
+                       hipGetErrorString(e));
+    }
+    h.host = static_cast<int32_t*>(p);
+    h.dev = static_cast<int32_t*>(d);
+  }
+  *out = h;
+  return 0;
+}
+
+int wait_host_word(const int32_t* w, hipStream_t s, int* seen) {
+  for (uint32_t i = 1;; ++i) {
+    if (__atomic_load_n(w, __ATOMIC_ACQUIRE)) {
+      *seen = 1;
+      return 0;
+    }
+    if ((i & 255) == 0) {  // every few microseconds: has the stream drained or failed?
+      const hipError_t e = hipStreamQuery(s);
+      if (e == hipSuccess) {
+        *seen = __atomic_load_n(w, __ATOMIC_ACQUIRE) != 0;
+        return 0;
+      }
+      if (e != hipErrorNotReady)
+        return set_error(-static_cast<int>(e), "waiting for a host word: %s",
+                         hipGetErrorString(e));
+    }
+    __builtin_ia32_pause();
+  }
+}
+
 }  // namespace tsc
 
 extern "C" const char* tsc_last_error(void) { return tsc::last_error(); }
-extern "C" int tsc_abi_version(void) { return 9; }
+extern "C" int tsc_abi_version(void) { return 10; }

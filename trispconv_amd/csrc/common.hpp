@@ -226,16 +226,60 @@ int64_t bitmap_entries(int64_t nw);
 int64_t bitmap_scan_scratch_words(int64_t nw);
 // With scan, that slot scan (scan_slot_blocks) runs in the same launch as
 // the first pass.
+// started (may be null): a word of pinned host memory the first launch sets
+// when it begins (signal_started).
 int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStream_t s,
-                const uint8_t* bytes = nullptr, const SlotScan* scan = nullptr);
+                const uint8_t* bytes = nullptr, const SlotScan* scan = nullptr,
+                int32_t* started = nullptr);
+// Two words of pinned host memory that kernels store into, one pair per host
+// thread and device (allocated on first use there and kept until the process
+// ends).  A build that must report bad coordinates before it returns, but
+// need not wait for the rest of its kernels, has its checking kernel store a
+// non-zero value into the flag word, and the kernel after it store 1 into
+// the started word when it begins (so the check has finished); the host
+// waits for the started word only.
+// After them, room for a build's per-slot counts (up to 4096 slots, plus
+// two words) that a kernel copies there, and one word per slot that the
+// kernel sets once that slot's count is there.
+struct HostStatus {
+  int32_t* host;  // host view: [kHostFlag] flag, [kHostStarted] started, counts, done words
+  int32_t* dev;   // the same words as kernels address them
+};
+constexpr int kHostFlag = 0;
+constexpr int kHostStarted = 32;  // another 128-byte line
+constexpr int kHostCounts = 64;
+constexpr int kHostMaxSlots = 4096;
+constexpr int kHostDone = kHostCounts + kHostMaxSlots + 32;  // past the counts' two extra words
+constexpr int kHostWords = kHostDone + kHostMaxSlots;
+int host_status(HostStatus* out);
+// Spins until the host word w (the host view of a HostStatus word) is
+// non-zero.  If the stream drains first (or reports an error) it stops
+// there; *seen = 0 then says the word was never set.
+int wait_host_word(const int32_t* w, hipStream_t s, int* seen);
+
+// Block 0's first thread stores 1 into a word of pinned host memory (may be
+// null): this kernel has begun, so every kernel before it on the stream has
+// finished.
+__device__ __forceinline__ void signal_started(int32_t* host_word) {
+  if (host_word && blockIdx.x == 0 && threadIdx.x == 0)
+    __hip_atomic_store(host_word, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // The submanifold build (tsc_subm_pairs) on a given workspace.  ws_limit > 0:
 // ws is that many bytes of fixed scratch, the bitmap is used only when it
 // fits and a build that fits in neither way is an argument error; 0: ws is
 // the caller's workspace of ws_bytes, sized by tsc_subm_workspace_bytes.
+// hs (may be null): the coordinate check also goes to hs's flag word, the
+// next kernel sets its started word, and the call waits for that before it
+// returns.  slot_blocks (may be null): the probe's per-(slot, block) counts
+// go there ([K][ceil(n / 256)] int32) and counts[0..K) are left for
+// tsc_subm_counts; otherwise they are summed into counts.  *raster (may be
+// null) = 1 when the map's columns are in (b,z,y,x) order.
 int subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size, const int32_t spatial[3],
                   const int32_t ksize[3], const int32_t dilation[3], void* ws, int64_t ws_bytes,
                   int64_t ws_limit, int32_t* cols_row, int32_t* nbr, int32_t* counts,
-                  tsc_stream_t stream);
+                  tsc_stream_t stream, const HostStatus* hs = nullptr,
+                  int32_t* slot_blocks = nullptr, int32_t* raster = nullptr);
 int exclusive_scan_u32(const uint32_t* src, int kind, int64_t n, uint32_t* out, int32_t* total,
                        uint32_t* scratch, hipStream_t s);
 

@@ -61,6 +61,15 @@ __device__ __forceinline__ int4 cell_coords(const SubmGeom& g, uint32_t cell) {
                    static_cast<int>(y), static_cast<int>(x));
 }
 
+// A row outside the grid: its status flag on the device and, when a caller
+// waits for the check instead of for the whole build, a non-zero word in
+// pinned host memory (a plain store; every writer stores 1).
+__device__ __forceinline__ void flag_bad_row(const SubmGeom& g, int b, int32_t* status,
+                                             int32_t* host_flag) {
+  atomicOr(status, (b < 0 || b >= g.B) ? TSC_FLAG_BATCH_OUT_OF_RANGE : TSC_FLAG_COORD_OUT_OF_GRID);
+  if (host_flag) __hip_atomic_store(host_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 // A map column of the bitmap path is one 8-byte entry: x = its row + 1 (0
 // while unassigned; repeated cells keep the largest row by atomicMax on x)
 // and y = its cell key.
@@ -68,13 +77,12 @@ __device__ __forceinline__ int4 cell_coords(const SubmGeom& g, uint32_t cell) {
 __global__ void __launch_bounds__(256) subm_insert_kernel(const int4* __restrict__ coords,
                                                           int64_t n, SubmGeom g,
                                                           unsigned long long* table,
-                                                          int32_t* status) {
+                                                          int32_t* status, int32_t* host_flag) {
   const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (r >= n) return;
   const int4 c = coords[r];  // (b, z, y, x)
   if (!in_grid(g, c.x, c.y, c.z, c.w)) {
-    atomicOr(status, (c.x < 0 || c.x >= g.B) ? TSC_FLAG_BATCH_OUT_OF_RANGE
-                                              : TSC_FLAG_COORD_OUT_OF_GRID);
+    flag_bad_row(g, c.x, status, host_flag);
     return;
   }
   hash_insert(table, g.mask, cell_key(g, c.x, c.y, c.z, c.w), static_cast<uint32_t>(r));
@@ -92,8 +100,9 @@ __global__ void __launch_bounds__(kRows) subm_probe_kernel(const int4* __restric
                                                            const unsigned long long* __restrict__ table,
                                                            int32_t* __restrict__ nbr,
                                                            int32_t* __restrict__ blk_cnt,
-                                                           int nblk) {
+                                                           int nblk, int32_t* started) {
   __shared__ int32_t s_cnt[kRows / kWave][64];  // per wave, per slot (slots < 64)
+  signal_started(started);
   const int t = threadIdx.x;
   const int w = t / kWave;
   const int64_t r = blockIdx.x * (int64_t)kRows + t;
@@ -176,13 +185,13 @@ __device__ __forceinline__ uint32_t hash64(uint64_t k) {
 __global__ void __launch_bounds__(256) subm_insert_wide_kernel(const int4* __restrict__ coords,
                                                                int64_t n, SubmGeom g,
                                                                unsigned long long* keys,
-                                                               int32_t* vals, int32_t* status) {
+                                                               int32_t* vals, int32_t* status,
+                                                               int32_t* host_flag) {
   const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (r >= n) return;
   const int4 c = coords[r];  // (b, z, y, x)
   if (!in_grid(g, c.x, c.y, c.z, c.w)) {
-    atomicOr(status, (c.x < 0 || c.x >= g.B) ? TSC_FLAG_BATCH_OUT_OF_RANGE
-                                              : TSC_FLAG_COORD_OUT_OF_GRID);
+    flag_bad_row(g, c.x, status, host_flag);
     return;
   }
   const unsigned long long key = cell_key64(g, c.x, c.y, c.z, c.w);
@@ -202,8 +211,9 @@ __global__ void __launch_bounds__(256) subm_insert_wide_kernel(const int4* __res
 __global__ void __launch_bounds__(kRows) subm_probe_wide_kernel(
     const int4* __restrict__ coords, int64_t n, int K, SubmGeom g,
     const unsigned long long* __restrict__ keys, const int32_t* __restrict__ vals,
-    int32_t* __restrict__ nbr, int32_t* __restrict__ blk_cnt, int nblk) {
+    int32_t* __restrict__ nbr, int32_t* __restrict__ blk_cnt, int nblk, int32_t* started) {
   __shared__ int32_t s_cnt[kRows / kWave][64];  // per wave, per slot (slots < 64)
+  signal_started(started);
   const int t = threadIdx.x;
   const int w = t / kWave;
   const int64_t r = blockIdx.x * (int64_t)kRows + t;
@@ -294,15 +304,14 @@ template <bool BYTES>
 __global__ void __launch_bounds__(256) subm_mark_kernel(const int4* __restrict__ coords, int64_t n,
                                                         SubmGeom g, uint2* wr,
                                                         uint8_t* __restrict__ bytes,
-                                                        int32_t* status,
+                                                        int32_t* status, int32_t* host_flag,
                                                         uint2* __restrict__ col) {
   const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (r >= n) return;
   col[r].x = 0u;
   const int4 c = coords[r];
   if (!in_grid(g, c.x, c.y, c.z, c.w)) {
-    atomicOr(status, (c.x < 0 || c.x >= g.B) ? TSC_FLAG_BATCH_OUT_OF_RANGE
-                                              : TSC_FLAG_COORD_OUT_OF_GRID);
+    flag_bad_row(g, c.x, status, host_flag);
     return;
   }
   const uint32_t cell = cell_key(g, c.x, c.y, c.z, c.w);
@@ -344,21 +353,24 @@ __global__ void __launch_bounds__(256) subm_rank_kernel(const int4* __restrict__
 // row gets a column after the n_unique cell columns (in no particular order;
 // the values computed for it do not depend on where it sits).  Nothing to do
 // when every row has a cell of its own.
+// A grid-stride loop over few blocks: when every cell has one row (the usual
+// case) the launch only reads n_unique, and a small grid makes that cheap.
 __global__ void __launch_bounds__(256) subm_place_kernel(const int4* __restrict__ coords, int64_t n,
                                                          SubmGeom g, const uint2* __restrict__ wr,
                                                          const int32_t* __restrict__ n_unique,
                                                          uint2* col_e, int32_t* n_extra) {
-  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (r >= n) return;
   const int32_t nu = *n_unique;
   if (nu == n) return;
-  const int4 c = coords[r];
-  if (!in_grid(g, c.x, c.y, c.z, c.w)) return;
-  const uint32_t cell = cell_key(g, c.x, c.y, c.z, c.w);
-  const uint32_t rank = cell_rank(wr[cell >> 5], cell);
-  if (col_e[rank].x != static_cast<uint32_t>(r + 1)) {
-    const int32_t c2 = nu + atomicAdd(n_extra, 1);  // < rows in the grid <= n
-    col_e[c2] = make_uint2(static_cast<uint32_t>(r + 1), cell);
+  for (int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; r < n;
+       r += (int64_t)gridDim.x * blockDim.x) {
+    const int4 c = coords[r];
+    if (!in_grid(g, c.x, c.y, c.z, c.w)) continue;
+    const uint32_t cell = cell_key(g, c.x, c.y, c.z, c.w);
+    const uint32_t rank = cell_rank(wr[cell >> 5], cell);
+    if (col_e[rank].x != static_cast<uint32_t>(r + 1)) {
+      const int32_t c2 = nu + atomicAdd(n_extra, 1);  // < rows in the grid <= n
+      col_e[c2] = make_uint2(static_cast<uint32_t>(r + 1), cell);
+    }
   }
 }
 
@@ -699,6 +711,39 @@ __global__ void __launch_bounds__(kRows) subm_fill_kernel(const int32_t* __restr
   }
 }
 
+// Block k: counts[k] = the sum of slot k's per-block counts (cnt [K][nblk];
+// none: counts[k] as it is), copied into host memory (host[k]; block 0 also
+// copies counts[K] and counts[K + 1]), then done[k] = 1 once they are
+// visible there.
+__global__ void __launch_bounds__(256) subm_counts_kernel(const int32_t* __restrict__ cnt,
+                                                          int nblk, int K,
+                                                          int32_t* __restrict__ counts,
+                                                          int32_t* host, int32_t* done) {
+  __shared__ int32_t s_part[256 / kWave];
+  const int k = blockIdx.x;
+  int32_t tot = 0;
+  if (cnt) {
+    int32_t acc = 0;
+    for (int i = threadIdx.x; i < nblk; i += blockDim.x) acc += cnt[(int64_t)k * nblk + i];
+    for (int off = kWave / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, kWave);
+    if (__lane_id() == 0) s_part[threadIdx.x / kWave] = acc;
+    __syncthreads();
+    for (int w = 0; w < 256 / kWave; ++w) tot += s_part[w];
+  }
+  if (threadIdx.x != 0) return;
+  if (cnt)
+    counts[k] = tot;
+  else
+    tot = counts[k];
+  __hip_atomic_store(&host[k], tot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  if (k == 0) {
+    __hip_atomic_store(&host[K], counts[K], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(&host[K + 1], counts[K + 1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+  // the values reach host memory before the word that announces them
+  __hip_atomic_store(&done[k], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
 }  // namespace
 
 static int64_t subm_capacity(int64_t n) {
@@ -802,7 +847,8 @@ extern "C" int64_t tsc_subm_workspace_bytes(int64_t n, int32_t k_vol, int32_t ba
 int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
                       const int32_t spatial[3], const int32_t ksize[3],
                       const int32_t dilation[3], void* ws, int64_t ws_bytes, int64_t ws_limit,
-                      int32_t* cols_row, int32_t* nbr, int32_t* counts, tsc_stream_t stream) {
+                      int32_t* cols_row, int32_t* nbr, int32_t* counts, tsc_stream_t stream,
+                      const HostStatus* hs, int32_t* slot_blocks, int32_t* raster) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   TSC_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "subm: n=%lld out of range", (long long)n);
   TSC_REQUIRE(batch_size > 0, "subm: batch_size must be positive");
@@ -830,11 +876,16 @@ int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
   TSC_REQUIRE(counts != nullptr, "subm: counts is null");
 
   int rc = 0;
+  if (raster) *raster = 0;
   if (n == 0) return fill_u32(reinterpret_cast<uint32_t*>(counts), K + 2, 0u, s);
   TSC_REQUIRE(coords && cols_row && nbr && ws, "subm: null pointer");
+  // the checking kernel's flag and the next kernel's start, in host memory
+  int32_t* host_flag = hs ? hs->dev + kHostFlag : nullptr;
+  int32_t* started = hs ? hs->dev + kHostStarted : nullptr;
 
   const int nblk = static_cast<int>(ceil_div(n, kRows));
   const SubmWork w = subm_carve(ws, n, K, cells, mode, nullptr);
+  int32_t* const blk_cnt = slot_blocks ? slot_blocks : w.blk_cnt;
   const int4* c4 = reinterpret_cast<const int4*>(coords);
   if (w.wr) {
     const int64_t nw = bitmap_words(cells);
@@ -850,44 +901,45 @@ int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
     TSC_LAUNCH_CHECK("subm_init");
     if (w.bytes)
       subm_mark_kernel<true><<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.bytes, counts + K,
-                                                              w.col);
+                                                              host_flag, w.col);
     else
       subm_mark_kernel<false><<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, nullptr,
-                                                               counts + K, w.col);
+                                                               counts + K, host_flag, w.col);
     TSC_LAUNCH_CHECK("subm_mark");
-    if ((rc = bitmap_scan(w.wr, nw, w.scan, w.n_unique, s, w.bytes))) return rc;
+    if (raster) *raster = 1;
+    if ((rc = bitmap_scan(w.wr, nw, w.scan, w.n_unique, s, w.bytes, nullptr, started))) return rc;
     subm_rank_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, w.col);
     TSC_LAUNCH_CHECK("subm_rank");
-    subm_place_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, w.col,
-                                                       w.n_extra);
+    subm_place_kernel<<<static_cast<unsigned>(std::min<int64_t>(ceil_div(n, 256), 128)), 256, 0,
+                        s>>>(c4, n, g, w.wr, w.n_unique, w.col, w.n_extra);
     TSC_LAUNCH_CHECK("subm_place");
     // slots from 64 on are added into the per-block table, which starts at 0
     if (K > 64 &&
-        (rc = fill_u32(reinterpret_cast<uint32_t*>(w.blk_cnt), (int64_t)nblk * K, 0u, s)))
+        (rc = fill_u32(reinterpret_cast<uint32_t*>(blk_cnt), (int64_t)nblk * K, 0u, s)))
       return rc;
     if (ks.x == 3 && 2 * dil.x < 32 && ks.y == 3 && ks.z == 3) {
       subm_probe_rows_kernel<3, 3, 3, false><<<ceil_div(n, 256), 256, 0, s>>>(
-          n, K, g, w.wr, nw, w.col, nullptr, w.n_unique, w.n_extra, cols_row, nbr, w.blk_cnt,
+          n, K, g, w.wr, nw, w.col, nullptr, w.n_unique, w.n_extra, cols_row, nbr, blk_cnt,
           nblk, counts);
       TSC_LAUNCH_CHECK("subm_probe_rows");
     } else if (ks.x == 3 && 2 * dil.x < 32) {
       subm_probe_rows_kernel<3, 0, 0, false><<<ceil_div(n, 256), 256, 0, s>>>(
-          n, K, g, w.wr, nw, w.col, nullptr, w.n_unique, w.n_extra, cols_row, nbr, w.blk_cnt,
+          n, K, g, w.wr, nw, w.col, nullptr, w.n_unique, w.n_extra, cols_row, nbr, blk_cnt,
           nblk, counts);
       TSC_LAUNCH_CHECK("subm_probe_rows");
     } else {
       subm_probe_cols_kernel<<<ceil_div(n, 256), 256, 0, s>>>(n, K, g, w.wr, w.col, w.n_unique,
-                                                              w.n_extra, cols_row, nbr, w.blk_cnt,
+                                                              w.n_extra, cols_row, nbr, blk_cnt,
                                                               nblk, counts);
       TSC_LAUNCH_CHECK("subm_probe_cols");
     }
-    if ((rc = sum_slot_blocks(w.blk_cnt, counts, K, nblk, s))) return rc;
+    if (!slot_blocks && (rc = sum_slot_blocks(blk_cnt, counts, K, nblk, s))) return rc;
   } else {
     if ((rc = fill_u32(reinterpret_cast<uint32_t*>(counts), K + 2, 0u, s))) return rc;
     const int64_t cap = subm_capacity(n);
     SubmGeom g{batch_size, shape, ks, dil, static_cast<uint32_t>(cap - 1)};
     if (K > 64 &&
-        (rc = fill_u32(reinterpret_cast<uint32_t*>(w.blk_cnt), (int64_t)nblk * K, 0u, s)))
+        (rc = fill_u32(reinterpret_cast<uint32_t*>(blk_cnt), (int64_t)nblk * K, 0u, s)))
       return rc;
     if ((rc = fill_u64(w.table, cap, kEmpty, s))) return rc;
     iota_kernel<<<ceil_div(n, 256), 256, 0, s>>>(cols_row, n);
@@ -895,18 +947,19 @@ int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
     if (w.vals) {
       if ((rc = fill_u32(reinterpret_cast<uint32_t*>(w.vals), cap, 0xffffffffu, s))) return rc;
       subm_insert_wide_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.table, w.vals,
-                                                               counts + K);
+                                                               counts + K, host_flag);
       TSC_LAUNCH_CHECK("subm_insert_wide");
-      subm_probe_wide_kernel<<<nblk, kRows, 0, s>>>(c4, n, K, g, w.table, w.vals, nbr, w.blk_cnt,
-                                                    nblk);
+      subm_probe_wide_kernel<<<nblk, kRows, 0, s>>>(c4, n, K, g, w.table, w.vals, nbr, blk_cnt,
+                                                    nblk, started);
       TSC_LAUNCH_CHECK("subm_probe_wide");
     } else {
-      subm_insert_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.table, counts + K);
+      subm_insert_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.table, counts + K,
+                                                          host_flag);
       TSC_LAUNCH_CHECK("subm_insert");
-      subm_probe_kernel<<<nblk, kRows, 0, s>>>(c4, n, K, g, w.table, nbr, w.blk_cnt, nblk);
+      subm_probe_kernel<<<nblk, kRows, 0, s>>>(c4, n, K, g, w.table, nbr, blk_cnt, nblk, started);
       TSC_LAUNCH_CHECK("subm_probe");
     }
-    if ((rc = scan_slot_blocks(w.blk_cnt, w.blk_off, counts, K, nblk, s))) return rc;
+    if (!slot_blocks && (rc = sum_slot_blocks(blk_cnt, counts, K, nblk, s))) return rc;
   }
   return 0;
 }
@@ -918,6 +971,83 @@ extern "C" int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_si
                               tsc_stream_t stream) {
   return subm_pairs_ws(coords, n, batch_size, spatial, ksize, dilation, ws, ws_bytes, 0, cols_row,
                        nbr, counts, stream);
+}
+
+extern "C" int64_t tsc_subm_slot_blocks_len(int64_t n, int32_t k_vol) {
+  if (n < 0 || k_vol <= 0) return -1;
+  return ceil_div(n > 0 ? n : 1, kRows) * k_vol;
+}
+
+extern "C" int tsc_subm_pairs_checked(const int32_t* coords, int64_t n, int32_t batch_size,
+                                      const int32_t spatial[3], const int32_t ksize[3],
+                                      const int32_t dilation[3], void* ws, int64_t ws_bytes,
+                                      int32_t* cols_row, int32_t* nbr, int32_t* counts,
+                                      int32_t* slot_blocks, int32_t result[2],
+                                      tsc_stream_t stream) {
+  TSC_REQUIRE(result != nullptr, "subm: result is null");
+  TSC_REQUIRE(slot_blocks != nullptr, "subm: slot_blocks is null");
+  result[0] = result[1] = 0;
+  HostStatus hs{};
+  if (int rc = host_status(&hs)) return rc;
+  hs.host[kHostFlag] = 0;
+  hs.host[kHostStarted] = 0;
+  int32_t raster = 0;
+  if (int rc = subm_pairs_ws(coords, n, batch_size, spatial, ksize, dilation, ws, ws_bytes, 0,
+                             cols_row, nbr, counts, stream, &hs, slot_blocks, &raster))
+    return rc;
+  result[1] = raster;
+  if (n == 0) return 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int seen = 0;
+  if (int rc = wait_host_word(hs.host + kHostStarted, s, &seen)) return rc;
+  if (!seen || __atomic_load_n(hs.host + kHostFlag, __ATOMIC_ACQUIRE) != 0) {
+    // a coordinate failed (or the stream drained before the word was seen):
+    // the exact flags, from the device's status word
+    hipError_t e = hipMemcpyAsync(&result[0], counts + ksize[0] * ksize[1] * ksize[2],
+                                  sizeof(int32_t), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess)
+      return set_error(-static_cast<int>(e), "subm: reading the status flags: %s",
+                       hipGetErrorString(e));
+  }
+  return 0;
+}
+
+extern "C" int tsc_subm_counts(const int32_t* slot_blocks, int64_t n, int32_t k_vol,
+                               int32_t* counts, int32_t* counts_host, tsc_stream_t stream) {
+  TSC_REQUIRE(n >= 0 && n < (int64_t(1) << 31) && k_vol > 0 && k_vol <= 4096,
+              "subm_counts: invalid sizes");
+  TSC_REQUIRE(counts, "subm_counts: null pointer");
+  TSC_REQUIRE(n == 0 || slot_blocks, "subm_counts: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int32_t* cnt = n > 0 ? slot_blocks : nullptr;
+  const int nblk = static_cast<int>(ceil_div(n > 0 ? n : 1, kRows));
+  if (!counts_host) {
+    if (!cnt) return 0;
+    return sum_slot_blocks(cnt, counts, k_vol, nblk, s);
+  }
+  // the sums go to the device counts and, with counts[K] and counts[K+1],
+  // straight into pinned host memory; a word per slot says its count is there
+  HostStatus hs{};
+  if (int rc = host_status(&hs)) return rc;
+  for (int k = 0; k < k_vol; ++k) hs.host[kHostDone + k] = 0;
+  subm_counts_kernel<<<k_vol, 256, 0, s>>>(cnt, nblk, k_vol, counts, hs.dev + kHostCounts,
+                                           hs.dev + kHostDone);
+  TSC_LAUNCH_CHECK("subm_counts");
+  int seen = 1;
+  for (int k = 0; k < k_vol && seen; ++k)
+    if (int rc = wait_host_word(hs.host + kHostDone + k, s, &seen)) return rc;
+  if (!seen) {
+    // the stream drained without the words showing: read the device copy
+    hipError_t e = hipMemcpyAsync(counts_host, counts, (k_vol + 2) * sizeof(int32_t),
+                                  hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    return e == hipSuccess ? 0 : set_error(-static_cast<int>(e), "subm_counts: %s",
+                                           hipGetErrorString(e));
+  }
+  for (int i = 0; i < k_vol + 2; ++i)
+    counts_host[i] = __atomic_load_n(hs.host + kHostCounts + i, __ATOMIC_ACQUIRE);
+  return 0;
 }
 
 extern "C" int tsc_subm_pairs_from_bitmap(const int32_t* coords, int64_t n, int32_t batch_size,

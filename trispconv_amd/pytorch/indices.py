@@ -8,11 +8,13 @@ device as padded int32 tables (slot k owns ``[k, :pair_num[k]]``) next to the
 output-major neighbour map the convolution reads; the reference-style lists
 of K int64 tensors are materialised on first access to ``pairs_in`` /
 ``pairs_out``.  ``pair_num`` is a CPU int64 tensor, as in the reference
-(indices.py:131), read with the one device-to-host copy each build makes.
+(indices.py:131): strided builds read it with the one device-to-host copy
+they make (their output count), submanifold builds on its first access.
 """
 from __future__ import annotations
 
-from typing import List, Optional, Sequence, Tuple
+import ctypes
+from typing import Callable, List, Optional, Sequence, Tuple
 
 import torch
 from torch.utils.weak import WeakIdKeyDictionary
@@ -79,8 +81,10 @@ class IndiceData:
         self.subm = subm
         self.pair_num = pair_num
         # a build whose counts stay on the device until pair_num is read:
-        # (counts [K + 1] int32, K); counts[K] holds the build's status flags
-        self._counts_pending: Optional[Tuple[torch.Tensor, int]] = None
+        # (counts [K + 2] int32, K, a function that returns them on the host,
+        # reading them on the build's stream, or None);
+        # counts[K] holds the build's status flags
+        self._counts_pending: Optional[Tuple[torch.Tensor, int, Optional[Callable[[], None]]]] = None
         self._pairs_in = pairs_in
         self._pairs_out = pairs_out
         # device tables
@@ -112,13 +116,14 @@ class IndiceData:
 
     @property
     def pair_num(self) -> torch.Tensor:
-        """Pairs per slot, a CPU int64 tensor (indices.py:131).  A build that
-        left its counts on the device (a submanifold build on a strided
-        layer's bitmap, which has no coordinates to check) is read here, on
-        first access, so the forward pass does not wait for it."""
+        """Pairs per slot, a CPU int64 tensor (indices.py:131).  Submanifold
+        builds leave their counts on the device (their coordinates are
+        checked before the build returns, or, on a strided layer's bitmap,
+        need no check); they are read here, on first access, so the forward
+        pass does not wait for them."""
         if self._pair_num is None and self._counts_pending is not None:
-            counts, K = self._counts_pending
-            host = counts.cpu()
+            counts, K, read = self._counts_pending
+            host = read() if read is not None else counts.cpu()
             if int(host[K]) & L.FLAG_ROWS_NOT_BITMAP:
                 raise RuntimeError("generate_subm_indice_pairs: coordinates are not the rows of "
                                    "the strided build they were registered with")
@@ -416,6 +421,18 @@ _STRIDED_BITMAPS = WeakIdKeyDictionary()
 _NARROW_CELLS = (1 << 32) - 1
 
 
+def _counts_to_host(counts: torch.Tensor, K: int, stream: int,
+                    slot_blocks: Optional[torch.Tensor] = None, n: int = 0) -> torch.Tensor:
+    """A submanifold build's counts [K + 2] on the host, read on the build's
+    stream (which need not be the current one any more); with slot_blocks,
+    the per-slot sums of the probe's block counts are made first."""
+    host = (ctypes.c_int32 * (K + 2))()
+    L.check(L.lib().tsc_subm_counts(slot_blocks.data_ptr() if slot_blocks is not None else None,
+                                    n if slot_blocks is not None else 0, K, counts.data_ptr(),
+                                    host, stream), "generate_subm_indice_pairs")
+    return torch.tensor(list(host), dtype=torch.int32)
+
+
 def _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil):
     """The submanifold build on a strided build's output set, through its
     bitmap, or None when ``indices`` is not such an output (unchanged)."""
@@ -433,9 +450,10 @@ def _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil):
     cols_row = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
     map_cols = torch.empty((K, n), dtype=torch.int32, device=dev)
     counts = torch.empty(K + 2, dtype=torch.int32, device=dev)
+    stream = L.stream_of(coords)
     L.check(L.lib().tsc_subm_pairs_from_bitmap(
         coords.data_ptr(), n, int(batch_size), L.i3(shape), L.i3(ks), L.i3(dil), ws.data_ptr(),
-        nwords, cols_row.data_ptr(), map_cols.data_ptr(), counts.data_ptr(), L.stream_of(coords)),
+        nwords, cols_row.data_ptr(), map_cols.data_ptr(), counts.data_ptr(), stream),
         "generate_subm_indice_pairs")
     # No read-back here: the rows are the registered output set (same tensor,
     # same version), so there is nothing to validate before the convolution.
@@ -448,7 +466,7 @@ def _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil):
         dilation=dil, subm=True, pin=None, pout=None, cnt_dev=None, pair_num=None,
         nbr=None, batch_size=int(batch_size), map_cols=map_cols, cols_row=cols_row[:n],
         raster=True)
-    d._counts_pending = (counts, K)
+    d._counts_pending = (counts, K, lambda: _counts_to_host(counts, K, stream))
     return d
 
 
@@ -472,28 +490,36 @@ def generate_subm_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size:
     ws = L.workspace(ws_bytes, dev)
     # The map by columns (in (b,z,y,x) order when the bitmap path runs; the
     # reference's pair lists are derived from it on first access), the column
-    # -> row table and the counts: one allocation, 256-byte aligned views.
+    # -> row table, the counts and the probe's per-(slot, block) counts: one
+    # allocation, 256-byte aligned views.
     n_al = _align64(max(n, 1))
-    tables = torch.empty(n_al + _align64(K * n) + K + 2, dtype=torch.int32, device=dev)
+    nb = int(lib.tsc_subm_slot_blocks_len(n, K))
+    tables = torch.empty(n_al + _align64(K * n) + _align64(K + 2) + nb, dtype=torch.int32,
+                         device=dev)
     cols_row = tables[:n]
     map_cols = tables[n_al:n_al + K * n].view(K, n)
     counts = tables[n_al + _align64(K * n):][:K + 2]
-    L.check(lib.tsc_subm_pairs(coords.data_ptr(), n, int(batch_size), L.i3(shape), L.i3(ks),
-                               L.i3(dil), ws.data_ptr(), ws.numel(), cols_row.data_ptr(),
-                               map_cols.data_ptr(), counts.data_ptr(), L.stream_of(coords)),
+    slot_blocks = tables[n_al + _align64(K * n) + _align64(K + 2):]
+    # Returns once the coordinates are checked (a row outside the grid raises
+    # here, as in the reference); the map is still being built on the stream,
+    # and the per-slot counts are summed and read only when pair_num is.
+    stream = L.stream_of(coords)
+    result = (ctypes.c_int32 * 2)()
+    L.check(lib.tsc_subm_pairs_checked(coords.data_ptr(), n, int(batch_size), L.i3(shape),
+                                       L.i3(ks), L.i3(dil), ws.data_ptr(), ws.numel(),
+                                       cols_row.data_ptr(), map_cols.data_ptr(),
+                                       counts.data_ptr(), slot_blocks.data_ptr(), result, stream),
             "generate_subm_indice_pairs")
-    # the result object is made while the kernels run; the counts and the
-    # status flags are read after
+    _raise_status(int(result[0]), "generate_subm_indice_pairs")
     d = IndiceData._from_tables(
         out_indices=indices, input_indices=indices, input_spatial_shape=spatial_shape,
         output_spatial_shape=spatial_shape, kernel_size=ks, stride=(1, 1, 1),
         padding=(0, 0, 0), dilation=dil, subm=True, pin=None, pout=None, cnt_dev=None,
         pair_num=None, nbr=None, batch_size=int(batch_size), map_cols=map_cols,
         cols_row=cols_row)
-    host = counts.cpu()
-    _raise_status(int(host[K]), "generate_subm_indice_pairs")
-    d.pair_num = host[:K].long()
-    d._raster = bool(host[K + 1])
+
+    d._counts_pending = (counts, K, lambda: _counts_to_host(counts, K, stream, slot_blocks, n))
+    d._raster = bool(result[1])
     return d
 
 
