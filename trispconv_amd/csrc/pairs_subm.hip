@@ -328,50 +328,36 @@ __device__ __forceinline__ uint32_t cell_rank(uint2 e, uint32_t cell) {
 
 // Column (rank of the row's cell) = the largest row with that cell, and the
 // cell.  When every row has a cell of its own (n_unique == n) the ranks are
-// distinct and plain stores do; otherwise repeated cells take the largest row
-// by atomicMax (entries start at 0; every writer stores the same cell).
+// distinct and plain stores do.  Otherwise repeated cells keep the largest
+// row by atomicMax (entries start at 0; every writer stores the same cell),
+// and every row that is not its cell's largest gets a column of its own
+// after the n_unique cell columns (in no particular order; the values
+// computed for it do not depend on where it sits).  The value atomicMax
+// returns names such a row exactly once: a row that finds a larger row
+// already there places itself; a row that finds a smaller one displaces
+// that row, which then never returns as the maximum, and places it.
 __global__ void __launch_bounds__(256) subm_rank_kernel(const int4* __restrict__ coords, int64_t n,
                                                         SubmGeom g, const uint2* __restrict__ wr,
                                                         const int32_t* __restrict__ n_unique,
-                                                        uint2* col) {
+                                                        uint2* col, int32_t* n_extra) {
   const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (r >= n) return;
-  const bool unique = *n_unique == n;
+  const int32_t nu = *n_unique;
   const int4 c = coords[r];
   if (!in_grid(g, c.x, c.y, c.z, c.w)) return;
   const uint32_t cell = cell_key(g, c.x, c.y, c.z, c.w);
   const uint32_t rank = cell_rank(wr[cell >> 5], cell);
-  if (unique) {
-    col[rank] = make_uint2(static_cast<uint32_t>(r + 1), cell);
-  } else {
-    col[rank].y = cell;
-    atomicMax(&col[rank].x, static_cast<uint32_t>(r + 1));
+  const uint32_t me = static_cast<uint32_t>(r + 1);
+  if (nu == n) {
+    col[rank] = make_uint2(me, cell);
+    return;
   }
-}
-
-// Columns of repeated coordinates: a row whose cell's last row is another
-// row gets a column after the n_unique cell columns (in no particular order;
-// the values computed for it do not depend on where it sits).  Nothing to do
-// when every row has a cell of its own.
-// A grid-stride loop over few blocks: when every cell has one row (the usual
-// case) the launch only reads n_unique, and a small grid makes that cheap.
-__global__ void __launch_bounds__(256) subm_place_kernel(const int4* __restrict__ coords, int64_t n,
-                                                         SubmGeom g, const uint2* __restrict__ wr,
-                                                         const int32_t* __restrict__ n_unique,
-                                                         uint2* col_e, int32_t* n_extra) {
-  const int32_t nu = *n_unique;
-  if (nu == n) return;
-  for (int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; r < n;
-       r += (int64_t)gridDim.x * blockDim.x) {
-    const int4 c = coords[r];
-    if (!in_grid(g, c.x, c.y, c.z, c.w)) continue;
-    const uint32_t cell = cell_key(g, c.x, c.y, c.z, c.w);
-    const uint32_t rank = cell_rank(wr[cell >> 5], cell);
-    if (col_e[rank].x != static_cast<uint32_t>(r + 1)) {
-      const int32_t c2 = nu + atomicAdd(n_extra, 1);  // < rows in the grid <= n
-      col_e[c2] = make_uint2(static_cast<uint32_t>(r + 1), cell);
-    }
-  }
+  col[rank].y = cell;
+  const uint32_t old = atomicMax(&col[rank].x, me);
+  if (old == 0u) return;                   // the first row of its cell so far
+  const uint32_t loser = old > me ? me : old;
+  const int32_t c2 = nu + atomicAdd(n_extra, 1);  // < rows in the grid <= n
+  col[c2] = make_uint2(loser, cell);
 }
 
 // Per-slot hit counts of the probes: per wave by ballot, per block in LDS.
@@ -908,11 +894,9 @@ int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
     TSC_LAUNCH_CHECK("subm_mark");
     if (raster) *raster = 1;
     if ((rc = bitmap_scan(w.wr, nw, w.scan, w.n_unique, s, w.bytes, nullptr, started))) return rc;
-    subm_rank_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, w.col);
+    subm_rank_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, w.col,
+                                                      w.n_extra);
     TSC_LAUNCH_CHECK("subm_rank");
-    subm_place_kernel<<<static_cast<unsigned>(std::min<int64_t>(ceil_div(n, 256), 128)), 256, 0,
-                        s>>>(c4, n, g, w.wr, w.n_unique, w.col, w.n_extra);
-    TSC_LAUNCH_CHECK("subm_place");
     // slots from 64 on are added into the per-block table, which starts at 0
     if (K > 64 &&
         (rc = fill_u32(reinterpret_cast<uint32_t*>(blk_cnt), (int64_t)nblk * K, 0u, s)))

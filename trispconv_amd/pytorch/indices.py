@@ -14,6 +14,7 @@ they make (their output count), submanifold builds on its first access.
 from __future__ import annotations
 
 import ctypes
+import functools
 from typing import Callable, List, Optional, Sequence, Tuple
 
 import torch
@@ -391,7 +392,9 @@ def _coords(indices: torch.Tensor, what: str) -> torch.Tensor:
     L.require_gpu(indices, what)
     if indices.ndim != 2 or indices.shape[1] != 4:
         raise ValueError(f"{what}: indices must be (N, 4) (b, z, y, x), got {tuple(indices.shape)}")
-    coords = indices.to(torch.int32).contiguous()
+    coords = indices
+    if coords.dtype != torch.int32 or not coords.is_contiguous():
+        coords = indices.to(torch.int32).contiguous()
     if coords.data_ptr() % 16:
         coords = coords.clone()  # the kernels read each row as one 16-byte vector
     return coords
@@ -483,44 +486,64 @@ def generate_subm_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size:
     n = coords.shape[0]
     dev = coords.device
     lib = L.lib()
-    ws_bytes = lib.tsc_subm_workspace_bytes(n, K, int(batch_size), L.i3(shape))
-    if ws_bytes < 0:
+    sz = _subm_sizes(n, K, int(batch_size), shape, ks, dil)
+    if sz.ws_bytes < 0:
         raise ValueError(f"generate_subm_indice_pairs: invalid batch size {batch_size} or "
                          f"spatial shape {shape}")
-    ws = L.workspace(ws_bytes, dev)
-    # The map by columns (in (b,z,y,x) order when the bitmap path runs; the
-    # reference's pair lists are derived from it on first access), the column
-    # -> row table, the counts and the probe's per-(slot, block) counts: one
-    # allocation, 256-byte aligned views.
-    n_al = _align64(max(n, 1))
-    nb = int(lib.tsc_subm_slot_blocks_len(n, K))
-    tables = torch.empty(n_al + _align64(K * n) + _align64(K + 2) + nb, dtype=torch.int32,
-                         device=dev)
-    cols_row = tables[:n]
-    map_cols = tables[n_al:n_al + K * n].view(K, n)
-    counts = tables[n_al + _align64(K * n):][:K + 2]
-    slot_blocks = tables[n_al + _align64(K * n) + _align64(K + 2):]
+    # The workspace, and one allocation for the map by columns (in (b,z,y,x)
+    # order when the bitmap path runs; the reference's pair lists are derived
+    # from it on first access), the column -> row table, the counts and the
+    # probe's per-(slot, block) counts, at 256-byte aligned offsets.  Only
+    # raw addresses are made before the launch; the views after it, while the
+    # GPU works.
+    ws = L.workspace(sz.ws_bytes, dev)
+    tables = torch.empty(sz.words, dtype=torch.int32, device=dev)
+    base = tables.data_ptr()
+    stream = L.stream_of(coords)
+    result = (ctypes.c_int32 * 2)()
     # Returns once the coordinates are checked (a row outside the grid raises
     # here, as in the reference); the map is still being built on the stream,
     # and the per-slot counts are summed and read only when pair_num is.
-    stream = L.stream_of(coords)
-    result = (ctypes.c_int32 * 2)()
-    L.check(lib.tsc_subm_pairs_checked(coords.data_ptr(), n, int(batch_size), L.i3(shape),
-                                       L.i3(ks), L.i3(dil), ws.data_ptr(), ws.numel(),
-                                       cols_row.data_ptr(), map_cols.data_ptr(),
-                                       counts.data_ptr(), slot_blocks.data_ptr(), result, stream),
+    L.check(lib.tsc_subm_pairs_checked(coords.data_ptr(), n, int(batch_size), sz.shape, sz.ks,
+                                       sz.dil, ws.data_ptr(), sz.ws_bytes, base,
+                                       base + 4 * sz.o_map, base + 4 * sz.o_counts,
+                                       base + 4 * sz.o_blocks, result, stream),
             "generate_subm_indice_pairs")
     _raise_status(int(result[0]), "generate_subm_indice_pairs")
+    cols_row = tables[:n]
+    map_cols = tables[sz.o_map:sz.o_map + K * n].view(K, n)
+    counts = tables[sz.o_counts:sz.o_counts + K + 2]
+    slot_blocks = tables[sz.o_blocks:]
     d = IndiceData._from_tables(
         out_indices=indices, input_indices=indices, input_spatial_shape=spatial_shape,
         output_spatial_shape=spatial_shape, kernel_size=ks, stride=(1, 1, 1),
         padding=(0, 0, 0), dilation=dil, subm=True, pin=None, pout=None, cnt_dev=None,
         pair_num=None, nbr=None, batch_size=int(batch_size), map_cols=map_cols,
         cols_row=cols_row)
-
     d._counts_pending = (counts, K, lambda: _counts_to_host(counts, K, stream, slot_blocks, n))
     d._raster = bool(result[1])
     return d
+
+
+class _SubmSizes:
+    """Sizes and ABI arguments of a submanifold build of one shape."""
+
+    def __init__(self, n, K, batch_size, shape, ks, dil):
+        lib = L.lib()
+        self.shape, self.ks, self.dil = L.i3(shape), L.i3(ks), L.i3(dil)
+        self.ws_bytes = int(lib.tsc_subm_workspace_bytes(n, K, batch_size, self.shape))
+        n_al = _align64(max(n, 1))
+        self.o_map = n_al
+        self.o_counts = n_al + _align64(K * n)
+        self.o_blocks = self.o_counts + _align64(K + 2)
+        self.words = self.o_blocks + int(lib.tsc_subm_slot_blocks_len(n, K))
+
+
+# The ctypes argument arrays are only read during a call, so one set serves
+# every build of a shape (a network builds the same shapes every pass).
+@functools.lru_cache(maxsize=64)
+def _subm_sizes(n, K, batch_size, shape, ks, dil) -> _SubmSizes:
+    return _SubmSizes(n, K, batch_size, shape, ks, dil)
 
 
 def generate_strided_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size: int,
