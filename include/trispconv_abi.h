@@ -171,7 +171,10 @@ TSC_API int tsc_pairs_from_map(const int32_t* nbr, int64_t n, int32_t k_vol, int
  *   tsc_subm_pairs_from_bitmap can build on.
  *   fill:  out_coords [n_out][4] sorted by (b,z,y,x); nbr [K][n_out];
  *          pairs_in/pairs_out [K][n] (slot k: input rows ascending, output
- *          rank of each).  The workspace must be the one `count` filled.
+ *          rank of each); in_ids [n] (may be null): each input row's id
+ *          among the rows with a pair (ascending), -1 for the others, which
+ *          tsc_inverse_fill_ids takes.  The workspace must be the one
+ *          `count` filled.
  * ------------------------------------------------------------------------ */
 TSC_API int64_t tsc_strided_workspace_bytes(int64_t n, int32_t k_vol, int32_t batch_size,
                                     const int32_t out_spatial[3] /* host */);
@@ -185,7 +188,7 @@ TSC_API int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_siz
                      const int32_t padding[3], const int32_t dilation[3],
                      const int32_t out_spatial[3], void* ws, int64_t ws_bytes, int64_t n_out,
                      int32_t* out_coords, int32_t* nbr, int32_t* pairs_in, int32_t* pairs_out,
-                     tsc_stream_t stream);
+                     int32_t* in_ids, tsc_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Inverse pairs.  Replaces the pair swap of SparseInverseConv3d
@@ -206,6 +209,15 @@ TSC_API int tsc_inverse_fill(const int32_t* fwd_pairs_in, const int32_t* fwd_pai
                      const int32_t* fwd_in_coords, int64_t n_fwd_in, void* ws, int64_t ws_bytes,
                      int64_t n_out, int32_t* out_coords, int32_t* nbr, int32_t* inv_pairs_out,
                      tsc_stream_t stream);
+/* The fill, for a forward built by tsc_strided_fill with in_ids: its ids
+ * are the compact ids that the count phase derives (n_out = that build's
+ * counts[K+2]), so neither the count nor a workspace is needed.  Same
+ * outputs as tsc_inverse_fill. */
+TSC_API int tsc_inverse_fill_ids(const int32_t* fwd_pairs_in, const int32_t* fwd_pairs_out,
+                                 const int32_t* fwd_counts, int32_t k_vol, int64_t cap,
+                                 const int32_t* in_ids, const int32_t* fwd_in_coords,
+                                 int64_t n_fwd_in, int64_t n_out, int32_t* out_coords,
+                                 int32_t* nbr, int32_t* inv_pairs_out, tsc_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Execution order for the convolution: output rows in spatial order, cut into

@@ -267,3 +267,142 @@ def test_bitmap_build_flags_rows_that_are_not_its_cells():
     host = counts.cpu()
     assert int(host[27]) & L.FLAG_ROWS_NOT_BITMAP
     assert int(nbr.max()) < n
+
+
+def _map_by_rows(lib, L, nbr_cols, cols_row, n, K):
+    """A column map in row order (tsc_map_to_rows): comparable across builds
+    that place the columns of repeated coordinates in different orders."""
+    rows = torch.full((K, n), -7, dtype=torch.int32, device=DEV)
+    L.check(lib.tsc_map_to_rows(nbr_cols.data_ptr(), cols_row.data_ptr(), n, n, K, rows.data_ptr(),
+                                L.stream_of(rows)), "map_to_rows")
+    return rows
+
+
+@pytest.mark.parametrize("shape,dups,what", [((20, 24, 28), 0, "bitmap"),
+                                             ((20, 24, 28), 300, "bitmap, repeats"),
+                                             ((640, 320, 200), 300, "hash, repeats")])
+def test_checked_build_matches_the_plain_build(shape, dups, what):
+    """tsc_subm_pairs_checked (returns at the coordinate check; counts summed
+    by tsc_subm_counts) against tsc_subm_pairs, through the C ABI: the same
+    map row by row, the same counts, status and column order."""
+    import ctypes
+
+    from trispconv_amd import _lib as L
+    lib = L.lib()
+    B, K = 2, 27
+    idx = _clustered_with_duplicates(7, shape, B, 3000, 16, dups)
+    say("checked vs plain subm build:", what, idx.shape)
+    c = torch.from_numpy(idx).to(DEV)
+    n = len(idx)
+    args = (L.i3(shape), L.i3((3, 3, 3)), L.i3((1, 1, 1)))
+    ws_bytes = lib.tsc_subm_workspace_bytes(n, K, B, args[0])
+    out = {}
+    for mode in ("plain", "checked"):
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+        cols = torch.empty(n, dtype=torch.int32, device=DEV)
+        nbr = torch.empty((K, n), dtype=torch.int32, device=DEV)
+        counts = torch.full((K + 2,), -5, dtype=torch.int32, device=DEV)
+        s = L.stream_of(c)
+        if mode == "plain":
+            L.check(lib.tsc_subm_pairs(c.data_ptr(), n, B, *args, ws.data_ptr(), ws_bytes,
+                                       cols.data_ptr(), nbr.data_ptr(), counts.data_ptr(), s),
+                    "plain")
+            host = counts.cpu().tolist()
+        else:
+            blocks = torch.empty(lib.tsc_subm_slot_blocks_len(n, K), dtype=torch.int32, device=DEV)
+            result = (ctypes.c_int32 * 2)()
+            L.check(lib.tsc_subm_pairs_checked(c.data_ptr(), n, B, *args, ws.data_ptr(), ws_bytes,
+                                               cols.data_ptr(), nbr.data_ptr(), counts.data_ptr(),
+                                               blocks.data_ptr(), result, s), "checked")
+            assert result[0] == 0, what
+            h = (ctypes.c_int32 * (K + 2))()
+            L.check(lib.tsc_subm_counts(blocks.data_ptr(), n, K, counts.data_ptr(), h, s),
+                    "counts")
+            host = list(h)
+            assert counts.cpu().tolist() == host, f"{what}: device and host counts"
+            assert result[1] == host[K + 1], f"{what}: column order flag"
+        out[mode] = (host, _map_by_rows(lib, L, nbr, cols, n, K).cpu())
+    assert out["plain"][0] == out["checked"][0], f"{what}: counts"
+    assert torch.equal(out["plain"][1], out["checked"][1]), f"{what}: map"
+    exp = OP.subm_pairs(idx, shape, B, 3, 1)
+    assert out["checked"][0][:K] == exp.pair_num.tolist(), f"{what}: counts vs oracle"
+
+
+def test_checked_build_reports_bad_coordinates():
+    """The early check reports a row outside the grid (and which kind) before
+    the build's kernels have finished; the Python build raises IndexError."""
+    import ctypes
+
+    from trispconv_amd import _lib as L
+    lib = L.lib()
+    shape, K = (8, 8, 8), 27
+    for bad, flag in (([0, 8, 1, 1], L.FLAG_COORD_OUT_OF_GRID),
+                      ([3, 1, 1, 1], L.FLAG_BATCH_OUT_OF_RANGE)):
+        idx = np.array([[0, 1, 1, 1], [0, 2, 2, 2], bad, [0, 1, 2, 1]], np.int32)
+        say("checked build, bad row:", bad)
+        c = torch.from_numpy(idx).to(DEV)
+        n = len(idx)
+        args = (L.i3(shape), L.i3((3, 3, 3)), L.i3((1, 1, 1)))
+        ws_bytes = lib.tsc_subm_workspace_bytes(n, K, 1, args[0])
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
+        cols = torch.empty(n, dtype=torch.int32, device=DEV)
+        nbr = torch.empty((K, n), dtype=torch.int32, device=DEV)
+        counts = torch.empty(K + 2, dtype=torch.int32, device=DEV)
+        blocks = torch.empty(lib.tsc_subm_slot_blocks_len(n, K), dtype=torch.int32, device=DEV)
+        result = (ctypes.c_int32 * 2)()
+        L.check(lib.tsc_subm_pairs_checked(c.data_ptr(), n, 1, *args, ws.data_ptr(), ws_bytes,
+                                           cols.data_ptr(), nbr.data_ptr(), counts.data_ptr(),
+                                           blocks.data_ptr(), result, L.stream_of(c)), "checked")
+        assert result[0] == flag, bad
+        with pytest.raises(IndexError):
+            generate_subm_indice_pairs(c, shape, 1, 3, 1)
+    torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("name", ["inverse_blob4x150k", "strided64_lidar2x200k"])
+def test_inverse_from_forward_ids_matches_the_counted_inverse(name):
+    """tsc_inverse_fill_ids (the ids the strided fill wrote) against
+    tsc_inverse_count + tsc_inverse_fill, through the C ABI, on a reduced
+    workload: out_coords, the map and the remapped ids bit for bit."""
+    from trispconv_amd import _lib as L
+    lib = L.lib()
+    w = workloads.make_workload(name, scale=0.05)
+    lay = w.layers[0]
+    say("inverse from forward ids:", name, w.indices.shape)
+    x = torch.from_numpy(w.indices).to(DEV)
+    fwd = generate_strided_indice_pairs(x, w.spatial_shape, w.batch_size, lay["kernel_size"],
+                                        lay["stride"], lay["padding"], lay["dilation"])
+    assert fwd._in_ids is not None
+    K, cap, n_in = fwd.K, fwd._pin.shape[1], len(w.indices)
+    s = L.stream_of(x)
+    ws = torch.empty(lib.tsc_inverse_workspace_bytes(n_in), dtype=torch.uint8, device=DEV)
+    counts = torch.empty(1, dtype=torch.int32, device=DEV)
+    L.check(lib.tsc_inverse_count(fwd._pin.data_ptr(), fwd._cnt.data_ptr(), K, cap, n_in,
+                                  ws.data_ptr(), ws.numel(), counts.data_ptr(), s), "count")
+    n_out = int(counts.cpu()[0])
+    assert n_out == fwd._n_in_paired
+    ids = fwd._in_ids.cpu().numpy()
+    assert int((ids >= 0).sum()) == n_out
+    assert np.array_equal(ids[ids >= 0], np.arange(n_out)), "ids ascend with the rows"
+    res = {}
+    for mode in ("count", "ids"):
+        oc = torch.empty((n_out, 4), dtype=torch.int32, device=DEV)
+        nbr = torch.empty((K, n_out), dtype=torch.int32, device=DEV)
+        ipo = torch.full((K, cap), -9, dtype=torch.int32, device=DEV)
+        if mode == "count":
+            L.check(lib.tsc_inverse_fill(fwd._pin.data_ptr(), fwd._pout.data_ptr(),
+                                         fwd._cnt.data_ptr(), K, cap, x.data_ptr(), n_in,
+                                         ws.data_ptr(), ws.numel(), n_out, oc.data_ptr(),
+                                         nbr.data_ptr(), ipo.data_ptr(), s), "fill")
+        else:
+            L.check(lib.tsc_inverse_fill_ids(fwd._pin.data_ptr(), fwd._pout.data_ptr(),
+                                             fwd._cnt.data_ptr(), K, cap, fwd._in_ids.data_ptr(),
+                                             x.data_ptr(), n_in, n_out, oc.data_ptr(),
+                                             nbr.data_ptr(), ipo.data_ptr(), s), "fill_ids")
+        res[mode] = (oc.cpu(), nbr.cpu(), ipo.cpu())
+    pn = fwd.pair_num.tolist()
+    for a, b, what in zip(res["count"], res["ids"], ("out_coords", "map", "ids")):
+        if what == "ids":  # only each slot's first pair_num[k] entries are written
+            a = torch.cat([a[k, :pn[k]] for k in range(K)])
+            b = torch.cat([b[k, :pn[k]] for k in range(K)])
+        assert torch.equal(a, b), f"{name}: {what}"

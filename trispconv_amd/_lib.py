@@ -51,11 +51,13 @@ _SIGNATURES = {
     "tsc_strided_count": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, c_i32p, c_i32p,
                                          c_i32p, _vp, _i64, _vp, _vp]),
     "tsc_strided_fill": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, c_i32p, c_i32p,
-                                        c_i32p, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp]),
+                                        c_i32p, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
     "tsc_inverse_workspace_bytes": (_i64, [_i64]),
     "tsc_inverse_count": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i64, _vp, _i64, _vp, _vp]),
     "tsc_inverse_fill": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i64, _vp, _i64, _vp, _i64, _i64,
                                         _vp, _vp, _vp, _vp]),
+    "tsc_inverse_fill_ids": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i64, _vp, _vp, _i64, _i64, _vp,
+                                            _vp, _vp, _vp]),
     "tsc_plan_workspace_bytes": (_i64, [_i64, _i32]),
     "tsc_conv_plan": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i64, _i32, _i32, c_i32p, _i64, _vp,
                                      _i64, _vp, _vp, _vp]),

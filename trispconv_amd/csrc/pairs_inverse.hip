@@ -13,6 +13,8 @@
 // neighbour map and the gathered output coordinates.
 #include "common.hpp"
 
+#include <algorithm>
+
 namespace tsc {
 namespace {
 
@@ -49,6 +51,27 @@ __global__ void __launch_bounds__(256) inverse_fill_kernel(const int32_t* __rest
   const int32_t o = static_cast<int32_t>(id_map[fwd_pin[e]]);
   inv_pout[e] = o;
   if (o < n_out) nbr[(int64_t)k * n_out + o] = fwd_pout[e];  // holds by construction
+}
+
+// The fill's first launch for ids made by the forward build: blocks below
+// emit_blocks write out_coords[id] = the row's coordinates for the rows with
+// an id; the others fill the map with -1.
+__global__ void __launch_bounds__(256) inverse_emit_ids_kernel(const int32_t* __restrict__ in_ids,
+                                                               const int4* __restrict__ in_coords,
+                                                               int64_t n, int4* __restrict__ out_coords,
+                                                               int64_t n_out, int emit_blocks,
+                                                               uint32_t* __restrict__ nbr,
+                                                               int64_t nbr_words) {
+  if (static_cast<int>(blockIdx.x) >= emit_blocks) {
+    for (int64_t j = (blockIdx.x - emit_blocks) * (int64_t)blockDim.x + threadIdx.x; j < nbr_words;
+         j += (int64_t)(gridDim.x - emit_blocks) * blockDim.x)
+      nbr[j] = 0xffffffffu;
+    return;
+  }
+  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int32_t id = in_ids[i];
+  if (id >= 0 && id < n_out) out_coords[id] = in_coords[i];  // id < n_out holds by construction
 }
 
 struct Buffers {
@@ -128,6 +151,39 @@ extern "C" int tsc_inverse_fill(const int32_t* fwd_pairs_in, const int32_t* fwd_
   dim3 grid(static_cast<unsigned>(ceil_div(cap, 256)), static_cast<unsigned>(k_vol));
   inverse_fill_kernel<<<grid, 256, 0, s>>>(fwd_pairs_in, fwd_pairs_out, fwd_counts, cap, k_vol,
                                            n_out, b.id_map, nbr, inv_pairs_out);
+  TSC_LAUNCH_CHECK("inverse_fill");
+  return 0;
+}
+
+extern "C" int tsc_inverse_fill_ids(const int32_t* fwd_pairs_in, const int32_t* fwd_pairs_out,
+                                    const int32_t* fwd_counts, int32_t k_vol, int64_t cap,
+                                    const int32_t* in_ids, const int32_t* fwd_in_coords,
+                                    int64_t n_fwd_in, int64_t n_out, int32_t* out_coords,
+                                    int32_t* nbr, int32_t* inv_pairs_out, tsc_stream_t stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  TSC_REQUIRE(k_vol > 0 && k_vol <= 65535, "inverse: invalid kernel volume %d", k_vol);
+  TSC_REQUIRE(n_fwd_in >= 0 && n_fwd_in < (int64_t(1) << 31) && cap >= n_fwd_in && n_out >= 0 &&
+                  n_out <= n_fwd_in,
+              "inverse: invalid sizes");
+  if (n_out == 0) return 0;
+  TSC_REQUIRE(fwd_pairs_in && fwd_pairs_out && fwd_counts && in_ids && fwd_in_coords &&
+                  out_coords && nbr && inv_pairs_out,
+              "inverse: null pointer");
+  const int emit_blocks = static_cast<int>(ceil_div(n_fwd_in, 256));
+  const int64_t nbr_words = n_out * k_vol;
+  const int fill_blocks =
+      static_cast<int>(std::min<int64_t>(std::max<int64_t>(ceil_div(nbr_words, 256), 1), 4096));
+  inverse_emit_ids_kernel<<<emit_blocks + fill_blocks, 256, 0, s>>>(
+      in_ids, reinterpret_cast<const int4*>(fwd_in_coords), n_fwd_in,
+      reinterpret_cast<int4*>(out_coords), n_out, emit_blocks, reinterpret_cast<uint32_t*>(nbr),
+      nbr_words);
+  TSC_LAUNCH_CHECK("inverse_emit_ids");
+  // every row a forward pair names has an id (it has that pair), so the ids
+  // read through pairs_in are never -1
+  dim3 grid(static_cast<unsigned>(ceil_div(cap, 256)), static_cast<unsigned>(k_vol));
+  inverse_fill_kernel<<<grid, 256, 0, s>>>(fwd_pairs_in, fwd_pairs_out, fwd_counts, cap, k_vol,
+                                           n_out, reinterpret_cast<const uint32_t*>(in_ids), nbr,
+                                           inv_pairs_out);
   TSC_LAUNCH_CHECK("inverse_fill");
   return 0;
 }

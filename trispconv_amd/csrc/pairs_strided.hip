@@ -246,8 +246,10 @@ __global__ void __launch_bounds__(kRows) strided_fill_kernel(const int4* __restr
                                                              int nblk, int64_t cap, int64_t n_out,
                                                              int32_t* __restrict__ nbr,
                                                              int32_t* __restrict__ pairs_in,
-                                                             int32_t* __restrict__ pairs_out) {
+                                                             int32_t* __restrict__ pairs_out,
+                                                             int32_t* __restrict__ in_ids) {
   __shared__ int32_t s_wcnt[kRows / kWave][64];
+  __shared__ int32_t s_paired[kRows / kWave];
   const int t = threadIdx.x;
   const int w = t / kWave;
   const int64_t i = blockIdx.x * (int64_t)kRows + t;
@@ -256,6 +258,20 @@ __global__ void __launch_bounds__(kRows) strided_fill_kernel(const int4* __restr
   const bool ok = valid && c.x >= 0 && c.x < g.B;
   const Cands<KZ, KY, KX> cand(g, c, ok);
   constexpr int KC = KZ * KY * KX;
+  if (in_ids) {
+    // The row's id among the input rows with a pair (the inverse's output
+    // rows, in ascending row order): the mark counted them per block into
+    // row K of the count table, whose scan gives each block's first id.
+    bool any = false;
+#pragma unroll
+    for (int k = 0; k < (KC ? KC : K); ++k) any |= cand.cell(g, k) >= 0;
+    const uint64_t with_pairs = __ballot(any);
+    if (__lane_id() == 0) s_paired[w] = static_cast<int32_t>(__popcll(with_pairs));
+    __syncthreads();
+    int32_t id = blk_off[(int64_t)K * nblk + blockIdx.x];
+    for (int ww = 0; ww < w; ++ww) id += s_paired[ww];
+    if (valid) in_ids[i] = any ? id + rank_in_wave(with_pairs) : -1;
+  }
   if constexpr (KC > 0 && KC <= 64) {
     // Fixed kernel shape: every slot's bitmap entry is loaded before any is
     // used (one straight-line batch of loads, no branch per slot), then the
@@ -402,9 +418,9 @@ template <int KZ, int KY, int KX>
 struct LaunchFill {
   static int run(const int4* c, int64_t n, int K, StridedGeom g, const uint2* wr,
                  const int32_t* blk_off, int nblk, int64_t cap, int64_t n_out, int32_t* nbr,
-                 int32_t* pin, int32_t* pout, hipStream_t s) {
+                 int32_t* pin, int32_t* pout, int32_t* in_ids, hipStream_t s) {
     strided_fill_kernel<KZ, KY, KX><<<nblk, kRows, 0, s>>>(c, n, K, g, wr, blk_off, nblk, cap,
-                                                           n_out, nbr, pin, pout);
+                                                           n_out, nbr, pin, pout, in_ids);
     TSC_LAUNCH_CHECK("strided_fill");
     return 0;
   }
@@ -488,7 +504,8 @@ extern "C" int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_
                                 const int32_t stride[3], const int32_t padding[3],
                                 const int32_t dilation[3], const int32_t out_spatial[3], void* ws,
                                 int64_t ws_bytes, int64_t n_out, int32_t* out_coords, int32_t* nbr,
-                                int32_t* pairs_in, int32_t* pairs_out, tsc_stream_t stream) {
+                                int32_t* pairs_in, int32_t* pairs_out, int32_t* in_ids,
+                                tsc_stream_t stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   StridedGeom g;
   int rc = check_geom(n, batch_size, spatial, ksize, stride, padding, dilation, out_spatial, &g);
@@ -499,6 +516,8 @@ extern "C" int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_
   carve(nullptr, L, K, &need);
   TSC_REQUIRE(ws && ws_bytes >= need, "strided: workspace too small");
   TSC_REQUIRE(n_out >= 0 && n_out <= L.cells, "strided: n_out=%lld invalid", (long long)n_out);
+  if (n > 0 && n_out == 0 && in_ids)  // no row has a pair
+    return fill_u32(reinterpret_cast<uint32_t*>(in_ids), n, 0xffffffffu, s);
   if (n == 0 || n_out == 0) return 0;
   TSC_REQUIRE(coords && out_coords && nbr && pairs_in && pairs_out, "strided: null pointer");
   Buffers b = carve(ws, L, K, nullptr);
@@ -512,5 +531,5 @@ extern "C" int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_
   TSC_LAUNCH_CHECK("strided_emit");
   return by_shape<LaunchFill>(g.ks, reinterpret_cast<const int4*>(coords), n, K, g,
                               static_cast<const uint2*>(b.wr), static_cast<const int32_t*>(b.blk_off),
-                              (int)L.nblk, n, n_out, nbr, pairs_in, pairs_out, s);
+                              (int)L.nblk, n, n_out, nbr, pairs_in, pairs_out, in_ids, s);
 }

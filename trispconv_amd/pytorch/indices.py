@@ -109,6 +109,9 @@ class IndiceData:
         # strided builds: input rows with at least one pair, i.e. the row
         # count of this layer's inverse, read with the build's counts
         self._n_in_paired: Optional[int] = None
+        # strided builds: each input row's id among the rows with a pair (-1
+        # for the others), the inverse's output ids
+        self._in_ids: Optional[torch.Tensor] = None
         # input rows the pairs may name: ids lie in [0, _in_bound) (the
         # builders' input rows; for user-assigned lists their largest id + 1)
         self._in_bound: Optional[int] = None
@@ -216,6 +219,7 @@ class IndiceData:
         self._nbr_ordered = None
         self._inverse_cache = None
         self._in_bound = None
+        self._in_ids = None
 
     # --------------------------------------------------- convolution inputs
     def neighbour_map(self, n_out: int, device, n_in: Optional[int] = None) -> torch.Tensor:
@@ -559,41 +563,61 @@ def generate_strided_indice_pairs(indices: torch.Tensor, spatial_shape, batch_si
     if min(out_shape) <= 0:
         raise ValueError(f"generate_strided_indice_pairs: empty output shape {out_shape}")
     lib = L.lib()
-    ws = L.workspace(lib.tsc_strided_workspace_bytes(n, K, int(batch_size), L.i3(out_shape)), dev)
+    sz = _strided_sizes(n, int(batch_size), shape, ks, st, pd, dil, out_shape)
+    ws = L.workspace(sz.ws_bytes, dev)
     counts = torch.empty(K + 3, dtype=torch.int32, device=dev)
-    geo = (L.i3(shape), L.i3(ks), L.i3(st), L.i3(pd), L.i3(dil), L.i3(out_shape))
     stream = L.stream_of(coords)
-    L.check(lib.tsc_strided_count(coords.data_ptr(), n, int(batch_size), *geo, ws.data_ptr(),
-                                  ws.numel(), counts.data_ptr(), stream),
+    L.check(lib.tsc_strided_count(coords.data_ptr(), n, int(batch_size), *sz.geo, ws.data_ptr(),
+                                  sz.ws_bytes, counts.data_ptr(), stream),
             "generate_strided_indice_pairs")
     host = counts.cpu()
     _raise_status(int(host[K + 1]), "generate_strided_indice_pairs")
     n_out = int(host[K])
     # the output coordinates (the next tensor's indices, with their own
     # storage and version counter); the map and the two pair tables in one
-    # allocation, 256-byte aligned views
+    # allocation at 256-byte aligned offsets, passed as raw addresses, the
+    # views made after the launch
     out_coords = torch.empty((n_out, 4), dtype=torch.int32, device=dev)
     o_pin = _align64(K * n_out)
     o_pout = o_pin + _align64(K * n)
-    tables = torch.empty(max(o_pout + K * n, 1), dtype=torch.int32, device=dev)
+    o_ids = o_pout + _align64(K * n)
+    tables = torch.empty(max(o_ids + n, 1), dtype=torch.int32, device=dev)
+    base = tables.data_ptr()
+    L.check(lib.tsc_strided_fill(coords.data_ptr(), n, int(batch_size), *sz.geo, ws.data_ptr(),
+                                 sz.ws_bytes, n_out, out_coords.data_ptr(), base,
+                                 base + 4 * o_pin, base + 4 * o_pout, base + 4 * o_ids, stream),
+            "generate_strided_indice_pairs")
     nbr = tables[:K * n_out].view(K, n_out)
     pin = tables[o_pin:o_pin + K * n].view(K, n)
     pout = tables[o_pout:o_pout + K * n].view(K, n)
-    L.check(lib.tsc_strided_fill(coords.data_ptr(), n, int(batch_size), *geo, ws.data_ptr(),
-                                 ws.numel(), n_out, out_coords.data_ptr(), nbr.data_ptr(),
-                                 pin.data_ptr(), pout.data_ptr(), stream),
-            "generate_strided_indice_pairs")
     data = IndiceData._from_tables(
         out_indices=out_coords, input_indices=indices, input_spatial_shape=shape,
         output_spatial_shape=out_shape, kernel_size=ks, stride=st, padding=pd, dilation=dil,
         subm=False, pin=pin, pout=pout, cnt_dev=counts[:K], pair_num=host[:K].long(), nbr=nbr,
         batch_size=int(batch_size), rows_raster=True)
     data._n_in_paired = int(host[K + 2])
-    cells = int(batch_size) * out_shape[0] * out_shape[1] * out_shape[2]
-    _STRIDED_BITMAPS[out_coords] = (ws, (cells + 31) // 32, tuple(out_shape), int(batch_size),
+    data._in_ids = tables[o_ids:o_ids + n]
+    _STRIDED_BITMAPS[out_coords] = (ws, sz.out_words, tuple(out_shape), int(batch_size),
                                     out_coords._version,
                                     (out_coords.data_ptr(), out_coords.storage_offset()))
     return data
+
+
+class _StridedSizes:
+    """Workspace size and ABI arguments of a strided build of one shape."""
+
+    def __init__(self, n, batch_size, shape, ks, st, pd, dil, out_shape):
+        K = ks[0] * ks[1] * ks[2]
+        self.geo = (L.i3(shape), L.i3(ks), L.i3(st), L.i3(pd), L.i3(dil), L.i3(out_shape))
+        self.ws_bytes = max(int(L.lib().tsc_strided_workspace_bytes(n, K, batch_size,
+                                                                      self.geo[5])), 1)
+        cells = batch_size * out_shape[0] * out_shape[1] * out_shape[2]
+        self.out_words = (cells + 31) // 32
+
+
+@functools.lru_cache(maxsize=64)
+def _strided_sizes(n, batch_size, shape, ks, st, pd, dil, out_shape) -> _StridedSizes:
+    return _StridedSizes(n, batch_size, shape, ks, st, pd, dil, out_shape)
 
 
 def generate_inverse_indice_pairs(fwd: IndiceData) -> IndiceData:
@@ -616,24 +640,38 @@ def generate_inverse_indice_pairs(fwd: IndiceData) -> IndiceData:
     cap = fwd._pin.shape[1]
     n_in = len(fwd.input_indices)
     lib = L.lib()
-    ws = L.workspace(lib.tsc_inverse_workspace_bytes(n_in), dev)
-    counts = torch.empty(1, dtype=torch.int32, device=dev)
     stream = L.stream_of(fwd._pin)
-    L.check(lib.tsc_inverse_count(fwd._pin.data_ptr(), fwd._cnt.data_ptr(), K, cap, n_in,
-                                  ws.data_ptr(), ws.numel(), counts.data_ptr(), stream),
-            "inverse pairs")
-    # a forward built here counted its paired input rows with its own pair
-    # counts, so the inverse needs no host read of its own
-    n_out = fwd._n_in_paired if (fwd._n_in_paired is not None and not from_lists) \
-        else int(counts.cpu()[0])
     in_coords = _coords(fwd.input_indices, "inverse pairs")
-    out_coords = torch.empty((n_out, 4), dtype=torch.int32, device=dev)
-    nbr = torch.empty((K, n_out), dtype=torch.int32, device=dev)
-    inv_pout = torch.empty((K, cap), dtype=torch.int32, device=dev)
-    L.check(lib.tsc_inverse_fill(fwd._pin.data_ptr(), fwd._pout.data_ptr(), fwd._cnt.data_ptr(), K,
-                                 cap, in_coords.data_ptr(), n_in, ws.data_ptr(), ws.numel(), n_out,
-                                 out_coords.data_ptr(), nbr.data_ptr(), inv_pout.data_ptr(),
-                                 stream), "inverse pairs")
+    if fwd._in_ids is not None and fwd._n_in_paired is not None and not from_lists:
+        # a forward built here: its fill gave every input row its output id
+        # and its count read gave the row count, so the inverse is one fill
+        n_out = fwd._n_in_paired
+        out_coords = torch.empty((n_out, 4), dtype=torch.int32, device=dev)
+        nbr = torch.empty((K, n_out), dtype=torch.int32, device=dev)
+        inv_pout = torch.empty((K, cap), dtype=torch.int32, device=dev)
+        L.check(lib.tsc_inverse_fill_ids(fwd._pin.data_ptr(), fwd._pout.data_ptr(),
+                                         fwd._cnt.data_ptr(), K, cap, fwd._in_ids.data_ptr(),
+                                         in_coords.data_ptr(), n_in, n_out, out_coords.data_ptr(),
+                                         nbr.data_ptr(), inv_pout.data_ptr(), stream),
+                "inverse pairs")
+    else:
+        ws = L.workspace(lib.tsc_inverse_workspace_bytes(n_in), dev)
+        counts = torch.empty(1, dtype=torch.int32, device=dev)
+        L.check(lib.tsc_inverse_count(fwd._pin.data_ptr(), fwd._cnt.data_ptr(), K, cap, n_in,
+                                      ws.data_ptr(), ws.numel(), counts.data_ptr(), stream),
+                "inverse pairs")
+        # a forward built here counted its paired input rows with its own
+        # pair counts, so the inverse needs no host read of its own
+        n_out = fwd._n_in_paired if (fwd._n_in_paired is not None and not from_lists) \
+            else int(counts.cpu()[0])
+        out_coords = torch.empty((n_out, 4), dtype=torch.int32, device=dev)
+        nbr = torch.empty((K, n_out), dtype=torch.int32, device=dev)
+        inv_pout = torch.empty((K, cap), dtype=torch.int32, device=dev)
+        L.check(lib.tsc_inverse_fill(fwd._pin.data_ptr(), fwd._pout.data_ptr(),
+                                     fwd._cnt.data_ptr(), K, cap, in_coords.data_ptr(), n_in,
+                                     ws.data_ptr(), ws.numel(), n_out, out_coords.data_ptr(),
+                                     nbr.data_ptr(), inv_pout.data_ptr(), stream),
+                "inverse pairs")
     if from_lists:
         # the inverse writes output id_map[pairs_in[k]] through slot k: an
         # input row listed twice within a slot would need two entries
