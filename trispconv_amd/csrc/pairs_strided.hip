@@ -258,34 +258,34 @@ __global__ void __launch_bounds__(kRows) strided_fill_kernel(const int4* __restr
   const bool ok = valid && c.x >= 0 && c.x < g.B;
   const Cands<KZ, KY, KX> cand(g, c, ok);
   constexpr int KC = KZ * KY * KX;
-  if (in_ids) {
-    // The row's id among the input rows with a pair (the inverse's output
-    // rows, in ascending row order): the mark counted them per block into
-    // row K of the count table, whose scan gives each block's first id.
-    bool any = false;
-#pragma unroll
-    for (int k = 0; k < (KC ? KC : K); ++k) any |= cand.cell(g, k) >= 0;
-    const uint64_t with_pairs = __ballot(any);
-    if (__lane_id() == 0) s_paired[w] = static_cast<int32_t>(__popcll(with_pairs));
-    __syncthreads();
+  // The row's id among the input rows with a pair (the inverse's output
+  // rows, in ascending row order): the mark counted them per block into row
+  // K of the count table, whose scan gives each block's first id; within the
+  // block, waves in order, lanes by ballot.
+  auto write_id = [&](bool any, uint64_t with_pairs) {
     int32_t id = blk_off[(int64_t)K * nblk + blockIdx.x];
     for (int ww = 0; ww < w; ++ww) id += s_paired[ww];
     if (valid) in_ids[i] = any ? id + rank_in_wave(with_pairs) : -1;
-  }
+  };
   if constexpr (KC > 0 && KC <= 64) {
     // Fixed kernel shape: every slot's bitmap entry is loaded before any is
     // used (one straight-line batch of loads, no branch per slot), then the
     // ranks and the stores.
     int64_t cell[KC];
     uint2 e[KC];
+    bool any = false;
 #pragma unroll
     for (int k = 0; k < KC; ++k) {
       cell[k] = cand.cell(g, k);
+      any |= cell[k] >= 0;
       const uint64_t hits = __ballot(cell[k] >= 0);
       if (__lane_id() == 0) s_wcnt[w][k] = __popcll(hits);
       e[k] = wr[cell[k] >= 0 ? cell[k] >> 5 : 0];  // entry 0 exists
     }
+    const uint64_t with_pairs = __ballot(any);
+    if (__lane_id() == 0) s_paired[w] = static_cast<int32_t>(__popcll(with_pairs));
     __syncthreads();
+    if (in_ids) write_id(any, with_pairs);
     // s_wcnt[w][k] becomes the block offset of wave w's slot-k pairs
     if (t < KC) {
       int run = blk_off[(int64_t)t * nblk + blockIdx.x];
@@ -315,6 +315,14 @@ __global__ void __launch_bounds__(kRows) strided_fill_kernel(const int4* __restr
     return;
   }
   const int KR = KC ? KC : K;
+  if (in_ids) {
+    bool any = false;
+    for (int k = 0; k < KR; ++k) any |= cand.cell(g, k) >= 0;
+    const uint64_t with_pairs = __ballot(any);
+    if (__lane_id() == 0) s_paired[w] = static_cast<int32_t>(__popcll(with_pairs));
+    __syncthreads();
+    write_id(any, with_pairs);
+  }
   for (int kb = 0; kb < KR; kb += 64) {
     const int kend = (KR - kb) < 64 ? (KR - kb) : 64;
 #pragma unroll
