@@ -1358,7 +1358,9 @@ __global__ void __launch_bounds__(256) conv_narrow_kernel(
   const int64_t pa = p0 + rl;  // processing position of this lane's A row
   const bool va = pa < n_out;
   const int32_t oa = va ? (order ? order[pa] : static_cast<int32_t>(pa)) : 0;
-  const int64_t col = nbr_ordered ? pa : oa;  // its column of the map
+  // its column of the map; lanes past the last row read column 0 (their
+  // loads are issued too, and then discarded)
+  const int64_t col = va ? (nbr_ordered ? pa : oa) : 0;
   const int nt_all = c_out / 16;
   const int nt0 = blockIdx.y * NT;
   uint64_t zero_addr = reinterpret_cast<uint64_t>(g_zero_row);
