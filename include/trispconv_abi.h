@@ -231,14 +231,19 @@ TSC_API int tsc_inverse_fill_ids(const int32_t* fwd_pairs_in, const int32_t* fwd
  *   otherwise they are put in Morton order of out_coords [n_out][4].
  *   order [n_out] receives the processing order (rows); nbr_ordered
  *   [K][n_out] (may be NULL) the map permuted into that order: entry (k, t)
- *   belongs to row order[t], so the convolution reads it contiguously.
+ *   belongs to row order[t], so the convolution reads it contiguously;
+ *   pos_masks [n_out] (may be NULL; K <= 32) the slot mask of each position
+ *   (bit k: row order[t] has a neighbour through slot k).  Placed right
+ *   after nbr_ordered (as its row K), it lets the convolution skip reading
+ *   every entry of a tile to learn which slots the tile uses
+ *   (nbr_ordered = 2 in tsc_conv_forward).
  * ------------------------------------------------------------------------ */
 TSC_API int64_t tsc_plan_workspace_bytes(int64_t n_out, int32_t k_vol);
 TSC_API int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_t raster,
                           const int32_t* out_coords, int64_t n_out, int32_t k_vol,
                           int32_t batch_size, const int32_t out_spatial[3] /* host */,
                           int64_t region_rows, void* ws, int64_t ws_bytes, int32_t* order,
-                          int32_t* nbr_ordered, tsc_stream_t stream);
+                          int32_t* nbr_ordered, int32_t* pos_masks, tsc_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Weights.  Replaces normalize_spconv_weight (trispconv/pytorch/weight.py:8-50)
@@ -269,7 +274,8 @@ TSC_API int tsc_pack_weight(const void* w, int32_t w_dtype, int32_t layout, int3
  *   nbr == NULL means the identity map with k_vol == 1 (1x1x1 layers).
  *   order == NULL means rows in index order.
  *   nbr_ordered != 0 means nbr is the plan's permuted map (entry (k, t)
- *   belongs to output row order[t]).
+ *   belongs to output row order[t]); 2 means its row K (nbr + K * n_out)
+ *   holds the plan's pos_masks as well (K <= 32).
  *   bias may be NULL; bias_dtype is its element type.
  * ------------------------------------------------------------------------ */
 TSC_API int tsc_conv_forward(const void* feat, int32_t dtype, int64_t n_in, int32_t c_in,

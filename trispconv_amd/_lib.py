@@ -60,7 +60,7 @@ _SIGNATURES = {
                                             _vp, _vp, _vp]),
     "tsc_plan_workspace_bytes": (_i64, [_i64, _i32]),
     "tsc_conv_plan": (ctypes.c_int, [_vp, _vp, _i32, _vp, _i64, _i32, _i32, c_i32p, _i64, _vp,
-                                     _i64, _vp, _vp, _vp]),
+                                     _i64, _vp, _vp, _vp, _vp]),
     "tsc_packed_weight_bytes": (_i64, [_i32, _i32, _i32, _i32]),
     "tsc_pack_weight": (ctypes.c_int, [_vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp, _vp]),
     "tsc_conv_forward": (ctypes.c_int, [_vp, _i32, _i64, _i32, _vp, _vp, _i32, _vp, _vp, _i32,

@@ -757,7 +757,13 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
       }
     };
     int32_t orow;
-    if (nbr_ordered) {
+    if (nbr_ordered == 2) {
+      // the plan's slot mask of each position follows the map as its row K
+      // (K <= 32): one word per row instead of all of its entries
+      const uint32_t pm = reinterpret_cast<const uint32_t*>(nbr)[(int64_t)K * n_out + (in ? tr : 0)];
+      orow = in ? order[tr] : -1;
+      m = orow >= 0 ? pm : 0u;
+    } else if (nbr_ordered) {
       issue(0, in ? tr : 0);
       orow = in ? (order ? order[tr] : static_cast<int32_t>(tr)) : -1;
     } else {
@@ -770,10 +776,12 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
       s_bias[t] = ep.bias ? load_param(ep.bias, ep.bias_dt, col) : 0.f;
       channel_affine(ep, col, s_scale[t], s_shift[t]);
     }
-    consume(0, orow);
-    for (int k0 = 32; k0 < K; k0 += 32) {
-      issue(k0, nbr_ordered ? (in ? tr : 0) : (orow >= 0 ? orow : 0));
-      consume(k0, orow);
+    if (nbr_ordered != 2) {
+      consume(0, orow);
+      for (int k0 = 32; k0 < K; k0 += 32) {
+        issue(k0, nbr_ordered ? (in ? tr : 0) : (orow >= 0 ? orow : 0));
+        consume(k0, orow);
+      }
     }
     uint32_t lo = static_cast<uint32_t>(m), hi = static_cast<uint32_t>(m >> 32);
 #pragma unroll
@@ -1766,6 +1774,9 @@ static int conv_forward(const void* feat, int32_t dtype, int64_t n_in, int32_t c
   TSC_REQUIRE(nbr || k_vol == 1, "conv: identity map needs k_vol == 1");
   TSC_REQUIRE(nbr || n_in >= n_out, "conv: identity map needs n_in >= n_out");
   TSC_REQUIRE(!nbr_ordered || (order && nbr), "conv: an ordered map needs its order");
+  TSC_REQUIRE(nbr_ordered >= 0 && nbr_ordered <= 2, "conv: nbr_ordered must be 0, 1 or 2");
+  TSC_REQUIRE(nbr_ordered != 2 || k_vol <= 32,
+              "conv: a map with its slot-mask row (nbr_ordered = 2) needs k_vol <= 32");
   const Path path = pick_path(dtype, c_in, c_out, k_vol);
   TSC_REQUIRE(column_tile == 0 || (path == kMfma && (column_tile == 32 || column_tile == 64 ||
                                                      column_tile == 128) &&

@@ -156,26 +156,31 @@ __global__ void __launch_bounds__(kConvTileRows) tile_key_kernel(
   }
 }
 
-// perm[i] = map column processed at position i; order[i] = its row.
-// Positions inside the first n_tiles full tiles come from tile tile_perm[i/256]
-// (when given); the rest stay where the sorts put them.
+// perm[i] = map column processed at position i; order[i] = its row;
+// pos_masks[i] (when given) = its slot mask.  Positions inside the first
+// n_tiles full tiles come from tile tile_perm[i/256] (when given); the rest
+// stay where the sorts put them.
 __global__ void __launch_bounds__(256) gather_rows_kernel(const uint32_t* __restrict__ pos,
                                                           const uint32_t* __restrict__ cols,
                                                           const int32_t* __restrict__ cols_row,
                                                           int64_t n,
                                                           const uint32_t* __restrict__ tile_perm,
                                                           int64_t n_tiles,
+                                                          const uint32_t* __restrict__ mask_pos,
                                                           uint32_t* __restrict__ perm,
-                                                          int32_t* __restrict__ order) {
+                                                          int32_t* __restrict__ order,
+                                                          uint32_t* __restrict__ pos_masks) {
   const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (i >= n) return;
   const int64_t tile = i / kConvTileRows;
   const int64_t src = (tile_perm && tile < n_tiles)
                           ? static_cast<int64_t>(tile_perm[tile]) * kConvTileRows + i % kConvTileRows
                           : i;
-  const uint32_t col = cols[pos[src]];
+  const uint32_t mp = pos[src];  // the column's Morton position
+  const uint32_t col = cols[mp];
   perm[i] = col;
   order[i] = cols_row ? cols_row[col] : static_cast<int32_t>(col);
+  if (pos_masks) pos_masks[i] = mask_pos[mp];
 }
 
 // nbr_ordered[k][t] = nbr[k][perm[t]], four positions per thread.  Blocks are
@@ -328,7 +333,7 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_
                              const int32_t* out_coords, int64_t n_out, int32_t k_vol,
                              int32_t batch_size, const int32_t out_spatial[3],
                              int64_t region_rows, void* ws, int64_t ws_bytes, int32_t* order,
-                             int32_t* nbr_ordered, tsc_stream_t stream) {
+                             int32_t* nbr_ordered, int32_t* pos_masks, tsc_stream_t stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   TSC_REQUIRE(n_out >= 0 && n_out < (int64_t(1) << 31), "plan: n_out out of range");
   TSC_REQUIRE(k_vol > 0 && batch_size > 0, "plan: invalid kernel volume or batch size");
@@ -339,6 +344,7 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_
   if (n_out == 0) return 0;
   TSC_REQUIRE(nbr && order && ws && (raster || out_coords), "plan: null pointer");
   TSC_REQUIRE(ws_bytes >= tsc_plan_workspace_bytes(n_out, k_vol), "plan: workspace too small");
+  TSC_REQUIRE(!pos_masks || k_vol <= 32, "plan: slot masks need k_vol <= 32 (got %d)", k_vol);
   Buffers b = carve(ws, n_out, nullptr);
   int rc;
 
@@ -414,8 +420,9 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_
     }
     tile_perm = tvi;
   }
-  gather_rows_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(vi, b.rows, cols_row, n_out, tile_perm,
-                                                          n_tiles, b.keys_b, order);
+  gather_rows_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(
+      vi, b.rows, cols_row, n_out, tile_perm, n_tiles, b.mask_pos, b.keys_b, order,
+      reinterpret_cast<uint32_t*>(pos_masks));
   TSC_LAUNCH_CHECK("plan_gather");
   if (nbr_ordered) {
     // int4 accesses need 16-byte aligned rows of the map and of the order

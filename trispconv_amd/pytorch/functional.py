@@ -87,7 +87,7 @@ def _bn_operands(ep: Epilogue, c_out: int, device) -> list:
 
 def _run(features: torch.Tensor, packed: PackedWeight, bias: Optional[torch.Tensor],
          nbr: Optional[torch.Tensor], order: Optional[torch.Tensor], n_out: int,
-         nbr_ordered: bool = False, epilogue: Optional[Epilogue] = None) -> torch.Tensor:
+         nbr_ordered: int = 0, epilogue: Optional[Epilogue] = None) -> torch.Tensor:
     """The fused kernel on features in the packed weight's dtype.  Features
     of another dtype are cast to it and the result cast back
     (functional.py:32-36, :51); for a dtype the kernels do not store (float64)

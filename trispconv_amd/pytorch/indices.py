@@ -105,6 +105,9 @@ class IndiceData:
         self._inverse_cache: Optional["IndiceData"] = None
         self._order_region = 0
         self._nbr_ordered: Optional[torch.Tensor] = None
+        # the convolution's nbr_ordered flag for it: 2 when the slot masks
+        # of the positions follow the map as its row K, else 1
+        self._ordered_flag = 1
         self._batch_size: Optional[int] = None
         # strided builds: input rows with at least one pair, i.e. the row
         # count of this layer's inverse, read with the build's counts
@@ -347,20 +350,30 @@ class IndiceData:
             lib = L.lib()
             ws = L.workspace(lib.tsc_plan_workspace_bytes(n_out, self.K), device)
             order = torch.empty(n_out, dtype=torch.int32, device=device)
-            nbr_ordered = torch.empty_like(nbr)
+            # with K <= 32 the permuted map gets one more row: each position's
+            # slot mask, so the convolution learns a tile's slots from one
+            # word per row instead of all of its entries
+            masks = self.K <= 32
+            ordered = torch.empty((self.K + int(masks)) * n_out, dtype=torch.int32,
+                                  device=device)
+            nbr_ordered = ordered[:self.K * n_out].view(self.K, n_out)
             L.check(lib.tsc_conv_plan(nbr.data_ptr(), L.ptr(cols_row), int(raster), L.ptr(coords),
                                       n_out, self.K, self._batch_bound(),
                                       L.i3(self.output_spatial_shape), region, ws.data_ptr(),
                                       ws.numel(), order.data_ptr(), nbr_ordered.data_ptr(),
+                                      ordered.data_ptr() + 4 * self.K * n_out if masks else None,
                                       L.stream_of(nbr)), "conv plan")
             self._order, self._order_region, self._nbr_ordered = order, region, nbr_ordered
+            self._ordered_flag = 2 if masks else 1
         return self._order
 
     def conv_operands(self, n_out: int, device, row_bytes: int = 256,
                       n_in: Optional[int] = None):
         """(map, order, ordered) for the fused convolution: the planned order
-        and its permuted map; for small layers the builder's own spatial
-        column order when it has one; else the row-major map.  ``n_in``, the
+        and its permuted map (ordered 2 when the map has the plan's row of
+        slot masks after it, else 1); for small layers the builder's own
+        spatial column order when it has one (ordered 1); else the row-major
+        map (ordered 0).  ``n_in``, the
         feature rows, must cover every input id the pairs name (IndexError,
         as the reference's ``features[in_ids]``)."""
         if self._map_cols is None and self._nbr is None:
@@ -372,10 +385,10 @@ class IndiceData:
                                  f"{bound - 1}, the features have {n_in} rows")
         order = self.execution_order(n_out, device, row_bytes)
         if order is not None:
-            return self._nbr_ordered, order, True
+            return self._nbr_ordered, order, self._ordered_flag
         if self._map_cols is not None and self._raster:
-            return self._map_cols, self._cols_row, True
-        return self.neighbour_map(n_out, device), None, False
+            return self._map_cols, self._cols_row, 1
+        return self.neighbour_map(n_out, device), None, 0
 
     def ordered_map(self) -> Optional[torch.Tensor]:
         """The neighbour map permuted into the execution order (None without one)."""
