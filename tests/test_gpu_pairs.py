@@ -406,3 +406,23 @@ def test_inverse_from_forward_ids_matches_the_counted_inverse(name):
             a = torch.cat([a[k, :pn[k]] for k in range(K)])
             b = torch.cat([b[k, :pn[k]] for k in range(K)])
         assert torch.equal(a, b), f"{name}: {what}"
+
+
+def test_pair_counts_read_on_the_build_stream():
+    """A submanifold build leaves its counts on the device; pair_num, read
+    later while another stream is current (and busy), sums and reads them on
+    the stream the build ran on, and equals the oracle's."""
+    w = workloads.make_workload("subm128_surface500k", scale=0.05)
+    idx = w.indices
+    say("pair counts across streams:", idx.shape)
+    s_build, s_other = torch.cuda.Stream(), torch.cuda.Stream()
+    x = torch.from_numpy(idx).to(DEV)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s_build):
+        got = generate_subm_indice_pairs(x, w.spatial_shape, 1, 3, 1)
+    with torch.cuda.stream(s_other):
+        torch.cuda._sleep(2_000_000)  # keep the other stream busy meanwhile
+        pn = got.pair_num
+    exp = OP.subm_pairs(idx, w.spatial_shape, 1, 3, 1)
+    assert pn.tolist() == exp.pair_num.tolist()
+    torch.cuda.synchronize()
