@@ -720,7 +720,7 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
   __shared__ float s_bias[BN];
   __shared__ float s_scale[BN];
   __shared__ float s_shift[BN];
-  __shared__ uint64_t s_mask[4];
+  __shared__ uint64_t s_bmask[TR / 32];  // slots used by each 32-row block
 
   const int t = threadIdx.x;
   const int lane = t & 63;
@@ -785,21 +785,28 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
     }
     uint32_t lo = static_cast<uint32_t>(m), hi = static_cast<uint32_t>(m >> 32);
 #pragma unroll
-    for (int off = WR / 2; off > 0; off >>= 1) {
+    for (int off = 16; off > 0; off >>= 1) {  // within each 32-lane half: one 32-row block
       lo |= __shfl_xor(lo, off, kWave);
       hi |= __shfl_xor(hi, off, kWave);
     }
-    if (t < TR && t % WR == 0) s_mask[t / WR] = (static_cast<uint64_t>(hi) << 32) | lo;
+    if (t < TR && t % 32 == 0) s_bmask[t / 32] = (static_cast<uint64_t>(hi) << 32) | lo;
   }
   __syncthreads();
-  const uint64_t umask_v = s_mask[0] | s_mask[1] | s_mask[2] | s_mask[3];
-  const uint64_t umask =
-      (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(umask_v >> 32))) << 32) |
-      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(umask_v));
-  const uint64_t wmask_v = s_mask[wave];
-  const uint64_t wmask =
-      (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(wmask_v >> 32))) << 32) |
-      __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(wmask_v));
+  auto uniform64 = [](uint64_t v) {
+    return (static_cast<uint64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32))) << 32) |
+           __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  };
+  uint64_t umask_v = 0;
+#pragma unroll
+  for (int b = 0; b < TR / 32; ++b) umask_v |= s_bmask[b];
+  const uint64_t umask = uniform64(umask_v);
+  uint64_t bmask[RB];  // slots used by each of this wave's 32-row blocks
+  uint64_t wmask = 0;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    bmask[rb] = uniform64(s_bmask[wave * RB + rb]);
+    wmask |= bmask[rb];
+  }
 
   auto advance = [&](int& k, int& c) {
     const bool done = k >= K;
@@ -811,6 +818,16 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
     k = k2;
   };
   auto uses = [&](int k) { return k < K && ((wmask >> k) & 1); };  // this wave computes slot k
+  // block rb of this wave computes slot k (a block none of whose rows uses
+  // slot k would only add exact zeros: its loads and MFMAs are skipped)
+  auto buses = [&](int rb, int k) { return k < K && ((bmask[rb] >> k) & 1); };
+  // blocks set of slot k: bit rb for block rb
+  auto blocks = [&](int k) {
+    int set = 0;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) set |= buses(rb, k) ? 1 << rb : 0;
+    return set;
+  };
 
   const uint4* Wv = reinterpret_cast<const uint4*>(W);
   const int nbt_all = c_out / 32;
@@ -851,12 +868,15 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
   auto dma_entries = [&](int P, int k) {  // slot k's entries of the wave's rows into buffer P
     dma_b32(orow_l >= 0 ? nbr + (int64_t)k * n_out + col_l : no_row, e_lds + P * 256);
   };
-  auto dma_rows = [&](int P, int c) {  // chunk c of the rows named by entry buffer P
+  // chunk c of the rows named by entry buffer P, for the blocks in set (four
+  // DMAs per 32-row block)
+  auto dma_rows = [&](int P, int c, int set) {
     int32_t j[2 * RB];
 #pragma unroll
     for (int g = 0; g < 2 * RB; ++g) j[g] = s_e[P * 64 + 16 * g + q];
 #pragma unroll
-    for (int g = 0; g < 2 * RB; ++g)
+    for (int g = 0; g < 2 * RB; ++g) {
+      if (!((set >> (g / 2)) & 1)) continue;
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
         const char* src =
@@ -864,13 +884,19 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
                       : zero_row + piece * 16;
         dma_b128(src, a_lds + (2 * g + hh) * 1024);
       }
+    }
   };
   auto wait_vm0 = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
-  auto wait_rows = [] {  // all but the 4 * RB youngest: the row DMAs of the next stage
-    if constexpr (RB == 2)
+  // all but the youngest 4 * nblk: the row DMAs of the next stage, for nblk
+  // blocks (the count must be exact: anything older, the slab and the
+  // entries, has to have landed)
+  auto wait_rows = [](int nblk) {
+    if (nblk == 2)
       asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else
+    else if (nblk == 1)
       asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   };
   auto wait_lgkm0 = [] { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); };
   const int qr = lane & 15;
@@ -900,7 +926,7 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
   }
   if (kn < K) dma_entries(1, kn);
   wait_vm0();
-  if (uses(kc)) dma_rows(0, cc);
+  dma_rows(0, cc, blocks(kc));
   wait_vm0();
   __syncthreads();
 
@@ -917,17 +943,20 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
     wait_vm0();
     if (kn < K) dma_slab(S ^ 1, kn, cn);
     if (kp < K) dma_entries(S, kp);
-    const bool cur = uses(kc);
+    const int cur = blocks(kc);
     uint4 a[RB][UB];
-    if (cur) {
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
+    for (int rb = 0; rb < RB; ++rb) {
+      if ((cur >> rb) & 1) {
 #pragma unroll
         for (int u = 0; u < UB; ++u) a[rb][u] = a_read(rb, u);
+      }
     }
     wait_lgkm0();
-    const bool nxt = uses(kn);
-    if (nxt) dma_rows(S ^ 1, cn);
+    const int nxt = blocks(kn);
+    dma_rows(S ^ 1, cn, nxt);
+    // the MFMAs of the blocks that use slot kc (a wave-uniform branch per
+    // block; one loop, so the register allocation is that of a full wave)
     if (cur) {
       const uint4* sw = s_w + S * SLAB_VECS;
 #pragma unroll
@@ -943,23 +972,23 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
             for (int e = 0; e < 4; ++e)
 #pragma unroll
               for (int rb = 0; rb < RB; ++rb) {
-                const float4 a4 = __builtin_bit_cast(float4, a[rb][u]);
-                const float as[4] = {a4.x, a4.y, a4.z, a4.w};
-                acc[rb][nb] = Op::run(as[e], bs[e], acc[rb][nb]);
+                if ((cur >> rb) & 1) {
+                  const float4 a4 = __builtin_bit_cast(float4, a[rb][u]);
+                  const float as[4] = {a4.x, a4.y, a4.z, a4.w};
+                  acc[rb][nb] = Op::run(as[e], bs[e], acc[rb][nb]);
+                }
               }
           } else {
             const V b = __builtin_bit_cast(V, bv);
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb)
-              acc[rb][nb] = Op::run(__builtin_bit_cast(V, a[rb][u]), b, acc[rb][nb]);
+              if ((cur >> rb) & 1)
+                acc[rb][nb] = Op::run(__builtin_bit_cast(V, a[rb][u]), b, acc[rb][nb]);
           }
         }
       }
     }
-    if (nxt)
-      wait_rows();
-    else
-      wait_vm0();
+    wait_rows(__builtin_popcount(nxt));
     __syncthreads();
     kc = kn;
     cc = cn;
