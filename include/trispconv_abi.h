@@ -87,14 +87,18 @@ TSC_API int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_size,
  * coordinate outside the grid raises there) with a wait on the check alone.
  * It blocks the calling thread until then (spinning on a word of pinned host
  * memory, one per host thread and device, allocated on first use), so it is
- * not for code under graph capture: use tsc_subm_pairs there. */
+ * not for code under graph capture: use tsc_subm_pairs there.  mask_row != 0
+ * (K <= 32): nbr has K + 1 rows and, when the columns come out in (b,z,y,x)
+ * order (result[1] = 1), row K receives each column's slot mask (bit k: the
+ * column's row has a neighbour through slot k), which tsc_conv_forward reads
+ * with nbr_ordered = 2. */
 TSC_API int64_t tsc_subm_slot_blocks_len(int64_t n, int32_t k_vol);
 TSC_API int tsc_subm_pairs_checked(const int32_t* coords, int64_t n, int32_t batch_size,
                                    const int32_t spatial[3] /* host */,
                                    const int32_t ksize[3] /* host */,
                                    const int32_t dilation[3] /* host */, void* ws,
                                    int64_t ws_bytes, int32_t* cols_row, int32_t* nbr,
-                                   int32_t* counts, int32_t* slot_blocks,
+                                   int32_t* counts, int32_t* slot_blocks, int32_t mask_row,
                                    int32_t result[2] /* host */, tsc_stream_t stream);
 /* counts[k] = sum of slot_blocks[k][*] for the n rows of a
  * tsc_subm_pairs_checked build (pair_num, indices.py:131), on the build's
@@ -133,13 +137,14 @@ TSC_API int tsc_subm_pairs_noalloc(const int32_t* coords, int64_t n, int32_t bat
  * tsc_subm_pairs (counts[K+1] = 1).  Kernels 3 cells wide in x, dilation
  * < 16 in x.  A neighbour whose rank is not below n (rows that are not the
  * bitmap's cells) is left out of the map and sets TSC_FLAG_ROWS_NOT_BITMAP
- * in counts[K]. */
+ * in counts[K].  mask_row != 0 (K <= 32): nbr has K + 1 rows and row K
+ * receives each column's slot mask, as in tsc_subm_pairs_checked. */
 TSC_API int tsc_subm_pairs_from_bitmap(const int32_t* coords, int64_t n, int32_t batch_size,
                                        const int32_t spatial[3] /* host */,
                                        const int32_t ksize[3] /* host */,
                                        const int32_t dilation[3] /* host */, const void* bitmap,
                                        int64_t bitmap_entries_n, int32_t* cols_row, int32_t* nbr,
-                                       int32_t* counts, tsc_stream_t stream);
+                                       int32_t* counts, int32_t mask_row, tsc_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Pair lists from a neighbour map (the reference's IndiceData.pairs_in /

@@ -263,7 +263,7 @@ def test_bitmap_build_flags_rows_that_are_not_its_cells():
     L.check(lib.tsc_subm_pairs_from_bitmap(half.data_ptr(), n, B, L.i3(shape), L.i3((3, 3, 3)),
                                            L.i3((1, 1, 1)), ws.data_ptr(), nwords,
                                            cols_row.data_ptr(), nbr.data_ptr(),
-                                           counts.data_ptr(), L.stream_of(half)), "bitmap build")
+                                           counts.data_ptr(), 0, L.stream_of(half)), "bitmap build")
     host = counts.cpu()
     assert int(host[27]) & L.FLAG_ROWS_NOT_BITMAP
     assert int(nbr.max()) < n
@@ -300,7 +300,8 @@ def test_checked_build_matches_the_plain_build(shape, dups, what):
     for mode in ("plain", "checked"):
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
         cols = torch.empty(n, dtype=torch.int32, device=DEV)
-        nbr = torch.empty((K, n), dtype=torch.int32, device=DEV)
+        nbr_all = torch.full(((K + 1) * n,), -3, dtype=torch.int32, device=DEV)
+        nbr = nbr_all[:K * n].view(K, n)
         counts = torch.full((K + 2,), -5, dtype=torch.int32, device=DEV)
         s = L.stream_of(c)
         if mode == "plain":
@@ -313,8 +314,12 @@ def test_checked_build_matches_the_plain_build(shape, dups, what):
             result = (ctypes.c_int32 * 2)()
             L.check(lib.tsc_subm_pairs_checked(c.data_ptr(), n, B, *args, ws.data_ptr(), ws_bytes,
                                                cols.data_ptr(), nbr.data_ptr(), counts.data_ptr(),
-                                               blocks.data_ptr(), result, s), "checked")
+                                               blocks.data_ptr(), 1, result, s), "checked")
             assert result[0] == 0, what
+            if result[1]:  # columns in (b,z,y,x) order: row K holds their slot masks
+                bits = (nbr >= 0).to(torch.int64) << torch.arange(K, device=DEV).view(K, 1)
+                want = bits.sum(0).to(torch.int32)
+                assert torch.equal(nbr_all[K * n:], want), f"{what}: slot-mask row"
             h = (ctypes.c_int32 * (K + 2))()
             L.check(lib.tsc_subm_counts(blocks.data_ptr(), n, K, counts.data_ptr(), h, s),
                     "counts")
@@ -352,7 +357,8 @@ def test_checked_build_reports_bad_coordinates():
         result = (ctypes.c_int32 * 2)()
         L.check(lib.tsc_subm_pairs_checked(c.data_ptr(), n, 1, *args, ws.data_ptr(), ws_bytes,
                                            cols.data_ptr(), nbr.data_ptr(), counts.data_ptr(),
-                                           blocks.data_ptr(), result, L.stream_of(c)), "checked")
+                                           blocks.data_ptr(), 0, result, L.stream_of(c)),
+                "checked")
         assert result[0] == flag, bad
         with pytest.raises(IndexError):
             generate_subm_indice_pairs(c, shape, 1, 3, 1)

@@ -196,10 +196,10 @@ def test_argument_errors_return_codes_without_gpu():
     # a build on an existing bitmap: 3-wide kernels only, and a bitmap that
     # covers the grid
     rc = lib.tsc_subm_pairs_from_bitmap(None, 10, 1, L.i3((8, 8, 8)), L.i3((5, 5, 5)),
-                                        L.i3((1, 1, 1)), None, 0, None, None, None, None)
+                                        L.i3((1, 1, 1)), None, 0, None, None, None, 0, None)
     assert rc == 1 and b"3 cells wide" in lib.tsc_last_error()
     rc = lib.tsc_subm_pairs_from_bitmap(None, 10, 1, L.i3((8, 8, 8)), L.i3((3, 3, 3)),
-                                        L.i3((1, 1, 1)), None, 0, None, None, None, None)
+                                        L.i3((1, 1, 1)), None, 0, None, None, None, 0, None)
     assert rc == 1 and b"bitmap" in lib.tsc_last_error()
     with pytest.raises(ValueError):
         L.check(1, "probe")

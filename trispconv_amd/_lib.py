@@ -37,13 +37,13 @@ _SIGNATURES = {
                                       _vp, _vp, _vp, _vp]),
     "tsc_subm_slot_blocks_len": (_i64, [_i64, _i32]),
     "tsc_subm_pairs_checked": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, _vp, _i64,
-                                              _vp, _vp, _vp, _vp, c_i32p, _vp]),
+                                              _vp, _vp, _vp, _vp, _i32, c_i32p, _vp]),
     "tsc_subm_counts": (ctypes.c_int, [_vp, _i64, _i32, _vp, c_i32p, _vp]),
     "tsc_subm_pairs_noalloc_limit": (_i64, []),
     "tsc_subm_pairs_noalloc": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, _vp, _vp,
                                               _vp, _vp]),
     "tsc_subm_pairs_from_bitmap": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, _vp,
-                                                  _i64, _vp, _vp, _vp, _vp]),
+                                                  _i64, _vp, _vp, _vp, _i32, _vp]),
     "tsc_map_to_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _vp, _vp]),
     "tsc_pairs_from_map_workspace_bytes": (_i64, [_i64, _i32]),
     "tsc_pairs_from_map": (ctypes.c_int, [_vp, _i64, _i32, _i64, _vp, _i64, _vp, _vp, _vp]),

@@ -271,7 +271,9 @@ __device__ __forceinline__ void signal_started(int32_t* host_word) {
 // the caller's workspace of ws_bytes, sized by tsc_subm_workspace_bytes.
 // hs (may be null): the coordinate check also goes to hs's flag word, the
 // next kernel sets its started word, and the call waits for that before it
-// returns.  slot_blocks (may be null): the probe's per-(slot, block) counts
+// returns.  mask_row != 0 (K <= 32): nbr has a row K, and the bitmap path's
+// probe writes each column's slot mask there.  slot_blocks (may be null): the
+// probe's per-(slot, block) counts
 // go there ([K][ceil(n / 256)] int32) and counts[0..K) are left for
 // tsc_subm_counts; otherwise they are summed into counts.  *raster (may be
 // null) = 1 when the map's columns are in (b,z,y,x) order.
@@ -279,7 +281,8 @@ int subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size, const in
                   const int32_t ksize[3], const int32_t dilation[3], void* ws, int64_t ws_bytes,
                   int64_t ws_limit, int32_t* cols_row, int32_t* nbr, int32_t* counts,
                   tsc_stream_t stream, const HostStatus* hs = nullptr,
-                  int32_t* slot_blocks = nullptr, int32_t* raster = nullptr);
+                  int32_t* slot_blocks = nullptr, int32_t* raster = nullptr,
+                  int32_t mask_row = 0);
 int exclusive_scan_u32(const uint32_t* src, int kind, int64_t n, uint32_t* out, int32_t* total,
                        uint32_t* scratch, hipStream_t s);
 

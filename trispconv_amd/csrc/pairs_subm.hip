@@ -391,7 +391,8 @@ __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
     int64_t n, int K, SubmGeom g, const uint2* __restrict__ wr,
     const uint2* __restrict__ col_e, const int32_t* __restrict__ n_unique,
     const int32_t* __restrict__ n_extra, int32_t* __restrict__ cols_row, int32_t* __restrict__ nbr,
-    int32_t* __restrict__ blk_cnt, int nblk, int32_t* __restrict__ counts) {
+    int32_t* __restrict__ blk_cnt, int nblk, int32_t* __restrict__ counts,
+    uint32_t* __restrict__ col_masks) {
   __shared__ int32_t s_cnt[64];
   const int t = threadIdx.x;
   if (t < 64) s_cnt[t] = 0;
@@ -401,6 +402,7 @@ __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
   const uint2 me = live ? col_e[col] : make_uint2(0u, 0u);
   if (col < n) cols_row[col] = static_cast<int32_t>(me.x) - 1;
   const int4 c = cell_coords(g, me.y);
+  uint32_t cmask = 0;  // the column's slot mask (slots below 32)
   for (int k0 = 0; k0 < K; k0 += kLook) {
     uint32_t cell[kLook];
     uint2 e[kLook];
@@ -430,9 +432,11 @@ __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
       const int k = k0 + i;
       if (k >= K) continue;
       if (col < n) nbr[(int64_t)k * n + col] = jr[i];
+      cmask |= (jr[i] >= 0 && k < 32 ? 1u : 0u) << (k & 31);
       count_hit(k, jr[i] >= 0, s_cnt, blk_cnt, nblk, counts);
     }
   }
+  if (col_masks && col < n) col_masks[col] = cmask;
   __syncthreads();
   if (t < K && t < 64) {
     if (blk_cnt)
@@ -468,7 +472,7 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
     const uint2* __restrict__ col_e, const int4* __restrict__ rows_coords,
     const int32_t* __restrict__ n_unique, const int32_t* __restrict__ n_extra,
     int32_t* __restrict__ cols_row, int32_t* __restrict__ nbr, int32_t* __restrict__ blk_cnt,
-    int nblk, int32_t* __restrict__ counts) {
+    int nblk, int32_t* __restrict__ counts, uint32_t* __restrict__ col_masks) {
   constexpr bool kStatic = KZ > 0 && KY > 0;
   constexpr int kRowsAtOnce = kStatic ? KY : 3;  // rows whose entries load together
   // the fixed-extent path stores whole batches without a row bound
@@ -494,6 +498,7 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
   const int n_rows = ksz * ksy;
   const bool lane_counts = (kStatic && KZ * KY * KX <= kWave) || K <= kWave;
   int32_t my_cnt = 0;  // lane k: the wave's hits through slot k
+  uint32_t cmask = 0;  // the column's slot mask (slots below 32)
   const int x_lo = c.w - (KX / 2) * g.dil.x;                 // the row's first cell
   const int x_first = x_lo > 0 ? x_lo : 0;                   // first cell inside the grid
   for (int q0 = 0; q0 < n_rows; q0 += kRowsAtOnce) {
@@ -601,7 +606,18 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
         for (int kx = 0; kx < KX; ++kx) nbr[(int64_t)(q * KX + kx) * n + col] = jr[i][kx];
       }
     }
+#pragma unroll
+    for (int i = 0; i < kRowsAtOnce; ++i) {
+      const int q = q0 + i;
+      if (!kStatic && q >= n_rows) continue;
+#pragma unroll
+      for (int kx = 0; kx < KX; ++kx) {
+        const int k = q * KX + kx;
+        cmask |= (jr[i][kx] >= 0 && k < 32 ? 1u : 0u) << (k & 31);
+      }
+    }
   }
+  if (col_masks && col < n) col_masks[col] = cmask;
   if (!lane_counts) return;
   s_cnt[t / kWave][lane] = my_cnt;
   __syncthreads();
@@ -834,7 +850,8 @@ int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
                       const int32_t spatial[3], const int32_t ksize[3],
                       const int32_t dilation[3], void* ws, int64_t ws_bytes, int64_t ws_limit,
                       int32_t* cols_row, int32_t* nbr, int32_t* counts, tsc_stream_t stream,
-                      const HostStatus* hs, int32_t* slot_blocks, int32_t* raster) {
+                      const HostStatus* hs, int32_t* slot_blocks, int32_t* raster,
+                      int32_t mask_row) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   TSC_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "subm: n=%lld out of range", (long long)n);
   TSC_REQUIRE(batch_size > 0, "subm: batch_size must be positive");
@@ -872,6 +889,10 @@ int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
   const int nblk = static_cast<int>(ceil_div(n, kRows));
   const SubmWork w = subm_carve(ws, n, K, cells, mode, nullptr);
   int32_t* const blk_cnt = slot_blocks ? slot_blocks : w.blk_cnt;
+  TSC_REQUIRE(!mask_row || K <= 32, "subm: a slot-mask row needs k_vol <= 32 (got %d)", K);
+  // the column slot masks, as row K of the map (the bitmap path's probes
+  // write them; the hash path's columns are the rows, which take no order)
+  uint32_t* const col_masks = mask_row ? reinterpret_cast<uint32_t*>(nbr + (int64_t)K * n) : nullptr;
   const int4* c4 = reinterpret_cast<const int4*>(coords);
   if (w.wr) {
     const int64_t nw = bitmap_words(cells);
@@ -904,17 +925,17 @@ int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
     if (ks.x == 3 && 2 * dil.x < 32 && ks.y == 3 && ks.z == 3) {
       subm_probe_rows_kernel<3, 3, 3, false><<<ceil_div(n, 256), 256, 0, s>>>(
           n, K, g, w.wr, nw, w.col, nullptr, w.n_unique, w.n_extra, cols_row, nbr, blk_cnt,
-          nblk, counts);
+          nblk, counts, col_masks);
       TSC_LAUNCH_CHECK("subm_probe_rows");
     } else if (ks.x == 3 && 2 * dil.x < 32) {
       subm_probe_rows_kernel<3, 0, 0, false><<<ceil_div(n, 256), 256, 0, s>>>(
           n, K, g, w.wr, nw, w.col, nullptr, w.n_unique, w.n_extra, cols_row, nbr, blk_cnt,
-          nblk, counts);
+          nblk, counts, col_masks);
       TSC_LAUNCH_CHECK("subm_probe_rows");
     } else {
       subm_probe_cols_kernel<<<ceil_div(n, 256), 256, 0, s>>>(n, K, g, w.wr, w.col, w.n_unique,
                                                               w.n_extra, cols_row, nbr, blk_cnt,
-                                                              nblk, counts);
+                                                              nblk, counts, col_masks);
       TSC_LAUNCH_CHECK("subm_probe_cols");
     }
     if (!slot_blocks && (rc = sum_slot_blocks(blk_cnt, counts, K, nblk, s))) return rc;
@@ -966,7 +987,7 @@ extern "C" int tsc_subm_pairs_checked(const int32_t* coords, int64_t n, int32_t 
                                       const int32_t spatial[3], const int32_t ksize[3],
                                       const int32_t dilation[3], void* ws, int64_t ws_bytes,
                                       int32_t* cols_row, int32_t* nbr, int32_t* counts,
-                                      int32_t* slot_blocks, int32_t result[2],
+                                      int32_t* slot_blocks, int32_t mask_row, int32_t result[2],
                                       tsc_stream_t stream) {
   TSC_REQUIRE(result != nullptr, "subm: result is null");
   TSC_REQUIRE(slot_blocks != nullptr, "subm: slot_blocks is null");
@@ -977,7 +998,7 @@ extern "C" int tsc_subm_pairs_checked(const int32_t* coords, int64_t n, int32_t 
   hs.host[kHostStarted] = 0;
   int32_t raster = 0;
   if (int rc = subm_pairs_ws(coords, n, batch_size, spatial, ksize, dilation, ws, ws_bytes, 0,
-                             cols_row, nbr, counts, stream, &hs, slot_blocks, &raster))
+                             cols_row, nbr, counts, stream, &hs, slot_blocks, &raster, mask_row))
     return rc;
   result[1] = raster;
   if (n == 0) return 0;
@@ -1038,7 +1059,7 @@ extern "C" int tsc_subm_pairs_from_bitmap(const int32_t* coords, int64_t n, int3
                                           const int32_t spatial[3], const int32_t ksize[3],
                                           const int32_t dilation[3], const void* bitmap,
                                           int64_t bitmap_entries_n, int32_t* cols_row, int32_t* nbr,
-                                          int32_t* counts, tsc_stream_t stream) {
+                                          int32_t* counts, int32_t mask_row, tsc_stream_t stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   TSC_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "subm: n=%lld out of range", (long long)n);
   TSC_REQUIRE(batch_size > 0, "subm: batch_size must be positive");
@@ -1060,6 +1081,8 @@ extern "C" int tsc_subm_pairs_from_bitmap(const int32_t* coords, int64_t n, int3
               "subm: bitmap of %lld entries, the grid needs %lld", (long long)bitmap_entries_n,
               (long long)nw);
   TSC_REQUIRE(counts != nullptr, "subm: counts is null");
+  TSC_REQUIRE(!mask_row || K <= 32, "subm: a slot-mask row needs k_vol <= 32 (got %d)", K);
+  uint32_t* const col_masks = mask_row ? reinterpret_cast<uint32_t*>(nbr + (int64_t)K * n) : nullptr;
   // counts[0..K] = 0 (counts[K]: no status flags), counts[K+1] = 1 (rows in
   // (b,z,y,x) order)
   subm_init_kernel<<<1, 256, 0, s>>>(nullptr, 0, counts, K, counts + K);
@@ -1071,10 +1094,12 @@ extern "C" int tsc_subm_pairs_from_bitmap(const int32_t* coords, int64_t n, int3
   const int4* c4 = reinterpret_cast<const int4*>(coords);
   if (ks.y == 3 && ks.z == 3)
     subm_probe_rows_kernel<3, 3, 3, true><<<ceil_div(n, 256), 256, 0, s>>>(
-        n, K, g, wr, nw, nullptr, c4, nullptr, nullptr, cols_row, nbr, nullptr, 0, counts);
+        n, K, g, wr, nw, nullptr, c4, nullptr, nullptr, cols_row, nbr, nullptr, 0, counts,
+        col_masks);
   else
     subm_probe_rows_kernel<3, 0, 0, true><<<ceil_div(n, 256), 256, 0, s>>>(
-        n, K, g, wr, nw, nullptr, c4, nullptr, nullptr, cols_row, nbr, nullptr, 0, counts);
+        n, K, g, wr, nw, nullptr, c4, nullptr, nullptr, cols_row, nbr, nullptr, 0, counts,
+        col_masks);
   TSC_LAUNCH_CHECK("subm_probe_rows");
   return 0;
 }

@@ -108,6 +108,8 @@ class IndiceData:
         # the convolution's nbr_ordered flag for it: 2 when the slot masks
         # of the positions follow the map as its row K, else 1
         self._ordered_flag = 1
+        # the builder's map by columns has each column's slot mask as row K
+        self._map_masks = False
         self._batch_size: Optional[int] = None
         # strided builds: input rows with at least one pair, i.e. the row
         # count of this layer's inverse, read with the build's counts
@@ -219,6 +221,7 @@ class IndiceData:
         self._pin = self._pout = self._cnt = self._nbr = self._order = None
         self._map_cols = self._cols_row = None
         self._raster = False
+        self._map_masks = False
         self._nbr_ordered = None
         self._inverse_cache = None
         self._in_bound = None
@@ -387,7 +390,7 @@ class IndiceData:
         if order is not None:
             return self._nbr_ordered, order, self._ordered_flag
         if self._map_cols is not None and self._raster:
-            return self._map_cols, self._cols_row, 1
+            return self._map_cols, self._cols_row, 2 if self._map_masks else 1
         return self.neighbour_map(n_out, device), None, 0
 
     def ordered_map(self) -> Optional[torch.Tensor]:
@@ -468,12 +471,14 @@ def _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil):
     n = coords.shape[0]
     dev = coords.device
     cols_row = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
-    map_cols = torch.empty((K, n), dtype=torch.int32, device=dev)
+    masks = K <= 32  # each column's slot mask as row K, for the convolution's set-up
+    map_all = torch.empty((K + int(masks)) * n, dtype=torch.int32, device=dev)
+    map_cols = map_all[:K * n].view(K, n)
     counts = torch.empty(K + 2, dtype=torch.int32, device=dev)
     stream = L.stream_of(coords)
     L.check(L.lib().tsc_subm_pairs_from_bitmap(
         coords.data_ptr(), n, int(batch_size), L.i3(shape), L.i3(ks), L.i3(dil), ws.data_ptr(),
-        nwords, cols_row.data_ptr(), map_cols.data_ptr(), counts.data_ptr(), stream),
+        nwords, cols_row.data_ptr(), map_cols.data_ptr(), counts.data_ptr(), int(masks), stream),
         "generate_subm_indice_pairs")
     # No read-back here: the rows are the registered output set (same tensor,
     # same version), so there is nothing to validate before the convolution.
@@ -486,6 +491,7 @@ def _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil):
         dilation=dil, subm=True, pin=None, pout=None, cnt_dev=None, pair_num=None,
         nbr=None, batch_size=int(batch_size), map_cols=map_cols, cols_row=cols_row[:n],
         raster=True)
+    d._map_masks = masks
     d._counts_pending = (counts, K, lambda: _counts_to_host(counts, K, stream))
     return d
 
@@ -524,7 +530,7 @@ def generate_subm_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size:
     L.check(lib.tsc_subm_pairs_checked(coords.data_ptr(), n, int(batch_size), sz.shape, sz.ks,
                                        sz.dil, ws.data_ptr(), sz.ws_bytes, base,
                                        base + 4 * sz.o_map, base + 4 * sz.o_counts,
-                                       base + 4 * sz.o_blocks, result, stream),
+                                       base + 4 * sz.o_blocks, int(sz.masks), result, stream),
             "generate_subm_indice_pairs")
     _raise_status(int(result[0]), "generate_subm_indice_pairs")
     cols_row = tables[:n]
@@ -539,6 +545,7 @@ def generate_subm_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size:
         cols_row=cols_row)
     d._counts_pending = (counts, K, lambda: _counts_to_host(counts, K, stream, slot_blocks, n))
     d._raster = bool(result[1])
+    d._map_masks = sz.masks and d._raster  # the bitmap path's probe wrote them
     return d
 
 
@@ -550,8 +557,9 @@ class _SubmSizes:
         self.shape, self.ks, self.dil = L.i3(shape), L.i3(ks), L.i3(dil)
         self.ws_bytes = int(lib.tsc_subm_workspace_bytes(n, K, batch_size, self.shape))
         n_al = _align64(max(n, 1))
+        self.masks = K <= 32  # each column's slot mask after the map, as its row K
         self.o_map = n_al
-        self.o_counts = n_al + _align64(K * n)
+        self.o_counts = n_al + _align64((K + int(self.masks)) * n)
         self.o_blocks = self.o_counts + _align64(K + 2)
         self.words = self.o_blocks + int(lib.tsc_subm_slot_blocks_len(n, K))
 
