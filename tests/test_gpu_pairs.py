@@ -432,3 +432,33 @@ def test_pair_counts_read_on_the_build_stream():
     exp = OP.subm_pairs(idx, w.spatial_shape, 1, 3, 1)
     assert pn.tolist() == exp.pair_num.tolist()
     torch.cuda.synchronize()
+
+
+def test_sparse_bitmap_skips_untouched_tiles():
+    """A grid sparse enough for the atomically marked bitmap (more than 64
+    cells per voxel): only the 1024-word tiles holding a row's cell are
+    zeroed, scanned and ranked, and probes read the others as empty.  Small
+    clusters straddle tile boundaries (y = 64k and z planes), with repeated
+    rows on top; the pairs must equal the oracle's."""
+    shape, B = (64, 512, 512), 2
+    cells = B * shape[0] * shape[1] * shape[2]
+    rng = np.random.default_rng(17)
+    parts = []
+    for b in range(B):
+        for _ in range(12):
+            # a 6^3 box around a tile boundary (y multiple of 64) or a z plane
+            z0 = int(rng.integers(1, shape[0] - 7))
+            y0 = int(rng.choice([63, 127, 255, 447])) - 3
+            x0 = int(rng.integers(0, shape[2] - 6))
+            zz, yy, xx = np.meshgrid(np.arange(6), np.arange(6), np.arange(6), indexing="ij")
+            box = np.stack([np.full(216, b), (z0 + zz).ravel(), (y0 + yy).ravel(),
+                            (x0 + xx).ravel()], 1)
+            parts.append(box[rng.random(216) < 0.6])
+    idx = np.unique(np.concatenate(parts).astype(np.int32), axis=0)
+    idx = np.concatenate([idx, idx[rng.choice(len(idx), 50)]])
+    idx = idx[rng.permutation(len(idx))]
+    n = len(idx)
+    words = -(-cells // 32)
+    assert cells > 64 * n and words <= 64 * n + (1 << 20)  # the atomically marked bitmap
+    _subm(idx, shape, B, 3, 1, "sparse bitmap, untouched tiles")
+    _subm(idx, shape, B, 3, (2, 2, 1), "sparse bitmap, dilated")

@@ -297,16 +297,22 @@ int exclusive_scan_u32(const uint32_t* src, int kind, int64_t n, uint32_t* out, 
 // `pre` is null, else from `pre`, their exclusive scan) and writes the ranks.
 constexpr int kBmThreads = 256;
 constexpr int kBmTile = kBmThreads * 4;
+static_assert(kBmTile == kBitmapTileWords, "one scan tile per touched flag");
 
 __global__ void __launch_bounds__(kBmThreads) bitmap_reduce_kernel(const uint4* __restrict__ wr2,
                                                                    int64_t nw,
                                                                    uint32_t* __restrict__ sums,
                                                                    int nsum, SlotScan scan,
-                                                                   int32_t* started) {
+                                                                   int32_t* started,
+                                                                   const uint8_t* __restrict__ touched) {
   __shared__ uint32_t s_wave[33];
   signal_started(started);
   if (static_cast<int>(blockIdx.x) >= nsum) {  // blocks past the tiles: a slot scan riding along
     slot_scan_block(scan, blockIdx.x - nsum, s_wave);
+    return;
+  }
+  if (touched && !touched[blockIdx.x]) {  // no word of this tile is set (block-uniform)
+    if (threadIdx.x == 0) sums[blockIdx.x] = 0;
     return;
   }
   const int64_t p = (blockIdx.x * (int64_t)kBmTile) / 2 + 2 * threadIdx.x;  // entry pairs
@@ -368,7 +374,8 @@ __global__ void __launch_bounds__(kBmThreads) bitmap_apply_kernel(uint4* __restr
                                                                   const uint32_t* __restrict__ sums,
                                                                   const uint32_t* __restrict__ pre,
                                                                   int nsum,
-                                                                  int32_t* __restrict__ n_unique) {
+                                                                  int32_t* __restrict__ n_unique,
+                                                                  const uint8_t* __restrict__ touched) {
   __shared__ uint32_t s_wave[33];
   uint32_t base;
   if (pre) {
@@ -383,6 +390,7 @@ __global__ void __launch_bounds__(kBmThreads) bitmap_apply_kernel(uint4* __restr
     base = blockIdx.x == 0 ? 0u : tot;
     if (blockIdx.x == 0 && threadIdx.x == 0) *n_unique = static_cast<int32_t>(tot);
   }
+  if (touched && !touched[blockIdx.x]) return;  // no set bit, no rank to write (block-uniform)
   const int64_t p = (blockIdx.x * (int64_t)kBmTile) / 2 + 2 * threadIdx.x;
   uint4 v[2];
   uint32_t c[4];
@@ -419,7 +427,9 @@ int64_t bitmap_scan_scratch_words(int64_t nw) {
 }
 
 int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStream_t s,
-                const uint8_t* bytes, const SlotScan* scan, int32_t* started) {
+                const uint8_t* bytes, const SlotScan* scan, int32_t* started,
+                const uint8_t* touched) {
+  TSC_REQUIRE(!touched || !bytes, "bitmap_scan: touched tiles are for bitmaps marked in place");
   const int64_t nsum = ceil_div(nw > 0 ? nw : 1, kBmTile);
   uint32_t* sums = scratch;
   uint32_t* pre = scratch + nsum;
@@ -434,7 +444,7 @@ int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStr
     TSC_LAUNCH_CHECK("bitmap_pack");
   } else {
     bitmap_reduce_kernel<<<grid, kBmThreads, 0, s>>>(wr2, nw, sums, static_cast<int>(nsum), sc,
-                                                     started);
+                                                     started, touched);
     TSC_LAUNCH_CHECK("bitmap_reduce");
   }
   const uint32_t* p = nullptr;
@@ -444,7 +454,8 @@ int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStr
     p = pre;
   }
   bitmap_apply_kernel<<<static_cast<unsigned>(nsum), kBmThreads, 0, s>>>(
-      wr2, nw, sums, p, static_cast<int>(nsum < kBmDirectTiles ? nsum : kBmDirectTiles), total);
+      wr2, nw, sums, p, static_cast<int>(nsum < kBmDirectTiles ? nsum : kBmDirectTiles), total,
+      touched);
   TSC_LAUNCH_CHECK("bitmap_apply");
   return 0;
 }

@@ -227,10 +227,14 @@ int64_t bitmap_scan_scratch_words(int64_t nw);
 // With scan, that slot scan (scan_slot_blocks) runs in the same launch as
 // the first pass.
 // started (may be null): a word of pinned host memory the first launch sets
-// when it begins (signal_started).
+// when it begins (signal_started).  touched (may be null): one byte per tile
+// of kBitmapTileWords words, 0 for tiles none of whose words is set; their
+// entries are neither read (they may hold anything) nor written, and count 0.
+constexpr int kBitmapTileWords = 1024;
+inline int64_t bitmap_tiles(int64_t nw) { return ceil_div(nw > 0 ? nw : 1, kBitmapTileWords); }
 int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStream_t s,
                 const uint8_t* bytes = nullptr, const SlotScan* scan = nullptr,
-                int32_t* started = nullptr);
+                int32_t* started = nullptr, const uint8_t* touched = nullptr);
 // Two words of pinned host memory that kernels store into, one pair per host
 // thread and device (allocated on first use there and kept until the process
 // ends).  A build that must report bad coordinates before it returns, but

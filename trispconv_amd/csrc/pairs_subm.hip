@@ -321,6 +321,44 @@ __global__ void __launch_bounds__(256) subm_mark_kernel(const int4* __restrict__
     atomicOr(&wr[cell >> 5].x, 1u << (cell & 31));
 }
 
+// Bitmaps marked by atomics (sparse grids): only the tiles of
+// kBitmapTileWords words that hold a row's cell are zeroed, scanned and
+// ranked.  touched[tile] = 1 for each row's tile (plain stores: every writer
+// stores 1); rows outside the grid are skipped (the mark flags them).
+__global__ void __launch_bounds__(256) subm_touch_kernel(const int4* __restrict__ coords, int64_t n,
+                                                         SubmGeom g, uint8_t* __restrict__ touched) {
+  const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (r >= n) return;
+  const int4 c = coords[r];
+  if (!in_grid(g, c.x, c.y, c.z, c.w)) return;
+  touched[(cell_key(g, c.x, c.y, c.z, c.w) >> 5) / kBitmapTileWords] = 1;
+}
+
+// One block per tile: the entries of a touched tile are zeroed (the others
+// are never read).  Entry pairs past the bitmap's end are its padding, also
+// zeroed while they lie in the last tile.
+__global__ void __launch_bounds__(256) subm_zero_touched_kernel(uint4* __restrict__ wr2,
+                                                                int64_t n_pairs,
+                                                                const uint8_t* __restrict__ touched) {
+  if (!touched[blockIdx.x]) return;
+  const int64_t p0 = blockIdx.x * (int64_t)(kBitmapTileWords / 2);
+#pragma unroll
+  for (int j = 0; j < kBitmapTileWords / 2 / 256; ++j) {
+    const int64_t p = p0 + j * 256 + threadIdx.x;
+    if (p < n_pairs) wr2[p] = make_uint4(0u, 0u, 0u, 0u);
+  }
+}
+
+// A bitmap entry, read as empty where its tile is untouched (touched may be
+// null: every tile is initialised).  The entry is loaded either way (the
+// address is in the bitmap) and the value selected, so the loads stay
+// unconditional.
+__device__ __forceinline__ uint2 entry_at(const uint2* __restrict__ wr,
+                                          const uint8_t* __restrict__ touched, uint32_t w) {
+  const uint2 e = wr[w];
+  return (!touched || touched[w / kBitmapTileWords]) ? e : make_uint2(0u, 0u);
+}
+
 // Rank of an occupied cell: occupied cells before it in (b,z,y,x) order.
 __device__ __forceinline__ uint32_t cell_rank(uint2 e, uint32_t cell) {
   return e.y + __popc(e.x & ((1u << (cell & 31)) - 1u));
@@ -392,7 +430,7 @@ __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
     const uint2* __restrict__ col_e, const int32_t* __restrict__ n_unique,
     const int32_t* __restrict__ n_extra, int32_t* __restrict__ cols_row, int32_t* __restrict__ nbr,
     int32_t* __restrict__ blk_cnt, int nblk, int32_t* __restrict__ counts,
-    uint32_t* __restrict__ col_masks) {
+    uint32_t* __restrict__ col_masks, const uint8_t* __restrict__ touched) {
   __shared__ int32_t s_cnt[64];
   const int t = threadIdx.x;
   if (t < 64) s_cnt[t] = 0;
@@ -417,7 +455,7 @@ __global__ void __launch_bounds__(256) subm_probe_cols_kernel(
       const int x = c.w + (kx - g.ks.x / 2) * g.dil.x;
       look[i] = live && k < K && in_grid(g, c.x, z, y, x);
       cell[i] = look[i] ? cell_key(g, c.x, z, y, x) : 0u;
-      e[i] = wr[cell[i] >> 5];  // entry 0 exists: unconditional reads
+      e[i] = entry_at(wr, touched, cell[i] >> 5);  // entry 0 exists: unconditional reads
     }
     int32_t jr[kLook];
 #pragma unroll
@@ -472,7 +510,8 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
     const uint2* __restrict__ col_e, const int4* __restrict__ rows_coords,
     const int32_t* __restrict__ n_unique, const int32_t* __restrict__ n_extra,
     int32_t* __restrict__ cols_row, int32_t* __restrict__ nbr, int32_t* __restrict__ blk_cnt,
-    int nblk, int32_t* __restrict__ counts, uint32_t* __restrict__ col_masks) {
+    int nblk, int32_t* __restrict__ counts, uint32_t* __restrict__ col_masks,
+    const uint8_t* __restrict__ touched) {
   constexpr bool kStatic = KZ > 0 && KY > 0;
   constexpr int kRowsAtOnce = kStatic ? KY : 3;  // rows whose entries load together
   // the fixed-extent path stores whole batches without a row bound
@@ -514,8 +553,8 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
       row_ok[i] = live && q < n_rows && in_grid(g, c.x, z, y, x_first);
       base[i] = row_ok[i] ? cell_key(g, c.x, z, y, x_first) : 0u;  // key of x_first
       const uint32_t w0 = base[i] >> 5;
-      e0[i] = wr[w0];
-      e1[i] = wr[w0 + 1 < nw ? w0 + 1 : w0];
+      e0[i] = entry_at(wr, touched, w0);
+      e1[i] = entry_at(wr, touched, w0 + 1 < nw ? w0 + 1 : w0);
     }
     int32_t jr[kRowsAtOnce][KX];
     bool hit[kRowsAtOnce][KX];
@@ -775,6 +814,7 @@ struct SubmWork {
   uint8_t* bytes;  // byte-per-cell occupancy (byte-marked bitmap builds)
   uint32_t* scan;  // bitmap scan scratch
   uint2* col;      // map columns: (row + 1, cell), 4 entries of padding
+  uint8_t* touched;  // atomic-marked bitmaps: a byte per scan tile holding a row's cell
   int32_t *n_unique, *n_extra, *blk_cnt, *blk_off;
 };
 
@@ -793,6 +833,7 @@ static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, int mode, 
     const int64_t nw = bitmap_words(cells);
     w.wr = c.take<uint2>(bitmap_entries(nw));
     if (mode == kSubmBytes) w.bytes = c.take<uint8_t>(bitmap_entries(nw) * 32);
+    else w.touched = c.take<uint8_t>(align_up(bitmap_tiles(nw), 16));
     w.scan = c.take<uint32_t>(bitmap_scan_scratch_words(nw));
     w.col = c.take<uint2>(m + 4);
     w.n_unique = c.take<int32_t>(1);
@@ -897,24 +938,32 @@ int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
   if (w.wr) {
     const int64_t nw = bitmap_words(cells);
     SubmGeom g{batch_size, shape, ks, dil, 0u};
-    // zero the marks: the byte map (the scan then writes every bitmap entry)
-    // or the bitmap entries themselves
-    const int64_t units = w.bytes ? bitmap_entries(nw) * 2 : ceil_div(nw, 2);  // 16-byte units
+    // zero the marks: the byte map (the scan then writes every bitmap entry),
+    // or for atomic marks the touched-tile flags; then the flags are set and
+    // only those tiles' entries zeroed
+    const int64_t units = w.bytes ? bitmap_entries(nw) * 2 : align_up(bitmap_tiles(nw), 16) / 16;
     uint4* marks = reinterpret_cast<uint4*>(w.bytes ? static_cast<void*>(w.bytes)
-                                                    : static_cast<void*>(w.wr));
+                                                    : static_cast<void*>(w.touched));
     const int64_t init_blocks = std::min<int64_t>(ceil_div(units, 256), 4096);
     subm_init_kernel<<<static_cast<unsigned>(init_blocks > 0 ? init_blocks : 1), 256, 0, s>>>(
         marks, units, counts, K, w.n_extra);
     TSC_LAUNCH_CHECK("subm_init");
-    if (w.bytes)
+    if (w.bytes) {
       subm_mark_kernel<true><<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.bytes, counts + K,
                                                               host_flag, w.col);
-    else
+    } else {
+      subm_touch_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.touched);
+      TSC_LAUNCH_CHECK("subm_touch");
+      subm_zero_touched_kernel<<<static_cast<unsigned>(bitmap_tiles(nw)), 256, 0, s>>>(
+          reinterpret_cast<uint4*>(w.wr), bitmap_entries(nw) / 2, w.touched);
+      TSC_LAUNCH_CHECK("subm_zero_touched");
       subm_mark_kernel<false><<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, nullptr,
                                                                counts + K, host_flag, w.col);
+    }
     TSC_LAUNCH_CHECK("subm_mark");
     if (raster) *raster = 1;
-    if ((rc = bitmap_scan(w.wr, nw, w.scan, w.n_unique, s, w.bytes, nullptr, started))) return rc;
+    if ((rc = bitmap_scan(w.wr, nw, w.scan, w.n_unique, s, w.bytes, nullptr, started, w.touched)))
+      return rc;
     subm_rank_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, w.col,
                                                       w.n_extra);
     TSC_LAUNCH_CHECK("subm_rank");
@@ -925,17 +974,17 @@ int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
     if (ks.x == 3 && 2 * dil.x < 32 && ks.y == 3 && ks.z == 3) {
       subm_probe_rows_kernel<3, 3, 3, false><<<ceil_div(n, 256), 256, 0, s>>>(
           n, K, g, w.wr, nw, w.col, nullptr, w.n_unique, w.n_extra, cols_row, nbr, blk_cnt,
-          nblk, counts, col_masks);
+          nblk, counts, col_masks, w.touched);
       TSC_LAUNCH_CHECK("subm_probe_rows");
     } else if (ks.x == 3 && 2 * dil.x < 32) {
       subm_probe_rows_kernel<3, 0, 0, false><<<ceil_div(n, 256), 256, 0, s>>>(
           n, K, g, w.wr, nw, w.col, nullptr, w.n_unique, w.n_extra, cols_row, nbr, blk_cnt,
-          nblk, counts, col_masks);
+          nblk, counts, col_masks, w.touched);
       TSC_LAUNCH_CHECK("subm_probe_rows");
     } else {
       subm_probe_cols_kernel<<<ceil_div(n, 256), 256, 0, s>>>(n, K, g, w.wr, w.col, w.n_unique,
                                                               w.n_extra, cols_row, nbr, blk_cnt,
-                                                              nblk, counts, col_masks);
+                                                              nblk, counts, col_masks, w.touched);
       TSC_LAUNCH_CHECK("subm_probe_cols");
     }
     if (!slot_blocks && (rc = sum_slot_blocks(blk_cnt, counts, K, nblk, s))) return rc;
@@ -1095,11 +1144,11 @@ extern "C" int tsc_subm_pairs_from_bitmap(const int32_t* coords, int64_t n, int3
   if (ks.y == 3 && ks.z == 3)
     subm_probe_rows_kernel<3, 3, 3, true><<<ceil_div(n, 256), 256, 0, s>>>(
         n, K, g, wr, nw, nullptr, c4, nullptr, nullptr, cols_row, nbr, nullptr, 0, counts,
-        col_masks);
+        col_masks, nullptr);
   else
     subm_probe_rows_kernel<3, 0, 0, true><<<ceil_div(n, 256), 256, 0, s>>>(
         n, K, g, wr, nw, nullptr, c4, nullptr, nullptr, cols_row, nbr, nullptr, 0, counts,
-        col_masks);
+        col_masks, nullptr);
   TSC_LAUNCH_CHECK("subm_probe_rows");
   return 0;
 }
