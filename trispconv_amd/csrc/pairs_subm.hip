@@ -308,7 +308,7 @@ __global__ void __launch_bounds__(256) subm_mark_kernel(const int4* __restrict__
                                                         uint2* __restrict__ col) {
   const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (r >= n) return;
-  col[r].x = 0u;
+  col[r] = make_uint2(0u, 0u);  // whole entries: no partly written sectors
   const int4 c = coords[r];
   if (!in_grid(g, c.x, c.y, c.z, c.w)) {
     flag_bad_row(g, c.x, status, host_flag);
