@@ -23,8 +23,9 @@
 //
 // Sorting: stable LSD radix passes with 9-bit digits (a 27-slot mask sorts
 // in three passes).  Each pass is a histogram kernel (per-block digit counts,
-// digit-major), one exclusive scan of all counts and a stable scatter in
-// which each wave ranks equal digits with nine ballots.  The first sort
+// digit-major), a scan of each digit's counts over the blocks (one workgroup
+// per digit) and a stable scatter, whose blocks add the digits' bases
+// themselves and in which each wave ranks equal digits with nine ballots.  The first sort
 // orders rows by their Morton code; the second carries Morton positions as
 // values and takes its digits from the mask at that position, then from the
 // region (position / region_rows).
@@ -225,15 +226,60 @@ __global__ void __launch_bounds__(kThreads) radix_hist_kernel(const uint32_t* __
   for (int r = threadIdx.x; r < kRadix; r += kThreads) hist[(int64_t)r * nblk + blockIdx.x] = s_h[r];
 }
 
+// One workgroup per digit: the exclusive scan of the digit's per-block counts
+// (hist_off[r][j] = items of digit r in blocks before j) and its total.
+__global__ void __launch_bounds__(kThreads) radix_digit_scan_kernel(
+    const uint32_t* __restrict__ hist, int nblk, uint32_t* __restrict__ hist_off,
+    uint32_t* __restrict__ digit_tot) {
+  __shared__ uint32_t s_wave[33];
+  const uint32_t* h = hist + (int64_t)blockIdx.x * nblk;
+  uint32_t* o = hist_off + (int64_t)blockIdx.x * nblk;
+  uint32_t carry = 0;
+  for (int base = 0; base < nblk; base += kThreads * 4) {
+    const int b0 = base + threadIdx.x * 4;  // four consecutive blocks per thread
+    uint32_t v[4];
+    uint32_t acc = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[j] = b0 + j < nblk ? h[b0 + j] : 0u;
+      acc += v[j];
+    }
+    uint32_t tot;
+    uint32_t run = carry + block_exclusive(acc, s_wave, &tot);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (b0 + j < nblk) o[b0 + j] = run;
+      run += v[j];
+    }
+    carry += tot;
+  }
+  if (threadIdx.x == 0) digit_tot[blockIdx.x] = carry;
+}
+
+// Each block starts digit r at (items of smaller digits) + hist_off[r][block]:
+// the digit bases are an exclusive scan of the digit totals, made by every
+// block in LDS (two digits per thread), so a pass needs no separate scan of
+// the digits.
+static_assert(kRadix == 2 * kThreads, "two digits per thread in the digit-base scan");
+
 __global__ void __launch_bounds__(kThreads) radix_scatter_kernel(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, int64_t n,
-    Digits d, const uint32_t* __restrict__ hist_off, int nblk, uint32_t* __restrict__ keys_out,
-    uint32_t* __restrict__ vals_out) {
+    Digits d, const uint32_t* __restrict__ hist_off, const uint32_t* __restrict__ digit_tot,
+    int nblk, uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out) {
   __shared__ uint32_t s_run[kRadix];                   // placed so far, per digit
   __shared__ uint32_t s_wc[kThreads / kWave][kRadix];  // this round, per wave, per digit
+  __shared__ uint32_t s_wave[33];
   const int t = threadIdx.x;
   const int w = t / kWave;
-  for (int r = t; r < kRadix; r += kThreads) s_run[r] = hist_off[(int64_t)r * nblk + blockIdx.x];
+  {
+    const uint32_t c0 = digit_tot[2 * t], c1 = digit_tot[2 * t + 1];
+    const uint32_t o0 = hist_off[(int64_t)(2 * t) * nblk + blockIdx.x];
+    const uint32_t o1 = hist_off[(int64_t)(2 * t + 1) * nblk + blockIdx.x];
+    uint32_t tot;
+    const uint32_t base = block_exclusive(c0 + c1, s_wave, &tot);
+    s_run[2 * t] = base + o0;
+    s_run[2 * t + 1] = base + c0 + o1;
+  }
   const int64_t base = blockIdx.x * (int64_t)kTile;
   for (int j = 0; j < kItems; ++j) {
     for (int r = t; r < kRadix; r += kThreads)
@@ -275,7 +321,7 @@ __global__ void __launch_bounds__(kThreads) radix_scatter_kernel(
 }
 
 struct Buffers {
-  uint32_t *keys_a, *keys_b, *vals_a, *vals_b, *rows, *mask_pos, *hist, *hist_off, *scratch;
+  uint32_t *keys_a, *keys_b, *vals_a, *vals_b, *rows, *mask_pos, *hist, *hist_off, *digit_tot;
 };
 
 Buffers carve(void* ws, int64_t n, int64_t* used) {
@@ -291,7 +337,7 @@ Buffers carve(void* ws, int64_t n, int64_t* used) {
   b.mask_pos = c.take<uint32_t>(m);
   b.hist = c.take<uint32_t>(nblk * kRadix);
   b.hist_off = c.take<uint32_t>(nblk * kRadix);
-  b.scratch = c.take<uint32_t>(scan_scratch_words(nblk * kRadix));
+  b.digit_tot = c.take<uint32_t>(kRadix);
   if (used) *used = c.used;
   return b;
 }
@@ -303,10 +349,10 @@ int radix_pass(const Buffers& b, const uint32_t* keys_in, const uint32_t* vals_i
   const int nblk = static_cast<int>(ceil_div(n, kTile));
   radix_hist_kernel<<<nblk, kThreads, 0, s>>>(vals_in, n, d, b.hist, nblk);
   TSC_LAUNCH_CHECK("plan_hist");
-  int rc = exclusive_scan_u32(b.hist, 2, (int64_t)nblk * kRadix, b.hist_off, nullptr, b.scratch, s);
-  if (rc) return rc;
-  radix_scatter_kernel<<<nblk, kThreads, 0, s>>>(keys_in, vals_in, n, d, b.hist_off, nblk, keys_out,
-                                                 vals_out);
+  radix_digit_scan_kernel<<<kRadix, kThreads, 0, s>>>(b.hist, nblk, b.hist_off, b.digit_tot);
+  TSC_LAUNCH_CHECK("plan_digit_scan");
+  radix_scatter_kernel<<<nblk, kThreads, 0, s>>>(keys_in, vals_in, n, d, b.hist_off, b.digit_tot,
+                                                 nblk, keys_out, vals_out);
   TSC_LAUNCH_CHECK("plan_scatter");
   return 0;
 }
