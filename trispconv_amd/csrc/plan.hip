@@ -99,17 +99,16 @@ __global__ void __launch_bounds__(256) spatial_key_kernel(const int4* __restrict
   keys[o] = (batch_shift >= 32 ? 0u : (static_cast<uint32_t>(c.x) << batch_shift)) | spatial;
 }
 
-__global__ void __launch_bounds__(256) iota_u32_kernel(uint32_t* p, int64_t n) {
-  const int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (i < n) p[i] = static_cast<uint32_t>(i);
-}
-
 // mask_row[o] = slot mask of output row o.  Lanes take consecutive rows, so
 // every slot's map column is read coalesced; eight slots' loads in flight.
+// vals (may be null): vals[o] = o as well (columns that are their own
+// Morton positions: mask_row is then mask_pos).
 __global__ void __launch_bounds__(256) row_mask_kernel(const int32_t* __restrict__ nbr, int64_t n,
-                                                       int K, uint32_t* __restrict__ mask_row) {
+                                                       int K, uint32_t* __restrict__ mask_row,
+                                                       uint32_t* __restrict__ vals) {
   const int64_t o = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (o >= n) return;
+  if (vals) vals[o] = static_cast<uint32_t>(o);
   uint32_t m = 0;
   for (int k0 = 0; k0 < K; k0 += 8) {
     int32_t v[8];
@@ -178,7 +177,7 @@ __global__ void __launch_bounds__(256) gather_rows_kernel(const uint32_t* __rest
                           ? static_cast<int64_t>(tile_perm[tile]) * kConvTileRows + i % kConvTileRows
                           : i;
   const uint32_t mp = pos[src];  // the column's Morton position
-  const uint32_t col = cols[mp];
+  const uint32_t col = cols ? cols[mp] : mp;  // null: columns in (b,z,y,x) order are their positions
   perm[i] = col;
   order[i] = cols_row ? cols_row[col] : static_cast<int32_t>(col);
   if (pos_masks) pos_masks[i] = mask_pos[mp];
@@ -397,8 +396,10 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_
   // ---- sort 1: map columns by the Morton code of their rows (columns that
   // are already in (b,z,y,x) order keep it)
   if (raster) {
-    iota_u32_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(b.rows, n_out);
-    TSC_LAUNCH_CHECK("plan_iota");
+    // each column is its own Morton position: its slot mask goes straight to
+    // mask_pos, with the positions as the values to sort
+    row_mask_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(nbr, n_out, k_vol, b.mask_pos, b.vals_a);
+    TSC_LAUNCH_CHECK("plan_row_mask");
   } else {
     int extent = out_spatial[0];
     if (out_spatial[1] > extent) extent = out_spatial[1];
@@ -425,11 +426,13 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_
   // ---- sort 2: Morton positions by (region, mask), stable
   // the sort-1 keys are dead now: keys_a holds each column's slot mask,
   // keys_b the final column permutation
-  row_mask_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(nbr, n_out, k_vol, b.keys_a);
-  TSC_LAUNCH_CHECK("plan_row_mask");
-  mask_at_pos_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(b.keys_a, n_out, b.rows, b.mask_pos,
-                                                          b.vals_a);
-  TSC_LAUNCH_CHECK("plan_mask");
+  if (!raster) {
+    row_mask_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(nbr, n_out, k_vol, b.keys_a, nullptr);
+    TSC_LAUNCH_CHECK("plan_row_mask");
+    mask_at_pos_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(b.keys_a, n_out, b.rows, b.mask_pos,
+                                                            b.vals_a);
+    TSC_LAUNCH_CHECK("plan_mask");
+  }
   uint32_t* vi = b.vals_a;
   uint32_t* vo = b.vals_b;
   const int mask_bits = k_vol < 32 ? k_vol : 32;
@@ -467,7 +470,7 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_
     tile_perm = tvi;
   }
   gather_rows_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(
-      vi, b.rows, cols_row, n_out, tile_perm, n_tiles, b.mask_pos, b.keys_b, order,
+      vi, raster ? nullptr : b.rows, cols_row, n_out, tile_perm, n_tiles, b.mask_pos, b.keys_b, order,
       reinterpret_cast<uint32_t*>(pos_masks));
   TSC_LAUNCH_CHECK("plan_gather");
   if (nbr_ordered) {
