@@ -16,8 +16,9 @@ them), inputs already resident in HBM:
   voxelnet_encoder4x60k  SparseSequential encoder, 11 conv layers with eval
                          BatchNorm1d + ReLU (fused into the conv stores), fp16
 
-Prints ONE JSON line.  Its top-level fields are the headline layer's
-(``value`` = voxels/s = N_in / step time); ``configs`` holds every workload:
+Prints one short JSON line per workload, the headline layer's last (its
+``value`` = voxels/s = N_in / step time); the full results, per layer, go to
+``--detail`` (default gpurun_out/bench_detail.json).  Each workload gets:
 voxels/s, effective TFLOP/s, per-layer conv times (HIP events on the stream
 the kernels run on, between the layers of the network run in order; each
 includes the few microseconds its event adds, so a network's layer times sum
@@ -64,6 +65,9 @@ def parse():
                     help="first run one elementwise negation over this many MiB (a copy-like "
                          "kernel of known size to scale FETCH_SIZE / WRITE_SIZE counters by)")
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--detail", default=str(ROOT / "gpurun_out" / "bench_detail.json"),
+                    help="file for every workload's full results (per layer); stdout gets one "
+                         "short line per workload, the headline last")
     return ap.parse_args()
 
 
@@ -613,6 +617,77 @@ def main():
         torch.cuda.empty_cache()
         log(args, json.dumps(results[name]))
     head = results[names[0]]
+    # every field of every workload, per layer, goes to a file; stdout gets
+    # one short line per workload, the headline line last
+    detail = Path(args.detail)
+    detail.parent.mkdir(parents=True, exist_ok=True)
+    detail.write_text(json.dumps({"configs": results}, indent=1))
+    for name in names[1:]:
+        print(json.dumps(config_line(results[name])), flush=True)
+    print(json.dumps(headline_line(head, args, detail)), flush=True)
+
+
+def _sig(x, digits=4):
+    """Floats rounded to a few significant digits, recursively (short lines)."""
+    if isinstance(x, float):
+        return float(f"{x:.{digits}g}")
+    if isinstance(x, dict):
+        return {k: _sig(v, digits) for k, v in x.items()}
+    if isinstance(x, (list, tuple)):
+        return [_sig(v, digits) for v in x]
+    return x
+
+
+_ROOF_KEYS = ("bound", "achieved", "peak", "unit", "frac", "traffic", "kernel", "kernel_ms",
+              "layer", "rows_out", "mfma_frac", "hbm_frac")
+
+
+def _short_roofline(r):
+    out = {k: r.get(k) for k in _ROOF_KEYS}
+    if r.get("traffic"):
+        out["traffic_over_algorithmic"] = r["traffic"] / r["algorithmic_bytes"]
+    out["algorithmic_bytes"] = r["algorithmic_bytes"]
+    return out
+
+
+def _short_cpu(cb):
+    if cb is None:
+        return None
+    keys = ("value", "unit", "cores", "kind", "dtype", "conv_pairs_frac", "pair_build_ms",
+            "conv_ms", "value_fp32", "conv_pairs_frac_fp32", "conv_ms_fp32")
+    out = {k: cb[k] for k in keys if k in cb}
+    out["sample"] = (f"{cb['dtype']} conv on {cb['conv_pairs_frac']:.3g} of every slot's pairs "
+                     "(scaled by its inverse), pair builds in full; reference torch op sequence "
+                     "on CPU tensors, median of 3")
+    return out
+
+
+def config_line(res):
+    """One workload as a short JSON line (~1 KB)."""
+    line = {
+        "config_result": res["workload"], "dtype": res["dtype"], "voxels": res["voxels"],
+        "batch": res["batch"], "pairs": res["pairs"], "ms_per_step": res["ms_per_step"],
+        "voxels_per_s": res["voxels_per_s"], "tflops_effective": res["tflops_effective"],
+        "pair_build_ms": res["pair_build_ms"], "plan_ms": res["plan_ms"],
+        "network_ms_cold": res["network_ms_cold"],
+    }
+    if "pair_build_hbm" in res:
+        line["pair_build_hbm_frac"] = res["pair_build_hbm"]["frac"]
+    if "layers" in res:
+        line["layer_conv_ms"] = [lay["conv_ms"] for lay in res["layers"]]
+        line["layer_pair_build_ms"] = [lay["pair_build_ms"] for lay in res["layers"]]
+        line["layer_pair_build_hbm_frac"] = [lay["pair_build_hbm"]["frac"]
+                                             for lay in res["layers"]]
+    for k in ("network_ms_graph", "graph_equal"):
+        if k in res:
+            line[k] = res[k]
+    line["roofline"] = _short_roofline(res["roofline"])
+    line["cpu_baseline"] = _short_cpu(res.get("cpu_baseline"))
+    return _sig(line)
+
+
+def headline_line(head, args, detail):
+    """The headline workload's line, the last one printed (under 2 KB)."""
     lay = head.get("layers_desc", [""])[0]
     line = {
         "metric": METRIC,
@@ -627,21 +702,22 @@ def main():
         "vs_baseline": None,
         "dtype": head["dtype"],
         "data": "synthetic (seeded voxels, N(0,1) features, kaiming-uniform KRSC weights, "
-                "U(-0.1,0.1) biases; random BatchNorm statistics in the encoder)",
+                "U(-0.1,0.1) biases)",
         "config": {"workload": head["workload"], "layer": lay, "voxels": head["voxels"],
                    "spatial_shape": head["spatial_shape"], "batch": head["batch"],
                    "pairs": head["pairs"]},
         "tflops_effective": head["tflops_effective"],
+        "conv_kernel_ms": head["roofline"]["kernel_ms"],
         "pair_build_ms": head["pair_build_ms"],
         "pair_build_with_counts_ms": head["pair_build_with_counts_ms"],
-        "pair_build_hbm": head.get("pair_build_hbm"),
+        "pair_build_hbm_frac": head.get("pair_build_hbm", {}).get("frac"),
         "plan_ms": head["plan_ms"],
-        "conv_kernel_ms": head["roofline"]["kernel_ms"],
-        "roofline": head["roofline"],
-        "cpu_baseline": head.get("cpu_baseline"),
-        "configs": results,
+        "network_ms_cold": head["network_ms_cold"],
+        "roofline": _short_roofline(head["roofline"]),
+        "cpu_baseline": _short_cpu(head.get("cpu_baseline")),
+        "detail": str(detail),
     }
-    print(json.dumps(line), flush=True)
+    return _sig(line, 5)
 
 
 if __name__ == "__main__":

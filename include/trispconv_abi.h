@@ -135,9 +135,11 @@ TSC_API int tsc_subm_pairs_noalloc(const int32_t* coords, int64_t n, int32_t bat
  * :143-259) skips zeroing, marking, scanning and ranking and runs only the
  * probe.  Writes cols_row[t] = t, nbr [K][n] by row, counts [K+2] as
  * tsc_subm_pairs (counts[K+1] = 1).  Kernels 3 cells wide in x, dilation
- * < 16 in x.  A neighbour whose rank is not below n (rows that are not the
- * bitmap's cells) is left out of the map and sets TSC_FLAG_ROWS_NOT_BITMAP
- * in counts[K].  mask_row != 0 (K <= 32): nbr has K + 1 rows and row K
+ * < 16 in x.  The rows must be the bitmap's first n occupied cells in rank
+ * order; otherwise TSC_FLAG_ROWS_NOT_BITMAP is set in counts[K]: a row whose
+ * own cell is empty or has another rank than the row (a permuted, foreign or
+ * out-of-grid row), or a neighbour whose rank is not below n (that neighbour
+ * is left out of the map).  mask_row != 0 (K <= 32): nbr has K + 1 rows and row K
  * receives each column's slot mask, as in tsc_subm_pairs_checked. */
 TSC_API int tsc_subm_pairs_from_bitmap(const int32_t* coords, int64_t n, int32_t batch_size,
                                        const int32_t spatial[3] /* host */,
@@ -339,8 +341,8 @@ TSC_API const char* tsc_conv_kernel_name(int32_t dtype, int32_t c_in, int32_t c_
  * Sparse -> dense.  Replaces SparseConvTensor.dense (trispconv/pytorch/
  * tensor.py:72-99): writes out, zero-filled, of shape (B, C, D, H, W) when
  * channels_first != 0 else (B, D, H, W, C), with row r's C features at its
- * coordinate.  elem_bytes is the feature element size (2 or 4; the values are
- * copied bit for bit).  A row whose coordinate lies outside [0,B) x [0,D) x
+ * coordinate.  elem_bytes is the feature element size (1, 2, 4 or 8: any
+ * dtype; the values are copied bit for bit).  A row whose coordinate lies outside [0,B) x [0,D) x
  * [0,H) x [0,W) is not written and sets *status to 1 (device int32, the
  * reference's range assertions).  out must be 16-byte aligned.
  * ------------------------------------------------------------------------ */

@@ -46,9 +46,12 @@ def conv_forward(features: np.ndarray, weight: np.ndarray, bias: Optional[np.nda
                  n_out: int, acc_dtype=np.float64) -> np.ndarray:
     """functional.py:38-51: slot-ordered gather -> matmul -> add, then bias.
 
-    Within one slot the output ids are distinct (indices.py:123-124 and
-    :235-240 emit each output at most once per slot), so a fancy-index ``+=``
-    is the same as ``index_add_``.
+    ``index_add_`` (functional.py:46) adds every row of a slot, so an output
+    id listed twice within a slot gets both contributions.  The generators'
+    lists name each output at most once per slot (indices.py:123-124 and
+    :235-240); there a fancy-index ``+=`` is the same, and it is used when a
+    slot's ids are distinct; lists assigned by hand may repeat ids, and those
+    slots accumulate with ``np.add.at``.
     """
     f = features.astype(acc_dtype, copy=False)
     w = weight.astype(acc_dtype, copy=False)
@@ -56,7 +59,11 @@ def conv_forward(features: np.ndarray, weight: np.ndarray, bias: Optional[np.nda
     for k, (pi, po) in enumerate(zip(pairs_in, pairs_out)):
         if len(pi) == 0:
             continue
-        out[po] += f[pi] @ w[k]
+        po = np.asarray(po, dtype=np.int64)
+        if np.bincount(po, minlength=n_out).max() > 1:
+            np.add.at(out, po, f[pi] @ w[k])
+        else:
+            out[po] += f[pi] @ w[k]
     if bias is not None:
         out = out + bias.astype(acc_dtype)
     return out

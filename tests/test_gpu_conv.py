@@ -351,8 +351,9 @@ def _conv_raw(feats, pw, bias, nbr, order, ordered, n_out, tile):
 def test_dma_kernel_matches_the_register_gather_kernel(dtype, rows, grid, monkeypatch):
     """A 128-column layer: the direct-to-LDS kernel (the layer's own choice)
     against the register-gather kernel forced to the same width, bit for bit,
-    with the map permuted into the execution order, with the row-major map
-    plus the order, and with the row-major map alone.  150k rows (586 tiles
+    with the map permuted into the execution order (with and without the
+    plan's row of slot masks, which only the direct-to-LDS kernel reads), with
+    the row-major map plus the order, and with the row-major map alone.  150k rows (586 tiles
     of 256 rows) take its 32-rows-per-wave form, 300k rows (1172 tiles) its
     64-rows-per-wave form; 50k rows (196 tiles) narrow the column tile to
     32."""
@@ -368,9 +369,16 @@ def test_dma_kernel_matches_the_register_gather_kernel(dtype, rows, grid, monkey
     order = data.execution_order(n, DEV, 128 * feats.element_size(), eager=True)
     assert order is not None
     permuted, order2, ordered = data.conv_operands(n, DEV, 128 * feats.element_size())
-    assert ordered and order2 is order
+    assert ordered == 2 and order2 is order
+    # the plan's row K after the permuted map: each position's slot mask
+    mask_row = permuted.as_strided((n,), (1,), permuted.storage_offset() + 27 * n)
+    bits = ((permuted >= 0).to(torch.int64)
+            << torch.arange(27, device=DEV, dtype=torch.int64).view(27, 1)).sum(0)
+    assert torch.equal(mask_row.to(torch.int64), bits)
     rowmajor = data.neighbour_map(n, DEV)
-    for label, ops in (("permuted map", (permuted, order, 1)), ("row-major map + order", (rowmajor, order, 0)),
+    for label, ops in (("permuted map + slot masks", (permuted, order, 2)),
+                       ("permuted map", (permuted, order, 1)),
+                       ("row-major map + order", (rowmajor, order, 0)),
                        ("row-major map", (rowmajor, None, 0))):
         say("dma vs register gather", dtype, label)
         dma = _conv_raw(feats, pw, m.bias, *ops, n, 0)

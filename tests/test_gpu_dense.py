@@ -45,6 +45,29 @@ def test_dense_matches_reference(dtype, channels_first, B, shape, C, n):
     assert torch.equal(got, ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.float64, torch.int64, torch.int16, torch.uint8,
+                                   torch.bool])
+@pytest.mark.parametrize("channels_first", [True, False])
+def test_dense_any_element_size(dtype, channels_first):
+    """The reference allocates the dense tensor in the features' own dtype,
+    whatever it is (tensor.py:84-88): 8-, 2- and 1-byte elements too."""
+    B, shape, C, n = 2, (5, 6, 7), 3, 120
+    say("dense any dtype:", dtype, channels_first)
+    idx = _unique_cells(7, B, shape, n)
+    g = torch.Generator().manual_seed(11)
+    if dtype.is_floating_point:
+        feats = torch.randn(n, C, generator=g, dtype=torch.float64).to(dtype)
+    elif dtype == torch.bool:
+        feats = torch.randint(0, 2, (n, C), generator=g).bool()
+    else:
+        feats = torch.randint(0, 100, (n, C), generator=g).to(dtype)
+    x = spconv.SparseConvTensor(feats.to(DEV), idx.to(DEV), list(shape), B)
+    got = x.dense(channels_first=channels_first).cpu()
+    ref = _reference_dense(feats, idx, B, shape, channels_first)
+    assert got.dtype == dtype and got.shape == ref.shape
+    assert torch.equal(got, ref)
+
+
 def test_dense_out_of_range_raises():
     idx = torch.tensor([[0, 1, 1, 1], [0, 4, 0, 0]], dtype=torch.int32, device=DEV)
     x = spconv.SparseConvTensor(torch.ones(2, 3, device=DEV), idx, [4, 4, 4], 1)

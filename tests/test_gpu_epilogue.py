@@ -281,8 +281,9 @@ def test_voxelnet_encoder_full_size_fused_against_oracle():
     running statistics) and a ReLU, fused into the conv stores.  Layer by
     layer on the GPU's own layer inputs, every output row against the fp64
     oracle (conv, bias, batch norm and ReLU in fp64) at the fp16 tolerance;
-    output coordinates exact; the whole forward equal to the layer-by-layer
-    chain bit for bit."""
+    output coordinates, pair_num and every slot's pair lists of every
+    indice_key exact; the whole forward equal to the layer-by-layer chain bit
+    for bit."""
     from trispconv_amd import workloads
 
     w = workloads.make_workload("voxelnet_encoder4x60k")
@@ -336,6 +337,17 @@ def test_voxelnet_encoder_full_size_fused_against_oracle():
                                      if m.subm else
                                      OP.strided_pairs(idx, shape, w.batch_size, m.kernel_size,
                                                       m.stride, m.padding, m.dilation))
+                # the layer's pair lists, bit for bit, once per key: the
+                # submanifold builds of layers 3, 6 and 9 run on the strided
+                # output bitmap (tsc_subm_pairs_from_bitmap)
+                got = y.indice_dict[key]
+                pr = oracle_pairs[key]
+                assert got.pair_num.tolist() == pr.pair_num.tolist(), (li, key)
+                for k in range(len(pr.pairs_in)):
+                    assert np.array_equal(got.pairs_in[k].cpu().numpy(), pr.pairs_in[k]), (li, k)
+                    assert np.array_equal(got.pairs_out[k].cpu().numpy(), pr.pairs_out[k]), (li, k)
+                say(f"encoder layer {li} key {key}: pair lists equal,",
+                    int(pr.pair_num.sum()), "pairs")
             pr = oracle_pairs[key]
             assert np.array_equal(y.indices.cpu().numpy(), pr.out_indices), li
             wt = OC.normalize_weight(to_np(m.weight).astype(np.float64), m.kernel_size,

@@ -269,6 +269,39 @@ def test_bitmap_build_flags_rows_that_are_not_its_cells():
     assert int(nbr.max()) < n
 
 
+def test_bitmap_build_on_permuted_rows_raises_at_first_reuse():
+    """The strided output coordinates permuted in place through ``.data``
+    (same tensor, address and version counter: a write the reuse key cannot
+    see).  The build on the strided bitmap checks every row's own cell rank on
+    the device, and the first reuse of the pairs under their key reads that
+    flag and raises."""
+    import trispconv.pytorch as spconv
+    idx = _tiny(47, (17, 18, 19), 2, 900)
+    fwd = generate_strided_indice_pairs(torch.from_numpy(idx).to(DEV), (17, 18, 19), 2, 3, 2, 1)
+    out = fwd.out_indices
+    shape = tuple(fwd.output_spatial_shape)
+    # unpermuted: the pairs' first reuse reads a clean flag
+    ok = generate_subm_indice_pairs(out, shape, 2, 3)
+    assert ok._deferred_check
+    conv = spconv.SubMConv3d(8, 8, 3, indice_key="s").to(DEV)
+    x = spconv.SparseConvTensor(torch.randn(len(out), 8, device=DEV), out, list(shape), 2)
+    x.indice_dict["s"] = ok
+    conv(conv(x))
+    assert not ok._deferred_check
+    perm = torch.randperm(len(out), generator=torch.Generator().manual_seed(0)).to(DEV)
+    version = out._version
+    out.data.copy_(out.data[perm])
+    assert out._version == version
+    say("bitmap build on permuted rows")
+    bad = generate_subm_indice_pairs(out, shape, 2, 3)
+    assert bad._deferred_check  # still taken for the registered output set
+    x = spconv.SparseConvTensor(torch.randn(len(out), 8, device=DEV), out, list(shape), 2)
+    x.indice_dict["s"] = bad
+    y = conv(x)
+    with pytest.raises(RuntimeError, match="not the rows"):
+        conv(y)
+
+
 def _map_by_rows(lib, L, nbr_cols, cols_row, n, K):
     """A column map in row order (tsc_map_to_rows): comparable across builds
     that place the columns of repeated coordinates in different orders."""

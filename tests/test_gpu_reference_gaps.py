@@ -2,7 +2,8 @@
 
 * user-assigned pair lists: ids out of range raise IndexError before any
   launch (the reference's ``features[in_ids]`` / ``index_add_``,
-  functional.py:46), an output named twice in a slot raises ValueError;
+  functional.py:46); an output named more than once within a slot gets every
+  contribution, as ``index_add_`` adds them;
 * the inverse built from user-assigned forward lists (modules.py:175-212
   remaps whatever lists it finds);
 * float64 features and weights of another dtype than the features run on
@@ -71,14 +72,8 @@ def test_user_lists_out_of_range_raise_index_error():
         say("user lists: bad", what, k_bad, val)
         with pytest.raises(IndexError):
             Fn.sparse_conv_forward(feats, W, None, _hand_copy(data, pin, pout), n)
-    # an output named twice within one slot
-    pin = [p.clone() for p in data.pairs_in]
-    pout = [p.clone() for p in data.pairs_out]
-    k = max(range(27), key=lambda s: pout[s].numel())
-    pout[k][1] = pout[k][0]
-    with pytest.raises(ValueError):
-        Fn.sparse_conv_forward(feats, W, None, _hand_copy(data, pin, pout), n)
     # mismatched list lengths
+    k = max(range(27), key=lambda s: data.pairs_out[s].numel())
     pout = [p.clone() for p in data.pairs_out]
     pout[k] = pout[k][:-1]
     with pytest.raises(ValueError):
@@ -88,6 +83,90 @@ def test_user_lists_out_of_range_raise_index_error():
         Fn.sparse_conv_forward(feats[: n // 2], W, None, _hand_copy(data), n)
     with pytest.raises(IndexError):
         Fn.sparse_conv_forward(feats[: n // 2], W, None, data, n)
+
+
+@pytest.mark.parametrize("dtype,c_in,c_out,reps", [
+    (torch.float32, 16, 16, 2),   # 54 map rows: narrow MFMA kernel
+    (torch.float16, 32, 32, 2),   # 54 map rows: 32x32-tile MFMA kernel
+    (torch.bfloat16, 32, 64, 3),  # 81 map rows: past the 64-slot tile kernels
+    (torch.float32, 5, 7, 3),     # VALU kernel
+])
+def test_user_lists_repeated_output_in_a_slot_sums(dtype, c_in, c_out, reps):
+    """Hand-built lists that name an output row more than once within a slot
+    (and an input row more than once): the reference's index_add_
+    (functional.py:46) adds every contribution; so does the fused kernel,
+    against the oracle's np.add.at accumulation."""
+    idx = _tiny(21, (12, 12, 12), 1, 600)
+    n = len(idx)
+    data = generate_subm_indice_pairs(torch.from_numpy(idx).to(DEV), (12, 12, 12), 1, 3)
+    rng = np.random.default_rng(c_in + reps)
+    pin = lists_np(data.pairs_in)
+    pout = lists_np(data.pairs_out)
+    for k in (0, 4, 13, 26):
+        if len(pout[k]) < 4:
+            continue
+        # duplicate a few pairs' outputs with other inputs, up to reps times
+        pick = rng.choice(len(pout[k]), size=min(5, len(pout[k])), replace=False)
+        extra_out = np.concatenate([pout[k][pick]] * (reps - 1))
+        extra_in = rng.integers(0, n, size=len(extra_out))
+        pout[k] = np.concatenate([pout[k], extra_out])
+        pin[k] = np.concatenate([pin[k], extra_in])
+        perm = rng.permutation(len(pout[k]))
+        pout[k], pin[k] = pout[k][perm], pin[k][perm]
+    hand = _hand_copy(data, [torch.from_numpy(p).to(DEV) for p in pin],
+                      [torch.from_numpy(p).to(DEV) for p in pout])
+    g = torch.Generator().manual_seed(2)
+    feats = torch.randn(n, c_in, generator=g).to(dtype)
+    W = (torch.randn(27, c_in, c_out, generator=g) / (27 * c_in) ** 0.5).to(dtype)
+    b = (torch.rand(c_out, generator=g) * 0.2 - 0.1).to(dtype)
+    say("repeated outputs:", dtype, c_in, c_out, reps)
+    out = Fn.sparse_conv_forward(feats.to(DEV), W.to(DEV), b.to(DEV), hand, n)
+    assert hand.slot_repeat == reps
+    ref = OC.conv_forward(rounded(to_np(feats), dtype), rounded(to_np(W), dtype),
+                          rounded(to_np(b), dtype), pin, pout, n)
+    tol = 1e-5 if dtype == torch.float32 else 1e-2
+    err = rel_err(to_np(out), ref)
+    say("  rel err", err)
+    assert err <= tol
+    # the same lists without the repeats run on the one-row-per-slot map
+    assert data.slot_repeat == 1
+
+
+def test_inverse_from_forward_lists_with_a_repeated_input_row():
+    """A forward pairs_in list that names an input row twice within a slot:
+    the inverse names that output twice (modules.py:175-212 remaps the lists
+    as they are) and adds both contributions."""
+    shape = (10, 12, 11)
+    idx = _tiny(23, shape, 1, 400)
+    fwd = generate_strided_indice_pairs(torch.from_numpy(idx).to(DEV), shape, 1, 3, 2, 1)
+    pin = lists_np(fwd.pairs_in)
+    pout = lists_np(fwd.pairs_out)
+    k = max(range(27), key=lambda s: len(pin[s]))
+    # pair the slot's first input row with one more output of this slot
+    extra_out = int(pout[k][1])
+    pin[k] = np.concatenate([pin[k], pin[k][:1]])
+    pout[k] = np.concatenate([pout[k], [extra_out]])
+    fwd.pairs_in = [torch.from_numpy(p).to(DEV) for p in pin]
+    fwd.pairs_out = [torch.from_numpy(p).to(DEV) for p in pout]
+    fwd.pair_num = torch.tensor([len(p) for p in pin], dtype=torch.long)
+    n_down = len(fwd.out_indices)
+    torch.manual_seed(6)
+    up = spconv.SparseInverseConv3d(16, 8, 3, indice_key="d").to(DEV)
+    xs = torch.randn(n_down, 16, device=DEV)
+    t = spconv.SparseConvTensor(xs, fwd.out_indices, list(fwd.output_spatial_shape), 1)
+    t.indice_dict["d"] = fwd
+    say("inverse with a repeated forward input row")
+    y = up(t)
+    exp_fwd = OP.OraclePairs(fwd.out_indices.cpu().numpy(), pin, pout,
+                             np.array([len(p) for p in pin]), idx, shape,
+                             tuple(fwd.output_spatial_shape), (3, 3, 3), (2, 2, 2), (1, 1, 1),
+                             (1, 1, 1), False)
+    inv = OP.inverse_pairs(exp_fwd)
+    assert np.array_equal(y.indices.cpu().numpy(), inv.out_indices)
+    w = OC.normalize_weight(to_np(up.weight).astype(np.float64), (3, 3, 3), 16, 8)
+    ref = OC.conv_forward(to_np(xs).astype(np.float64), w, to_np(up.bias).astype(np.float64),
+                          inv.pairs_in, inv.pairs_out, len(inv.out_indices))
+    assert rel_err(to_np(y.features), ref) <= 1e-5
 
 
 def test_reassigning_one_list_keeps_the_other():
@@ -177,11 +256,30 @@ def test_float64_features_compute_in_fp32_and_come_back_float64():
     err = rel_err(y.features.detach().cpu().numpy(), ref)
     say("float64 features", err)
     assert err <= 1e-5
-    # a strided layer and its inverse in float64 as well
+    # a strided layer and its inverse in float64 as well, each against the
+    # oracle on its own (GPU-computed) float64 input, at the same tolerance
     down = spconv.SparseConv3d(24, 32, 3, stride=2, padding=1, indice_key="d").to(DEV).double()
     up = spconv.SparseInverseConv3d(32, 16, 3, indice_key="d").to(DEV).double()
-    z = up(down(y))
-    assert z.features.dtype == torch.float64 and torch.isfinite(z.features).all()
+    with torch.no_grad():
+        down.bias.uniform_(-0.1, 0.1)
+        up.bias.uniform_(-0.1, 0.1)
+    d = down(y)
+    z = up(d)
+    assert d.features.dtype == torch.float64 and z.features.dtype == torch.float64
+    pd = OP.strided_pairs(idx, shape, 1, 3, 2, 1)
+    assert np.array_equal(d.indices.cpu().numpy(), pd.out_indices)
+    wd = OC.normalize_weight(down.weight.detach().cpu().numpy(), (3, 3, 3), 24, 32)
+    ref_d = OC.conv_forward(y.features.detach().cpu().numpy(), wd, down.bias.detach().cpu().numpy(),
+                            pd.pairs_in, pd.pairs_out, len(pd.out_indices))
+    err_d = rel_err(d.features.detach().cpu().numpy(), ref_d)
+    pu = OP.inverse_pairs(pd)
+    assert np.array_equal(z.indices.cpu().numpy(), pu.out_indices)
+    wu = OC.normalize_weight(up.weight.detach().cpu().numpy(), (3, 3, 3), 32, 16)
+    ref_u = OC.conv_forward(d.features.detach().cpu().numpy(), wu, up.bias.detach().cpu().numpy(),
+                            pu.pairs_in, pu.pairs_out, len(pu.out_indices))
+    err_u = rel_err(z.features.detach().cpu().numpy(), ref_u)
+    say("float64 strided", err_d, "inverse", err_u)
+    assert err_d <= 1e-5 and err_u <= 1e-5
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])

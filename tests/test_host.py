@@ -5,6 +5,7 @@ Mirrors the CPU-checkable parts of the reference's tests/test_tensor.py,
 test_indices_strided.py:119-127 and modules.py:46-51 / :149-155.
 """
 import ctypes
+import os
 import re
 from pathlib import Path
 
@@ -152,6 +153,54 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert getattr(lib, name) is not None
     assert lib.tsc_abi_version() == L.ABI_VERSION
+
+
+def test_indice_data_is_a_dataclass_with_the_reference_fields():
+    """IndiceData is a dataclass with the reference's twelve fields in its
+    order (indices.py:10-23): fields, replace, asdict and field-wise ==."""
+    import dataclasses
+    from trispconv.pytorch.indices import IndiceData
+    names = [f.name for f in dataclasses.fields(IndiceData)]
+    assert names == ["out_indices", "pairs_in", "pairs_out", "pair_num", "input_indices",
+                     "input_spatial_shape", "output_spatial_shape", "kernel_size", "stride",
+                     "padding", "dilation", "subm"]
+    assert all(f.default is dataclasses.MISSING for f in dataclasses.fields(IndiceData))
+    idx = torch.zeros(3, 4, dtype=torch.int32)
+    pin = [torch.tensor([0, 1]), torch.tensor([2])]
+    pout = [torch.tensor([1, 2]), torch.tensor([0])]
+    d = IndiceData(idx, pin, pout, torch.tensor([2, 1]), idx, (4, 4, 4), (4, 4, 4), (2, 1, 1),
+                   (1, 1, 1), (0, 0, 0), (1, 1, 1), False)
+    assert dataclasses.is_dataclass(d)
+    d2 = dataclasses.replace(d, subm=True)
+    assert d2.subm and not d.subm and d2.pairs_in is d.pairs_in
+    assert d == dataclasses.replace(d)
+    assert d != d2
+    a = dataclasses.asdict(d)
+    assert list(a) == names
+    assert torch.equal(a["pairs_out"][0], pout[0]) and torch.equal(a["pair_num"], d.pair_num)
+    # the lazy fields are still settable, as plain dataclass fields are
+    d.pair_num = torch.tensor([1, 1])
+    assert d.pair_num.tolist() == [1, 1]
+
+
+def test_integration_load_snippet_runs_as_written():
+    """The 'Build and load' snippet of INTEGRATION.md, executed as written
+    from the repository root: it loads the built library and asserts its ABI
+    version (no GPU call)."""
+    text = (ROOT / "INTEGRATION.md").read_text()
+    section = text.split("## Build and load", 1)[1]
+    blocks = re.findall(r"```python\n(.*?)```", section, flags=re.S)
+    assert blocks, "no python block under 'Build and load'"
+    snippet = blocks[0]
+    assert "tsc_abi_version()" in snippet
+    cwd = os.getcwd()
+    try:
+        os.chdir(ROOT)
+        scope: dict = {}
+        exec(compile(snippet, "INTEGRATION.md", "exec"), scope)
+    finally:
+        os.chdir(cwd)
+    assert scope["lib"].tsc_abi_version() == L.ABI_VERSION
 
 
 def test_workspace_queries_are_host_only():

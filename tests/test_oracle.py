@@ -334,3 +334,32 @@ def test_torch_path_conv_native_dtype_matches_oracle(dt):
     tol = {torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 4e-2}[dt]
     err = np.abs(out.double().numpy() - ref).max() / np.abs(ref).max()
     assert err < tol
+
+
+def test_oracle_conv_sums_an_output_repeated_within_a_slot():
+    """Hand-assigned lists may name an output row more than once within a
+    slot; the reference's CPU branch adds every pair with index_add_
+    (functional.py:46).  The oracle's accumulation is pinned against torch's
+    own index_add_ over the same lists, slot by slot, in float64."""
+    rng = np.random.default_rng(41)
+    n_in, n_out, c_in, c_out, K = 30, 12, 5, 4, 3
+    f = rng.standard_normal((n_in, c_in))
+    w = rng.standard_normal((K, c_in, c_out))
+    b = rng.standard_normal(c_out)
+    pin = [rng.integers(0, n_in, 20), rng.integers(0, n_in, 0), rng.integers(0, n_in, 9)]
+    pout = [rng.integers(0, n_out, 20), rng.integers(0, n_out, 0),
+            np.array([3, 3, 3, 0, 1, 3, 11, 0, 3])]
+    assert np.bincount(pout[0]).max() > 1  # slot 0 repeats outputs too
+    got = OC.conv_forward(f, w, b, pin, pout, n_out)
+    ref = torch.zeros(n_out, c_out, dtype=torch.float64)
+    ft, wt = torch.from_numpy(f), torch.from_numpy(w)
+    for k in range(K):
+        if len(pin[k]):
+            ref.index_add_(0, torch.from_numpy(pout[k]), ft[torch.from_numpy(pin[k])] @ wt[k])
+    ref = ref + torch.from_numpy(b)
+    assert np.allclose(got, ref.numpy(), rtol=0, atol=1e-12)
+    # a plain fancy-index += would keep one contribution per repeated output:
+    # the check above tells the two apart
+    once = np.zeros((n_out, c_out))
+    once[pout[2]] += f[pin[2]] @ w[2]
+    assert not np.allclose(once[3], (f[pin[2][pout[2] == 3]] @ w[2]).sum(0))

@@ -124,7 +124,9 @@ def test_noalloc_rejects_builds_beyond_its_scratch():
     n = int(limit // 16) + 1024
     B, shape = 1, (1 << 12, 1 << 12, 1 << 12)
     c = torch.zeros((n, 4), dtype=torch.int32, device=DEV)
-    cols_row, nbr, counts = _outputs(4, 27)
+    # outputs sized for the n rows: were the size check ever to let the call
+    # through, the kernels would still write inside them
+    cols_row, nbr, counts = _outputs(n, 27)
     rc = lib.tsc_subm_pairs_noalloc(c.data_ptr(), n, B, L.i3(shape), L.i3((3, 3, 3)),
                                     L.i3((1, 1, 1)), cols_row.data_ptr(), nbr.data_ptr(),
                                     counts.data_ptr(), L.stream_of(c))

@@ -463,7 +463,25 @@ int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStr
 // --------------------------------------------------- host status words --
 namespace {
 constexpr int kMaxStatusDevices = 64;
-thread_local HostStatus t_status[kMaxStatusDevices] = {};
+
+// Blocks of threads that have ended, per device, handed to the next thread
+// that needs one.  A block is idle when its thread ends: every call that
+// enqueues a write into it waits for that write before it returns, and each
+// call clears the words it waits on first.  So a program that builds pairs
+// from many short-lived threads holds as many blocks as it has such threads
+// alive at once, not one per thread it ever started.
+std::mutex g_free_mu;
+std::vector<HostStatus> g_free_blocks[kMaxStatusDevices];
+
+struct ThreadStatus {
+  HostStatus dev[kMaxStatusDevices] = {};
+  ~ThreadStatus() {
+    std::lock_guard<std::mutex> lock(g_free_mu);
+    for (int d = 0; d < kMaxStatusDevices; ++d)
+      if (dev[d].host) g_free_blocks[d].push_back(dev[d]);
+  }
+};
+thread_local ThreadStatus t_status;
 }  // namespace
 
 int host_status(HostStatus* out) {
@@ -473,7 +491,14 @@ int host_status(HostStatus* out) {
     return set_error(-static_cast<int>(e), "host_status: hipGetDevice: %s", hipGetErrorString(e));
   TSC_REQUIRE(dev >= 0 && dev < kMaxStatusDevices, "host_status: device %d beyond %d devices",
               dev, kMaxStatusDevices);
-  HostStatus& h = t_status[dev];
+  HostStatus& h = t_status.dev[dev];
+  if (!h.host) {
+    std::lock_guard<std::mutex> lock(g_free_mu);
+    if (!g_free_blocks[dev].empty()) {
+      h = g_free_blocks[dev].back();
+      g_free_blocks[dev].pop_back();
+    }
+  }
   if (!h.host) {
     void* p = nullptr;
     e = hipHostMalloc(&p, kHostWords * sizeof(int32_t), hipHostMallocMapped | hipHostMallocCoherent);

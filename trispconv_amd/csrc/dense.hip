@@ -29,7 +29,8 @@ __global__ void __launch_bounds__(256) zero_kernel(uint4* __restrict__ p, int64_
   if (blockIdx.x == 0 && threadIdx.x < tail_bytes) tail[threadIdx.x] = 0;
 }
 
-// One thread per (row, channel), channel fastest; `esize` bytes per element.
+// One thread per (row, channel), channel fastest; E is a raw element of the
+// features' size (1, 2, 4 or 8 bytes: every dtype the features may have).
 template <typename E>
 __global__ void __launch_bounds__(256) scatter_kernel(const E* __restrict__ feat,
                                                       const int4* __restrict__ coords, int64_t n,
@@ -65,7 +66,8 @@ extern "C" int tsc_dense_scatter(const void* feat, int32_t elem_bytes, int64_t n
                                  const int32_t spatial[3], int32_t channels_first, void* out,
                                  int32_t* status, tsc_stream_t stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
-  TSC_REQUIRE(elem_bytes == 2 || elem_bytes == 4, "dense: element size must be 2 or 4 bytes");
+  TSC_REQUIRE(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4 || elem_bytes == 8,
+              "dense: element size must be 1, 2, 4 or 8 bytes");
   TSC_REQUIRE(n >= 0 && c > 0 && batch_size > 0 && spatial, "dense: invalid sizes");
   TSC_REQUIRE(spatial[0] > 0 && spatial[1] > 0 && spatial[2] > 0, "dense: spatial shape must be positive");
   TSC_REQUIRE(out && status, "dense: null pointer");
@@ -85,16 +87,19 @@ extern "C" int tsc_dense_scatter(const void* feat, int32_t elem_bytes, int64_t n
   const int64_t work = n * c;
   const unsigned grid = static_cast<unsigned>(std::min<int64_t>(ceil_div(work, 256), 65536));
   const int4* c4 = reinterpret_cast<const int4*>(coords);
-  if (elem_bytes == 2)
-    scatter_kernel<uint16_t><<<grid, 256, 0, s>>>(static_cast<const uint16_t*>(feat), c4, n, c,
-                                                  batch_size, spatial[0], spatial[1], spatial[2],
-                                                  channels_first, static_cast<uint16_t*>(out),
-                                                  status);
-  else
-    scatter_kernel<uint32_t><<<grid, 256, 0, s>>>(static_cast<const uint32_t*>(feat), c4, n, c,
-                                                  batch_size, spatial[0], spatial[1], spatial[2],
-                                                  channels_first, static_cast<uint32_t*>(out),
-                                                  status);
+  // the values are moved as raw elements of their size: any dtype of that size
+  auto launch = [&](auto tag) {
+    using E = decltype(tag);
+    scatter_kernel<E><<<grid, 256, 0, s>>>(static_cast<const E*>(feat), c4, n, c, batch_size,
+                                           spatial[0], spatial[1], spatial[2], channels_first,
+                                           static_cast<E*>(out), status);
+  };
+  switch (elem_bytes) {
+    case 1: launch(uint8_t{}); break;
+    case 2: launch(uint16_t{}); break;
+    case 4: launch(uint32_t{}); break;
+    default: launch(uint64_t{}); break;
+  }
   TSC_LAUNCH_CHECK("dense_scatter");
   return 0;
 }

@@ -573,15 +573,22 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
       }
     }
     if constexpr (IDENT) {
+      // the kernel row through the row's own cell (offset 0 on every axis:
+      // slot ks/2 of each extent)
+      const int q_self = (ksz / 2) * ksy + ksy / 2;
 #pragma unroll
       for (int i = 0; i < kRowsAtOnce; ++i)
 #pragma unroll
         for (int kx = 0; kx < KX; ++kx) {
           // a rank outside the rows: the rows are not the bitmap's cells
-          if (hit[i][kx] && rank[i][kx] >= static_cast<uint64_t>(n)) {
-            atomicOr(&counts[K], TSC_FLAG_ROWS_NOT_BITMAP);
-            hit[i][kx] = false;
-          }
+          const bool beyond = hit[i][kx] && rank[i][kx] >= static_cast<uint64_t>(n);
+          // the row's own cell must be occupied and carry the row's own rank;
+          // with no rank beyond n either, the rows are exactly the first n
+          // occupied cells in rank order (a permuted or foreign row set fails)
+          const bool self_bad = live && q0 + i == q_self && kx == KX / 2 &&
+                                !(hit[i][kx] && rank[i][kx] == static_cast<uint64_t>(col));
+          if (beyond || self_bad) atomicOr(&counts[K], TSC_FLAG_ROWS_NOT_BITMAP);
+          if (beyond) hit[i][kx] = false;
           jr[i][kx] = hit[i][kx] ? static_cast<int32_t>(rank[i][kx]) : -1;
         }
     } else if (g.dil.x != 1) {

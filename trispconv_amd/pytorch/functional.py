@@ -156,6 +156,10 @@ def sparse_conv_forward(features: torch.Tensor, weight: Union[torch.Tensor, Pack
     elem = torch.empty((), dtype=weight.dtype).element_size()
     nbr, order, ordered = indice_data.conv_operands(N_out, features.device, weight.c_in * elem,
                                                     n_in=features.shape[0])
+    # user-assigned lists that name an output row more than once within a
+    # slot: the map runs each repeat as a slot of its own (slot k*m + j for
+    # the j-th occurrence), so the weight's slots repeat with it
+    weight = weight.with_slots_repeated(indice_data.slot_repeat)
     return _run(features, weight, bias, nbr, order, N_out, ordered, epilogue)
 
 

@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import ctypes
 import functools
+from dataclasses import dataclass
 from typing import Callable, List, Optional, Sequence, Tuple
 
 import torch
@@ -64,8 +65,28 @@ def _encode_coords(indices: torch.Tensor, D: int, H: int, W: int) -> torch.Tenso
     return i[:, 0] * (D * H * W) + i[:, 1] * (H * W) + i[:, 2] * W + i[:, 3]
 
 
+@dataclass(init=False, repr=False)
 class IndiceData:
-    """Pairs of one layer (indices.py:10-23), backed by device tables."""
+    """Pairs of one layer (indices.py:10-23), backed by device tables.
+
+    A dataclass with the reference's twelve fields in its order, so
+    ``dataclasses.fields``, ``replace``, ``asdict`` and field-wise ``==``
+    behave as on the reference's.  ``pairs_in``, ``pairs_out`` and
+    ``pair_num`` are properties over the device tables (made on first
+    access); the tables and caches are plain attributes, not fields."""
+
+    out_indices: torch.Tensor           # (N_out, 4) int32
+    pairs_in: List[torch.Tensor]        # K int64 tensors
+    pairs_out: List[torch.Tensor]       # K int64 tensors
+    pair_num: torch.Tensor              # (K,) int64, CPU
+    input_indices: torch.Tensor         # (N_in, 4) int32
+    input_spatial_shape: Tuple[int, ...]
+    output_spatial_shape: Tuple[int, ...]
+    kernel_size: Tuple[int, ...]
+    stride: Tuple[int, ...]
+    padding: Tuple[int, ...]
+    dilation: Tuple[int, ...]
+    subm: bool
 
     def __init__(self, out_indices: torch.Tensor, pairs_in: Optional[List[torch.Tensor]],
                  pairs_out: Optional[List[torch.Tensor]], pair_num: torch.Tensor,
@@ -122,9 +143,15 @@ class IndiceData:
         self._in_bound: Optional[int] = None
         # convolutions run on these pairs so far without an execution order
         self._conv_uses = 0
+        # map rows per slot (user-assigned lists with repeated outputs)
+        self._slot_repeat = 1
+        # a build whose status flags are read on its first reuse (a
+        # submanifold build on a strided layer's bitmap: its rows are checked
+        # against that bitmap on the device, with no read-back at build time)
+        self._deferred_check = False
+        self._uses = 0
 
-    @property
-    def pair_num(self) -> torch.Tensor:
+    def _get_pair_num(self) -> torch.Tensor:
         """Pairs per slot, a CPU int64 tensor (indices.py:131).  Submanifold
         builds leave their counts on the device (their coordinates are
         checked before the build returns, or, on a strided layer's bitmap,
@@ -140,8 +167,7 @@ class IndiceData:
             self._counts_pending = None
         return self._pair_num
 
-    @pair_num.setter
-    def pair_num(self, value: torch.Tensor) -> None:
+    def _set_pair_num(self, value: torch.Tensor) -> None:
         self._pair_num = value
         self._counts_pending = None
 
@@ -165,29 +191,25 @@ class IndiceData:
         k = self.kernel_size
         return int(k[0]) * int(k[1]) * int(k[2])
 
-    @property
-    def pairs_in(self) -> List[torch.Tensor]:
+    def _get_pairs_in(self) -> List[torch.Tensor]:
         if self._pairs_in is None:
             self._ensure_tables()
             self._pairs_in = self._slot_views(self._pin)
         return self._pairs_in
 
-    @pairs_in.setter
-    def pairs_in(self, value: List[torch.Tensor]) -> None:
+    def _set_pairs_in(self, value: List[torch.Tensor]) -> None:
         if self._pairs_out is None and (self._pout is not None or self._map_cols is not None):
             self.pairs_out  # keep the other list: the tables it comes from go
         self._pairs_in = value
         self._drop_tables()
 
-    @property
-    def pairs_out(self) -> List[torch.Tensor]:
+    def _get_pairs_out(self) -> List[torch.Tensor]:
         if self._pairs_out is None:
             self._ensure_tables()
             self._pairs_out = self._slot_views(self._pout)
         return self._pairs_out
 
-    @pairs_out.setter
-    def pairs_out(self, value: List[torch.Tensor]) -> None:
+    def _set_pairs_out(self, value: List[torch.Tensor]) -> None:
         if self._pairs_in is None and (self._pin is not None or self._map_cols is not None):
             self.pairs_in  # keep the other list: the tables it comes from go
         self._pairs_out = value
@@ -226,6 +248,7 @@ class IndiceData:
         self._inverse_cache = None
         self._in_bound = None
         self._in_ids = None
+        self._slot_repeat = 1
 
     # --------------------------------------------------- convolution inputs
     def neighbour_map(self, n_out: int, device, n_in: Optional[int] = None) -> torch.Tensor:
@@ -280,27 +303,54 @@ class IndiceData:
                              f"{n_out} output rows")
 
     def _user_map(self, n_out: int, n_in: Optional[int], device) -> torch.Tensor:
-        """[K][n_out] map of user-assigned lists, checked with one host read:
-        ids in range, and no output row twice within a slot (the map holds one
-        input per slot and output, as every generator's lists do)."""
+        """[K*m][n_out] map of user-assigned lists, checked with one host read
+        (ids in range).
+
+        The reference adds every pair of a slot with ``index_add_``
+        (functional.py:46), so a list that names an output row twice within a
+        slot adds both contributions.  The map holds one input per (row,
+        output): the j-th occurrence of an output within slot k (in list
+        order) goes to map row k*m + j, m the largest multiplicity, and the
+        convolution runs with each slot's weight repeated m times
+        (``slot_repeat``).  Slot k's contributions stay together and in list
+        order, so the sums keep the slot-ascending order; m is 1 for lists
+        without repeats (every generator's)."""
         K = self.K
         slot, cat_in, cat_out, sizes = self._user_lists(n_in, n_out, device)
-        nbr = torch.full((K, n_out), -1, dtype=torch.int32, device=device)
+        self._slot_repeat = 1
         if not slot.numel():
             self._in_bound = 0
-            return nbr
-        # scatter with clamped ids, so that the check below reads a map
-        # written in bounds whatever the lists hold
+            return torch.full((K, n_out), -1, dtype=torch.int32, device=device)
+        # clamped ids, so that the scatter below stays in bounds whatever the
+        # lists hold (out-of-range ids raise after the one host read)
         hi_in = (n_in if n_in is not None else 1 << 31) - 1
-        nbr[slot, cat_out.clamp(0, max(n_out - 1, 0))] = cat_in.clamp(0, hi_in).int()
+        out_c = cat_out.clamp(0, max(n_out - 1, 0))
+        # occurrence rank of each pair among the pairs of its (slot, output):
+        # a stable sort keeps list order within a run of equal keys
+        key = slot * max(n_out, 1) + out_c
+        skey, perm = torch.sort(key, stable=True)
+        pos = torch.arange(len(key), device=device)
+        run_start = torch.ones_like(skey, dtype=torch.bool)
+        run_start[1:] = skey[1:] != skey[:-1]
+        first = torch.where(run_start, pos, torch.zeros_like(pos)).cummax(0).values
+        rank = torch.empty_like(pos)
+        rank[perm] = pos - first
         stats = torch.stack([cat_in.min(), cat_in.max(), cat_out.min(), cat_out.max(),
-                             (nbr >= 0).sum()]).cpu().tolist()
+                             rank.max()]).cpu().tolist()
         self._range_error(*stats[:4], n_in, n_out, "sparse_conv_forward")
-        if stats[4] != len(slot):
-            raise ValueError("sparse_conv_forward: a pairs_out list names one output row twice "
-                             "within a slot; each slot maps an output row at most once")
+        m = int(stats[4]) + 1
+        nbr = torch.full((K * m, n_out), -1, dtype=torch.int32, device=device)
+        nbr[slot * m + rank, out_c] = cat_in.clamp(0, hi_in).int()
+        self._slot_repeat = m
         self._in_bound = int(stats[1]) + 1
         return nbr
+
+    @property
+    def slot_repeat(self) -> int:
+        """How many map rows each slot has: 1, or for user-assigned lists that
+        name an output row more than once within a slot, the largest such
+        count (the map's row k*m + j is the j-th occurrence in slot k)."""
+        return self._slot_repeat
 
     def _tables_from_lists(self, device) -> None:
         """Padded device tables (and counts) from user-assigned lists, for the
@@ -338,7 +388,8 @@ class IndiceData:
         next layer with this indice_key, or the next forward); ``eager``
         builds it at once.
         """
-        if n_out < _PLAN_MIN_ROWS or n_out * int(row_bytes) < _PLAN_MIN_BYTES:
+        if n_out < _PLAN_MIN_ROWS or n_out * int(row_bytes) < _PLAN_MIN_BYTES \
+                or self._slot_repeat != 1:
             return None
         region = int(min(max(_REGION_BYTES // max(int(row_bytes), 1), 2048), 1 << 30))
         if self._order is None or self._order_region != region:
@@ -379,6 +430,14 @@ class IndiceData:
         map (ordered 0).  ``n_in``, the
         feature rows, must cover every input id the pairs name (IndexError,
         as the reference's ``features[in_ids]``)."""
+        if self._deferred_check:
+            self._uses += 1
+            if self._uses >= 2:
+                # the first reuse under the key reads the build's counts and
+                # status flags once (pair_num raises when the rows were not
+                # the registered strided output set)
+                self._deferred_check = False
+                self.pair_num  # noqa: B018
         if self._map_cols is None and self._nbr is None:
             self.neighbour_map(n_out, device, n_in)  # user-assigned lists: checked here
         if n_in is not None:
@@ -406,6 +465,15 @@ class IndiceData:
     def __repr__(self) -> str:
         return (f"IndiceData(subm={self.subm}, K={self.K}, n_out={len(self.out_indices)}, "
                 f"pairs={int(self.pair_num.sum()) if self.pair_num.numel() else 0})")
+
+
+# The three lazy fields are properties over the device tables.  They are set
+# on the class after the dataclass decorator has recorded the fields, so that
+# the fields carry no default (a property in the class body would be taken
+# for one).
+IndiceData.pair_num = property(IndiceData._get_pair_num, IndiceData._set_pair_num)
+IndiceData.pairs_in = property(IndiceData._get_pairs_in, IndiceData._set_pairs_in)
+IndiceData.pairs_out = property(IndiceData._get_pairs_out, IndiceData._set_pairs_out)
 
 
 def _coords(indices: torch.Tensor, what: str) -> torch.Tensor:
@@ -482,9 +550,10 @@ def _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil):
         "generate_subm_indice_pairs")
     # No read-back here: the rows are the registered output set (same tensor,
     # same version), so there is nothing to validate before the convolution.
-    # The counts and the status flag (rows that are not the bitmap's cells,
-    # whose neighbours the kernel leaves out of the map) are read with
-    # pair_num.
+    # The probe checks on the device that every row is the bitmap's cell of
+    # its own rank and that no neighbour lies beyond the rows; the counts and
+    # that status flag are read with pair_num, or at the build's first reuse
+    # (the second convolution on it), whichever comes first.
     d = IndiceData._from_tables(
         out_indices=indices, input_indices=indices, input_spatial_shape=shape,
         output_spatial_shape=shape, kernel_size=ks, stride=(1, 1, 1), padding=(0, 0, 0),
@@ -493,6 +562,7 @@ def _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil):
         raster=True)
     d._map_masks = masks
     d._counts_pending = (counts, K, lambda: _counts_to_host(counts, K, stream))
+    d._deferred_check = True
     return d
 
 
@@ -693,12 +763,19 @@ def generate_inverse_indice_pairs(fwd: IndiceData) -> IndiceData:
                                      ws.data_ptr(), ws.numel(), n_out, out_coords.data_ptr(),
                                      nbr.data_ptr(), inv_pout.data_ptr(), stream),
                 "inverse pairs")
-    if from_lists:
-        # the inverse writes output id_map[pairs_in[k]] through slot k: an
-        # input row listed twice within a slot would need two entries
-        if int((nbr >= 0).sum()) != int(fwd._cnt.sum()):
-            raise ValueError("SparseInverseConv3d: a forward pairs_in list names one input row "
-                             "twice within a slot; each slot maps a row at most once")
+    if from_lists and int((nbr >= 0).sum()) != int(fwd._cnt.sum()):
+        # a forward pairs_in list names an input row twice within a slot, so
+        # the inverse's pairs_out names that output twice: the reference adds
+        # both (index_add_, functional.py:46).  The remapped lists become the
+        # inverse's own lists, whose map runs repeats as slots of their own.
+        cnt = fwd._cnt.tolist()
+        inv_in = [fwd._pout[k, :int(c)].long() for k, c in enumerate(cnt)]
+        inv_out = [inv_pout[k, :int(c)].long() for k, c in enumerate(cnt)]
+        d = IndiceData(out_coords, inv_in, inv_out, fwd.pair_num, fwd.out_indices,
+                       fwd.output_spatial_shape, fwd.input_spatial_shape, fwd.kernel_size,
+                       fwd.stride, fwd.padding, fwd.dilation, False)
+        d._batch_size = fwd._batch_size
+        return d
     return IndiceData._from_tables(
         out_indices=out_coords, input_indices=fwd.out_indices,
         input_spatial_shape=fwd.output_spatial_shape,

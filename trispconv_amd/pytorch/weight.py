@@ -56,10 +56,27 @@ def normalize_spconv_weight(w: torch.Tensor, kernel_size: Tuple[int, int, int], 
 class PackedWeight:
     """A weight in the convolution kernel's layout for one compute dtype."""
 
-    __slots__ = ("data", "k_vol", "c_in", "c_out", "dtype")
+    __slots__ = ("data", "k_vol", "c_in", "c_out", "dtype", "source")
 
-    def __init__(self, data: torch.Tensor, k_vol: int, c_in: int, c_out: int, dtype: torch.dtype):
+    def __init__(self, data: torch.Tensor, k_vol: int, c_in: int, c_out: int, dtype: torch.dtype,
+                 source: Optional[tuple] = None):
         self.data, self.k_vol, self.c_in, self.c_out, self.dtype = data, k_vol, c_in, c_out, dtype
+        # (weight tensor, kernel size) it was packed from
+        self.source = source
+
+    def with_slots_repeated(self, m: int) -> "PackedWeight":
+        """The weight of a kernel whose slot k is repeated m times in a row
+        (slot k*m + j holds W[k]), packed anew from the source weight: the
+        convolution over lists that name an output row more than once within
+        a slot runs each repeat as a slot of its own."""
+        if m == 1:
+            return self
+        if self.source is None:
+            raise RuntimeError("PackedWeight: no source weight to repeat slots from")
+        w, ks = self.source
+        internal = normalize_spconv_weight(w.detach(), ks, self.c_in, self.c_out)
+        rep = internal.repeat_interleave(m, dim=0).contiguous()
+        return pack_weight(rep, (rep.shape[0], 1, 1), self.c_in, self.c_out, self.dtype)
 
 
 def pack_weight(w: torch.Tensor, kernel_size, in_channels: int, out_channels: int,
@@ -78,7 +95,7 @@ def pack_weight(w: torch.Tensor, kernel_size, in_channels: int, out_channels: in
     L.check(lib.tsc_pack_weight(src.data_ptr(), L.dtype_code(src.dtype), layout, K, in_channels,
                                 out_channels, code, data.data_ptr(), L.stream_of(src)),
             "pack_weight")
-    return PackedWeight(data, K, in_channels, out_channels, dtype)
+    return PackedWeight(data, K, in_channels, out_channels, dtype, (w, tuple(kernel_size)))
 
 
 def _rebuild_conv_weight(data: torch.Tensor, requires_grad: bool) -> "ConvWeight":
