@@ -387,6 +387,45 @@ def test_dma_kernel_matches_the_register_gather_kernel(dtype, rows, grid, monkey
         assert torch.isfinite(dma.float()).all()
 
 
+@pytest.mark.parametrize("dtype,c", [(torch.float16, 64), (torch.bfloat16, 64), (torch.float32, 32)])
+def test_dma_kernel_short_stage_lists_and_epilogue(dtype, c):
+    """conv_dma_kernel at 64 rows per wave (layers of at least 1024 tiles of
+    256 rows) on a sparse grid where most tiles use one to three slots, with
+    one channel chunk (a stage per slot): tiles of one or two stages, shorter
+    than its prefetch, and a partial last tile.  Bit for bit against the
+    register-gather kernel (forced column tile) and, with a fused batch norm
+    and ReLU, against the fp64 oracle on a sample of rows."""
+    n_rows = 1055 * 256 - 77
+    idx = _tiny(57, (256, 256, 256), 1, n_rows)
+    x = torch.from_numpy(idx).to(DEV)
+    n = len(idx)
+    feats = torch.randn(n, c, generator=torch.Generator().manual_seed(8)).to(DEV).to(dtype)
+    data = generate_subm_indice_pairs(x, (256, 256, 256), 1, 3)
+    m = _module("subm", c, 64, 3, dtype=dtype, seed=13)
+    pw = m._packed_weight(dtype)
+    assert L.lib().tsc_conv_kernel_name(L.dtype_code(dtype), c, 64, 27, n) == b"conv_dma_kernel"
+    pn = data.pair_num
+    say("dma kernel short lists", dtype, n, "pairs per row", float(pn.sum()) / n)
+    assert float(pn.sum()) / n < 2.0  # mostly one or two slots per row
+    own = Fn.sparse_conv_forward(feats, pw, m.bias, data, n)
+    reg = _with_tile(feats, pw, m.bias, data, n, 64)
+    assert torch.equal(own, reg)
+    g = torch.Generator().manual_seed(3)
+    mean, var = torch.rand(64, generator=g) * 0.2 - 0.1, torch.rand(64, generator=g) + 0.5
+    gamma, beta = torch.rand(64, generator=g) + 0.5, torch.rand(64, generator=g) * 0.4 - 0.2
+    ep = Fn.Epilogue(mean.to(DEV), var.to(DEV), gamma.to(DEV), beta.to(DEV), 1e-5, True)
+    fused = Fn.sparse_conv_forward(feats, pw, m.bias, data, n, epilogue=ep)
+    rows = np.random.default_rng(1).choice(n, size=4000, replace=False)
+    w = OC.normalize_weight(to_np(m.weight).astype(np.float64), (3, 3, 3), c, 64)
+    ref = oracle_rows(to_np(feats).astype(np.float64), w, to_np(m.bias).astype(np.float64),
+                      lists_np(data.pairs_in), lists_np(data.pairs_out), rows)
+    ref = np.maximum((ref - mean.double().numpy()) / np.sqrt(var.double().numpy() + 1e-5)
+                     * gamma.double().numpy() + beta.double().numpy(), 0.0)
+    err = rel_err(to_np(fused)[rows], ref)
+    say("  fused rel err", err)
+    assert err <= TOL[dtype]
+
+
 def test_raw_internal_weight_and_user_built_indice_data():
     """sparse_conv_forward with a (K, C_in, C_out) tensor and hand-made pair lists."""
     idx = _tiny(14, (10, 10, 10), 1, 300)

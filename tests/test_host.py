@@ -389,7 +389,7 @@ def test_dma_kernels_own_m0(tmp_path):
     assert len(names) >= 6, "expected the f16, bf16 and f32 instantiations"
     for name in names:
         body = text[text.index(name + ":"):]
-        body = body[:body.index("s_endpgm")]
+        body = body[:body.index(".Lfunc_end")]  # the whole function, every exit
         lines = [ln.split(";")[0].strip() for ln in body.splitlines()]
         lines = [ln for ln in lines if ln and not ln.startswith((".", "#"))]
         n_dma = 0
