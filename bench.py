@@ -18,7 +18,8 @@ them), inputs already resident in HBM:
 
 Prints one short JSON line per workload, the headline layer's last (its
 ``value`` = voxels/s = N_in / step time); the full results, per layer, go to
-``--detail`` (default gpurun_out/bench_detail.json).  Each workload gets:
+``--detail`` (default: trispconv_bench_detail.json in the temp directory).
+Each workload gets:
 voxels/s, effective TFLOP/s, per-layer conv times (HIP events on the stream
 the kernels run on, between the layers of the network run in order; each
 includes the few microseconds its event adds, so a network's layer times sum
@@ -36,6 +37,7 @@ import json
 import os
 import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -66,7 +68,8 @@ def parse():
                     help="first run one elementwise negation over this many MiB (a copy-like "
                          "kernel of known size to scale FETCH_SIZE / WRITE_SIZE counters by)")
     ap.add_argument("--verbose", action="store_true")
-    ap.add_argument("--detail", default=str(ROOT / "gpurun_out" / "bench_detail.json"),
+    ap.add_argument("--detail",
+                    default=str(Path(tempfile.gettempdir()) / "trispconv_bench_detail.json"),
                     help="file for every workload's full results (per layer); stdout gets one "
                          "short line per workload, the headline last")
     return ap.parse_args()

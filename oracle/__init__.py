@@ -4,7 +4,7 @@ This package restates, in numpy, the algorithms of the reference package
 (trispconv/pytorch/indices.py, functional.py, weight.py and the inverse branch
 of modules.py) so that the HIP path can be checked against it.  Only the
 test-suite, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may import it, and only as the checker or as the timed CPU
+``bench.py`` may import it, and only to check results or as the timed CPU
 baseline.  The product path (``trispconv_amd``) never imports it and has no
 CPU fallback.
 

@@ -1,4 +1,4 @@
-"""Helpers shared by the GPU parity tests (the oracle is only the checker)."""
+"""Helpers shared by the GPU parity tests (the oracle only checks results)."""
 from __future__ import annotations
 
 import sys

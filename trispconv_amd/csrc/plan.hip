@@ -266,7 +266,7 @@ __global__ void __launch_bounds__(kThreads) radix_scatter_kernel(
     Digits d, const uint32_t* __restrict__ hist_off, const uint32_t* __restrict__ digit_tot,
     int nblk, uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out) {
   __shared__ uint32_t s_run[kRadix];                   // placed so far, per digit
-  __shared__ uint32_t s_wc[kThreads / kWave][kRadix];  // this round, per wave, per digit
+  __shared__ uint32_t s_wc[kThreads / kWave][kRadix];  // this pass, per wave, per digit
   __shared__ uint32_t s_wave[33];
   const int t = threadIdx.x;
   const int w = t / kWave;
