@@ -613,6 +613,17 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
   constexpr int CHUNKS = ROW_BYTES / 16;            // 16-byte pieces per row
   constexpr int PR = mfma_stage_rows(ROW_BYTES);    // rows staged per wave and pass
   char* stage = reinterpret_cast<char*>(s_nbr) + wave * PR * STRIDE;
+  // this lane's columns' bias and batch norm, read once: the staging stores
+  // go through a pointer the compiler cannot tell apart from these arrays, so
+  // read in the loop they would be loaded again after every store
+  float cbias[NB], cscale[NB], cshift[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int cl = nb * 32 + (lane & 31);
+    cbias[nb] = s_bias[cl];
+    cscale[nb] = s_scale[cl];
+    cshift[nb] = s_shift[cl];
+  }
 #pragma unroll
   for (int pass = 0; pass < 64 / PR; ++pass) {
     __syncthreads();                                // the staging area is free
@@ -627,7 +638,7 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
         for (int nb = 0; nb < NB; ++nb) {
           const int cl = nb * 32 + (lane & 31);
           *reinterpret_cast<T*>(stage + row * STRIDE + cl * (int)sizeof(T)) =
-              from_f32<T>(finish(acc[rb][nb][i] + s_bias[cl], s_scale[cl], s_shift[cl], affine,
+              from_f32<T>(finish(acc[rb][nb][i] + cbias[nb], cscale[nb], cshift[nb], affine,
                                  relu));
         }
       }
@@ -1013,6 +1024,15 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
   static_assert((size_t)4 * PR * STRIDE <= dma_pool_bytes<T, BN, RB>(), "staging exceeds the pool");
   static_assert(WR % PR == 0, "whole passes");
   char* stage = pool + wave * PR * STRIDE;
+  // this lane's columns' bias and batch norm in registers (see conv_mfma_kernel)
+  float cbias[NB], cscale[NB], cshift[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int cl = nb * 32 + (lane & 31);
+    cbias[nb] = s_bias[cl];
+    cscale[nb] = s_scale[cl];
+    cshift[nb] = s_shift[cl];
+  }
 #pragma unroll
   for (int pass = 0; pass < WR / PR; ++pass) {
     __syncthreads();
@@ -1027,7 +1047,7 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
         for (int nb = 0; nb < NB; ++nb) {
           const int cl = nb * 32 + (lane & 31);
           *reinterpret_cast<T*>(stage + row * STRIDE + cl * (int)sizeof(T)) =
-              from_f32<T>(finish(acc[rb][nb][i] + s_bias[cl], s_scale[cl], s_shift[cl], affine,
+              from_f32<T>(finish(acc[rb][nb][i] + cbias[nb], cscale[nb], cshift[nb], affine,
                                  relu));
         }
       }
