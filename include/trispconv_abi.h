@@ -235,7 +235,9 @@ TSC_API int tsc_inverse_fill_ids(const int32_t* fwd_pairs_in, const int32_t* fwd
  *   nbr [K][n_out] is a map by columns: column t belongs to row cols_row[t]
  *   (cols_row == NULL: column t is row t).  raster != 0 says the columns are
  *   already in (b,z,y,x) order (the submanifold builder's bitmap path);
- *   otherwise they are put in Morton order of out_coords [n_out][4].
+ *   otherwise they are put in Morton order of out_coords [n_out][4] when
+ *   there is more than one region (region_rows < n_out; with one region the
+ *   column order breaks ties and out_coords may be NULL).
  *   order [n_out] receives the processing order (rows); nbr_ordered
  *   [K][n_out] (may be NULL) the map permuted into that order: entry (k, t)
  *   belongs to row order[t], so the convolution reads it contiguously;

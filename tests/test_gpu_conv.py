@@ -527,6 +527,29 @@ def test_plan_tiles_mask_sorted_heaviest_first(row_bytes, monkeypatch):
         assert hi - r0 == len(np.unique(order[r0:hi]))
 
 
+@pytest.mark.parametrize("c_in,dtype,first", [(128, torch.float16, True), (64, torch.float32, True),
+                                               (32, torch.float16, False)])
+def test_plan_on_first_use_only_for_wide_spatially_ordered_maps(c_in, dtype, first, monkeypatch):
+    """A bitmap build's map (columns in (b,z,y,x) order) is planned at its
+    first convolution when the gathered rows are at least 256 bytes wide;
+    narrower rows run the first convolution unplanned and plan at the second.
+    Either way the outputs are the same bits."""
+    monkeypatch.setattr(I, "_PLAN_MIN_BYTES", 0)  # an order even for this small layer
+    idx = _tiny(16, (40, 40, 40), 1, 6000)
+    x = torch.from_numpy(idx).to(DEV)
+    feats = torch.randn(len(idx), c_in, generator=torch.Generator().manual_seed(4)).to(DEV).to(dtype)
+    data = generate_subm_indice_pairs(x, (40, 40, 40), 1, 3)
+    assert data._raster
+    m = _module("subm", c_in, 32, 3, dtype=dtype, seed=6)
+    pw = m._packed_weight(dtype)
+    n = len(idx)
+    one = Fn.sparse_conv_forward(feats, pw, m.bias, data, n)
+    assert (data.ordered_map() is not None) == first
+    two = Fn.sparse_conv_forward(feats, pw, m.bias, data, n)
+    assert data.ordered_map() is not None
+    assert torch.equal(one, two)
+
+
 def test_unkeyed_subm_layers_share_one_build(monkeypatch):
     """Submanifold layers without an indice_key reuse the pairs of their
     coordinate tensor while it is unchanged; an in-place change rebuilds."""

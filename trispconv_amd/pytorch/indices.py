@@ -44,6 +44,9 @@ _PLAN_MIN_BYTES = 24 << 20  # output rows x gathered row bytes
 # sets better and beat L2-sized (4 MiB) regions despite the longer reuse
 # distance, since the cache behind L2 still holds the gathered rows.
 _REGION_BYTES = 128 << 20
+# Gathered row bytes from which a spatially ordered map is planned on its
+# first use (see IndiceData.execution_order).
+_PLAN_FIRST_USE_ROW_BYTES = 256
 
 
 def _to3(x) -> Tuple[int, int, int]:
@@ -382,11 +385,19 @@ class IndiceData:
         (the partial tile last).  Built once per region size and cached; None
         for small layers.
 
-        The order costs about as much as two uses of it save, and it never
-        changes an output bit, so the first convolution over these pairs runs
-        without one and the order is built when the pairs are used again (the
-        next layer with this indice_key, or the next forward); ``eager``
-        builds it at once.
+        The order never changes an output bit.  When the map's columns are
+        already in (b,z,y,x) order (a bitmap build's columns, a strided
+        build's output rows) and the gathered rows are wide (at least 256
+        bytes), the plan pays for itself on its first use (measured: the
+        500k-row 128-channel SubM layer 0.55 ms unplanned against 0.17 +
+        0.37 ms, the 166k-row 64-channel fp32 strided layer 0.36 against
+        0.11 + 0.16 ms), so it is built then.  Otherwise it costs more than
+        one use saves (the 600k-row 64-channel bf16 inverse layer: 0.16 ms
+        unplanned against 0.145 + 0.065 ms; the 674k-row 32-channel bf16
+        strided layer: about 0.12 against 0.20 + 0.076 ms): the first
+        convolution runs without one and the order is built when the pairs
+        are used again (the next layer with this indice_key, or the next
+        forward).  ``eager`` builds it at once.
         """
         if n_out < _PLAN_MIN_ROWS or n_out * int(row_bytes) < _PLAN_MIN_BYTES \
                 or self._slot_repeat != 1:
@@ -394,12 +405,14 @@ class IndiceData:
         region = int(min(max(_REGION_BYTES // max(int(row_bytes), 1), 2048), 1 << 30))
         if self._order is None or self._order_region != region:
             self._conv_uses += 1
-            if self._conv_uses < 2 and not eager:
+            raster = self._raster if self._map_cols is not None else self._rows_raster
+            first_use = raster and int(row_bytes) >= _PLAN_FIRST_USE_ROW_BYTES
+            if self._conv_uses < 2 and not eager and not first_use:
                 return None
             if self._map_cols is not None:  # the builder's columns, maybe in spatial order
-                nbr, cols_row, raster = self._map_cols, self._cols_row, self._raster
+                nbr, cols_row = self._map_cols, self._cols_row
             else:
-                nbr, cols_row, raster = self.neighbour_map(n_out, device), None, self._rows_raster
+                nbr, cols_row = self.neighbour_map(n_out, device), None
             coords = None if raster else _coords(self.out_indices, "conv plan")
             lib = L.lib()
             ws = L.workspace(lib.tsc_plan_workspace_bytes(n_out, self.K), device)
