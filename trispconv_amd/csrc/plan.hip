@@ -22,6 +22,10 @@
 // Output values never depend on the order: every row's fp32 accumulation
 // sees the same slots in the same ascending order and absent slots add zero.
 //
+// The permuted map is gathered from a row-major copy of the map (maps of up
+// to 32 slots), which the mask pass writes: one 128-byte row per position
+// instead of one scattered entry per slot.
+//
 // Sorting: stable LSD radix passes with 9-bit digits (a 27-slot mask sorts
 // in three passes).  Each pass is a histogram kernel (per-block digit counts,
 // digit-major), a scan of each digit's counts over the blocks (one workgroup
@@ -209,6 +213,72 @@ __global__ void __launch_bounds__(256) permute_map_kernel(const int32_t* __restr
   }
 }
 
+// For maps of up to 32 slots: the slot mask of each column, as
+// row_mask_kernel, and a row-major copy of the map, nbr_t[c][k] = nbr[k][c]
+// in rows of 32 entries (128 bytes; entries k >= K hold -1), from which the
+// permute reads one line per position instead of K scattered entries.  A
+// block stages 256 columns of every slot in LDS and writes their rows as
+// 16-byte vectors.
+__global__ void __launch_bounds__(256) map_rows_kernel(const int32_t* __restrict__ nbr, int64_t n,
+                                                       int K, int32_t* __restrict__ nbr_t,
+                                                       uint32_t* __restrict__ mask_row,
+                                                       uint32_t* __restrict__ vals) {
+  __shared__ int32_t s_e[32][257];
+  const int t = threadIdx.x;
+  const int64_t c0 = blockIdx.x * (int64_t)256;
+  const int64_t c = c0 + t;
+  uint32_t m = 0;
+  for (int k0 = 0; k0 < 32; k0 += 8) {
+    int32_t v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      v[i] = (c < n && k0 + i < K) ? nbr[(int64_t)(k0 + i) * n + c] : -1;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      s_e[k0 + i][t] = v[i];
+      m |= (v[i] >= 0 ? 1u : 0u) << (k0 + i);
+    }
+  }
+  if (c < n) {
+    mask_row[c] = m;
+    if (vals) vals[c] = static_cast<uint32_t>(c);
+  }
+  __syncthreads();
+  int4* rows = reinterpret_cast<int4*>(nbr_t);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int i = j * 256 + t;  // 16-byte piece i: row i / 8, entries 4 (i % 8) ..
+    const int r = i >> 3, q = i & 7;
+    if (c0 + r < n)
+      rows[(c0 + r) * 8 + q] = make_int4(s_e[4 * q][r], s_e[4 * q + 1][r], s_e[4 * q + 2][r],
+                                         s_e[4 * q + 3][r]);
+  }
+}
+
+// nbr_ordered[k][t] = nbr[k][perm[t]] from the row-major copy: each wave
+// takes 64 positions, reads their rows two at a time (lanes 0..31 and
+// 32..63 each read one 128-byte row, entry k by lane k), and writes every
+// slot's 64 entries as one coalesced run after a transpose in LDS.
+__global__ void __launch_bounds__(256) permute_rows_kernel(const int32_t* __restrict__ nbr_t,
+                                                           const uint32_t* __restrict__ perm,
+                                                           int64_t n, int K,
+                                                           int32_t* __restrict__ out) {
+  __shared__ int32_t s_e[4][32][65];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t p0 = (blockIdx.x * (int64_t)4 + w) * 64;
+  const int k = lane & 31, half = lane >> 5;
+  const uint32_t my_col = p0 + lane < n ? perm[p0 + lane] : 0u;
+#pragma unroll 8
+  for (int j = 0; j < 32; ++j) {
+    const int pp = 2 * j + half;  // this half's position
+    const uint32_t col = __shfl(my_col, pp, kWave);
+    s_e[w][k][pp] = p0 + pp < n ? nbr_t[(int64_t)col * 32 + k] : -1;
+  }
+  __syncthreads();
+  if (p0 + lane < n)
+    for (int kk = 0; kk < K; ++kk) out[(int64_t)kk * n + p0 + lane] = s_e[w][kk][lane];
+}
+
 __global__ void __launch_bounds__(kThreads) radix_hist_kernel(const uint32_t* __restrict__ vals,
                                                               int64_t n, Digits d,
                                                               uint32_t* __restrict__ hist,
@@ -322,13 +392,15 @@ __global__ void __launch_bounds__(kThreads) radix_scatter_kernel(
 
 struct Buffers {
   uint32_t *keys_a, *keys_b, *vals_a, *vals_b, *rows, *mask_pos, *hist, *hist_off, *digit_tot;
+  int32_t* nbr_t;  // the map's row-major copy (K <= 32), else null
 };
 
-Buffers carve(void* ws, int64_t n, int64_t* used) {
+Buffers carve(void* ws, int64_t n, int K, int64_t* used) {
   Carver c(ws);
   const int64_t m = n > 0 ? n : 1;
   const int64_t nblk = ceil_div(m, kTile);
   Buffers b;
+  b.nbr_t = K <= 32 ? c.take<int32_t>(m * 32) : nullptr;
   b.keys_a = c.take<uint32_t>(m);
   b.keys_b = c.take<uint32_t>(m);
   b.vals_a = c.take<uint32_t>(m);
@@ -371,7 +443,7 @@ using namespace tsc;
 extern "C" int64_t tsc_plan_workspace_bytes(int64_t n_out, int32_t k_vol) {
   (void)k_vol;
   int64_t used = 0;
-  carve(nullptr, n_out, &used);
+  carve(nullptr, n_out, k_vol, &used);
   return used;
 }
 
@@ -392,7 +464,7 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_
               "plan: null pointer");
   TSC_REQUIRE(ws_bytes >= tsc_plan_workspace_bytes(n_out, k_vol), "plan: workspace too small");
   TSC_REQUIRE(!pos_masks || k_vol <= 32, "plan: slot masks need k_vol <= 32 (got %d)", k_vol);
-  Buffers b = carve(ws, n_out, nullptr);
+  Buffers b = carve(ws, n_out, k_vol, nullptr);
   int rc;
   // With one region the spatial order only breaks ties between equal slot
   // masks (the column order does that instead; measured on the 600k-row
@@ -404,7 +476,11 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_
   if (raster) {
     // each column is its own Morton position: its slot mask goes straight to
     // mask_pos, with the positions as the values to sort
-    row_mask_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(nbr, n_out, k_vol, b.mask_pos, b.vals_a);
+    if (b.nbr_t)
+      map_rows_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(nbr, n_out, k_vol, b.nbr_t, b.mask_pos,
+                                                           b.vals_a);
+    else
+      row_mask_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(nbr, n_out, k_vol, b.mask_pos, b.vals_a);
     TSC_LAUNCH_CHECK("plan_row_mask");
   } else {
     int extent = out_spatial[0];
@@ -433,7 +509,11 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_
   // the sort-1 keys are dead now: keys_a holds each column's slot mask,
   // keys_b the final column permutation
   if (!raster) {
-    row_mask_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(nbr, n_out, k_vol, b.keys_a, nullptr);
+    if (b.nbr_t)
+      map_rows_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(nbr, n_out, k_vol, b.nbr_t, b.keys_a,
+                                                           nullptr);
+    else
+      row_mask_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(nbr, n_out, k_vol, b.keys_a, nullptr);
     TSC_LAUNCH_CHECK("plan_row_mask");
     mask_at_pos_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(b.keys_a, n_out, b.rows, b.mask_pos,
                                                             b.vals_a);
@@ -479,7 +559,11 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_
       vi, raster ? nullptr : b.rows, cols_row, n_out, tile_perm, n_tiles, b.mask_pos, b.keys_b, order,
       reinterpret_cast<uint32_t*>(pos_masks));
   TSC_LAUNCH_CHECK("plan_gather");
-  if (nbr_ordered) {
+  if (nbr_ordered && b.nbr_t) {
+    permute_rows_kernel<<<static_cast<unsigned>(ceil_div(n_out, 256)), 256, 0, s>>>(
+        b.nbr_t, b.keys_b, n_out, k_vol, nbr_ordered);
+    TSC_LAUNCH_CHECK("plan_permute_rows");
+  } else if (nbr_ordered) {
     // int4 accesses need 16-byte aligned rows of the map and of the order
     const bool vec = (n_out & 3) == 0 && (reinterpret_cast<uintptr_t>(nbr_ordered) & 15) == 0;
     const int64_t chunks = ceil_div(ceil_div(n_out, 4), 256);  // blocks per slot
