@@ -265,6 +265,38 @@ def test_deterministic_and_order_independent(c_in, c_out, dtype, monkeypatch):
     assert torch.equal(a, b) and torch.equal(a, c) and torch.equal(a, d)
 
 
+@pytest.mark.parametrize("kind,k,s,p", [("subm", (5, 5, 5), 1, 0), ("subm", (1, 3, 3), 1, 0),
+                                        ("strided", (2, 2, 2), 2, 0), ("strided", 3, 2, 1)])
+def test_plan_permutes_every_slot_count(kind, k, s, p, monkeypatch):
+    """The plan's permuted map is the map read through the order, entry for
+    entry, for maps of up to 32 slots (gathered from a row-major copy) and of
+    more (125 slots: gathered slot by slot), on a submanifold build's columns
+    and a strided build's rows; the planned convolution equals the unplanned
+    one bit for bit."""
+    monkeypatch.setattr(I, "_PLAN_MIN_BYTES", 0)  # an order even for these small layers
+    idx = _tiny(41, (28, 28, 28), 2, 3000)
+    x = torch.from_numpy(idx).to(DEV)
+    if kind == "subm":
+        data = generate_subm_indice_pairs(x, (28, 28, 28), 2, k)
+    else:
+        data = generate_strided_indice_pairs(x, (28, 28, 28), 2, k, s, p)
+    n_out = len(data.out_indices)
+    feats = torch.randn(len(idx), 16, generator=torch.Generator().manual_seed(6)).to(DEV)
+    m = _module(kind, 16, 32, k, s, p, dtype=torch.float32, seed=15)
+    pw = m._packed_weight(torch.float32)
+    plain = Fn._run(feats, pw, m.bias, data.neighbour_map(n_out, DEV), None, n_out)
+    order = data.execution_order(n_out, DEV, 64, eager=True)
+    assert order is not None
+    o = order.long().cpu()
+    assert torch.equal(torch.sort(o).values, torch.arange(n_out))
+    nbr = data.neighbour_map(n_out, DEV).cpu()
+    perm = data.ordered_map().cpu()
+    say("plan permute", kind, k, nbr.shape)
+    assert torch.equal(perm, nbr[:, o])
+    planned = Fn.sparse_conv_forward(feats, pw, m.bias, data, n_out)
+    assert torch.equal(planned, plain)
+
+
 @pytest.mark.parametrize("c_in,c_out,dtype", [(64, 64, torch.float16), (32, 32, torch.bfloat16),
                                               (64, 96, torch.float32)])
 def test_slot_split_kernel_matches_the_256_row_kernel(c_in, c_out, dtype):
