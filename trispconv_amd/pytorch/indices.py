@@ -153,6 +153,9 @@ class IndiceData:
         # against that bitmap on the device, with no read-back at build time)
         self._deferred_check = False
         self._uses = 0
+        # for such a build: (an event recorded right behind it, a pinned host
+        # copy of its status word made before that event)
+        self._status_copy: Optional[Tuple[torch.cuda.Event, torch.Tensor]] = None
 
     def _get_pair_num(self) -> torch.Tensor:
         """Pairs per slot, a CPU int64 tensor (indices.py:131).  Submanifold
@@ -446,11 +449,20 @@ class IndiceData:
         if self._deferred_check:
             self._uses += 1
             if self._uses >= 2:
-                # the first reuse under the key reads the build's counts and
-                # status flags once (pair_num raises when the rows were not
-                # the registered strided output set)
+                # the first reuse under the key reads the build's status
+                # flags once and raises when the rows were not the registered
+                # strided output set; it waits for the build alone (its event),
+                # so the convolutions queued after the build keep the GPU busy
                 self._deferred_check = False
-                self.pair_num  # noqa: B018
+                if self._status_copy is not None:
+                    done, flag = self._status_copy
+                    done.synchronize()
+                    self._status_copy = None
+                    if int(flag[0]) & L.FLAG_ROWS_NOT_BITMAP:
+                        raise RuntimeError("generate_subm_indice_pairs: coordinates are not the "
+                                           "rows of the strided build they were registered with")
+                else:
+                    self.pair_num  # noqa: B018
         if self._map_cols is None and self._nbr is None:
             self.neighbour_map(n_out, device, n_in)  # user-assigned lists: checked here
         if n_in is not None:
@@ -564,9 +576,14 @@ def _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil):
     # No read-back here: the rows are the registered output set (same tensor,
     # same version), so there is nothing to validate before the convolution.
     # The probe checks on the device that every row is the bitmap's cell of
-    # its own rank and that no neighbour lies beyond the rows; the counts and
-    # that status flag are read with pair_num, or at the build's first reuse
-    # (the second convolution on it), whichever comes first.
+    # its own rank and that no neighbour lies beyond the rows; that status
+    # flag is read with pair_num, or at the build's first reuse (the second
+    # convolution on it), whichever comes first.  For the reuse its word is
+    # copied to pinned host memory right behind the build, with an event.
+    flag = torch.empty(1, dtype=torch.int32, pin_memory=True)
+    flag.copy_(counts[K:K + 1], non_blocking=True)
+    done = torch.cuda.Event()
+    done.record(torch.cuda.current_stream(dev))
     d = IndiceData._from_tables(
         out_indices=indices, input_indices=indices, input_spatial_shape=shape,
         output_spatial_shape=shape, kernel_size=ks, stride=(1, 1, 1), padding=(0, 0, 0),
@@ -576,6 +593,7 @@ def _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil):
     d._map_masks = masks
     d._counts_pending = (counts, K, lambda: _counts_to_host(counts, K, stream))
     d._deferred_check = True
+    d._status_copy = (done, flag)
     return d
 
 
