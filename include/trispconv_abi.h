@@ -168,7 +168,7 @@ TSC_API int tsc_pairs_from_map(const int32_t* nbr, int64_t n, int32_t k_vol, int
  * Strided pairs.  Replaces generate_strided_indice_pairs
  * (trispconv/pytorch/indices.py:143-259): candidate generation (:177-195),
  * unique(sorted) of output keys (:215-229) and the per-slot split (:235-244).
- * Two phases around the one host read of the counts:
+ * Two phases; the counts are read to the host once, after both are queued:
  *   count: counts [K+3]: counts[k] = pairs in slot k, counts[K] = n_out,
  *          counts[K+1] = status flags, counts[K+2] = input rows with at
  *          least one pair (the row count of this layer's inverse, known
@@ -180,8 +180,15 @@ TSC_API int tsc_pairs_from_map(const int32_t* nbr, int64_t n, int32_t k_vol, int
  *          pairs_in/pairs_out [K][n] (slot k: input rows ascending, output
  *          rank of each); in_ids [n] (may be null): each input row's id
  *          among the rows with a pair (ascending), -1 for the others, which
- *          tsc_inverse_fill_ids takes.  The workspace must be the one
- *          `count` filled.
+ *          tsc_inverse_fill_ids takes.  The workspace and counts must be
+ *          the ones `count` filled, and fill runs behind it on the same
+ *          stream: its kernels read n_out from counts[K] on the device, so
+ *          it can be launched before the counts reach the host.  out_cap
+ *          is the number of rows out_coords and the map have room for (the
+ *          map's row stride is n_out, not out_cap).  When n_out > out_cap
+ *          neither out_coords nor nbr is written (the pair lists and in_ids
+ *          still are): read the counts and call fill again with room for
+ *          n_out rows.
  * ------------------------------------------------------------------------ */
 TSC_API int64_t tsc_strided_workspace_bytes(int64_t n, int32_t k_vol, int32_t batch_size,
                                     const int32_t out_spatial[3] /* host */);
@@ -193,9 +200,10 @@ TSC_API int tsc_strided_count(const int32_t* coords, int64_t n, int32_t batch_si
 TSC_API int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_size,
                      const int32_t spatial[3], const int32_t ksize[3], const int32_t stride[3],
                      const int32_t padding[3], const int32_t dilation[3],
-                     const int32_t out_spatial[3], void* ws, int64_t ws_bytes, int64_t n_out,
-                     int32_t* out_coords, int32_t* nbr, int32_t* pairs_in, int32_t* pairs_out,
-                     int32_t* in_ids, tsc_stream_t stream);
+                     const int32_t out_spatial[3], void* ws, int64_t ws_bytes,
+                     const int32_t* counts, int64_t out_cap, int32_t* out_coords, int32_t* nbr,
+                     int32_t* pairs_in, int32_t* pairs_out, int32_t* in_ids,
+                     tsc_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Inverse pairs.  Replaces the pair swap of SparseInverseConv3d

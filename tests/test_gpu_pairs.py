@@ -107,6 +107,80 @@ def test_strided_and_inverse_pairs_unusual(k, s, p, d):
         _inverse(g, e, f"inverse k={k} s={s} p={p} d={d}")
 
 
+@pytest.mark.parametrize("room", ["none", "one short", "exact", "learned"])
+def test_strided_outputs_beyond_their_room_are_filled_again(room, monkeypatch):
+    """The strided fill is queued before the output count reaches the host,
+    with room for a guessed number of rows; a build whose count exceeds it is
+    filled again at its exact size.  Either way the outputs are the oracle's;
+    the ratio a build gives becomes its geometry's guess."""
+    from trispconv_amd.pytorch import indices as IM
+    idx = _tiny(29, (9, 10, 11), 2, 300)
+    exp_n = len(OP.strided_pairs(idx, (9, 10, 11), 2, 3, 2, 1, 1).out_indices)
+    caps = {"none": 0, "one short": exp_n - 1, "exact": exp_n}
+    monkeypatch.setattr(IM, "_STRIDED_OUT_RATIO", {})
+    if room != "learned":
+        monkeypatch.setattr(IM, "_strided_out_cap", lambda key, n, cells: caps[room])
+    g, e = _strided(idx, (9, 10, 11), 2, 3, 2, 1, 1, f"room {room}")
+    _inverse(g, e, f"inverse, room {room}")
+    key = (2, (9, 10, 11), (3, 3, 3), (2, 2, 2), (1, 1, 1), (1, 1, 1))
+    assert IM._STRIDED_OUT_RATIO[key] == exp_n / len(idx)
+    if room == "learned":
+        cap = IM._strided_out_cap(key, len(idx), 10**9)
+        assert exp_n <= cap <= exp_n * 1.0625 + 257
+        g, e = _strided(idx, (9, 10, 11), 2, 3, 2, 1, 1, "room learned, second build")
+
+
+def test_strided_fill_with_too_little_room_writes_no_outputs():
+    """Through the C ABI: a fill whose out_cap is below n_out leaves
+    out_coords and the map untouched and still writes the pair lists and the
+    input ids; with room to spare it writes the map [K][n_out] from the
+    buffer's start and nothing past it."""
+    from trispconv_amd import _lib as L
+    from trispconv_amd.pytorch import indices as IM
+    lib = L.lib()
+    idx = _tiny(31, (9, 10, 11), 2, 300)
+    x = torch.from_numpy(idx).to(DEV)
+    shape, ks, st, pd, dl = (9, 10, 11), (3, 3, 3), (2, 2, 2), (1, 1, 1), (1, 1, 1)
+    out_shape = IM._output_spatial_shape(shape, ks, st, pd, dl)
+    K, n = 27, len(idx)
+    geo = (L.i3(shape), L.i3(ks), L.i3(st), L.i3(pd), L.i3(dl), L.i3(out_shape))
+    wsb = lib.tsc_strided_workspace_bytes(n, K, 2, geo[5])
+    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+    counts = torch.empty(K + 3, dtype=torch.int32, device=DEV)
+    s = L.stream_of(x)
+    L.check(lib.tsc_strided_count(x.data_ptr(), n, 2, *geo, ws.data_ptr(), wsb,
+                                  counts.data_ptr(), s), "count")
+    n_out = int(counts.cpu()[K])
+    exp = OP.strided_pairs(idx, shape, 2, ks, st, pd, dl)
+    assert n_out == len(exp.out_indices)
+    res = {}
+    for out_cap in (n_out - 1, n_out + 100):
+        say("strided fill, out_cap", out_cap, "n_out", n_out)
+        oc = torch.full((out_cap, 4), -7, dtype=torch.int32, device=DEV)
+        nbr = torch.full((K * out_cap,), -7, dtype=torch.int32, device=DEV)
+        pin = torch.full((K, n), -7, dtype=torch.int32, device=DEV)
+        pout = torch.full((K, n), -7, dtype=torch.int32, device=DEV)
+        ids = torch.full((n,), -7, dtype=torch.int32, device=DEV)
+        L.check(lib.tsc_strided_fill(x.data_ptr(), n, 2, *geo, ws.data_ptr(), wsb,
+                                     counts.data_ptr(), out_cap, oc.data_ptr(), nbr.data_ptr(),
+                                     pin.data_ptr(), pout.data_ptr(), ids.data_ptr(), s), "fill")
+        res[out_cap] = (oc.cpu(), nbr.cpu(), pin.cpu(), pout.cpu(), ids.cpu())
+    oc, nbr, pin, pout, ids = res[n_out - 1]
+    assert bool((oc == -7).all()) and bool((nbr == -7).all()), "no outputs without room"
+    oc2, nbr2, pin2, pout2, ids2 = res[n_out + 100]
+    assert np.array_equal(oc2[:n_out].numpy(), exp.out_indices)
+    assert bool((oc2[n_out:] == -7).all()) and bool((nbr2[K * n_out:] == -7).all())
+    pn = exp.pair_num
+    for k in range(K):
+        assert np.array_equal(pin2[k, :pn[k]].numpy(), exp.pairs_in[k]), f"pairs_in[{k}]"
+        assert np.array_equal(pout2[k, :pn[k]].numpy(), exp.pairs_out[k]), f"pairs_out[{k}]"
+        m = nbr2[k * n_out:(k + 1) * n_out].numpy()
+        want = np.full(n_out, -1, np.int32)
+        want[exp.pairs_out[k]] = exp.pairs_in[k]
+        assert np.array_equal(m, want), f"map row {k}"
+    assert torch.equal(pin, pin2) and torch.equal(pout, pout2) and torch.equal(ids, ids2)
+
+
 def test_empty_and_single_inputs():
     empty = np.zeros((0, 4), np.int32)
     _subm(empty, (4, 4, 4), 1, 3, 1, "empty subm")

@@ -51,7 +51,8 @@ _SIGNATURES = {
     "tsc_strided_count": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, c_i32p, c_i32p,
                                          c_i32p, _vp, _i64, _vp, _vp]),
     "tsc_strided_fill": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, c_i32p, c_i32p,
-                                        c_i32p, _vp, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _vp]),
+                                        c_i32p, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _vp,
+                                        _vp]),
     "tsc_inverse_workspace_bytes": (_i64, [_i64]),
     "tsc_inverse_count": (ctypes.c_int, [_vp, _vp, _i32, _i64, _i64, _vp, _i64, _vp, _vp]),
     "tsc_inverse_fill": (ctypes.c_int, [_vp, _vp, _vp, _i32, _i64, _vp, _i64, _vp, _i64, _i64,
@@ -75,7 +76,7 @@ _SIGNATURES = {
                                          _vp, _vp]),
 }
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _lib: Optional[ctypes.CDLL] = None
 

@@ -542,4 +542,4 @@ int wait_host_word(const int32_t* w, hipStream_t s, int* seen) {
 }  // namespace tsc
 
 extern "C" const char* tsc_last_error(void) { return tsc::last_error(); }
-extern "C" int tsc_abi_version(void) { return 10; }
+extern "C" int tsc_abi_version(void) { return 11; }

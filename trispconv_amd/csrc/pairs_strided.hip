@@ -181,24 +181,35 @@ __global__ void __launch_bounds__(kRows) strided_mark_kernel(const int4* __restr
   }
 }
 
+// The output count the count pass left on the device, or 0 when it exceeds
+// the capacity the caller sized the output coordinates and the map for (then
+// neither is written; the caller reads the count and fills again).
+__device__ __forceinline__ int64_t outputs_within(const int32_t* n_out_dev, int64_t out_cap) {
+  const int64_t n_out = *n_out_dev;
+  return n_out <= out_cap ? n_out : 0;
+}
+
 // One thread per bitmap entry: decode every set bit, in ascending order, into
 // its (b, z, y, x) row at the entry's rank.
-// Blocks from emit_blocks on instead fill the map with -1 (one launch for both).
+// Blocks from emit_blocks on instead fill the map [K][n_out] with -1 (one
+// launch for both).
 __global__ void __launch_bounds__(256) strided_emit_kernel(const uint2* __restrict__ wr,
                                                            int64_t nwords, StridedGeom g,
                                                            int4* __restrict__ out_coords,
-                                                           int64_t n_out, int emit_blocks,
-                                                           uint32_t* __restrict__ map,
-                                                           int64_t map_words) {
+                                                           const int32_t* __restrict__ n_out_dev,
+                                                           int64_t out_cap, int emit_blocks,
+                                                           uint32_t* __restrict__ map, int K) {
+  const int64_t n_out = outputs_within(n_out_dev, out_cap);
   if (static_cast<int>(blockIdx.x) >= emit_blocks) {
     const int64_t nb = gridDim.x - emit_blocks;
+    const int64_t map_words = n_out * K;
     for (int64_t i = (blockIdx.x - emit_blocks) * (int64_t)blockDim.x + threadIdx.x; i < map_words;
          i += nb * blockDim.x)
       map[i] = 0xffffffffu;
     return;
   }
   const int64_t wi = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (wi >= nwords) return;
+  if (wi >= nwords || n_out == 0) return;
   const uint2 e = wr[wi];
   uint32_t bits = e.x;
   if (!bits) return;
@@ -237,19 +248,25 @@ __global__ void __launch_bounds__(256) strided_emit_kernel(const uint2* __restri
 
 // Pair lists in ascending input row per slot (block offsets from the per-slot
 // scan, wave offsets from per-wave counts, lanes ranked by ballot) and the
-// output-major map.  Slots are taken 64 at a time (one LDS count row each).
+// output-major map [K][n_out] (n_out read from the device; the map is left
+// unwritten when n_out exceeds out_cap).  Slots are taken 64 at a time (one
+// LDS count row each).
 template <int KZ, int KY, int KX>
 __global__ void __launch_bounds__(kRows) strided_fill_kernel(const int4* __restrict__ coords,
                                                              int64_t n, int K, StridedGeom g,
                                                              const uint2* __restrict__ wr,
                                                              const int32_t* __restrict__ blk_off,
-                                                             int nblk, int64_t cap, int64_t n_out,
+                                                             int nblk, int64_t cap,
+                                                             const int32_t* __restrict__ n_out_dev,
+                                                             int64_t out_cap,
                                                              int32_t* __restrict__ nbr,
                                                              int32_t* __restrict__ pairs_in,
                                                              int32_t* __restrict__ pairs_out,
                                                              int32_t* __restrict__ in_ids) {
   __shared__ int32_t s_wcnt[kRows / kWave][64];
   __shared__ int32_t s_paired[kRows / kWave];
+  const int64_t n_out = *n_out_dev;
+  const bool to_map = n_out <= out_cap;
   const int t = threadIdx.x;
   const int w = t / kWave;
   const int64_t i = blockIdx.x * (int64_t)kRows + t;
@@ -309,7 +326,7 @@ __global__ void __launch_bounds__(kRows) strided_fill_kernel(const int4* __restr
       if (cell[k] >= 0 && slot_pos < cap && rank < n_out) {
         pairs_in[(int64_t)k * cap + slot_pos] = static_cast<int32_t>(i);
         pairs_out[(int64_t)k * cap + slot_pos] = rank;
-        nbr[(int64_t)k * n_out + rank] = static_cast<int32_t>(i);
+        if (to_map) nbr[(int64_t)k * n_out + rank] = static_cast<int32_t>(i);
       }
     }
     return;
@@ -350,7 +367,7 @@ __global__ void __launch_bounds__(kRows) strided_fill_kernel(const int4* __restr
         if (slot_pos < cap && rank < n_out) {
           pairs_in[(int64_t)k * cap + slot_pos] = static_cast<int32_t>(i);
           pairs_out[(int64_t)k * cap + slot_pos] = rank;
-          nbr[(int64_t)k * n_out + rank] = static_cast<int32_t>(i);
+          if (to_map) nbr[(int64_t)k * n_out + rank] = static_cast<int32_t>(i);
         }
       }
     }
@@ -425,10 +442,12 @@ struct LaunchMark {
 template <int KZ, int KY, int KX>
 struct LaunchFill {
   static int run(const int4* c, int64_t n, int K, StridedGeom g, const uint2* wr,
-                 const int32_t* blk_off, int nblk, int64_t cap, int64_t n_out, int32_t* nbr,
-                 int32_t* pin, int32_t* pout, int32_t* in_ids, hipStream_t s) {
+                 const int32_t* blk_off, int nblk, int64_t cap, const int32_t* n_out_dev,
+                 int64_t out_cap, int32_t* nbr, int32_t* pin, int32_t* pout, int32_t* in_ids,
+                 hipStream_t s) {
     strided_fill_kernel<KZ, KY, KX><<<nblk, kRows, 0, s>>>(c, n, K, g, wr, blk_off, nblk, cap,
-                                                           n_out, nbr, pin, pout, in_ids);
+                                                           n_out_dev, out_cap, nbr, pin, pout,
+                                                           in_ids);
     TSC_LAUNCH_CHECK("strided_fill");
     return 0;
   }
@@ -511,9 +530,9 @@ extern "C" int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_
                                 const int32_t spatial[3], const int32_t ksize[3],
                                 const int32_t stride[3], const int32_t padding[3],
                                 const int32_t dilation[3], const int32_t out_spatial[3], void* ws,
-                                int64_t ws_bytes, int64_t n_out, int32_t* out_coords, int32_t* nbr,
-                                int32_t* pairs_in, int32_t* pairs_out, int32_t* in_ids,
-                                tsc_stream_t stream) {
+                                int64_t ws_bytes, const int32_t* counts, int64_t out_cap,
+                                int32_t* out_coords, int32_t* nbr, int32_t* pairs_in,
+                                int32_t* pairs_out, int32_t* in_ids, tsc_stream_t stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   StridedGeom g;
   int rc = check_geom(n, batch_size, spatial, ksize, stride, padding, dilation, out_spatial, &g);
@@ -523,21 +542,24 @@ extern "C" int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_
   int64_t need = 0;
   carve(nullptr, L, K, &need);
   TSC_REQUIRE(ws && ws_bytes >= need, "strided: workspace too small");
-  TSC_REQUIRE(n_out >= 0 && n_out <= L.cells, "strided: n_out=%lld invalid", (long long)n_out);
-  if (n > 0 && n_out == 0 && in_ids)  // no row has a pair
-    return fill_u32(reinterpret_cast<uint32_t*>(in_ids), n, 0xffffffffu, s);
-  if (n == 0 || n_out == 0) return 0;
-  TSC_REQUIRE(coords && out_coords && nbr && pairs_in && pairs_out, "strided: null pointer");
+  TSC_REQUIRE(counts != nullptr, "strided: counts is null");
+  TSC_REQUIRE(out_cap >= 0 && out_cap < (int64_t(1) << 31), "strided: out_cap=%lld invalid",
+              (long long)out_cap);
+  if (n == 0) return 0;
+  TSC_REQUIRE(coords && pairs_in && pairs_out && (out_cap == 0 || (out_coords && nbr)),
+              "strided: null pointer");
   Buffers b = carve(ws, L, K, nullptr);
-  // the output coordinates, and the map's -1 fill, in one launch
+  // the output coordinates, and the map's -1 fill, in one launch; both take
+  // n_out from counts[K] on the device, so this call needs no host read
   const int emit_blocks = static_cast<int>(ceil_div(L.nwords, 256));
-  const int64_t map_words = n_out * K;
-  const int fill_blocks = static_cast<int>(std::min<int64_t>(std::max<int64_t>(ceil_div(map_words, 256), 1), 4096));
+  const int fill_blocks = static_cast<int>(
+      std::min<int64_t>(std::max<int64_t>(ceil_div(out_cap * K, 256), 1), 4096));
   strided_emit_kernel<<<emit_blocks + fill_blocks, 256, 0, s>>>(
-      b.wr, L.nwords, g, reinterpret_cast<int4*>(out_coords), n_out, emit_blocks,
-      reinterpret_cast<uint32_t*>(nbr), map_words);
+      b.wr, L.nwords, g, reinterpret_cast<int4*>(out_coords), counts + K, out_cap, emit_blocks,
+      reinterpret_cast<uint32_t*>(nbr), K);
   TSC_LAUNCH_CHECK("strided_emit");
   return by_shape<LaunchFill>(g.ks, reinterpret_cast<const int4*>(coords), n, K, g,
                               static_cast<const uint2*>(b.wr), static_cast<const int32_t*>(b.blk_off),
-                              (int)L.nblk, n, n_out, nbr, pairs_in, pairs_out, in_ids, s);
+                              (int)L.nblk, n, counts + K, out_cap, nbr, pairs_in, pairs_out, in_ids,
+                              s);
 }

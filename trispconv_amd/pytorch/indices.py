@@ -16,7 +16,7 @@ from __future__ import annotations
 import ctypes
 import functools
 from dataclasses import dataclass
-from typing import Callable, List, Optional, Sequence, Tuple
+from typing import Callable, Dict, List, Optional, Sequence, Tuple
 
 import torch
 from torch.utils.weak import WeakIdKeyDictionary
@@ -692,23 +692,46 @@ def generate_strided_indice_pairs(indices: torch.Tensor, spatial_shape, batch_si
     L.check(lib.tsc_strided_count(coords.data_ptr(), n, int(batch_size), *sz.geo, ws.data_ptr(),
                                   sz.ws_bytes, counts.data_ptr(), stream),
             "generate_strided_indice_pairs")
-    host = counts.cpu()
+    # the counts go to the host behind the count pass; the fill is queued
+    # before they arrive, with room for the rows this geometry's largest
+    # output ratio so far predicts, and is queued again at the exact size in
+    # the rare build that outgrows it
+    host = torch.empty(K + 3, dtype=torch.int32, pin_memory=True)
+    host.copy_(counts, non_blocking=True)
+    counted = torch.cuda.Event()
+    counted.record(torch.cuda.current_stream(dev))
+    geo_key = (int(batch_size), shape, ks, st, pd, dil)
+    cap = _strided_out_cap(geo_key, n, sz.cells)
+
+    def fill(out_cap: int):
+        # the output coordinates (the next tensor's indices, with their own
+        # storage and version counter); the map and the two pair tables in
+        # one allocation at 256-byte aligned offsets, passed as raw
+        # addresses, the views made after the launch
+        out_coords = torch.empty((out_cap, 4), dtype=torch.int32, device=dev)
+        o_pin = _align64(K * out_cap)
+        tables = torch.empty(max(o_pin + 2 * _align64(K * n) + n, 1), dtype=torch.int32,
+                             device=dev)
+        base = tables.data_ptr()
+        L.check(lib.tsc_strided_fill(coords.data_ptr(), n, int(batch_size), *sz.geo,
+                                     ws.data_ptr(), sz.ws_bytes, counts.data_ptr(), out_cap,
+                                     out_coords.data_ptr(), base, base + 4 * o_pin,
+                                     base + 4 * (o_pin + _align64(K * n)),
+                                     base + 4 * (o_pin + 2 * _align64(K * n)), stream),
+                "generate_strided_indice_pairs")
+        return out_coords, tables, o_pin
+
+    out_coords, tables, o_pin = fill(cap)
+    counted.synchronize()
     _raise_status(int(host[K + 1]), "generate_strided_indice_pairs")
     n_out = int(host[K])
-    # the output coordinates (the next tensor's indices, with their own
-    # storage and version counter); the map and the two pair tables in one
-    # allocation at 256-byte aligned offsets, passed as raw addresses, the
-    # views made after the launch
-    out_coords = torch.empty((n_out, 4), dtype=torch.int32, device=dev)
-    o_pin = _align64(K * n_out)
+    if n > 0:
+        _STRIDED_OUT_RATIO[geo_key] = max(_STRIDED_OUT_RATIO.get(geo_key, 0.0), n_out / n)
+    if n_out > cap:
+        out_coords, tables, o_pin = fill(n_out)
+    out_coords = out_coords[:n_out]
     o_pout = o_pin + _align64(K * n)
     o_ids = o_pout + _align64(K * n)
-    tables = torch.empty(max(o_ids + n, 1), dtype=torch.int32, device=dev)
-    base = tables.data_ptr()
-    L.check(lib.tsc_strided_fill(coords.data_ptr(), n, int(batch_size), *sz.geo, ws.data_ptr(),
-                                 sz.ws_bytes, n_out, out_coords.data_ptr(), base,
-                                 base + 4 * o_pin, base + 4 * o_pout, base + 4 * o_ids, stream),
-            "generate_strided_indice_pairs")
     nbr = tables[:K * n_out].view(K, n_out)
     pin = tables[o_pin:o_pin + K * n].view(K, n)
     pout = tables[o_pout:o_pout + K * n].view(K, n)
@@ -733,8 +756,25 @@ class _StridedSizes:
         self.geo = (L.i3(shape), L.i3(ks), L.i3(st), L.i3(pd), L.i3(dil), L.i3(out_shape))
         self.ws_bytes = max(int(L.lib().tsc_strided_workspace_bytes(n, K, batch_size,
                                                                       self.geo[5])), 1)
-        cells = batch_size * out_shape[0] * out_shape[1] * out_shape[2]
-        self.out_words = (cells + 31) // 32
+        self.cells = batch_size * out_shape[0] * out_shape[1] * out_shape[2]
+        self.out_words = (self.cells + 31) // 32
+
+
+# Largest n_out / n each strided geometry (batch size, input shape, kernel,
+# stride, padding, dilation) has given in this process.  A build sizes its
+# output coordinates and map for that ratio (n rows while it is unknown)
+# before its count reaches the host; a build that outgrows it is filled again.
+_STRIDED_OUT_RATIO: Dict[tuple, float] = {}
+
+
+def _strided_out_cap(geo_key: tuple, n: int, cells: int) -> int:
+    """Rows of room for a strided build's outputs before its count is known:
+    1/16 above the geometry's largest ratio so far, and never more than the
+    output grid's cells."""
+    if n == 0:
+        return 0
+    ratio = _STRIDED_OUT_RATIO.get(geo_key, 1.0)
+    return int(min(cells, (1 << 31) - 1, int(n * ratio * 1.0625) + 256))
 
 
 @functools.lru_cache(maxsize=64)
