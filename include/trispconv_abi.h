@@ -65,9 +65,23 @@ TSC_API int tsc_abi_version(void);
  * in (b,z,y,x) order (bitmap path), 0 when they are the rows in order (hash
  * path, cols_row[t] = t).  The reference's pair lists follow from the map
  * with tsc_map_to_rows and tsc_pairs_from_map.
+ *
+ * Byte marks.  On dense grids the bitmap build marks each occupied cell with
+ * a byte first.  A caller that builds repeatedly on one stream can keep
+ * those bytes between builds (tsc_*_marks_bytes of them, zeroed once when
+ * allocated) and pass them with a generation value gen in 1..255, a new one
+ * per build: a build writes gen and reads only gen, so nothing zeroes the
+ * marks before a build (one launch and one pass over the grid fewer).  The
+ * caller zeroes them again before reusing a value, and two builds that may
+ * overlap (other streams) need marks of their own.  The workspace is then
+ * the size given with marks_outside = 1.  tsc_*_marks_bytes returns 0 when
+ * a build of that shape does not mark through bytes (it then ignores marks).
  * ------------------------------------------------------------------------ */
 TSC_API int64_t tsc_subm_workspace_bytes(int64_t n, int32_t k_vol, int32_t batch_size,
-                                         const int32_t spatial[3] /* host */);
+                                         const int32_t spatial[3] /* host */,
+                                         int32_t marks_outside);
+TSC_API int64_t tsc_subm_marks_bytes(int64_t n, int32_t k_vol, int32_t batch_size,
+                                     const int32_t spatial[3] /* host */);
 TSC_API int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_size,
                            const int32_t spatial[3] /* host */, const int32_t ksize[3] /* host */,
                            const int32_t dilation[3] /* host */, void* ws, int64_t ws_bytes,
@@ -91,13 +105,15 @@ TSC_API int tsc_subm_pairs(const int32_t* coords, int64_t n, int32_t batch_size,
  * (K <= 32): nbr has K + 1 rows and, when the columns come out in (b,z,y,x)
  * order (result[1] = 1), row K receives each column's slot mask (bit k: the
  * column's row has a neighbour through slot k), which tsc_conv_forward reads
- * with nbr_ordered = 2. */
+ * with nbr_ordered = 2.  marks (may be null), marks_size, gen: byte marks
+ * kept by the caller (above). */
 TSC_API int64_t tsc_subm_slot_blocks_len(int64_t n, int32_t k_vol);
 TSC_API int tsc_subm_pairs_checked(const int32_t* coords, int64_t n, int32_t batch_size,
                                    const int32_t spatial[3] /* host */,
                                    const int32_t ksize[3] /* host */,
                                    const int32_t dilation[3] /* host */, void* ws,
-                                   int64_t ws_bytes, int32_t* cols_row, int32_t* nbr,
+                                   int64_t ws_bytes, void* marks, int64_t marks_size,
+                                   int32_t gen, int32_t* cols_row, int32_t* nbr,
                                    int32_t* counts, int32_t* slot_blocks, int32_t mask_row,
                                    int32_t result[2] /* host */, tsc_stream_t stream);
 /* counts[k] = sum of slot_blocks[k][*] for the n rows of a
@@ -175,7 +191,9 @@ TSC_API int tsc_pairs_from_map(const int32_t* nbr, int64_t n, int32_t k_vol, int
  *          with the same host read).
  *   The workspace begins with the output grid's occupancy bitmap, one
  *   (word, rank) 8-byte entry per 32 cells, ranks = output rows, which
- *   tsc_subm_pairs_from_bitmap can build on.
+ *   tsc_subm_pairs_from_bitmap can build on.  marks (may be null),
+ *   marks_size, gen: byte marks kept by the caller, as for the submanifold
+ *   build (tsc_strided_marks_bytes; the workspace sized with marks_outside).
  *   fill:  out_coords [n_out][4] sorted by (b,z,y,x); nbr [K][n_out];
  *          pairs_in/pairs_out [K][n] (slot k: input rows ascending, output
  *          rank of each); in_ids [n] (may be null): each input row's id
@@ -191,12 +209,15 @@ TSC_API int tsc_pairs_from_map(const int32_t* nbr, int64_t n, int32_t k_vol, int
  *          n_out rows.
  * ------------------------------------------------------------------------ */
 TSC_API int64_t tsc_strided_workspace_bytes(int64_t n, int32_t k_vol, int32_t batch_size,
-                                    const int32_t out_spatial[3] /* host */);
+                                    const int32_t out_spatial[3] /* host */,
+                                    int32_t marks_outside);
+TSC_API int64_t tsc_strided_marks_bytes(int64_t n, int32_t k_vol, int32_t batch_size,
+                                        const int32_t out_spatial[3] /* host */);
 TSC_API int tsc_strided_count(const int32_t* coords, int64_t n, int32_t batch_size,
                       const int32_t spatial[3], const int32_t ksize[3], const int32_t stride[3],
                       const int32_t padding[3], const int32_t dilation[3],
-                      const int32_t out_spatial[3], void* ws, int64_t ws_bytes, int32_t* counts,
-                      tsc_stream_t stream);
+                      const int32_t out_spatial[3], void* ws, int64_t ws_bytes, void* marks,
+                      int64_t marks_size, int32_t gen, int32_t* counts, tsc_stream_t stream);
 TSC_API int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_size,
                      const int32_t spatial[3], const int32_t ksize[3], const int32_t stride[3],
                      const int32_t padding[3], const int32_t dilation[3],

@@ -144,11 +144,11 @@ def test_strided_fill_with_too_little_room_writes_no_outputs():
     out_shape = IM._output_spatial_shape(shape, ks, st, pd, dl)
     K, n = 27, len(idx)
     geo = (L.i3(shape), L.i3(ks), L.i3(st), L.i3(pd), L.i3(dl), L.i3(out_shape))
-    wsb = lib.tsc_strided_workspace_bytes(n, K, 2, geo[5])
+    wsb = lib.tsc_strided_workspace_bytes(n, K, 2, geo[5], 0)
     ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
     counts = torch.empty(K + 3, dtype=torch.int32, device=DEV)
     s = L.stream_of(x)
-    L.check(lib.tsc_strided_count(x.data_ptr(), n, 2, *geo, ws.data_ptr(), wsb,
+    L.check(lib.tsc_strided_count(x.data_ptr(), n, 2, *geo, ws.data_ptr(), wsb, None, 0, 0,
                                   counts.data_ptr(), s), "count")
     n_out = int(counts.cpu()[K])
     exp = OP.strided_pairs(idx, shape, 2, ks, st, pd, dl)
@@ -215,6 +215,128 @@ def _clustered_with_duplicates(seed, shape, B, n, box, dups):
     idx = np.concatenate(parts).astype(np.int32)
     idx = np.concatenate([idx, idx[rng.choice(len(idx), size=dups)]])
     return idx[rng.permutation(len(idx))]
+
+
+def _stream_marks():
+    from trispconv_amd import _lib as L
+    from trispconv_amd.pytorch import indices as IM
+    probe = torch.zeros(1, device=DEV)
+    return IM._MARKS.get((probe.device.index, L.stream_of(probe)))
+
+
+def test_byte_marks_kept_between_builds_never_leak():
+    """SubM and strided builds on one stream share byte marks that no build
+    zeroes.  Builds on shrinking coordinate sets of one grid (every cell of a
+    later set was marked by an earlier build), a build that raises on a bad
+    batch index followed by good ones, the values running out (zeroed, then
+    1 again) and a larger grid (new marks) all give the oracle's pairs."""
+    shape, B = (20, 22, 24), 2
+    big = _tiny(51, shape, B, 1800)
+    small = big[: len(big) // 3]
+    for what, idx in (("all", big), ("a third", small), ("all again", big), ("a third", small)):
+        _subm(idx, shape, B, 3, 1, f"kept marks, subm on {what}")
+        g, e = _strided(idx, shape, B, 3, 2, 1, 1, f"kept marks, strided on {what}")
+    m = _stream_marks()
+    assert m is not None and m.buf is not None and 2 <= m.gen <= 255
+    bad = big.copy()
+    bad[5, 0] = B  # batch index out of range
+    with pytest.raises(IndexError, match="batch index"):
+        generate_subm_indice_pairs(torch.from_numpy(bad).to(DEV), shape, B, 3, 1)
+    with pytest.raises(IndexError, match="batch index"):
+        generate_strided_indice_pairs(torch.from_numpy(bad).to(DEV), shape, B, 3, 2, 1)
+    _subm(small, shape, B, 3, 1, "kept marks, subm after a bad build")
+    _strided(small, shape, B, 3, 2, 1, 1, "kept marks, strided after a bad build")
+    m.gen = 253  # three values left: the fourth build zeroes the marks first
+    for i in range(3):
+        _subm(big if i % 2 else small, shape, B, 3, 1, f"kept marks, values running out {i}")
+        _strided(small if i % 2 else big, shape, B, 3, 2, 1, 1, f"values running out {i}")
+    assert m.gen <= 6
+    size = m.buf.numel()
+    wide = (40, 44, 48)
+    _subm(_tiny(53, wide, B, 12000), wide, B, 3, 1, "kept marks, larger grid")
+    assert _stream_marks().buf.numel() > size
+
+
+def test_byte_marks_through_the_c_abi():
+    """tsc_subm_pairs_checked and tsc_strided_count with caller-kept marks and
+    a new value per build, against the same builds with the marks in the
+    workspace: the same map, counts, output set and status flags."""
+    import ctypes
+    from trispconv_amd import _lib as L
+    lib = L.lib()
+    shape, B, K = (20, 22, 24), 2, 27
+    args = (L.i3(shape), L.i3((3, 3, 3)), L.i3((1, 1, 1)))
+    mb = lib.tsc_subm_marks_bytes(3000, K, B, args[0])
+    assert mb > 0
+    marks = torch.zeros(mb, dtype=torch.uint8, device=DEV)
+    for gen, seed in ((1, 61), (2, 62), (3, 61)):
+        idx = _tiny(seed, shape, B, 1500 if seed == 61 else 700)
+        if gen == 3:
+            idx[7, 0] = -1  # a bad batch index: the flag comes from the marks' status words
+        c = torch.from_numpy(idx).to(DEV)
+        n = len(idx)
+        out = {}
+        for mode in ("workspace", "kept"):
+            say("byte marks through the C ABI:", mode, "gen", gen, "n", n)
+            kept = mode == "kept"
+            wsb = lib.tsc_subm_workspace_bytes(n, K, B, args[0], int(kept))
+            ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+            cols = torch.empty(n, dtype=torch.int32, device=DEV)
+            nbr = torch.empty((K, n), dtype=torch.int32, device=DEV)
+            counts = torch.empty(K + 2, dtype=torch.int32, device=DEV)
+            blocks = torch.empty(lib.tsc_subm_slot_blocks_len(n, K), dtype=torch.int32,
+                                 device=DEV)
+            result = (ctypes.c_int32 * 2)()
+            L.check(lib.tsc_subm_pairs_checked(
+                c.data_ptr(), n, B, *args, ws.data_ptr(), wsb,
+                marks.data_ptr() if kept else None, mb if kept else 0, gen if kept else 0,
+                cols.data_ptr(), nbr.data_ptr(), counts.data_ptr(), blocks.data_ptr(), 0, result,
+                L.stream_of(c)), "checked")
+            torch.cuda.synchronize()
+            st = (result[0], result[1])
+            if st[0] == 0:
+                L.check(lib.tsc_subm_counts(blocks.data_ptr(), n, K, counts.data_ptr(), None,
+                                            L.stream_of(c)), "counts")
+            out[mode] = (st, cols.cpu(), nbr.cpu(), counts.cpu())
+        assert out["workspace"][0] == out["kept"][0], gen
+        assert (out["kept"][0][0] != 0) == (gen == 3)
+        if gen != 3:
+            for a, b in zip(out["workspace"][1:], out["kept"][1:]):
+                assert torch.equal(a, b), gen
+        # strided, same marks and the next value
+        sgen = gen + 3
+        sh_out = (10, 11, 12)
+        geo = (L.i3(shape), L.i3((3, 3, 3)), L.i3((2, 2, 2)), L.i3((1, 1, 1)), L.i3((1, 1, 1)),
+               L.i3(sh_out))
+        smb = lib.tsc_strided_marks_bytes(n, K, B, geo[5])
+        assert 0 < smb <= mb
+        res = {}
+        for mode in ("workspace", "kept"):
+            kept = mode == "kept"
+            wsb = lib.tsc_strided_workspace_bytes(n, K, B, geo[5], int(kept))
+            ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+            counts = torch.empty(K + 3, dtype=torch.int32, device=DEV)
+            L.check(lib.tsc_strided_count(c.data_ptr(), n, B, *geo, ws.data_ptr(), wsb,
+                                          marks.data_ptr() if kept else None, mb if kept else 0,
+                                          sgen if kept else 0, counts.data_ptr(),
+                                          L.stream_of(c)), "strided count")
+            h = counts.cpu()
+            n_out = int(h[K])
+            oc = torch.empty((max(n_out, 1), 4), dtype=torch.int32, device=DEV)
+            nb = torch.empty(K * max(n_out, 1), dtype=torch.int32, device=DEV)
+            pin = torch.empty((K, n), dtype=torch.int32, device=DEV)
+            pout = torch.empty((K, n), dtype=torch.int32, device=DEV)
+            L.check(lib.tsc_strided_fill(c.data_ptr(), n, B, *geo, ws.data_ptr(), wsb,
+                                         counts.data_ptr(), n_out, oc.data_ptr(), nb.data_ptr(),
+                                         pin.data_ptr(), pout.data_ptr(), None, L.stream_of(c)),
+                    "strided fill")
+            pn = h[:K].tolist()
+            res[mode] = (h, oc[:n_out].cpu(), nb[:K * n_out].cpu(),
+                         torch.cat([pin[k, :pn[k]] for k in range(K)]).cpu(),
+                         torch.cat([pout[k, :pn[k]] for k in range(K)]).cpu())
+        for a, b in zip(res["workspace"], res["kept"]):
+            assert torch.equal(a, b), ("strided", gen)
+        assert (int(res["kept"][0][K + 1]) != 0) == (gen == 3)
 
 
 # The submanifold builder looks cells up in an occupancy bitmap when the grid
@@ -402,7 +524,7 @@ def test_checked_build_matches_the_plain_build(shape, dups, what):
     c = torch.from_numpy(idx).to(DEV)
     n = len(idx)
     args = (L.i3(shape), L.i3((3, 3, 3)), L.i3((1, 1, 1)))
-    ws_bytes = lib.tsc_subm_workspace_bytes(n, K, B, args[0])
+    ws_bytes = lib.tsc_subm_workspace_bytes(n, K, B, args[0], 0)
     out = {}
     for mode in ("plain", "checked"):
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
@@ -420,7 +542,8 @@ def test_checked_build_matches_the_plain_build(shape, dups, what):
             blocks = torch.empty(lib.tsc_subm_slot_blocks_len(n, K), dtype=torch.int32, device=DEV)
             result = (ctypes.c_int32 * 2)()
             L.check(lib.tsc_subm_pairs_checked(c.data_ptr(), n, B, *args, ws.data_ptr(), ws_bytes,
-                                               cols.data_ptr(), nbr.data_ptr(), counts.data_ptr(),
+                                               None, 0, 0, cols.data_ptr(), nbr.data_ptr(),
+                                               counts.data_ptr(),
                                                blocks.data_ptr(), 1, result, s), "checked")
             assert result[0] == 0, what
             if result[1]:  # columns in (b,z,y,x) order: row K holds their slot masks
@@ -455,7 +578,7 @@ def test_checked_build_reports_bad_coordinates():
         c = torch.from_numpy(idx).to(DEV)
         n = len(idx)
         args = (L.i3(shape), L.i3((3, 3, 3)), L.i3((1, 1, 1)))
-        ws_bytes = lib.tsc_subm_workspace_bytes(n, K, 1, args[0])
+        ws_bytes = lib.tsc_subm_workspace_bytes(n, K, 1, args[0], 0)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=DEV)
         cols = torch.empty(n, dtype=torch.int32, device=DEV)
         nbr = torch.empty((K, n), dtype=torch.int32, device=DEV)
@@ -463,7 +586,8 @@ def test_checked_build_reports_bad_coordinates():
         blocks = torch.empty(lib.tsc_subm_slot_blocks_len(n, K), dtype=torch.int32, device=DEV)
         result = (ctypes.c_int32 * 2)()
         L.check(lib.tsc_subm_pairs_checked(c.data_ptr(), n, 1, *args, ws.data_ptr(), ws_bytes,
-                                           cols.data_ptr(), nbr.data_ptr(), counts.data_ptr(),
+                                           None, 0, 0, cols.data_ptr(), nbr.data_ptr(),
+                                           counts.data_ptr(),
                                            blocks.data_ptr(), 0, result, L.stream_of(c)),
                 "checked")
         assert result[0] == flag, bad

@@ -206,14 +206,28 @@ def test_integration_load_snippet_runs_as_written():
 def test_workspace_queries_are_host_only():
     lib = L.lib()
     # dense enough for the occupancy bitmap: a word and its rank per 32 cells
-    assert lib.tsc_subm_workspace_bytes(500_000, 27, 1, L.i3((256, 256, 256))) >= \
+    assert lib.tsc_subm_workspace_bytes(500_000, 27, 1, L.i3((256, 256, 256)), 0) >= \
         2 * (256 ** 3 // 32) * 4
     assert lib.tsc_pairs_from_map_workspace_bytes(500_000, 27) >= 2 * 27 * (500_000 // 256) * 4
     # very sparse grid: the hash (2N..4N 8-byte slots), far below the bitmap
-    sparse = lib.tsc_subm_workspace_bytes(60_000, 27, 4, L.i3((41, 1600, 1408)))
+    sparse = lib.tsc_subm_workspace_bytes(60_000, 27, 4, L.i3((41, 1600, 1408)), 0)
     assert 1 << 20 <= sparse < 4 * 41 * 1600 * 1408 // 8
-    assert lib.tsc_subm_workspace_bytes(10, 27, 0, L.i3((4, 4, 4))) == -1
-    assert lib.tsc_strided_workspace_bytes(1000, 27, 2, L.i3((21, 800, 704))) > 2 * 21 * 800 * 704 // 8
+    assert lib.tsc_subm_workspace_bytes(10, 27, 0, L.i3((4, 4, 4)), 0) == -1
+    assert lib.tsc_strided_workspace_bytes(1000, 27, 2, L.i3((21, 800, 704)), 0) > \
+        2 * 21 * 800 * 704 // 8
+    # byte marks: a byte per cell of a dense grid plus status words, else none;
+    # a workspace without them is smaller by their size
+    dense = L.i3((256, 256, 256))
+    mb = lib.tsc_subm_marks_bytes(500_000, 27, 1, dense)
+    assert mb >= 256 ** 3 and mb % 16 == 0
+    assert lib.tsc_subm_workspace_bytes(500_000, 27, 1, dense, 0) - \
+        lib.tsc_subm_workspace_bytes(500_000, 27, 1, dense, 1) >= 256 ** 3
+    assert lib.tsc_subm_marks_bytes(60_000, 27, 4, L.i3((41, 1600, 1408))) == 0
+    lidar = L.i3((21, 800, 704))
+    assert lib.tsc_strided_marks_bytes(400_000, 27, 2, lidar) >= 2 * 21 * 800 * 704
+    assert lib.tsc_strided_marks_bytes(1000, 27, 2, lidar) == 0  # sparse: atomic marks
+    assert lib.tsc_strided_workspace_bytes(400_000, 27, 2, lidar, 0) - \
+        lib.tsc_strided_workspace_bytes(400_000, 27, 2, lidar, 1) >= 2 * 21 * 800 * 704
     assert lib.tsc_inverse_workspace_bytes(1000) >= 8000
     assert lib.tsc_plan_workspace_bytes(1000, 27) >= 16000
     # MFMA-eligible layers pack 2-byte weights, others fp32
@@ -238,7 +252,7 @@ def test_argument_errors_return_codes_without_gpu():
     assert rc == 1 and b"out of range" in lib.tsc_last_error()
     rc = lib.tsc_strided_count(None, 10, 1, L.i3((8, 8, 8)), L.i3((3, 3, 3)), L.i3((2, 2, 2)),
                                L.i3((1, 1, 1)), L.i3((1, 1, 1)), L.i3((5, 5, 5)), None, 0, None,
-                               None)
+                               0, 0, None, None)
     assert rc == 1 and b"output shape" in lib.tsc_last_error()
     rc = lib.tsc_conv_forward(None, 7, 1, 1, None, None, 0, None, None, 0, 1, 1, 1, None, None)
     assert rc == 1 and b"dtype" in lib.tsc_last_error()

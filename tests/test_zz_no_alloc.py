@@ -46,7 +46,7 @@ def _outputs(n, K):
 def _with_workspace(c, B, shape, ks, dil):
     lib = L.lib()
     n, K = c.shape[0], ks[0] * ks[1] * ks[2]
-    ws = L.workspace(lib.tsc_subm_workspace_bytes(n, K, B, L.i3(shape)), DEV)
+    ws = L.workspace(lib.tsc_subm_workspace_bytes(n, K, B, L.i3(shape), 0), DEV)
     cols_row, nbr, counts = _outputs(n, K)
     L.check(lib.tsc_subm_pairs(c.data_ptr(), n, B, L.i3(shape), L.i3(ks), L.i3(dil),
                                ws.data_ptr(), ws.numel(), cols_row.data_ptr(), nbr.data_ptr(),

@@ -32,12 +32,14 @@ _i32 = ctypes.c_int32
 _SIGNATURES = {
     "tsc_last_error": (ctypes.c_char_p, []),
     "tsc_abi_version": (ctypes.c_int, []),
-    "tsc_subm_workspace_bytes": (_i64, [_i64, _i32, _i32, c_i32p]),
+    "tsc_subm_workspace_bytes": (_i64, [_i64, _i32, _i32, c_i32p, _i32]),
+    "tsc_subm_marks_bytes": (_i64, [_i64, _i32, _i32, c_i32p]),
     "tsc_subm_pairs": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, _vp, _i64,
                                       _vp, _vp, _vp, _vp]),
     "tsc_subm_slot_blocks_len": (_i64, [_i64, _i32]),
     "tsc_subm_pairs_checked": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, _vp, _i64,
-                                              _vp, _vp, _vp, _vp, _i32, c_i32p, _vp]),
+                                              _vp, _i64, _i32, _vp, _vp, _vp, _vp, _i32, c_i32p,
+                                              _vp]),
     "tsc_subm_counts": (ctypes.c_int, [_vp, _i64, _i32, _vp, c_i32p, _vp]),
     "tsc_subm_pairs_noalloc_limit": (_i64, []),
     "tsc_subm_pairs_noalloc": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, _vp, _vp,
@@ -47,9 +49,10 @@ _SIGNATURES = {
     "tsc_map_to_rows": (ctypes.c_int, [_vp, _vp, _i64, _i64, _i32, _vp, _vp]),
     "tsc_pairs_from_map_workspace_bytes": (_i64, [_i64, _i32]),
     "tsc_pairs_from_map": (ctypes.c_int, [_vp, _i64, _i32, _i64, _vp, _i64, _vp, _vp, _vp]),
-    "tsc_strided_workspace_bytes": (_i64, [_i64, _i32, _i32, c_i32p]),
+    "tsc_strided_workspace_bytes": (_i64, [_i64, _i32, _i32, c_i32p, _i32]),
+    "tsc_strided_marks_bytes": (_i64, [_i64, _i32, _i32, c_i32p]),
     "tsc_strided_count": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, c_i32p, c_i32p,
-                                         c_i32p, _vp, _i64, _vp, _vp]),
+                                         c_i32p, _vp, _i64, _vp, _i64, _i32, _vp, _vp]),
     "tsc_strided_fill": (ctypes.c_int, [_vp, _i64, _i32, c_i32p, c_i32p, c_i32p, c_i32p, c_i32p,
                                         c_i32p, _vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _vp,
                                         _vp]),
@@ -76,7 +79,7 @@ _SIGNATURES = {
                                          _vp, _vp]),
 }
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _lib: Optional[ctypes.CDLL] = None
 

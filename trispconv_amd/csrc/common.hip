@@ -119,6 +119,7 @@ __device__ void slot_scan_block(const SlotScan& a, int k, uint32_t* s_wave) {
       totals[k] = static_cast<int32_t>(carry);
     else
       *extra_total = static_cast<int32_t>(carry);
+    if (k == 0 && a.mark_words) *a.status = mark_flags(a.mark_words, a.gen);
   }
 }
 
@@ -329,22 +330,33 @@ __global__ void __launch_bounds__(kBmThreads) bitmap_reduce_kernel(const uint4* 
   if (threadIdx.x == 0) sums[blockIdx.x] = tot;
 }
 
-// The reduce pass for occupancy given as one byte per cell (0 or 1): packs
-// each word's 32 bytes into its bit mask (word x, y zeroed; words past nw,
-// the entry padding, read zero bytes) and sums the tile's popcounts.  Four
-// bytes b0..b3 of a little-endian dword map to the nibble b0 + 2b1 + 4b2 +
-// 8b3 in the top byte of dword * 0x01020408 (no carries reach it).
-__device__ __forceinline__ uint32_t pack_bytes(uint4 a, uint4 b) {
-  auto nib = [](uint32_t v) { return (v * 0x01020408u) >> 24; };
-  return nib(a.x) | nib(a.y) << 4 | nib(a.z) << 8 | nib(a.w) << 12 | nib(b.x) << 16 |
-         nib(b.y) << 20 | nib(b.z) << 24 | nib(b.w) << 28;
+// The reduce pass for occupancy given as one byte per cell (set where the
+// byte equals the build's generation value): packs each word's 32 bytes into
+// its bit mask (word x, y zeroed; the padding word past nw packs bytes that
+// no build marks) and sums the tile's popcounts.
+// A byte y of v ^ (gen * 0x01010101) is 0 exactly where v's byte equals gen,
+// and then, only then, bit 7 of ~(((y & 0x7f) + 0x7f) | y) is set (the sum
+// stays within the byte).  Those bits, moved to bit 0 of their bytes b0..b3,
+// give the nibble b0 + 2b1 + 4b2 + 8b3 in the top byte of dword * 0x01020408
+// (no carries reach it).
+__device__ __forceinline__ uint32_t marked_nibble(uint32_t v, uint32_t rep) {
+  const uint32_t y = v ^ rep;
+  const uint32_t z = ~(((y & 0x7f7f7f7fu) + 0x7f7f7f7fu) | y) & 0x80808080u;
+  return ((z >> 7) * 0x01020408u) >> 24;
+}
+
+__device__ __forceinline__ uint32_t pack_bytes(uint4 a, uint4 b, uint32_t rep) {
+  return marked_nibble(a.x, rep) | marked_nibble(a.y, rep) << 4 | marked_nibble(a.z, rep) << 8 |
+         marked_nibble(a.w, rep) << 12 | marked_nibble(b.x, rep) << 16 |
+         marked_nibble(b.y, rep) << 20 | marked_nibble(b.z, rep) << 24 |
+         marked_nibble(b.w, rep) << 28;
 }
 
 __global__ void __launch_bounds__(kBmThreads) bitmap_pack_kernel(const uint4* __restrict__ bytes,
                                                                  uint4* __restrict__ wr2, int64_t nw,
                                                                  uint32_t* __restrict__ sums,
                                                                  int nsum, SlotScan scan,
-                                                                 int32_t* started) {
+                                                                 int32_t* started, uint32_t gen) {
   __shared__ uint32_t s_wave[33];
   signal_started(started);
   if (static_cast<int>(blockIdx.x) >= nsum) {  // blocks past the tiles: a slot scan riding along
@@ -359,8 +371,9 @@ __global__ void __launch_bounds__(kBmThreads) bitmap_pack_kernel(const uint4* __
       // words 2(p + j) and 2(p + j) + 1: 64 bytes, four 16-byte loads (the
       // byte map covers whole entry pairs)
       const uint4* src = bytes + 4 * (p + j);
-      const uint32_t m0 = pack_bytes(src[0], src[1]);
-      const uint32_t m1 = pack_bytes(src[2], src[3]);
+      const uint32_t rep = gen * 0x01010101u;
+      const uint32_t m0 = pack_bytes(src[0], src[1], rep);
+      const uint32_t m1 = pack_bytes(src[2], src[3], rep);
       wr2[p + j] = make_uint4(m0, 0u, m1, 0u);
       acc += __popc(m0) + __popc(m1);
     }
@@ -428,8 +441,10 @@ int64_t bitmap_scan_scratch_words(int64_t nw) {
 
 int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStream_t s,
                 const uint8_t* bytes, const SlotScan* scan, int32_t* started,
-                const uint8_t* touched) {
+                const uint8_t* touched, uint32_t gen) {
   TSC_REQUIRE(!touched || !bytes, "bitmap_scan: touched tiles are for bitmaps marked in place");
+  TSC_REQUIRE(!bytes || (gen >= 1 && gen <= 255), "bitmap_scan: mark value %u outside 1..255",
+              gen);
   const int64_t nsum = ceil_div(nw > 0 ? nw : 1, kBmTile);
   uint32_t* sums = scratch;
   uint32_t* pre = scratch + nsum;
@@ -440,7 +455,7 @@ int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStr
   const unsigned grid = static_cast<unsigned>(nsum + sc.blocks());
   if (bytes) {
     bitmap_pack_kernel<<<grid, kBmThreads, 0, s>>>(reinterpret_cast<const uint4*>(bytes), wr2, nw,
-                                                   sums, static_cast<int>(nsum), sc, started);
+                                                   sums, static_cast<int>(nsum), sc, started, gen);
     TSC_LAUNCH_CHECK("bitmap_pack");
   } else {
     bitmap_reduce_kernel<<<grid, kBmThreads, 0, s>>>(wr2, nw, sums, static_cast<int>(nsum), sc,
@@ -542,4 +557,4 @@ int wait_host_word(const int32_t* w, hipStream_t s, int* seen) {
 }  // namespace tsc
 
 extern "C" const char* tsc_last_error(void) { return tsc::last_error(); }
-extern "C" int tsc_abi_version(void) { return 11; }
+extern "C" int tsc_abi_version(void) { return 12; }

@@ -196,6 +196,11 @@ struct SlotScan {
   int32_t* totals;
   int K, nblk;
   int32_t* extra_total;
+  // with mark_words: *status = the flags the marks' status words hold for
+  // generation gen (mark_flags), written by the first slot's block
+  const uint32_t* mark_words = nullptr;
+  uint32_t gen = 0;
+  int32_t* status = nullptr;
   __host__ __device__ int blocks() const { return cnt ? K + (extra_total ? 1 : 0) : 0; }
 };
 
@@ -224,6 +229,26 @@ int64_t scan_scratch_words(int64_t n);
 // and writes the total to *total.
 int64_t bitmap_entries(int64_t nw);
 int64_t bitmap_scan_scratch_words(int64_t nw);
+
+// Occupancy marked as one byte per cell (bitmap builds on dense grids): the
+// bytes of whole bitmap entries (32 per entry), then kMarkWords status words.
+// A build stores its generation value gen (1..255) into the byte of each cell
+// it marks and, for a row it rejects, into that row's status word; it reads a
+// byte or a word as set only when it holds gen.  So marks left by earlier
+// builds need no zeroing until a value comes round again.  Status words:
+// kMarkBatch (a batch index outside [0, B)), kMarkGrid (a coordinate outside
+// the grid).
+constexpr int kMarkWords = 4;
+constexpr int kMarkBatch = 0, kMarkGrid = 1;
+inline int64_t marks_bytes(int64_t nw) { return bitmap_entries(nw) * 32 + 4 * kMarkWords; }
+inline uint32_t* mark_words(uint8_t* marks, int64_t nw) {
+  return reinterpret_cast<uint32_t*>(marks + bitmap_entries(nw) * 32);
+}
+// The status flags (TSC_FLAG_*) the status words hold for generation gen.
+__device__ __forceinline__ int32_t mark_flags(const uint32_t* words, uint32_t gen) {
+  return (words[kMarkBatch] == gen ? TSC_FLAG_BATCH_OUT_OF_RANGE : 0) |
+         (words[kMarkGrid] == gen ? TSC_FLAG_COORD_OUT_OF_GRID : 0);
+}
 // With scan, that slot scan (scan_slot_blocks) runs in the same launch as
 // the first pass.
 // started (may be null): a word of pinned host memory the first launch sets
@@ -232,9 +257,12 @@ int64_t bitmap_scan_scratch_words(int64_t nw);
 // entries are neither read (they may hold anything) nor written, and count 0.
 constexpr int kBitmapTileWords = 1024;
 inline int64_t bitmap_tiles(int64_t nw) { return ceil_div(nw > 0 ? nw : 1, kBitmapTileWords); }
+// bytes (may be null): byte marks (above) to pack, a cell occupied where its
+// byte equals gen.
 int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStream_t s,
                 const uint8_t* bytes = nullptr, const SlotScan* scan = nullptr,
-                int32_t* started = nullptr, const uint8_t* touched = nullptr);
+                int32_t* started = nullptr, const uint8_t* touched = nullptr,
+                uint32_t gen = 1);
 // Two words of pinned host memory that kernels store into, one pair per host
 // thread and device (allocated on first use there and kept until the process
 // ends).  A build that must report bad coordinates before it returns, but
@@ -280,13 +308,18 @@ __device__ __forceinline__ void signal_started(int32_t* host_word) {
 // probe's per-(slot, block) counts
 // go there ([K][ceil(n / 256)] int32) and counts[0..K) are left for
 // tsc_subm_counts; otherwise they are summed into counts.  *raster (may be
-// null) = 1 when the map's columns are in (b,z,y,x) order.
+// null) = 1 when the map's columns are in (b,z,y,x) order.  marks (may be
+// null): byte marks of marks_size bytes that the caller keeps between builds,
+// taken instead of the workspace's when the build marks through bytes, with
+// gen (1..255) as this build's value; ws then needs the size
+// tsc_subm_workspace_bytes gives with marks_outside.
 int subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size, const int32_t spatial[3],
                   const int32_t ksize[3], const int32_t dilation[3], void* ws, int64_t ws_bytes,
                   int64_t ws_limit, int32_t* cols_row, int32_t* nbr, int32_t* counts,
                   tsc_stream_t stream, const HostStatus* hs = nullptr,
                   int32_t* slot_blocks = nullptr, int32_t* raster = nullptr,
-                  int32_t mask_row = 0);
+                  int32_t mask_row = 0, uint8_t* marks = nullptr, int64_t marks_size = 0,
+                  int32_t gen = 0);
 int exclusive_scan_u32(const uint32_t* src, int kind, int64_t n, uint32_t* out, int32_t* total,
                        uint32_t* scratch, hipStream_t s);
 

@@ -93,15 +93,20 @@ struct Cands<0, 0, 0> {
 };
 
 // Marks every candidate output cell and counts each slot's pairs per block.
-// BYTES: one byte per output cell, set by plain stores (every writer stores
-// 1); the scan packs the bytes into the bitmap.  Otherwise the cells' bits are
-// set with device-scope atomics, which on this part are carried out beyond
-// the XCD's L2: several times the cost of the byte stores plus the packing
-// pass, so they are kept for sparse output grids only.
+// BYTES: byte marks (common.hpp): each candidate cell's byte, and for a row
+// whose batch index is out of range the status word kMarkBatch, receive the
+// build's generation value gen by plain stores (every writer stores the same
+// value); the scan packs the bytes equal to gen into the bitmap and writes
+// the status flags.  Otherwise the cells' bits are set with device-scope
+// atomics, which on this part are carried out beyond the XCD's L2: several
+// times the cost of the byte stores plus the packing pass, so they are kept
+// for sparse output grids only; bad rows then raise their flag in *status.
 template <int KZ, int KY, int KX, bool BYTES>
 __global__ void __launch_bounds__(kRows) strided_mark_kernel(const int4* __restrict__ coords,
                                                              int64_t n, int K, StridedGeom g,
                                                              uint2* wr, uint8_t* __restrict__ bytes,
+                                                             uint32_t* __restrict__ mark_words,
+                                                             uint32_t gen,
                                                              int32_t* __restrict__ blk_cnt,
                                                              int nblk, int32_t* status,
                                                              int32_t* __restrict__ paired) {
@@ -113,14 +118,20 @@ __global__ void __launch_bounds__(kRows) strided_mark_kernel(const int4* __restr
   const bool valid = i < n;
   const int4 c = valid ? coords[i] : make_int4(-1, 0, 0, 0);
   const bool ok = valid && c.x >= 0 && c.x < g.B;
-  if (valid && !ok) atomicOr(status, TSC_FLAG_BATCH_OUT_OF_RANGE);
+  if (valid && !ok) {
+    if constexpr (BYTES)
+      mark_words[kMarkBatch] = gen;
+    else
+      atomicOr(status, TSC_FLAG_BATCH_OUT_OF_RANGE);
+  }
   const Cands<KZ, KY, KX> cand(g, c, ok);
   constexpr int KC = KZ * KY * KX;
   if constexpr (BYTES) {
+    const uint8_t mark = static_cast<uint8_t>(gen);
 #pragma unroll
     for (int k = 0; k < (KC ? KC : K); ++k) {
       const int64_t cell = cand.cell(g, k);
-      if (cell >= 0) bytes[cell] = 1;
+      if (cell >= 0) bytes[cell] = mark;
     }
   } else if constexpr (KC > 0) {
     // One atomic per bitmap word a (kz, ky) row of candidates touches, not
@@ -396,20 +407,22 @@ Layout layout(int64_t n, int32_t batch, const int32_t* out) {
 
 struct Buffers {
   uint2* wr;       // output-cell bitmap entries (word, rank)
-  uint8_t* bytes;  // byte-per-cell marks (byte-marked builds)
   uint32_t* scan;  // bitmap scan scratch
   int32_t* blk_cnt;
   int32_t* blk_off;
+  uint8_t* bytes;  // byte marks (byte-marked builds whose marks the caller does not keep)
 };
 
-Buffers carve(void* ws, const Layout& L, int K, int64_t* used) {
+// The byte marks come last, so the other buffers sit at the same offsets
+// whether or not the workspace holds them (the fill never reads them).
+Buffers carve(void* ws, const Layout& L, int K, int64_t* used, bool marks_outside = false) {
   Carver c(ws);
   Buffers b;
   b.wr = c.take<uint2>(bitmap_entries(L.nwords));
-  b.bytes = L.bytes ? c.take<uint8_t>(bitmap_entries(L.nwords) * 32) : nullptr;
   b.scan = c.take<uint32_t>(bitmap_scan_scratch_words(L.nwords));
   b.blk_cnt = c.take<int32_t>(L.nblk * (K + 1));  // row K: rows with a pair, per block
   b.blk_off = c.take<int32_t>(L.nblk * (K + 1));
+  b.bytes = L.bytes && !marks_outside ? c.take<uint8_t>(marks_bytes(L.nwords)) : nullptr;
   if (used) *used = c.used;
   return b;
 }
@@ -427,13 +440,14 @@ int by_shape(const Box& ks, A... a) {
 template <int KZ, int KY, int KX>
 struct LaunchMark {
   static int run(const int4* c, int64_t n, int K, StridedGeom g, uint2* wr, uint8_t* bytes,
-                 int32_t* blk_cnt, int nblk, int32_t* status, int32_t* paired, hipStream_t s) {
+                 uint32_t* mwords, uint32_t gen, int32_t* blk_cnt, int nblk, int32_t* status,
+                 int32_t* paired, hipStream_t s) {
     if (bytes)
-      strided_mark_kernel<KZ, KY, KX, true><<<nblk, kRows, 0, s>>>(c, n, K, g, wr, bytes, blk_cnt,
-                                                                   nblk, status, paired);
+      strided_mark_kernel<KZ, KY, KX, true><<<nblk, kRows, 0, s>>>(
+          c, n, K, g, wr, bytes, mwords, gen, blk_cnt, nblk, status, paired);
     else
-      strided_mark_kernel<KZ, KY, KX, false><<<nblk, kRows, 0, s>>>(c, n, K, g, wr, nullptr,
-                                                                    blk_cnt, nblk, status, paired);
+      strided_mark_kernel<KZ, KY, KX, false><<<nblk, kRows, 0, s>>>(
+          c, n, K, g, wr, nullptr, nullptr, 0u, blk_cnt, nblk, status, paired);
     TSC_LAUNCH_CHECK("strided_mark");
     return 0;
   }
@@ -482,17 +496,26 @@ int check_geom(int64_t n, int32_t batch, const int32_t* spatial, const int32_t* 
 using namespace tsc;
 
 extern "C" int64_t tsc_strided_workspace_bytes(int64_t n, int32_t k_vol, int32_t batch_size,
-                                               const int32_t out_spatial[3]) {
+                                               const int32_t out_spatial[3],
+                                               int32_t marks_outside) {
   int64_t used = 0;
-  carve(nullptr, layout(n, batch_size, out_spatial), k_vol, &used);
+  carve(nullptr, layout(n, batch_size, out_spatial), k_vol, &used, marks_outside != 0);
   return used;
+}
+
+extern "C" int64_t tsc_strided_marks_bytes(int64_t n, int32_t k_vol, int32_t batch_size,
+                                           const int32_t out_spatial[3]) {
+  (void)k_vol;
+  const Layout L = layout(n, batch_size, out_spatial);
+  return L.bytes ? marks_bytes(L.nwords) : 0;
 }
 
 extern "C" int tsc_strided_count(const int32_t* coords, int64_t n, int32_t batch_size,
                                  const int32_t spatial[3], const int32_t ksize[3],
                                  const int32_t stride[3], const int32_t padding[3],
                                  const int32_t dilation[3], const int32_t out_spatial[3], void* ws,
-                                 int64_t ws_bytes, int32_t* counts, tsc_stream_t stream) {
+                                 int64_t ws_bytes, void* marks, int64_t marks_size, int32_t gen,
+                                 int32_t* counts, tsc_stream_t stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   StridedGeom g;
   int rc = check_geom(n, batch_size, spatial, ksize, stride, padding, dilation, out_spatial, &g);
@@ -500,30 +523,52 @@ extern "C" int tsc_strided_count(const int32_t* coords, int64_t n, int32_t batch
   const int K = ksize[0] * ksize[1] * ksize[2];
   TSC_REQUIRE(K <= 4096, "strided: kernel volume %d too large", K);
   const Layout L = layout(n, batch_size, out_spatial);
+  // the caller's byte marks, used when this build marks through bytes
+  const bool outside = marks != nullptr && L.bytes;
+  if (outside) {
+    TSC_REQUIRE(marks_size >= marks_bytes(L.nwords),
+                "strided: marks of %lld bytes, this grid needs %lld", (long long)marks_size,
+                (long long)marks_bytes(L.nwords));
+    TSC_REQUIRE(gen >= 1 && gen <= 255, "strided: mark value %d outside 1..255", gen);
+  }
   int64_t need = 0;
-  carve(nullptr, L, K, &need);
+  carve(nullptr, L, K, &need, outside);
   TSC_REQUIRE(ws && ws_bytes >= need, "strided: workspace too small (%lld < %lld)",
               (long long)ws_bytes, (long long)need);
   TSC_REQUIRE(counts != nullptr, "strided: counts is null");
-  Buffers b = carve(ws, L, K, nullptr);
-  // zero the counters and the marks (the byte map, which the scan turns into
-  // every bitmap entry, or the bitmap entries), in one launch
-  uint32_t* marks = reinterpret_cast<uint32_t*>(b.bytes ? static_cast<void*>(b.bytes)
-                                                        : static_cast<void*>(b.wr));
-  const int64_t mark_words = (b.bytes ? 8 : 2) * bitmap_entries(L.nwords);
-  if ((rc = fill2_u32(reinterpret_cast<uint32_t*>(counts), K + 3, 0u, marks, mark_words, 0u, s)))
-    return rc;
-  if (n == 0) return 0;
+  Buffers b = carve(ws, L, K, nullptr, outside);
+  uint8_t* const bytes = outside ? static_cast<uint8_t*>(marks) : b.bytes;
+  uint32_t* const mwords = bytes ? mark_words(bytes, L.nwords) : nullptr;
+  const uint32_t mark_gen = outside ? static_cast<uint32_t>(gen) : 1u;
+  // zero the counters and the marks (the byte marks, which the scan turns
+  // into every bitmap entry, or the bitmap entries), in one launch.  Marks
+  // the caller keeps are not zeroed (this build's generation value tells its
+  // marks apart), and every counter is then written by the scan: no launch.
+  if (!outside) {
+    uint32_t* zero = reinterpret_cast<uint32_t*>(bytes ? static_cast<void*>(bytes)
+                                                       : static_cast<void*>(b.wr));
+    const int64_t zero_words = bytes ? marks_bytes(L.nwords) / 4 : 2 * bitmap_entries(L.nwords);
+    if ((rc = fill2_u32(reinterpret_cast<uint32_t*>(counts), K + 3, 0u, zero, zero_words, 0u, s)))
+      return rc;
+  }
+  if (n == 0) return 0;  // (outside needs n > 0: the fill above zeroed the counts)
   TSC_REQUIRE(coords != nullptr, "strided: coords is null");
   if (K > 64 && (rc = fill_u32(reinterpret_cast<uint32_t*>(b.blk_cnt), L.nblk * K, 0u, s)))
     return rc;
   if ((rc = by_shape<LaunchMark>(g.ks, reinterpret_cast<const int4*>(coords), n, K, g, b.wr,
-                                 b.bytes, b.blk_cnt, (int)L.nblk, counts + K + 1,
+                                 bytes, mwords, mark_gen, b.blk_cnt, (int)L.nblk, counts + K + 1,
                                  b.blk_cnt + (int64_t)K * L.nblk, s)))
     return rc;
-  // the per-slot scan of the block counts rides in the bitmap scan's first launch
-  const SlotScan slots{b.blk_cnt, b.blk_off, counts, K, (int)L.nblk, counts + K + 2};
-  return bitmap_scan(b.wr, L.nwords, b.scan, counts + K, s, b.bytes, &slots);
+  // the per-slot scan of the block counts rides in the bitmap scan's first
+  // launch; with byte marks it also writes the status flags
+  SlotScan slots{b.blk_cnt, b.blk_off, counts, K, (int)L.nblk, counts + K + 2};
+  if (mwords) {
+    slots.mark_words = mwords;
+    slots.gen = mark_gen;
+    slots.status = counts + K + 1;
+  }
+  return bitmap_scan(b.wr, L.nwords, b.scan, counts + K, s, bytes, &slots, nullptr, nullptr,
+                     mark_gen);
 }
 
 extern "C" int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_size,
@@ -540,7 +585,7 @@ extern "C" int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_
   const int K = ksize[0] * ksize[1] * ksize[2];
   const Layout L = layout(n, batch_size, out_spatial);
   int64_t need = 0;
-  carve(nullptr, L, K, &need);
+  carve(nullptr, L, K, &need, true);  // the fill reads no marks
   TSC_REQUIRE(ws && ws_bytes >= need, "strided: workspace too small");
   TSC_REQUIRE(counts != nullptr, "strided: counts is null");
   TSC_REQUIRE(out_cap >= 0 && out_cap < (int64_t(1) << 31), "strided: out_cap=%lld invalid",
@@ -548,7 +593,7 @@ extern "C" int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_
   if (n == 0) return 0;
   TSC_REQUIRE(coords && pairs_in && pairs_out && (out_cap == 0 || (out_coords && nbr)),
               "strided: null pointer");
-  Buffers b = carve(ws, L, K, nullptr);
+  Buffers b = carve(ws, L, K, nullptr, true);
   // the output coordinates, and the map's -1 fill, in one launch; both take
   // n_out from counts[K] on the device, so this call needs no host read
   const int emit_blocks = static_cast<int>(ceil_div(L.nwords, 256));

@@ -293,30 +293,43 @@ __global__ void __launch_bounds__(256) subm_init_kernel(uint4* __restrict__ wr2,
 }
 
 // Marks each row's cell occupied; rows outside the grid only raise a status
-// flag.  Also marks every column unassigned (the rank pass fills them in).
-// BYTES: one byte per cell, set by plain stores (every writer stores 1, so
-// races are harmless); the scan packs the bytes into the bitmap.  Otherwise
-// the cell's bit is set by a device-scope atomicOr, which on this part is
-// carried out beyond the XCD's L2 (the L2s are not coherent with each other):
-// several times the cost of the byte store and the packing pass together,
-// taken only where the byte map would be large (sparse grids).
+// flag.  Also marks every column unassigned (the rank pass fills them in) and
+// clears the count of repeated rows the rank pass takes.
+// BYTES: byte marks (common.hpp): the cell's byte and a bad row's status word
+// receive the build's generation value gen by plain stores (every writer
+// stores the same value, so races are harmless); the scan packs the bytes
+// equal to gen into the bitmap, and the rank pass turns the status words
+// into the status flags.  Otherwise the cell's bit is set by a device-scope
+// atomicOr, which on this part is carried out beyond the XCD's L2 (the L2s
+// are not coherent with each other): several times the cost of the byte
+// store and the packing pass together, taken only where the byte map would
+// be large (sparse grids); bad rows raise their flag in *status.
 template <bool BYTES>
 __global__ void __launch_bounds__(256) subm_mark_kernel(const int4* __restrict__ coords, int64_t n,
                                                         SubmGeom g, uint2* wr,
                                                         uint8_t* __restrict__ bytes,
-                                                        int32_t* status, int32_t* host_flag,
-                                                        uint2* __restrict__ col) {
+                                                        uint32_t* __restrict__ mark_words,
+                                                        uint32_t gen, int32_t* status,
+                                                        int32_t* host_flag,
+                                                        uint2* __restrict__ col,
+                                                        int32_t* __restrict__ n_extra) {
   const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (r == 0) *n_extra = 0;
   if (r >= n) return;
   col[r] = make_uint2(0u, 0u);  // whole entries: no partly written sectors
   const int4 c = coords[r];
   if (!in_grid(g, c.x, c.y, c.z, c.w)) {
-    flag_bad_row(g, c.x, status, host_flag);
+    if constexpr (BYTES) {
+      mark_words[(c.x < 0 || c.x >= g.B) ? kMarkBatch : kMarkGrid] = gen;
+      if (host_flag) __hip_atomic_store(host_flag, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    } else {
+      flag_bad_row(g, c.x, status, host_flag);
+    }
     return;
   }
   const uint32_t cell = cell_key(g, c.x, c.y, c.z, c.w);
   if constexpr (BYTES)
-    bytes[cell] = 1;
+    bytes[cell] = static_cast<uint8_t>(gen);
   else
     atomicOr(&wr[cell >> 5].x, 1u << (cell & 31));
 }
@@ -374,11 +387,20 @@ __device__ __forceinline__ uint32_t cell_rank(uint2 e, uint32_t cell) {
 // returns names such a row exactly once: a row that finds a larger row
 // already there places itself; a row that finds a smaller one displaces
 // that row, which then never returns as the maximum, and places it.
+// With byte marks (mark_words), thread 0 also writes the status flags and
+// the column-order flag: counts[K] = mark_flags, counts[K + 1] = 1.
 __global__ void __launch_bounds__(256) subm_rank_kernel(const int4* __restrict__ coords, int64_t n,
                                                         SubmGeom g, const uint2* __restrict__ wr,
                                                         const int32_t* __restrict__ n_unique,
-                                                        uint2* col, int32_t* n_extra) {
+                                                        uint2* col, int32_t* n_extra,
+                                                        const uint32_t* __restrict__ mark_words,
+                                                        uint32_t gen, int32_t* __restrict__ counts,
+                                                        int K) {
   const int64_t r = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (r == 0 && mark_words) {
+    counts[K] = mark_flags(mark_words, gen);
+    counts[K + 1] = 1;
+  }
   if (r >= n) return;
   const int32_t nu = *n_unique;
   const int4 c = coords[r];
@@ -831,7 +853,10 @@ enum SubmMode { kSubmHash = 0, kSubmBitmap = 1, kSubmBytes = 2 };
 
 static int64_t bitmap_words(int64_t cells) { return ceil_div(cells, 32); }
 
-static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, int mode, int64_t* used) {
+// marks_outside: the byte marks are the caller's (kept between builds), not
+// part of the workspace.
+static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, int mode, int64_t* used,
+                           bool marks_outside = false) {
   Carver c(ws);
   const int64_t m = n > 0 ? n : 1;
   const int64_t nblk = ceil_div(m, kRows);
@@ -839,8 +864,11 @@ static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, int mode, 
   if (mode != kSubmHash) {
     const int64_t nw = bitmap_words(cells);
     w.wr = c.take<uint2>(bitmap_entries(nw));
-    if (mode == kSubmBytes) w.bytes = c.take<uint8_t>(bitmap_entries(nw) * 32);
-    else w.touched = c.take<uint8_t>(align_up(bitmap_tiles(nw), 16));
+    if (mode == kSubmBytes) {
+      if (!marks_outside) w.bytes = c.take<uint8_t>(marks_bytes(nw));
+    } else {
+      w.touched = c.take<uint8_t>(align_up(bitmap_tiles(nw), 16));
+    }
     w.scan = c.take<uint32_t>(bitmap_scan_scratch_words(nw));
     w.col = c.take<uint2>(m + 4);
     w.n_unique = c.take<int32_t>(1);
@@ -879,16 +907,30 @@ __global__ void iota_kernel(int32_t* p, int64_t n) {
 
 using namespace tsc;
 
-extern "C" int64_t tsc_subm_workspace_bytes(int64_t n, int32_t k_vol, int32_t batch_size,
-                                            const int32_t spatial[3]) {
+static int64_t subm_cells(int64_t n, int32_t k_vol, int32_t batch_size, const int32_t* spatial) {
   if (n < 0 || k_vol <= 0 || batch_size <= 0 || !spatial) return -1;
   if (spatial[0] <= 0 || spatial[1] <= 0 || spatial[2] <= 0 ||
       (int64_t)batch_size * spatial[0] * spatial[1] > (int64_t(1) << 62) / spatial[2])
     return -1;
-  const int64_t cells = (int64_t)batch_size * spatial[0] * spatial[1] * spatial[2];
+  return (int64_t)batch_size * spatial[0] * spatial[1] * spatial[2];
+}
+
+extern "C" int64_t tsc_subm_workspace_bytes(int64_t n, int32_t k_vol, int32_t batch_size,
+                                            const int32_t spatial[3], int32_t marks_outside) {
+  const int64_t cells = subm_cells(n, k_vol, batch_size, spatial);
+  if (cells < 0) return -1;
   int64_t used = 0;
-  subm_carve(nullptr, n, k_vol, cells, subm_pick_mode(n, k_vol, cells, INT64_MAX), &used);
+  subm_carve(nullptr, n, k_vol, cells, subm_pick_mode(n, k_vol, cells, INT64_MAX), &used,
+             marks_outside != 0);
   return used;
+}
+
+extern "C" int64_t tsc_subm_marks_bytes(int64_t n, int32_t k_vol, int32_t batch_size,
+                                        const int32_t spatial[3]) {
+  const int64_t cells = subm_cells(n, k_vol, batch_size, spatial);
+  if (cells < 0) return -1;
+  return subm_pick_mode(n, k_vol, cells, INT64_MAX) == kSubmBytes ? marks_bytes(bitmap_words(cells))
+                                                                   : 0;
 }
 
 // The build on a given workspace.  ws_limit > 0: the workspace is that many
@@ -899,7 +941,7 @@ int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
                       const int32_t dilation[3], void* ws, int64_t ws_bytes, int64_t ws_limit,
                       int32_t* cols_row, int32_t* nbr, int32_t* counts, tsc_stream_t stream,
                       const HostStatus* hs, int32_t* slot_blocks, int32_t* raster,
-                      int32_t mask_row) {
+                      int32_t mask_row, uint8_t* marks, int64_t marks_size, int32_t gen) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   TSC_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "subm: n=%lld out of range", (long long)n);
   TSC_REQUIRE(batch_size > 0, "subm: batch_size must be positive");
@@ -914,8 +956,16 @@ int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
   const int K = ks.z * ks.y * ks.x;
   TSC_REQUIRE(K <= 4096, "subm: kernel volume %d too large", K);
   const int mode = subm_pick_mode(n, K, cells, ws_limit > 0 ? ws_limit : INT64_MAX);
+  // the caller's byte marks, used when this build marks through bytes
+  const bool outside = marks != nullptr && mode == kSubmBytes;
+  if (outside) {
+    TSC_REQUIRE(marks_size >= marks_bytes(bitmap_words(cells)),
+                "subm: marks of %lld bytes, this grid needs %lld", (long long)marks_size,
+                (long long)marks_bytes(bitmap_words(cells)));
+    TSC_REQUIRE(gen >= 1 && gen <= 255, "subm: mark value %d outside 1..255", gen);
+  }
   int64_t need = 0;
-  subm_carve(nullptr, n, K, cells, mode, &need);
+  subm_carve(nullptr, n, K, cells, mode, &need, outside);
   if (ws_limit > 0)
     TSC_REQUIRE(need <= ws_limit,
                 "subm: this build needs %lld bytes of scratch, more than the %lld the "
@@ -935,7 +985,9 @@ int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
   int32_t* started = hs ? hs->dev + kHostStarted : nullptr;
 
   const int nblk = static_cast<int>(ceil_div(n, kRows));
-  const SubmWork w = subm_carve(ws, n, K, cells, mode, nullptr);
+  SubmWork w = subm_carve(ws, n, K, cells, mode, nullptr, outside);
+  if (outside) w.bytes = marks;
+  const uint32_t mark_gen = outside ? static_cast<uint32_t>(gen) : 1u;
   int32_t* const blk_cnt = slot_blocks ? slot_blocks : w.blk_cnt;
   TSC_REQUIRE(!mask_row || K <= 32, "subm: a slot-mask row needs k_vol <= 32 (got %d)", K);
   // the column slot masks, as row K of the map (the bitmap path's probes
@@ -945,34 +997,42 @@ int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
   if (w.wr) {
     const int64_t nw = bitmap_words(cells);
     SubmGeom g{batch_size, shape, ks, dil, 0u};
-    // zero the marks: the byte map (the scan then writes every bitmap entry),
-    // or for atomic marks the touched-tile flags; then the flags are set and
-    // only those tiles' entries zeroed
-    const int64_t units = w.bytes ? bitmap_entries(nw) * 2 : align_up(bitmap_tiles(nw), 16) / 16;
-    uint4* marks = reinterpret_cast<uint4*>(w.bytes ? static_cast<void*>(w.bytes)
-                                                    : static_cast<void*>(w.touched));
-    const int64_t init_blocks = std::min<int64_t>(ceil_div(units, 256), 4096);
-    subm_init_kernel<<<static_cast<unsigned>(init_blocks > 0 ? init_blocks : 1), 256, 0, s>>>(
-        marks, units, counts, K, w.n_extra);
-    TSC_LAUNCH_CHECK("subm_init");
+    uint32_t* const mwords = w.bytes ? mark_words(w.bytes, nw) : nullptr;
+    // zero the marks: the byte marks (the scan then writes every bitmap
+    // entry), or for atomic marks the touched-tile flags, whose tiles alone
+    // are then zeroed.  Marks kept by the caller are not zeroed: this build's
+    // generation value tells its marks apart, and the rank pass writes the
+    // counters the init would clear.
+    if (!outside) {
+      const int64_t units = w.bytes ? marks_bytes(nw) / 16 : align_up(bitmap_tiles(nw), 16) / 16;
+      uint4* zero = reinterpret_cast<uint4*>(w.bytes ? static_cast<void*>(w.bytes)
+                                                     : static_cast<void*>(w.touched));
+      const int64_t init_blocks = std::min<int64_t>(ceil_div(units, 256), 4096);
+      subm_init_kernel<<<static_cast<unsigned>(init_blocks > 0 ? init_blocks : 1), 256, 0, s>>>(
+          zero, units, counts, K, w.n_extra);
+      TSC_LAUNCH_CHECK("subm_init");
+    }
     if (w.bytes) {
-      subm_mark_kernel<true><<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.bytes, counts + K,
-                                                              host_flag, w.col);
+      subm_mark_kernel<true><<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.bytes, mwords,
+                                                              mark_gen, counts + K, host_flag,
+                                                              w.col, w.n_extra);
     } else {
       subm_touch_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.touched);
       TSC_LAUNCH_CHECK("subm_touch");
       subm_zero_touched_kernel<<<static_cast<unsigned>(bitmap_tiles(nw)), 256, 0, s>>>(
           reinterpret_cast<uint4*>(w.wr), bitmap_entries(nw) / 2, w.touched);
       TSC_LAUNCH_CHECK("subm_zero_touched");
-      subm_mark_kernel<false><<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, nullptr,
-                                                               counts + K, host_flag, w.col);
+      subm_mark_kernel<false><<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, nullptr, nullptr,
+                                                               0u, counts + K, host_flag, w.col,
+                                                               w.n_extra);
     }
     TSC_LAUNCH_CHECK("subm_mark");
     if (raster) *raster = 1;
-    if ((rc = bitmap_scan(w.wr, nw, w.scan, w.n_unique, s, w.bytes, nullptr, started, w.touched)))
+    if ((rc = bitmap_scan(w.wr, nw, w.scan, w.n_unique, s, w.bytes, nullptr, started, w.touched,
+                          mark_gen)))
       return rc;
     subm_rank_kernel<<<ceil_div(n, 256), 256, 0, s>>>(c4, n, g, w.wr, w.n_unique, w.col,
-                                                      w.n_extra);
+                                                      w.n_extra, mwords, mark_gen, counts, K);
     TSC_LAUNCH_CHECK("subm_rank");
     // slots from 64 on are added into the per-block table, which starts at 0
     if (K > 64 &&
@@ -1042,6 +1102,7 @@ extern "C" int64_t tsc_subm_slot_blocks_len(int64_t n, int32_t k_vol) {
 extern "C" int tsc_subm_pairs_checked(const int32_t* coords, int64_t n, int32_t batch_size,
                                       const int32_t spatial[3], const int32_t ksize[3],
                                       const int32_t dilation[3], void* ws, int64_t ws_bytes,
+                                      void* marks, int64_t marks_size, int32_t gen,
                                       int32_t* cols_row, int32_t* nbr, int32_t* counts,
                                       int32_t* slot_blocks, int32_t mask_row, int32_t result[2],
                                       tsc_stream_t stream) {
@@ -1054,7 +1115,8 @@ extern "C" int tsc_subm_pairs_checked(const int32_t* coords, int64_t n, int32_t 
   hs.host[kHostStarted] = 0;
   int32_t raster = 0;
   if (int rc = subm_pairs_ws(coords, n, batch_size, spatial, ksize, dilation, ws, ws_bytes, 0,
-                             cols_row, nbr, counts, stream, &hs, slot_blocks, &raster, mask_row))
+                             cols_row, nbr, counts, stream, &hs, slot_blocks, &raster, mask_row,
+                             static_cast<uint8_t*>(marks), marks_size, gen))
     return rc;
   result[1] = raster;
   if (n == 0) return 0;

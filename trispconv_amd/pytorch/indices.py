@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import ctypes
 import functools
+import threading
 from dataclasses import dataclass
 from typing import Callable, Dict, List, Optional, Sequence, Tuple
 
@@ -532,6 +533,55 @@ def _raise_status(status: int, what: str) -> None:
 _STRIDED_BITMAPS = WeakIdKeyDictionary()
 
 
+class _Marks:
+    """Byte marks (a byte per grid cell, then a few status words) that the
+    bitmap pair builds on one stream share.  Each build marks with a value of
+    its own, 1..255, and reads only that value, so no build zeroes them
+    first; they are zeroed when the values run out, and replaced by a larger,
+    zeroed buffer when a build needs more."""
+
+    __slots__ = ("buf", "gen", "lock")
+
+    def __init__(self):
+        self.buf: Optional[torch.Tensor] = None
+        self.gen = 0
+        self.lock = threading.Lock()
+
+    def take(self, nbytes: int, device) -> Tuple[int, int, int]:
+        """(address, size, value) for the next build on this stream."""
+        with self.lock:  # host threads sharing a stream get distinct values
+            if self.buf is None or self.buf.numel() < nbytes:
+                self.buf = None
+                self.buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+                self.gen = 0
+            if self.gen == 255:
+                self.buf.zero_()
+                self.gen = 0
+            self.gen += 1
+            return self.buf.data_ptr(), self.buf.numel(), self.gen
+
+
+# (device index, stream) -> the marks of the builds on that stream.  Builds on
+# one stream run in order and can share marks; builds on two streams may
+# overlap and get marks of their own.  Each is as large as the largest grid
+# built on its stream, and kept until the process ends.
+_MARKS: Dict[Tuple[int, int], _Marks] = {}
+_MARKS_LOCK = threading.Lock()
+
+
+def _marks_for(device, stream: int, nbytes: int) -> Tuple[Optional[int], int, int]:
+    """Marks for a build of nbytes of byte marks on ``stream`` (None when the
+    build marks no bytes)."""
+    if nbytes <= 0:
+        return None, 0, 0
+    key = (device.index, stream)
+    m = _MARKS.get(key)
+    if m is None:
+        with _MARKS_LOCK:
+            m = _MARKS.setdefault(key, _Marks())
+    return m.take(nbytes, device)
+
+
 # A submanifold build on a bitmap packs cell ids in 32 bits: grids of this
 # many cells or more take the 64-bit-key hash build instead.
 _NARROW_CELLS = (1 << 32) - 1
@@ -624,12 +674,14 @@ def generate_subm_indice_pairs(indices: torch.Tensor, spatial_shape, batch_size:
     tables = torch.empty(sz.words, dtype=torch.int32, device=dev)
     base = tables.data_ptr()
     stream = L.stream_of(coords)
+    marks, marks_size, gen = _marks_for(dev, stream, sz.marks_bytes)
     result = (ctypes.c_int32 * 2)()
     # Returns once the coordinates are checked (a row outside the grid raises
     # here, as in the reference); the map is still being built on the stream,
     # and the per-slot counts are summed and read only when pair_num is.
     L.check(lib.tsc_subm_pairs_checked(coords.data_ptr(), n, int(batch_size), sz.shape, sz.ks,
-                                       sz.dil, ws.data_ptr(), sz.ws_bytes, base,
+                                       sz.dil, ws.data_ptr(), sz.ws_bytes, marks, marks_size,
+                                       gen, base,
                                        base + 4 * sz.o_map, base + 4 * sz.o_counts,
                                        base + 4 * sz.o_blocks, int(sz.masks), result, stream),
             "generate_subm_indice_pairs")
@@ -656,7 +708,10 @@ class _SubmSizes:
     def __init__(self, n, K, batch_size, shape, ks, dil):
         lib = L.lib()
         self.shape, self.ks, self.dil = L.i3(shape), L.i3(ks), L.i3(dil)
-        self.ws_bytes = int(lib.tsc_subm_workspace_bytes(n, K, batch_size, self.shape))
+        # byte marks, when the build uses them, are kept per stream (_Marks)
+        self.marks_bytes = int(lib.tsc_subm_marks_bytes(n, K, batch_size, self.shape))
+        self.ws_bytes = int(lib.tsc_subm_workspace_bytes(n, K, batch_size, self.shape,
+                                                         int(self.marks_bytes > 0)))
         n_al = _align64(max(n, 1))
         self.masks = K <= 32  # each column's slot mask after the map, as its row K
         self.o_map = n_al
@@ -689,8 +744,9 @@ def generate_strided_indice_pairs(indices: torch.Tensor, spatial_shape, batch_si
     ws = L.workspace(sz.ws_bytes, dev)
     counts = torch.empty(K + 3, dtype=torch.int32, device=dev)
     stream = L.stream_of(coords)
+    marks, marks_size, gen = _marks_for(dev, stream, sz.marks_bytes)
     L.check(lib.tsc_strided_count(coords.data_ptr(), n, int(batch_size), *sz.geo, ws.data_ptr(),
-                                  sz.ws_bytes, counts.data_ptr(), stream),
+                                  sz.ws_bytes, marks, marks_size, gen, counts.data_ptr(), stream),
             "generate_strided_indice_pairs")
     # the counts go to the host behind the count pass; the fill is queued
     # before they arrive, with room for the rows this geometry's largest
@@ -754,8 +810,10 @@ class _StridedSizes:
     def __init__(self, n, batch_size, shape, ks, st, pd, dil, out_shape):
         K = ks[0] * ks[1] * ks[2]
         self.geo = (L.i3(shape), L.i3(ks), L.i3(st), L.i3(pd), L.i3(dil), L.i3(out_shape))
-        self.ws_bytes = max(int(L.lib().tsc_strided_workspace_bytes(n, K, batch_size,
-                                                                      self.geo[5])), 1)
+        # byte marks, when the build uses them, are kept per stream (_Marks)
+        self.marks_bytes = int(L.lib().tsc_strided_marks_bytes(n, K, batch_size, self.geo[5]))
+        self.ws_bytes = max(int(L.lib().tsc_strided_workspace_bytes(
+            n, K, batch_size, self.geo[5], int(self.marks_bytes > 0))), 1)
         self.cells = batch_size * out_shape[0] * out_shape[1] * out_shape[2]
         self.out_words = (self.cells + 31) // 32
 
