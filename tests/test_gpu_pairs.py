@@ -224,12 +224,14 @@ def _stream_marks():
     return IM._MARKS.get((probe.device.index, L.stream_of(probe)))
 
 
-def test_byte_marks_kept_between_builds_never_leak():
+def test_byte_marks_kept_between_builds_never_leak(monkeypatch):
     """SubM and strided builds on one stream share byte marks that no build
     zeroes.  Builds on shrinking coordinate sets of one grid (every cell of a
     later set was marked by an earlier build), a build that raises on a bad
     batch index followed by good ones, the values running out (zeroed, then
     1 again) and a larger grid (new marks) all give the oracle's pairs."""
+    from trispconv_amd.pytorch import indices as IM
+    monkeypatch.setattr(IM, "_MARKS", {})  # marks sized by this test's grids alone
     shape, B = (20, 22, 24), 2
     big = _tiny(51, shape, B, 1800)
     small = big[: len(big) // 3]
