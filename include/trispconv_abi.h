@@ -72,8 +72,10 @@ TSC_API int tsc_abi_version(void);
  * allocated) and pass them with a generation value gen in 1..255, a new one
  * per build: a build writes gen and reads only gen, so nothing zeroes the
  * marks before a build (one launch and one pass over the grid fewer).  The
- * caller zeroes them again before reusing a value, and two builds that may
- * overlap (other streams) need marks of their own.  The workspace is then
+ * caller zeroes them again before reusing a value.  Marks serve one
+ * sequence of builds: builds on other streams, and builds that other host
+ * threads launch on the same stream (their launches may interleave with
+ * these), need marks of their own.  The workspace is then
  * the size given with marks_outside = 1.  tsc_*_marks_bytes returns 0 when
  * a build of that shape does not mark through bytes (it then ignores marks).
  * ------------------------------------------------------------------------ */

@@ -221,7 +221,7 @@ def _stream_marks():
     from trispconv_amd import _lib as L
     from trispconv_amd.pytorch import indices as IM
     probe = torch.zeros(1, device=DEV)
-    return IM._MARKS.get((probe.device.index, L.stream_of(probe)))
+    return IM._MARKS.by_stream.get((probe.device.index, L.stream_of(probe)))
 
 
 def test_byte_marks_kept_between_builds_never_leak(monkeypatch):
@@ -231,7 +231,7 @@ def test_byte_marks_kept_between_builds_never_leak(monkeypatch):
     batch index followed by good ones, the values running out (zeroed, then
     1 again) and a larger grid (new marks) all give the oracle's pairs."""
     from trispconv_amd.pytorch import indices as IM
-    monkeypatch.setattr(IM, "_MARKS", {})  # marks sized by this test's grids alone
+    monkeypatch.setattr(IM, "_MARKS", IM._ThreadMarks())  # marks sized by this test's grids alone
     shape, B = (20, 22, 24), 2
     big = _tiny(51, shape, B, 1800)
     small = big[: len(big) // 3]
@@ -257,6 +257,35 @@ def test_byte_marks_kept_between_builds_never_leak(monkeypatch):
     wide = (40, 44, 48)
     _subm(_tiny(53, wide, B, 12000), wide, B, 3, 1, "kept marks, larger grid")
     assert _stream_marks().buf.numel() > size
+
+
+def test_byte_marks_of_two_host_threads_on_one_stream():
+    """Two host threads building on the same stream at once: their launches
+    interleave on the stream, so each thread keeps marks of its own; every
+    build gives the oracle's pairs."""
+    import threading
+    shape, B = (20, 22, 24), 2
+    sets = [_tiny(71 + t, shape, B, 900 + 300 * t) for t in range(2)]
+    exp = [OP.subm_pairs(idx, shape, B, 3, 1) for idx in sets]
+    errors = []
+
+    def work(t):
+        try:
+            x = torch.from_numpy(sets[t]).to(DEV)
+            for i in range(12):
+                got = generate_subm_indice_pairs(x, shape, B, 3, 1)
+                _check_lists(got, exp[t], f"thread {t} build {i}")
+        except BaseException as e:  # reported by the main thread
+            errors.append(e)
+
+    say("two host threads building on one stream")
+    threads = [threading.Thread(target=work, args=(t,)) for t in range(2)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=120)
+    assert not any(th.is_alive() for th in threads)
+    assert not errors, errors[0]
 
 
 def test_byte_marks_through_the_c_abi():

@@ -535,38 +535,44 @@ _STRIDED_BITMAPS = WeakIdKeyDictionary()
 
 class _Marks:
     """Byte marks (a byte per grid cell, then a few status words) that the
-    bitmap pair builds on one stream share.  Each build marks with a value of
-    its own, 1..255, and reads only that value, so no build zeroes them
-    first; they are zeroed when the values run out, and replaced by a larger,
-    zeroed buffer when a build needs more."""
+    bitmap pair builds one host thread launches on one stream share.  Each
+    build marks with a value of its own, 1..255, and reads only that value,
+    so no build zeroes them first; they are zeroed when the values run out,
+    and replaced by a larger, zeroed buffer when a build needs more."""
 
-    __slots__ = ("buf", "gen", "lock")
+    __slots__ = ("buf", "gen")
 
     def __init__(self):
         self.buf: Optional[torch.Tensor] = None
         self.gen = 0
-        self.lock = threading.Lock()
 
     def take(self, nbytes: int, device) -> Tuple[int, int, int]:
         """(address, size, value) for the next build on this stream."""
-        with self.lock:  # host threads sharing a stream get distinct values
-            if self.buf is None or self.buf.numel() < nbytes:
-                self.buf = None
-                self.buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-                self.gen = 0
-            if self.gen == 255:
-                self.buf.zero_()
-                self.gen = 0
-            self.gen += 1
-            return self.buf.data_ptr(), self.buf.numel(), self.gen
+        if self.buf is None or self.buf.numel() < nbytes:
+            self.buf = None
+            self.buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+            self.gen = 0
+        if self.gen == 255:
+            self.buf.zero_()
+            self.gen = 0
+        self.gen += 1
+        return self.buf.data_ptr(), self.buf.numel(), self.gen
 
 
-# (device index, stream) -> the marks of the builds on that stream.  Builds on
-# one stream run in order and can share marks; builds on two streams may
-# overlap and get marks of their own.  Each is as large as the largest grid
-# built on its stream, and kept until the process ends.
-_MARKS: Dict[Tuple[int, int], _Marks] = {}
-_MARKS_LOCK = threading.Lock()
+class _ThreadMarks(threading.local):
+    """Per host thread: (device index, stream) -> the marks of the builds
+    this thread launches on that stream.  One thread's builds on one stream
+    run one after another and can share marks.  Builds on two streams may
+    overlap, and two threads' launches on one stream may interleave (one
+    build's mark between another's mark and scan), so each pair gets marks
+    of its own.  Each is as large as the largest grid built there, and is
+    freed with its thread."""
+
+    def __init__(self):
+        self.by_stream: Dict[Tuple[int, int], _Marks] = {}
+
+
+_MARKS = _ThreadMarks()
 
 
 def _marks_for(device, stream: int, nbytes: int) -> Tuple[Optional[int], int, int]:
@@ -575,10 +581,9 @@ def _marks_for(device, stream: int, nbytes: int) -> Tuple[Optional[int], int, in
     if nbytes <= 0:
         return None, 0, 0
     key = (device.index, stream)
-    m = _MARKS.get(key)
+    m = _MARKS.by_stream.get(key)
     if m is None:
-        with _MARKS_LOCK:
-            m = _MARKS.setdefault(key, _Marks())
+        m = _MARKS.by_stream[key] = _Marks()
     return m.take(nbytes, device)
 
 
