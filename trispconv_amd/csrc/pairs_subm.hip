@@ -884,13 +884,19 @@ static SubmWork subm_carve(void* ws, int64_t n, int K, int64_t cells, int mode, 
   return w;
 }
 
+// Grids of at most this many cells mark through bytes however few rows they
+// hold: packing a byte map of up to 4 MB costs less than the three launches
+// of the atomic path's touched tiles (flag clear, touch, tile zeroing).
+constexpr int64_t kSmallByteGrid = int64_t(1) << 22;
+
 // Bitmap or hash: the bitmap while the grid is dense enough (and its cell ids
 // fit 32 bits), marked through a byte map while that is at most 64 bytes per
-// row; with a workspace limit, the first of these that fits.
+// row or the grid is small; with a workspace limit, the first of these that
+// fits.
 static int subm_pick_mode(int64_t n, int K, int64_t cells, int64_t ws_limit) {
   if (!(cells < kNarrowCells && subm_use_bitmap(n, cells))) return kSubmHash;
   int64_t used = 0;
-  if (cells <= 64 * n) {
+  if (cells <= 64 * n || cells <= kSmallByteGrid) {
     subm_carve(nullptr, n, K, cells, kSubmBytes, &used);
     if (used <= ws_limit) return kSubmBytes;
   }
