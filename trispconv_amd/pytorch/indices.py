@@ -604,6 +604,13 @@ def _counts_to_host(counts: torch.Tensor, K: int, stream: int,
     return torch.tensor(list(host), dtype=torch.int32)
 
 
+# The ctypes shape arrays are only read during a call, so one set serves
+# every build of a shape.
+@functools.lru_cache(maxsize=64)
+def _shape_args(shape, ks, dil):
+    return L.i3(shape), L.i3(ks), L.i3(dil)
+
+
 def _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil):
     """The submanifold build on a strided build's output set, through its
     bitmap, or None when ``indices`` is not such an output (unchanged)."""
@@ -618,16 +625,21 @@ def _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil):
     K = ks[0] * ks[1] * ks[2]
     n = coords.shape[0]
     dev = coords.device
-    cols_row = torch.empty(max(n, 1), dtype=torch.int32, device=dev)
     masks = K <= 32  # each column's slot mask as row K, for the convolution's set-up
-    map_all = torch.empty((K + int(masks)) * n, dtype=torch.int32, device=dev)
-    map_cols = map_all[:K * n].view(K, n)
-    counts = torch.empty(K + 2, dtype=torch.int32, device=dev)
+    # cols_row, the map (with its mask row) and the counts in one allocation
+    # at 256-byte aligned offsets; raw addresses for the launch, views after
+    o_map = _align64(max(n, 1))
+    o_counts = o_map + _align64((K + int(masks)) * n)
+    tables = torch.empty(o_counts + K + 2, dtype=torch.int32, device=dev)
+    base = tables.data_ptr()
     stream = L.stream_of(coords)
     L.check(L.lib().tsc_subm_pairs_from_bitmap(
-        coords.data_ptr(), n, int(batch_size), L.i3(shape), L.i3(ks), L.i3(dil), ws.data_ptr(),
-        nwords, cols_row.data_ptr(), map_cols.data_ptr(), counts.data_ptr(), int(masks), stream),
+        coords.data_ptr(), n, int(batch_size), *_shape_args(shape, ks, dil), ws.data_ptr(),
+        nwords, base, base + 4 * o_map, base + 4 * o_counts, int(masks), stream),
         "generate_subm_indice_pairs")
+    cols_row = tables[:n]
+    map_cols = tables[o_map:o_map + K * n].view(K, n)
+    counts = tables[o_counts:o_counts + K + 2]
     # No read-back here: the rows are the registered output set (same tensor,
     # same version), so there is nothing to validate before the convolution.
     # The probe checks on the device that every row is the bitmap's cell of
@@ -643,7 +655,7 @@ def _subm_on_strided_bitmap(indices, coords, shape, batch_size, ks, dil):
         out_indices=indices, input_indices=indices, input_spatial_shape=shape,
         output_spatial_shape=shape, kernel_size=ks, stride=(1, 1, 1), padding=(0, 0, 0),
         dilation=dil, subm=True, pin=None, pout=None, cnt_dev=None, pair_num=None,
-        nbr=None, batch_size=int(batch_size), map_cols=map_cols, cols_row=cols_row[:n],
+        nbr=None, batch_size=int(batch_size), map_cols=map_cols, cols_row=cols_row,
         raster=True)
     d._map_masks = masks
     d._counts_pending = (counts, K, lambda: _counts_to_host(counts, K, stream))
