@@ -525,15 +525,18 @@ def test_full_size_workloads(name):
         torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("row_bytes", [256, 2048, 1 << 17])
-def test_plan_tiles_mask_sorted_heaviest_first(row_bytes, monkeypatch):
+@pytest.mark.parametrize("row_bytes,per_sample", [(256, 6000), (2048, 6000), (1 << 17, 6000),
+                                                  (1 << 17, 12000)])
+def test_plan_tiles_mask_sorted_heaviest_first(row_bytes, per_sample, monkeypatch):
     """The execution order is a permutation of the output rows.  Cut into
     256-row tiles (the convolution's workgroup tiles), each full tile is sorted
     by slot mask, and inside each region the full tiles come in non-increasing
-    number of slots used by their rows; the partial tile, if any, is last and
-    mask-sorted too.  row_bytes = 2^17 makes regions of 2048 rows."""
+    number of slots used by their rows, tiles of equal count in their mask
+    order (a stable sort); the partial tile, if any, is last and mask-sorted
+    too.  row_bytes = 2^17 makes regions of 2048 rows: six of them sort the
+    tiles in one workgroup (keys of 9 bits), twelve in radix passes."""
     monkeypatch.setattr(I, "_PLAN_MIN_BYTES", 0)  # an order even for this small layer
-    idx = _tiny(15, (40, 40, 40), 2, 6000)
+    idx = _tiny(15, (40, 40, 40), 2, per_sample)
     x = torch.from_numpy(idx).to(DEV)
     data = generate_subm_indice_pairs(x, (40, 40, 40), 2, 3)
     n = len(idx)
@@ -553,6 +556,9 @@ def test_plan_tiles_mask_sorted_heaviest_first(row_bytes, monkeypatch):
     for r0 in range(0, n_full, per_region):
         u = used[r0:r0 + per_region]
         assert (np.diff(u) <= 0).all(), f"tiles of the region at row {r0 * 256} not heaviest first"
+        for t in range(r0 + 1, min(r0 + per_region, n_full)):
+            if used[t] == used[t - 1]:
+                assert mask[t * 256] >= mask[t * 256 - 1], f"tiles {t - 1}, {t}: not stable"
     # the same tiles as a plain mask sort inside regions: each region's multiset of rows holds
     for r0 in range(0, n_full * 256, region):
         hi = min(r0 + region, n_full * 256)

@@ -390,6 +390,60 @@ __global__ void __launch_bounds__(kThreads) radix_scatter_kernel(
   }
 }
 
+// Short lists with keys of at most kDigitBits bits (a layer's full tiles, up
+// to kSmallSortMax of them) are sorted by one workgroup in one launch instead
+// of a radix pass's three: the digit counts in LDS and their scan, then
+// rounds of kRadix items in index order, each item placed as in the radix
+// scatter (lanes ranked by ballots, waves in order), so the sort is stable.
+constexpr int64_t kSmallSortMax = int64_t(1) << 16;
+
+__global__ void __launch_bounds__(kRadix) small_sort_kernel(const uint32_t* __restrict__ keys,
+                                                            const uint32_t* __restrict__ vals,
+                                                            int n, uint32_t* __restrict__ vals_out) {
+  __shared__ uint32_t s_run[kRadix];                  // per digit: count, then next place
+  __shared__ uint32_t s_wc[kRadix / kWave][kRadix];   // this round, per wave, per digit
+  __shared__ uint32_t s_wave[33];
+  const int t = threadIdx.x;  // also the digit whose counts this thread keeps
+  const int w = t / kWave;
+  s_run[t] = 0;
+  __syncthreads();
+  for (int i = t; i < n; i += kRadix) atomicAdd(&s_run[keys[i] & (kRadix - 1u)], 1u);
+  __syncthreads();
+  const uint32_t count = s_run[t];
+  uint32_t tot;
+  const uint32_t first = block_exclusive(count, s_wave, &tot);
+  s_run[t] = first;
+  for (int base = 0; base < n; base += kRadix) {
+#pragma unroll
+    for (int ww = 0; ww < kRadix / kWave; ++ww) s_wc[ww][t] = 0;
+    __syncthreads();
+    const int i = base + t;
+    const bool valid = i < n;
+    const uint32_t dg = valid ? keys[i] & (kRadix - 1u) : 0u;
+    const uint32_t val = valid ? vals[i] : 0u;
+    // lanes of this wave holding the same digit
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < kDigitBits; ++b) {
+      const uint64_t ones = __ballot((dg >> b) & 1u);
+      peers &= ((dg >> b) & 1u) ? ones : ~ones;
+    }
+    const int rank = rank_in_wave(peers);
+    if (valid && rank == 0) s_wc[w][dg] = __popcll(peers);
+    __syncthreads();
+    if (valid) {
+      uint32_t pos = s_run[dg] + rank;
+      for (int ww = 0; ww < w; ++ww) pos += s_wc[ww][dg];
+      if (pos < static_cast<uint32_t>(n)) vals_out[pos] = val;  // always, with consistent counts
+    }
+    __syncthreads();
+    uint32_t add = 0;
+#pragma unroll
+    for (int ww = 0; ww < kRadix / kWave; ++ww) add += s_wc[ww][t];
+    s_run[t] += add;
+  }
+}
+
 struct Buffers {
   uint32_t *keys_a, *keys_b, *vals_a, *vals_b, *rows, *mask_pos, *hist, *hist_off, *digit_tot;
   int32_t* nbr_t;  // the map's row-major copy (K <= 32), else null
@@ -547,13 +601,19 @@ extern "C" int tsc_conv_plan(const int32_t* nbr, const int32_t* cols_row, int32_
     TSC_LAUNCH_CHECK("plan_tile_key");
     const int key_bits = bits_for(static_cast<uint64_t>((n_tiles - 1) / tiles_per_region)) + 6;
     uint32_t *tki = b.keys_a, *tko = b.keys_a + n_tiles, *tvi = vo, *tvo = vo + n_tiles;
-    for (int p = 0; p < (key_bits + kDigitBits - 1) / kDigitBits; ++p) {
-      const Digits d{kFromKey, kDigitBits * p, tki, nullptr, 1u};
-      if ((rc = radix_pass(b, tki, tvi, tko, tvo, n_tiles, d, s))) return rc;
-      std::swap(tki, tko);
-      std::swap(tvi, tvo);
+    if (key_bits <= kDigitBits && n_tiles <= kSmallSortMax) {
+      small_sort_kernel<<<1, kRadix, 0, s>>>(tki, tvi, static_cast<int>(n_tiles), tvo);
+      TSC_LAUNCH_CHECK("plan_small_sort");
+      tile_perm = tvo;
+    } else {
+      for (int p = 0; p < (key_bits + kDigitBits - 1) / kDigitBits; ++p) {
+        const Digits d{kFromKey, kDigitBits * p, tki, nullptr, 1u};
+        if ((rc = radix_pass(b, tki, tvi, tko, tvo, n_tiles, d, s))) return rc;
+        std::swap(tki, tko);
+        std::swap(tvi, tvo);
+      }
+      tile_perm = tvi;
     }
-    tile_perm = tvi;
   }
   gather_rows_kernel<<<ceil_div(n_out, 256), 256, 0, s>>>(
       vi, raster ? nullptr : b.rows, cols_row, n_out, tile_perm, n_tiles, b.mask_pos, b.keys_b, order,
