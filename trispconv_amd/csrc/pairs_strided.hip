@@ -14,7 +14,9 @@
 // gives each cell's rank in sorted order directly, so output coordinates come
 // out sorted by (b,z,y,x) and ranks need no sort and no search.  Pair lists are
 // compacted per slot in ascending input order with the same block-offset +
-// wave-ballot scheme as the submanifold builder.
+// wave-ballot scheme as the submanifold builder.  Two calls, count and fill;
+// the fill reads the output count from the device, so it is queued right
+// behind the count and the counts reach the host while it runs.
 #include "common.hpp"
 
 #include <algorithm>

@@ -16,9 +16,11 @@
 //     column.  Columns are the occupied cells in rank order (then any earlier
 //     rows of repeated coordinates), so a wave's 64 lookups touch neighbouring
 //     cells and share cache lines, its map writes are contiguous, and a column
-//     reads its own cell from its entry (no gather of its row's coordinates).  Where the grid has at most 64 cells per row the bits are
-//     first marked as one byte per cell with plain stores and packed by the
-//     scan; sparser grids set them with atomics;
+//     reads its own cell from its entry (no gather of its row's coordinates).  Where the grid has at most 64 cells per row, or at most
+//     2^22 cells, the bits are first marked as one byte per cell with plain
+//     stores (the build's generation value, so marks a caller keeps between
+//     builds need no zeroing) and packed by the scan; sparser grids set them
+//     with atomics;
 //   * open-addressing hash of 2N..4N 64-bit slots otherwise, probed in row
 //     order (columns are rows).
 // The reference's pair lists are derived from the map only when asked for
