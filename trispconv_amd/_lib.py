@@ -132,7 +132,7 @@ _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 def stream_of(t: torch.Tensor) -> int:
     """The caller's current stream on ``t``'s device, as a hipStream_t."""
     if _raw_stream is not None:
-        return _raw_stream(t.device.index)
+        return _raw_stream(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 

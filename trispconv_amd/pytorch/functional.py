@@ -71,12 +71,16 @@ def _bn_operands(ep: Epilogue, c_out: int, device) -> list:
             raise ValueError("sparse_conv_forward: batch-norm weight/bias without statistics")
         return [None] * 4
     ts = (ep.mean, ep.var, ep.weight, ep.bias)
+    where = device.index if device.index is not None else torch.cuda.current_device()
+    dt = None
     for t in ts:
-        if t is not None and (t.device != device or t.numel() != c_out):
+        if t is None:
+            continue
+        if t.get_device() != where or t.numel() != c_out:
             raise ValueError("sparse_conv_forward: batch-norm tensors must have "
                              f"{c_out} entries on {device}")
-    dts = {t.dtype for t in ts if t is not None}
-    dt = dts.pop() if len(dts) == 1 else torch.float32
+        # one dtype shared by all of them, else fp32
+        dt = t.dtype if dt is None or dt == t.dtype else torch.float32
     if dt not in _PARAM_DTYPES:
         dt = torch.float32
     # only their addresses are passed: tensors already in that form go as they are
@@ -113,7 +117,7 @@ def _run(features: torch.Tensor, packed: PackedWeight, bias: Optional[torch.Tens
     out = torch.empty((n_out, packed.c_out), dtype=feats.dtype, device=feats.device)
     b = None
     if bias is not None:
-        b = bias if bias.device == feats.device and bias.is_contiguous() \
+        b = bias if bias.get_device() == feats.get_device() and bias.is_contiguous() \
             and bias.dtype in _PARAM_DTYPES else \
             bias.detach().to(feats.device).contiguous()
         if b.dtype not in _PARAM_DTYPES:
@@ -153,7 +157,7 @@ def sparse_conv_forward(features: torch.Tensor, weight: Union[torch.Tensor, Pack
         K, c_in, c_out = weight.shape
         weight = pack_weight(weight, (K, 1, 1), c_in, c_out,
                              compute_dtype(features.dtype, weight.dtype))
-    elem = torch.empty((), dtype=weight.dtype).element_size()
+    elem = weight.dtype.itemsize
     nbr, order, ordered = indice_data.conv_operands(N_out, features.device, weight.c_in * elem,
                                                     n_in=features.shape[0])
     # user-assigned lists that name an output row more than once within a

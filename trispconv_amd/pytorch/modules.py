@@ -146,14 +146,14 @@ class SparseConvolution(SparseModule):
 
     def _forward_subm(self, x: SparseConvTensor, epilogue=None) -> SparseConvTensor:
         data = self._get_or_compute_subm_indice(x)
-        n_out = len(data.out_indices)
+        n_out = data.out_indices.shape[0]
         out = sparse_conv_forward(x.features, self._packed_weight(x.features.dtype), self.bias,
                                   data, n_out, epilogue)
         return _derived(x, out, data.out_indices, x.spatial_shape)
 
     def _forward_strided(self, x: SparseConvTensor, epilogue=None) -> SparseConvTensor:
         data = self._get_or_compute_strided_indice(x)
-        n_out = len(data.out_indices)
+        n_out = data.out_indices.shape[0]
         out = sparse_conv_forward(x.features, self._packed_weight(x.features.dtype), self.bias,
                                   data, n_out, epilogue)
         return _derived(x, out, data.out_indices, list(data.output_spatial_shape))
@@ -217,6 +217,9 @@ class SparseInverseConv3d(SparseConvolution):
                          indice_key=indice_key, algo=algo)
 
 
+_FUSED_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+
+
 def _plain(m: nn.Module) -> bool:
     return not (m._forward_hooks or m._forward_pre_hooks)
 
@@ -226,18 +229,20 @@ def _fusable(mods: List[nn.Module], i: int, conv: SparseConvolution,
     """The epilogue that modules i, i+1 (an eval-mode BatchNorm1d over the
     conv's channels, then a ReLU; either may be missing) amount to, and how
     many modules it covers."""
-    if not (x.features.is_cuda and _plain(conv)
-            and x.features.dtype in (torch.float32, torch.float16, torch.bfloat16)):
+    f = x.features
+    if not (f.is_cuda and _plain(conv) and f.dtype in _FUSED_DTYPES):
         return None, 0
     bn_parts = (None, None, None, None, 0.0)
     used = 0
     if i < len(mods):
         bn = mods[i]
         if (type(bn) is nn.BatchNorm1d and not bn.training and bn.track_running_stats
-                and bn.running_mean is not None and bn.num_features == conv.out_channels
-                and _plain(bn)):
-            parts = (bn.running_mean, bn.running_var, bn.weight, bn.bias)
-            if all(t is None or t.device == x.features.device for t in parts):
+                and bn.num_features == conv.out_channels and _plain(bn)):
+            buffers, params = bn._buffers, bn._parameters
+            parts = (buffers.get("running_mean"), buffers.get("running_var"),
+                     params.get("weight"), params.get("bias"))
+            where = f.get_device()
+            if parts[0] is not None and all(t is None or t.get_device() == where for t in parts):
                 bn_parts = parts + (float(bn.eps),)
                 used = 1
     relu = False
