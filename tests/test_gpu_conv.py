@@ -265,6 +265,34 @@ def test_deterministic_and_order_independent(c_in, c_out, dtype, monkeypatch):
     assert torch.equal(a, b) and torch.equal(a, c) and torch.equal(a, d)
 
 
+@pytest.mark.parametrize("c_in,c_out,dtype", [(16, 16, torch.float32), (20, 16, torch.float32),
+                                              (32, 16, torch.float16), (32, 48, torch.bfloat16)])
+def test_narrow_kernel_on_a_sparse_grid(c_in, c_out, dtype, monkeypatch):
+    """The narrow kernel on a sparse grid (4000 voxels in 48^3: about two
+    pairs per row, most of a wave's slots empty), with steps of one slot (16
+    f32, 32 f16 channels) and steps across two slots (20 f32 channels): the
+    oracle's values, and the same bits in map order, in a planned order and
+    in the reverse of it."""
+    monkeypatch.setattr(I, "_PLAN_MIN_BYTES", 0)
+    shape = (48, 48, 48)
+    idx = _tiny(41, shape, 1, 4000)
+    feats_np = np.random.default_rng(42).standard_normal((len(idx), c_in)).astype(np.float32)
+    m = _module("subm", c_in, c_out, 3, dtype=dtype, seed=c_in + c_out)
+    _check_layer(m, feats_np, idx, shape, 1, dtype, what=f"sparse narrow {c_in}->{c_out}")
+    x = torch.from_numpy(idx).to(DEV)
+    feats = torch.from_numpy(feats_np).to(DEV).to(dtype)
+    data = generate_subm_indice_pairs(x, shape, 1, 3)
+    pw = m._packed_weight(dtype)
+    a = Fn.sparse_conv_forward(feats, pw, m.bias, data, len(idx))
+    b = Fn.sparse_conv_forward(feats, pw, m.bias, data, len(idx))  # planned on the second use
+    assert data._order is not None
+    nbr = data.neighbour_map(len(idx), feats.device)
+    c = Fn._run(feats, pw, m.bias, nbr, None, len(idx))
+    rev = torch.flip(data._order, [0]).contiguous()
+    d = Fn._run(feats, pw, m.bias, nbr, rev, len(idx))
+    assert torch.equal(a, b) and torch.equal(a, c) and torch.equal(a, d)
+
+
 @pytest.mark.parametrize("kind,k,s,p", [("subm", (5, 5, 5), 1, 0), ("subm", (1, 3, 3), 1, 0),
                                         ("strided", (2, 2, 2), 2, 0), ("strided", 3, 2, 1)])
 def test_plan_permutes_every_slot_count(kind, k, s, p, monkeypatch):
