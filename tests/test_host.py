@@ -256,6 +256,18 @@ def test_argument_errors_return_codes_without_gpu():
     assert rc == 1 and b"output shape" in lib.tsc_last_error()
     rc = lib.tsc_conv_forward(None, 7, 1, 1, None, None, 0, None, None, 0, 1, 1, 1, None, None)
     assert rc == 1 and b"dtype" in lib.tsc_last_error()
+    # byte marks kept by the caller: too few bytes for the grid, or a mark
+    # value outside 1..255, are refused before anything is launched (the
+    # marks address is never touched)
+    geo = (L.i3((8, 8, 8)), L.i3((3, 3, 3)), L.i3((2, 2, 2)), L.i3((1, 1, 1)), L.i3((1, 1, 1)),
+           L.i3((4, 4, 4)))
+    need = lib.tsc_strided_marks_bytes(10, 27, 1, geo[5])
+    assert need >= 64 and need % 16 == 0
+    rc = lib.tsc_strided_count(None, 10, 1, *geo, None, 0, 16, need - 1, 1, None, None)
+    assert rc == 1 and b"marks of" in lib.tsc_last_error()
+    for gen in (0, 256):
+        rc = lib.tsc_strided_count(None, 10, 1, *geo, None, 0, 16, need, gen, None, None)
+        assert rc == 1 and b"mark value" in lib.tsc_last_error()
     # a build on an existing bitmap: 3-wide kernels only, and a bitmap that
     # covers the grid
     rc = lib.tsc_subm_pairs_from_bitmap(None, 10, 1, L.i3((8, 8, 8)), L.i3((5, 5, 5)),
