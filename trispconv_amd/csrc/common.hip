@@ -352,10 +352,10 @@ __device__ __forceinline__ uint32_t pack_bytes(uint4 a, uint4 b, uint32_t rep) {
          marked_nibble(b.w, rep) << 28;
 }
 
-// One thread per entry pair (512 per tile): twice the waves of the other
-// bitmap passes, for a pass that only streams the byte marks (measured: the
-// 16.7 MB surface build 0.0720-0.0729 -> 0.0710-0.0732 ms, the 23.6 MB LiDAR
-// strided build 0.0956-0.0970 -> 0.0938-0.0943 ms).
+// One thread per entry pair (512 per tile): twice the waves of two pairs a
+// thread, for a pass that only streams the byte marks (measured: the 16.7 MB
+// surface build 0.0720-0.0729 -> 0.0710-0.0732 ms, the 23.6 MB LiDAR strided
+// build 0.0956-0.0970 -> 0.0938-0.0943 ms).
 constexpr int kPackThreads = kBmTile / 2;
 
 __global__ void __launch_bounds__(kPackThreads) bitmap_pack_kernel(const uint4* __restrict__ bytes,
@@ -387,13 +387,21 @@ __global__ void __launch_bounds__(kPackThreads) bitmap_pack_kernel(const uint4* 
   if (threadIdx.x == 0) sums[blockIdx.x] = tot;
 }
 
-__global__ void __launch_bounds__(kBmThreads) bitmap_apply_kernel(uint4* __restrict__ wr2, int64_t nw,
-                                                                  const uint32_t* __restrict__ sums,
-                                                                  const uint32_t* __restrict__ pre,
-                                                                  int nsum,
-                                                                  int32_t* __restrict__ n_unique,
-                                                                  const uint8_t* __restrict__ touched) {
+// One thread per entry pair (512 per tile), like the pack pass; the pair is
+// loaded before the tile-sum scan, so the two round trips overlap.
+__global__ void __launch_bounds__(kPackThreads) bitmap_apply_kernel(uint4* __restrict__ wr2,
+                                                                    int64_t nw,
+                                                                    const uint32_t* __restrict__ sums,
+                                                                    const uint32_t* __restrict__ pre,
+                                                                    int nsum,
+                                                                    int32_t* __restrict__ n_unique,
+                                                                    const uint8_t* __restrict__ touched) {
   __shared__ uint32_t s_wave[33];
+  // a tile without a set bit has no rank to write (block-uniform)
+  const bool live = !touched || touched[blockIdx.x];
+  const int64_t p = (blockIdx.x * (int64_t)kBmTile) / 2 + threadIdx.x;
+  const bool in = live && 2 * p < nw;
+  uint4 v = in ? wr2[p] : make_uint4(0u, 0u, 0u, 0u);
   uint32_t base;
   if (pre) {
     base = pre[blockIdx.x];
@@ -401,35 +409,22 @@ __global__ void __launch_bounds__(kBmThreads) bitmap_apply_kernel(uint4* __restr
     // this tile's offset, and on block 0 the total, from the tile sums
     const int lim = blockIdx.x == 0 ? nsum : static_cast<int>(blockIdx.x);
     uint32_t part = 0;
-    for (int i = threadIdx.x; i < lim; i += kBmThreads) part += sums[i];
+    for (int i = threadIdx.x; i < lim; i += kPackThreads) part += sums[i];
     uint32_t tot;
     block_exclusive(part, s_wave, &tot);
     base = blockIdx.x == 0 ? 0u : tot;
     if (blockIdx.x == 0 && threadIdx.x == 0) *n_unique = static_cast<int32_t>(tot);
   }
-  if (touched && !touched[blockIdx.x]) return;  // no set bit, no rank to write (block-uniform)
-  const int64_t p = (blockIdx.x * (int64_t)kBmTile) / 2 + 2 * threadIdx.x;
-  uint4 v[2];
-  uint32_t c[4];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    v[j] = 2 * (p + j) < nw ? wr2[p + j] : make_uint4(0u, 0u, 0u, 0u);
-    c[2 * j] = __popc(v[j].x);
-    c[2 * j + 1] = __popc(v[j].z);
-  }
+  if (!live) return;
+  const uint32_t c0 = __popc(v.x), c1 = __popc(v.z);
   uint32_t tot;
-  uint32_t run = base + block_exclusive(c[0] + c[1] + c[2] + c[3], s_wave, &tot);
+  const uint32_t run = base + block_exclusive(c0 + c1, s_wave, &tot);
   // a rank is only looked up for a set bit, so pairs of empty words keep
   // theirs unwritten (on sparse grids nearly every pair: the pass then mostly
   // reads)
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    v[j].y = run;
-    run += c[2 * j];
-    v[j].w = run;
-    run += c[2 * j + 1];
-    if (2 * (p + j) < nw && (v[j].x | v[j].z)) wr2[p + j] = v[j];
-  }
+  v.y = run;
+  v.w = run + c0;
+  if (in && (v.x | v.z)) wr2[p] = v;
 }
 
 // Bitmap scans of up to this many tiles let every apply block sum the tile
@@ -473,7 +468,7 @@ int bitmap_scan(uint2* wr, int64_t nw, uint32_t* scratch, int32_t* total, hipStr
     if (rc) return rc;
     p = pre;
   }
-  bitmap_apply_kernel<<<static_cast<unsigned>(nsum), kBmThreads, 0, s>>>(
+  bitmap_apply_kernel<<<static_cast<unsigned>(nsum), kPackThreads, 0, s>>>(
       wr2, nw, sums, p, static_cast<int>(nsum < kBmDirectTiles ? nsum : kBmDirectTiles), total,
       touched);
   TSC_LAUNCH_CHECK("bitmap_apply");
