@@ -259,6 +259,29 @@ def test_byte_marks_kept_between_builds_never_leak(monkeypatch):
     assert _stream_marks().buf.numel() > size
 
 
+def test_byte_marks_over_a_random_sequence_of_builds(monkeypatch):
+    """Thirty SubM and strided builds in a seeded random order on one stream,
+    on grids of random shapes (so the kept marks grow now and then) and
+    random densities, with the mark values made to run out halfway: every
+    build gives the oracle's pairs and output set."""
+    from trispconv_amd.pytorch import indices as IM
+    monkeypatch.setattr(IM, "_MARKS", IM._ThreadMarks())
+    rng = np.random.default_rng(81)
+    for step in range(30):
+        shape = tuple(int(v) for v in rng.integers(6, 36, size=3))
+        B = int(rng.integers(1, 3))
+        n = int(rng.integers(1, max(2, shape[0] * shape[1] * shape[2] // 3)))
+        idx = _tiny(int(rng.integers(1 << 30)), shape, B, min(n, 2500))
+        if step == 15:
+            m = _stream_marks()
+            if m is not None:
+                m.gen = 254
+        if rng.random() < 0.5:
+            _subm(idx, shape, B, 3, 1, f"random sequence {step}: subm {shape} x{B}")
+        else:
+            _strided(idx, shape, B, 3, 2, 1, 1, f"random sequence {step}: strided {shape} x{B}")
+
+
 def test_byte_marks_of_two_host_threads_on_one_stream():
     """Two host threads building on the same stream at once: their launches
     interleave on the stream, so each thread keeps marks of its own; every
