@@ -1,10 +1,12 @@
 """The reference-side bindings shown in the boundary document, executed as
 written on the GPU.
 
-Seam 1 (``sparse_conv_forward`` over the reference's pair lists) and seam 2
-(``generate_subm_indice_pairs`` with its pair lists) are taken from
-INTEGRATION.md's code blocks and run with a small ``_tsc`` module in place
-of the binding module they import: the library, its error check, the shape
+Seam 1 (``sparse_conv_forward`` over the reference's pair lists), seam 2
+(``generate_subm_indice_pairs`` with its pair lists), seam 3
+(``generate_strided_indice_pairs``, the fill queued before the count is
+read) and seam 4 (the inverse's pair swap) are taken from INTEGRATION.md's
+code blocks and run with a small ``_tsc`` module in place of the binding
+module they call: the library, its error check, the shape
 arrays and the current stream.  Their outputs must equal this package's: the
 same pair lists and pair counts bit for bit, and the same convolution bits
 (the kernel sums each output in the same order whatever map it is given).
@@ -108,3 +110,27 @@ def test_seam_1_conv_snippet_runs_as_written(dtype):
     exp = Fn.sparse_conv_forward(feats, weight, bias, data, n)
     assert got.dtype == dtype and got.shape == (n, 64)
     assert torch.equal(got, exp)
+
+
+def test_seam_3_and_4_strided_and_inverse_snippets_run_as_written():
+    from trispconv.pytorch.indices import generate_inverse_indice_pairs, generate_strided_indice_pairs
+    shape, B = (21, 18, 25), 2
+    idx = _tiny(95, shape, B, 1500)
+    x = torch.from_numpy(idx).to(DEV)
+    s3 = _run_snippet("## Seam 3", IndiceData=IndiceData, _to3=_to3)
+    s4 = _run_snippet("## Seam 4", IndiceData=IndiceData)
+    say("INTEGRATION seam 3 and 4 snippets:", idx.shape, shape)
+    got = s3["generate_strided_indice_pairs"](x, shape, B, 3, 2, 1, 1)
+    exp = generate_strided_indice_pairs(x, shape, B, 3, 2, 1, 1)
+    assert tuple(got.output_spatial_shape) == tuple(exp.output_spatial_shape)
+    assert torch.equal(got.out_indices, exp.out_indices)
+    assert torch.equal(got.pair_num, exp.pair_num)
+    for k in range(27):
+        assert torch.equal(got.pairs_in[k].cpu(), exp.pairs_in[k].cpu()), k
+        assert torch.equal(got.pairs_out[k].cpu(), exp.pairs_out[k].cpu()), k
+    inv_got = s4["inverse_indice_pairs"](got)
+    inv_exp = generate_inverse_indice_pairs(exp)
+    assert torch.equal(inv_got.out_indices, inv_exp.out_indices)
+    for k in range(27):
+        assert torch.equal(inv_got.pairs_in[k].cpu(), inv_exp.pairs_in[k].cpu()), k
+        assert torch.equal(inv_got.pairs_out[k].cpu(), inv_exp.pairs_out[k].cpu()), k
