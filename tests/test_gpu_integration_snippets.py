@@ -4,7 +4,8 @@ written on the GPU.
 Seam 1 (``sparse_conv_forward`` over the reference's pair lists), seam 2
 (``generate_subm_indice_pairs`` with its pair lists), seam 3
 (``generate_strided_indice_pairs``, the fill queued before the count is
-read) and seam 4 (the inverse's pair swap) are taken from INTEGRATION.md's
+read), seam 4 (the inverse's pair swap) and seam 5 (``dense()``) are taken
+from INTEGRATION.md's
 code blocks and run with a small ``_tsc`` module in place of the binding
 module they call: the library, its error check, the shape
 arrays and the current stream.  Their outputs must equal this package's: the
@@ -134,3 +135,16 @@ def test_seam_3_and_4_strided_and_inverse_snippets_run_as_written():
     for k in range(27):
         assert torch.equal(inv_got.pairs_in[k].cpu(), inv_exp.pairs_in[k].cpu()), k
         assert torch.equal(inv_got.pairs_out[k].cpu(), inv_exp.pairs_out[k].cpu()), k
+
+
+@pytest.mark.parametrize("channels_first", [True, False])
+def test_seam_5_dense_snippet_runs_as_written(channels_first):
+    import trispconv.pytorch as spconv
+    shape, B = (9, 10, 11), 2
+    idx = _tiny(97, shape, B, 300)
+    feats = torch.randn(len(idx), 5, generator=torch.Generator().manual_seed(3)).to(DEV)
+    t = spconv.SparseConvTensor(feats, torch.from_numpy(idx).to(DEV), list(shape), B)
+    scope = _run_snippet("## Seam 5")
+    say("INTEGRATION seam 5 snippet:", channels_first)
+    got = scope["dense"](t, channels_first)
+    assert torch.equal(got, t.dense(channels_first))
