@@ -5,12 +5,12 @@ Seam 1 (``sparse_conv_forward`` over the reference's pair lists), seam 2
 (``generate_subm_indice_pairs`` with its pair lists), seam 3
 (``generate_strided_indice_pairs``, the fill queued before the count is
 read), seam 4 (the inverse's pair swap) and seam 5 (``dense()``) are taken
-from INTEGRATION.md's
-code blocks and run with a small ``_tsc`` module in place of the binding
-module they call: the library, its error check, the shape
-arrays and the current stream.  Their outputs must equal this package's: the
-same pair lists and pair counts bit for bit, and the same convolution bits
-(the kernel sums each output in the same order whatever map it is given).
+from the document's code blocks and run with a small ``_tsc`` module in
+place of the binding module they call: the library, its error check, the
+shape arrays and the current stream.  Their outputs must equal this
+package's: the same pair lists, pair counts and output coordinates bit for
+bit, and the same convolution bits (the kernel sums each output in the same
+order whatever map it is given).
 """
 import re
 from pathlib import Path
@@ -28,6 +28,7 @@ from trispconv_amd.pytorch.weight import normalize_spconv_weight
 
 pytestmark = [pytest.mark.gpu, needs_gpu]
 ROOT = Path(__file__).resolve().parent.parent
+BOUNDARY_DOC = ROOT / "INTEGRATION.md"
 
 
 class _Tsc:
@@ -56,13 +57,13 @@ def _run_snippet(heading: str, **names) -> dict:
     """Executes the first python block under ``heading`` and returns its
     names; the binding module it calls (and may import) is the ``_tsc``
     above."""
-    text = (ROOT / "INTEGRATION.md").read_text()
+    text = BOUNDARY_DOC.read_text()
     section = text.split(heading, 1)[1]
     block = re.findall(r"```python\n(.*?)```", section, flags=re.S)[0]
     assert "_tsc." in block
     _Tsc.lib = L.lib()
     scope = {"torch": torch, "_tsc": _Tsc, **names}
-    exec(compile(block.replace("from . import _tsc", "pass"), "INTEGRATION.md", "exec"), scope)
+    exec(compile(block.replace("from . import _tsc", "pass"), str(BOUNDARY_DOC), "exec"), scope)
     return scope
 
 
@@ -84,7 +85,7 @@ def test_seam_2_subm_pairs_snippet_runs_as_written():
     idx = _tiny(91, shape, B, 1800)
     x = torch.from_numpy(idx).to(DEV)
     scope = _run_snippet("## Seam 2", IndiceData=IndiceData, _to3=_to3)
-    say("INTEGRATION seam 2 snippet:", idx.shape, shape)
+    say("boundary document, seam 2 snippet:", idx.shape, shape)
     got = scope["generate_subm_indice_pairs"](x, shape, B, 3, 1)
     exp = generate_subm_indice_pairs(x, shape, B, 3, 1)
     assert torch.equal(got.pair_num, exp.pair_num)
@@ -106,7 +107,7 @@ def test_seam_1_conv_snippet_runs_as_written(dtype):
     bias = (torch.randn(64, generator=g) * 0.1).to(DEV).to(dtype)
     weight = normalize_spconv_weight(krsc, (3, 3, 3), 32, 64)  # (K, C_in, C_out)
     scope = _run_snippet("## Seam 1 ", )
-    say("INTEGRATION seam 1 snippet:", dtype, n)
+    say("boundary document, seam 1 snippet:", dtype, n)
     got = scope["sparse_conv_forward"](feats, weight, bias, data, n)
     exp = Fn.sparse_conv_forward(feats, weight, bias, data, n)
     assert got.dtype == dtype and got.shape == (n, 64)
@@ -120,7 +121,7 @@ def test_seam_3_and_4_strided_and_inverse_snippets_run_as_written():
     x = torch.from_numpy(idx).to(DEV)
     s3 = _run_snippet("## Seam 3", IndiceData=IndiceData, _to3=_to3)
     s4 = _run_snippet("## Seam 4", IndiceData=IndiceData)
-    say("INTEGRATION seam 3 and 4 snippets:", idx.shape, shape)
+    say("boundary document, seam 3 and 4 snippets:", idx.shape, shape)
     got = s3["generate_strided_indice_pairs"](x, shape, B, 3, 2, 1, 1)
     exp = generate_strided_indice_pairs(x, shape, B, 3, 2, 1, 1)
     assert tuple(got.output_spatial_shape) == tuple(exp.output_spatial_shape)
@@ -145,6 +146,6 @@ def test_seam_5_dense_snippet_runs_as_written(channels_first):
     feats = torch.randn(len(idx), 5, generator=torch.Generator().manual_seed(3)).to(DEV)
     t = spconv.SparseConvTensor(feats, torch.from_numpy(idx).to(DEV), list(shape), B)
     scope = _run_snippet("## Seam 5")
-    say("INTEGRATION seam 5 snippet:", channels_first)
+    say("boundary document, seam 5 snippet:", channels_first)
     got = scope["dense"](t, channels_first)
     assert torch.equal(got, t.dense(channels_first))

@@ -184,7 +184,7 @@ def test_indice_data_is_a_dataclass_with_the_reference_fields():
 
 
 def test_integration_load_snippet_runs_as_written():
-    """The 'Build and load' snippet of INTEGRATION.md, executed as written
+    """The 'Build and load' snippet of the boundary document, executed as written
     from the repository root: it loads the built library and asserts its ABI
     version (no GPU call)."""
     text = (ROOT / "INTEGRATION.md").read_text()
