@@ -31,6 +31,8 @@
 #include "common.hpp"
 
 #include <algorithm>
+#include <type_traits>
+#include <utility>
 
 namespace tsc {
 namespace {
@@ -702,6 +704,218 @@ __global__ void __launch_bounds__(256) subm_probe_rows_kernel(
   }
 }
 
+// Pointers into global memory (so that a store through one is a global store,
+// not a flat one, also where the compiler cannot trace it to a kernel argument).
+typedef __attribute__((address_space(1))) char global_char;
+typedef __attribute__((address_space(1))) int32_t global_int;
+
+// Lane L of v = the wave-uniform value x: one v_writelane_b32.
+template <int L>
+__device__ __forceinline__ void write_lane(int32_t& v, int32_t x) {
+  static_assert(L >= 0 && L < kWave, "lane out of range");
+  asm("v_writelane_b32 %0, %1, %2" : "+v"(v) : "s"(x), "n"(L));
+}
+
+// Lanes set in m take a, the others b (one v_cndmask_b32 on values already
+// loaded).
+__device__ __forceinline__ uint32_t select_lanes(uint64_t m, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(r) : "v"(b), "v"(a), "s"(m));
+  return r;
+}
+
+// f(std::integral_constant<int, Q>{}) for Q = 0, 1, ... in order.
+template <typename F, int... Q>
+__device__ __forceinline__ void for_each_index(F&& f, std::integer_sequence<int, Q...>) {
+  (f(std::integral_constant<int, Q>{}), ...);
+}
+
+// The 3x3x3 kernel with dil.x == 1, for grids of fewer than 2^29 rows.  With
+// every lane busy the probe is bound by its vector instructions (about 1,060
+// per column in subm_probe_rows_kernel), not by its loads and stores, so this
+// form spends far fewer.  A kernel row's three cells are consecutive cells of
+// one bitmap word or two:
+//  - one funnel shift of the two words gives the row's three occupancy bits
+//    (h, bit kx for cell x - 1 + kx), masked by the x bounds (vmask, one per
+//    column) and the row's z and y bounds (bit q of rv, one per column);
+//  - the row's hits are consecutive occupied cells, so they have consecutive
+//    ranks: the j-th hit in kx order has rank r0 + j, r0 the first hit's.
+//    So the column entries r0, r0 + 1 and r0 + 2 are loaded unconditionally
+//    (the column array carries 4 entries of padding) and picked by the bits
+//    of h below kx; IDENT takes the ranks themselves;
+//  - a slot's hit count is the popcount of its lane mask, and a row's three
+//    counts go into one lane by a lane write; the slot mask is the rows' h
+//    side by side.
+// No store is under a lane condition, so the compiler keeps every load ahead
+// of the stores: lanes past the last column work as the last column and
+// store the same values to it, and the counts leave them out.  Loads and
+// stores address a scalar base plus a 32-bit lane offset (the slot bases are
+// opaque to the compiler, which would otherwise rebuild them per lane with
+// 64-bit multiplies).  The map, its counts and its slot masks equal
+// subm_probe_rows_kernel's.  TOUCHED: the entries of untouched tiles read as
+// empty (the atomic-marked bitmap).
+constexpr int64_t kProbe333Rows = int64_t(1) << 29;
+
+template <bool IDENT, bool TOUCHED>
+__global__ void __launch_bounds__(256) subm_probe_333_kernel(
+    int64_t n, SubmGeom g, const uint2* __restrict__ wr, int64_t nw,
+    const uint2* __restrict__ col_e, const int4* __restrict__ rows_coords,
+    const int32_t* __restrict__ n_unique, const int32_t* __restrict__ n_extra,
+    int32_t* __restrict__ cols_row, int32_t* __restrict__ nbr, int32_t* __restrict__ blk_cnt,
+    int nblk, int32_t* __restrict__ counts, uint32_t* __restrict__ col_masks,
+    const uint8_t* __restrict__ touched) {
+  constexpr int K = 27;
+  __shared__ int32_t s_cnt[kRows / kWave][9];
+  const int t = threadIdx.x;
+  const int lane = t & (kWave - 1);
+  const uint32_t un = static_cast<uint32_t>(n);  // 0 < n < 2^29
+  const uint32_t col_t = blockIdx.x * static_cast<uint32_t>(kRows) + static_cast<uint32_t>(t);
+  const uint64_t real = __ballot(col_t < un);  // lanes of real columns
+  const uint32_t col = col_t < un ? col_t : un - 1;
+  int4 c;  // (b, z, y, x)
+  bool live;
+  uint32_t key;
+  if constexpr (IDENT) {
+    live = true;
+    c = rows_coords[col];
+    key = cell_key(g, c.x, c.y, c.z, c.w);
+    cols_row[col] = static_cast<int32_t>(col);
+  } else {
+    live = col < static_cast<uint32_t>(*n_unique + *n_extra);  // the other columns are empty
+    const uint2 me = live ? col_e[col] : make_uint2(0u, 0u);
+    cols_row[col] = static_cast<int32_t>(me.x) - 1;
+    key = me.y;
+    c = cell_coords(g, key);
+  }
+  // x: the row's cells are x - 1, x, x + 1; its first cell inside the grid
+  // is x_first, shift = x_first - (x - 1)
+  const int x_lo = c.w - 1;
+  const int x_first = x_lo > 0 ? x_lo : 0;
+  const uint32_t shift = static_cast<uint32_t>(x_first - x_lo) & 31u;
+  const uint32_t W = static_cast<uint32_t>(g.shape.x);
+  const uint32_t vmask = (static_cast<uint32_t>(x_lo) < W ? 1u : 0u) |
+                         (static_cast<uint32_t>(c.w) < W ? 2u : 0u) |
+                         (static_cast<uint32_t>(c.w + 1) < W ? 4u : 0u);
+  const uint32_t key_first = key + static_cast<uint32_t>(x_first - c.w);
+  // rows: bit kz * 3 + ky of rv when (b, z + (kz - 1) dz, y + (ky - 1) dy,
+  // x_first) is inside the grid
+  const bool col_ok = live && static_cast<uint32_t>(c.x) < static_cast<uint32_t>(g.B) &&
+                      static_cast<uint32_t>(x_first) < W;
+  const uint32_t D = static_cast<uint32_t>(g.shape.z), H = static_cast<uint32_t>(g.shape.y);
+  const uint32_t yf = (static_cast<uint32_t>(c.z - g.dil.y) < H ? 1u : 0u) |
+                      (static_cast<uint32_t>(c.z) < H ? 2u : 0u) |
+                      (static_cast<uint32_t>(c.z + g.dil.y) < H ? 4u : 0u);
+  uint32_t rv = (static_cast<uint32_t>(c.y - g.dil.z) < D ? yf : 0u) |
+                (static_cast<uint32_t>(c.y) < D ? yf << 3 : 0u) |
+                (static_cast<uint32_t>(c.y + g.dil.z) < D ? yf << 6 : 0u);
+  rv = col_ok ? rv : 0u;
+  const uint32_t plane = W * H;
+  const uint32_t last_w = static_cast<uint32_t>(nw - 1);
+  const char* const ce = reinterpret_cast<const char*>(col_e);
+  const uint32_t col4 = col << 2;
+  const uint64_t slot_bytes = static_cast<uint64_t>(n) * sizeof(int32_t);
+  global_char* slot = (global_char*)nbr;
+  uint32_t cmask = 0;
+  int32_t my_cnt = 0;  // lane q: the wave's hits through slots 3q .. 3q + 2
+  bool bad = false;    // IDENT: the rows are not the bitmap's cells
+  auto kernel_row = [&](auto qc) {
+    constexpr int q = decltype(qc)::value;
+    constexpr int kz = q / 3, ky = q % 3;
+    const uint32_t row_off = static_cast<uint32_t>((kz - 1) * g.dil.z) * plane +
+                             static_cast<uint32_t>((ky - 1) * g.dil.y) * W;
+    const uint32_t okm = static_cast<uint32_t>(__builtin_amdgcn_sbfe(static_cast<int>(rv), q, 1));
+    const uint32_t base = (key_first + row_off) & okm;  // cell 0 for rows outside the grid
+    const uint32_t w0 = base >> 5;
+    const uint32_t w1 = w0 + 1 < last_w ? w0 + 1 : last_w;  // past the last word: cells x >= W
+    uint2 e0 = wr[w0], e1 = wr[w1];
+    if constexpr (TOUCHED) {
+      const bool t0 = touched[w0 / kBitmapTileWords], t1 = touched[w1 / kBitmapTileWords];
+      e0 = t0 ? e0 : make_uint2(0u, 0u);
+      e1 = t1 ? e1 : make_uint2(0u, 0u);
+    }
+    const uint32_t lo = base & 31u;  // the row's first cell's bit in e0
+    const uint32_t bits = __builtin_amdgcn_alignbit(e1.x, e0.x, lo);
+    uint32_t h = (bits << shift) & vmask & okm;
+    // The first hit's rank.  An entry's rank field is only defined where its
+    // pair of entries holds a set bit, so it comes from the entry holding the
+    // hit: from e0 when a cell at or past the row's first one is set in e0
+    // (where the row's cells reach into e1 they are e0's last cells, so such
+    // a cell is the row's; cells masked by the x bound lie past any hit),
+    // otherwise from e1, whose cells below the hit are the row's and empty.
+    // Without a hit it is 0, so that the column loads stay in their array.
+    // (A select by hand: as a C++ select the compiler branches around each
+    // rank load and waits for it there, one memory round trip per row.)
+    const uint32_t r_e0 = e0.y + __popc(e0.x & ~(0xffffffffu << lo));
+    uint32_t r0 = select_lanes(__ballot((e0.x >> lo) != 0u), r_e0, e1.y);
+    r0 = h ? r0 : 0u;
+    int32_t jr0, jr1, jr2;
+    if constexpr (IDENT) {
+      // a hit ranked n or more: the rows are not the bitmap's cells; it is dropped
+      if (r0 + static_cast<uint32_t>(__popc(h)) > un) {
+        bad = true;
+        uint32_t room = un > r0 ? un - r0 : 0u, kept = 0u;
+#pragma unroll
+        for (int kx = 0; kx < 3; ++kx)
+          if ((h >> kx) & 1u) {
+            if (room) {
+              kept |= 1u << kx;
+              --room;
+            }
+          }
+        h = kept;
+      }
+      jr0 = (h & 1u) ? static_cast<int32_t>(r0) : -1;
+      jr1 = (h & 2u) ? static_cast<int32_t>(r0 + (h & 1u)) : -1;
+      jr2 = (h & 4u) ? static_cast<int32_t>(r0 + __popc(h & 3u)) : -1;
+      // the row's own cell must be occupied and carry the row's own rank; with
+      // no rank beyond n either, the rows are exactly the first n occupied
+      // cells in rank order (a permuted or foreign row set fails)
+      if (q == 4) bad = bad || jr1 != static_cast<int32_t>(col);
+    } else {
+      const uint32_t* v = reinterpret_cast<const uint32_t*>(ce + (r0 << 3));
+      const int32_t m0 = static_cast<int32_t>(v[0]) - 1, m1 = static_cast<int32_t>(v[2]) - 1,
+                    m2 = static_cast<int32_t>(v[4]) - 1;  // rows of ranks r0 .. r0 + 2
+      const bool b0 = h & 1u, b1 = h & 2u;
+      jr0 = b0 ? m0 : -1;
+      jr1 = b1 ? (b0 ? m1 : m0) : -1;
+      const int32_t u = b1 ? m1 : m0, w = b1 ? m2 : m1;
+      jr2 = (h & 4u) ? (b0 ? w : u) : -1;
+    }
+    // a hit is a non-negative map entry (every occupied rank's column holds
+    // its row + 1 >= 1), so the counts and the slot mask come from h; lane q
+    // of my_cnt holds the row's three slot counts (at most 64 each) in
+    // 10-bit fields
+    const uint32_t c0 = static_cast<uint32_t>(__popcll(__ballot(h & 1u) & real));
+    const uint32_t c1 = static_cast<uint32_t>(__popcll(__ballot(h & 2u) & real));
+    const uint32_t c2 = static_cast<uint32_t>(__popcll(__ballot(h & 4u) & real));
+    write_lane<q>(my_cnt, static_cast<int32_t>(c0 | (c1 << 10) | (c2 << 20)));
+    cmask |= h << (3 * q);
+    const int32_t jr[3] = {jr0, jr1, jr2};
+#pragma unroll
+    for (int kx = 0; kx < 3; ++kx) {
+      *(global_int*)(slot + col4) = jr[kx];
+      slot += slot_bytes;
+      asm("" : "+s"(slot));
+    }
+  };
+  for_each_index(kernel_row, std::make_integer_sequence<int, 9>{});
+  if constexpr (IDENT) {
+    if (bad) atomicOr(&counts[K], TSC_FLAG_ROWS_NOT_BITMAP);
+  }
+  if (col_masks) col_masks[col] = cmask;
+  if (lane < 9) s_cnt[t / kWave][lane] = my_cnt;
+  __syncthreads();
+  if (t < K) {
+    int32_t sum = 0;
+#pragma unroll
+    for (int w = 0; w < kRows / kWave; ++w) sum += (s_cnt[w][t / 3] >> (10 * (t % 3))) & 1023;
+    if (blk_cnt)
+      blk_cnt[(int64_t)t * nblk + blockIdx.x] = sum;
+    else if (sum)
+      atomicAdd(&counts[t], sum);
+  }
+}
+
 // Row-order hit counts per (slot, block) of a row-major map, for the
 // compaction offsets of the pair lists.
 __global__ void __launch_bounds__(kRows) map_count_kernel(const int32_t* __restrict__ nbr, int64_t n,
@@ -1046,7 +1260,17 @@ int tsc::subm_pairs_ws(const int32_t* coords, int64_t n, int32_t batch_size,
     if (K > 64 &&
         (rc = fill_u32(reinterpret_cast<uint32_t*>(blk_cnt), (int64_t)nblk * K, 0u, s)))
       return rc;
-    if (ks.x == 3 && 2 * dil.x < 32 && ks.y == 3 && ks.z == 3) {
+    if (ks.x == 3 && ks.y == 3 && ks.z == 3 && dil.x == 1 && n < kProbe333Rows) {
+      if (w.touched)
+        subm_probe_333_kernel<false, true><<<ceil_div(n, kRows), kRows, 0, s>>>(
+            n, g, w.wr, nw, w.col, nullptr, w.n_unique, w.n_extra, cols_row, nbr, blk_cnt, nblk,
+            counts, col_masks, w.touched);
+      else
+        subm_probe_333_kernel<false, false><<<ceil_div(n, kRows), kRows, 0, s>>>(
+            n, g, w.wr, nw, w.col, nullptr, w.n_unique, w.n_extra, cols_row, nbr, blk_cnt, nblk,
+            counts, col_masks, nullptr);
+      TSC_LAUNCH_CHECK("subm_probe_333");
+    } else if (ks.x == 3 && 2 * dil.x < 32 && ks.y == 3 && ks.z == 3) {
       subm_probe_rows_kernel<3, 3, 3, false><<<ceil_div(n, 256), 256, 0, s>>>(
           n, K, g, w.wr, nw, w.col, nullptr, w.n_unique, w.n_extra, cols_row, nbr, blk_cnt,
           nblk, counts, col_masks, w.touched);
@@ -1218,7 +1442,11 @@ extern "C" int tsc_subm_pairs_from_bitmap(const int32_t* coords, int64_t n, int3
   SubmGeom g{batch_size, shape, ks, dil, 0u};
   const uint2* wr = static_cast<const uint2*>(bitmap);
   const int4* c4 = reinterpret_cast<const int4*>(coords);
-  if (ks.y == 3 && ks.z == 3)
+  if (ks.y == 3 && ks.z == 3 && dil.x == 1 && n < kProbe333Rows)
+    subm_probe_333_kernel<true, false><<<ceil_div(n, kRows), kRows, 0, s>>>(
+        n, g, wr, nw, nullptr, c4, nullptr, nullptr, cols_row, nbr, nullptr, 0, counts, col_masks,
+        nullptr);
+  else if (ks.y == 3 && ks.z == 3)
     subm_probe_rows_kernel<3, 3, 3, true><<<ceil_div(n, 256), 256, 0, s>>>(
         n, K, g, wr, nw, nullptr, c4, nullptr, nullptr, cols_row, nbr, nullptr, 0, counts,
         col_masks, nullptr);
