@@ -9,6 +9,8 @@
 #include <cstdint>
 #include <cstdio>
 #include <string>
+#include <type_traits>
+#include <utility>
 
 #include "../../include/trispconv_abi.h"
 
@@ -122,6 +124,32 @@ __device__ __forceinline__ uint64_t lanes_below() {
 
 __device__ __forceinline__ int rank_in_wave(uint64_t ballot) {
   return __popcll(ballot & lanes_below());
+}
+
+// Pointers into global memory (so that a store through one is a global store,
+// not a flat one, also where the compiler cannot trace it to a kernel argument).
+typedef __attribute__((address_space(1))) char global_char;
+typedef __attribute__((address_space(1))) int32_t global_int;
+
+// Lane L of v = the wave-uniform value x: one v_writelane_b32.
+template <int L>
+__device__ __forceinline__ void write_lane(int32_t& v, int32_t x) {
+  static_assert(L >= 0 && L < kWave, "lane out of range");
+  asm("v_writelane_b32 %0, %1, %2" : "+v"(v) : "s"(x), "n"(L));
+}
+
+// Lanes set in m take a, the others b (one v_cndmask_b32 on values already
+// loaded).
+__device__ __forceinline__ uint32_t select_lanes(uint64_t m, uint32_t a, uint32_t b) {
+  uint32_t r;
+  asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(r) : "v"(b), "v"(a), "s"(m));
+  return r;
+}
+
+// f(std::integral_constant<int, Q>{}) for Q = 0, 1, ... in order.
+template <typename F, int... Q>
+__device__ __forceinline__ void for_each_index(F&& f, std::integer_sequence<int, Q...>) {
+  (f(std::integral_constant<int, Q>{}), ...);
 }
 
 // ------------------------------------------------------------ conversions --

@@ -429,6 +429,246 @@ Buffers carve(void* ws, const Layout& L, int K, int64_t* used, bool marks_outsid
   return b;
 }
 
+// ---------------------------------------------------------------------------
+// Narrow builds of the fixed kernel shapes: output grids of fewer than 2^30
+// cells and every axis with out < 2^24 and out * stride^2 < 2^32 (with fewer
+// than 2^29 input rows).  All of a row's candidate arithmetic is then 32-bit.
+// An axis value v = c + pad - a * dil is a candidate iff v < out * stride as
+// an unsigned number (a negative v fails too) and v is a multiple of the
+// stride; its output coordinate v / stride is one multiply-high by the
+// axis's rounded-up reciprocal, exact for v * stride < 2^32.  An axis value
+// that is no candidate carries kFar = 2^30, so a slot's cell is one
+// three-way add, and a candidate iff it is below kFar (up to three kFar terms
+// plus a cell below 2^30 stay below 2^32).  The general kernels above spend
+// most of their time on 64-bit multiplies and the divisions, and with every
+// lane busy these builds are bound by their vector instructions.
+constexpr uint32_t kFar = 1u << 30;
+
+struct NarrowGeom {
+  uint32_t mag[3];  // z, y, x: ceil(2^32 / stride), 0 for stride 1
+  uint32_t lim[3];  // out * stride
+  uint32_t plane;   // oH * oW
+  uint32_t vol;     // oD * oH * oW
+};
+
+bool narrow_geom(const StridedGeom& g, int64_t n, const Layout& L, NarrowGeom* ng) {
+  if (L.cells >= kFar || n >= (int64_t(1) << 29)) return false;
+  const int32_t st[3] = {g.st.z, g.st.y, g.st.x}, out[3] = {g.out.z, g.out.y, g.out.x};
+  for (int a = 0; a < 3; ++a) {
+    if (out[a] >= (1 << 24) || (uint64_t)out[a] * st[a] * st[a] >= (uint64_t(1) << 32))
+      return false;
+    ng->mag[a] = st[a] == 1 ? 0u
+                            : static_cast<uint32_t>(((uint64_t(1) << 32) + st[a] - 1) / st[a]);
+    ng->lim[a] = static_cast<uint32_t>(out[a]) * static_cast<uint32_t>(st[a]);
+  }
+  ng->plane = static_cast<uint32_t>(out[1]) * static_cast<uint32_t>(out[2]);
+  ng->vol = static_cast<uint32_t>(out[0]) * ng->plane;
+  return true;
+}
+
+// Output coordinate of axis value v (v < lim: v * stride < 2^32), or kFar
+// for no candidate; the output coordinate is then scaled by `scale` and
+// `base` is added (the row's cell offset along that axis).
+__device__ __forceinline__ uint32_t narrow_axis(int v, int st, uint32_t mag, uint32_t lim,
+                                                uint32_t scale, uint32_t base, bool ok) {
+  const uint32_t u = static_cast<uint32_t>(v);
+  const uint32_t q = mag ? __umulhi(u, mag) : u;  // u / st for u < lim
+  const bool cand = ok && u < lim && u == __umul24(q, static_cast<uint32_t>(st));
+  return cand ? base + q * scale : kFar;
+}
+
+template <int KZ, int KY, int KX>
+struct NarrowCands {
+  static constexpr int K = KZ * KY * KX;
+  uint32_t zt[KZ], yt[KY], xt[KX];
+  bool any;  // some slot has a candidate
+  __device__ __forceinline__ NarrowCands(const StridedGeom& g, const NarrowGeom& ng,
+                                         const int4& c, bool ok) {
+    const uint32_t row = static_cast<uint32_t>(c.x) * ng.vol;  // batch b's first cell
+    uint32_t mz = kFar, my = kFar, mx = kFar;
+#pragma unroll
+    for (int a = 0; a < KZ; ++a) {
+      zt[a] = narrow_axis(c.y + g.pad.z - a * g.dil.z, g.st.z, ng.mag[0], ng.lim[0], ng.plane,
+                          row, ok);
+      mz = min(mz, zt[a]);
+    }
+#pragma unroll
+    for (int a = 0; a < KY; ++a) {
+      yt[a] = narrow_axis(c.z + g.pad.y - a * g.dil.y, g.st.y, ng.mag[1], ng.lim[1],
+                          static_cast<uint32_t>(g.out.x), 0u, true);  // q * oW < 2^30
+      my = min(my, yt[a]);
+    }
+#pragma unroll
+    for (int a = 0; a < KX; ++a) {
+      xt[a] = narrow_axis(c.w + g.pad.x - a * g.dil.x, g.st.x, ng.mag[2], ng.lim[2], 1u, 0u,
+                          true);
+      mx = min(mx, xt[a]);
+    }
+    any = mz < kFar && my < kFar && mx < kFar;
+  }
+  // slot k = (kz*KY + ky)*KX + kx, k a compile-time constant
+  template <int k>
+  __device__ __forceinline__ uint32_t cell() const {
+    return zt[k / (KY * KX)] + yt[(k / KX) % KY] + xt[k % KX];
+  }
+};
+
+// Per-wave slot counts, three 10-bit fields per lane (lane k / 3 holds slots
+// 3(k/3) .. 3(k/3) + 2): one lane write per three slots.
+template <int k, int KC>
+__device__ __forceinline__ void count_slot(int32_t& lanes, uint32_t& packed, bool hit) {
+  packed |= static_cast<uint32_t>(__popcll(__ballot(hit))) << (10 * (k % 3));
+  if constexpr (k % 3 == 2 || k == KC - 1) {
+    write_lane<k / 3>(lanes, static_cast<int32_t>(packed));
+    packed = 0;
+  }
+}
+
+__device__ __forceinline__ int32_t count_field(int32_t packed, int k) {
+  return (packed >> (10 * (k % 3))) & 1023;
+}
+
+// strided_mark_kernel's byte-marking form for narrow builds: the same marks,
+// counts and per-block paired rows.
+template <int KZ, int KY, int KX>
+__global__ void __launch_bounds__(kRows) strided_mark_narrow_kernel(
+    const int4* __restrict__ coords, int64_t n, StridedGeom g, NarrowGeom ng,
+    uint8_t* __restrict__ bytes, uint32_t* __restrict__ mark_words, uint32_t gen,
+    int32_t* __restrict__ blk_cnt, int nblk, int32_t* __restrict__ paired) {
+  constexpr int KC = KZ * KY * KX;
+  constexpr int NW = (KC + 2) / 3;
+  __shared__ int32_t s_cnt[kRows / kWave][NW];
+  __shared__ int32_t s_paired[kRows / kWave];
+  const int t = threadIdx.x;
+  const int w = t / kWave;
+  const int lane = t & (kWave - 1);
+  const int64_t i = blockIdx.x * (int64_t)kRows + t;
+  const bool valid = i < n;
+  const int4 c = valid ? coords[i] : make_int4(-1, 0, 0, 0);
+  const bool ok = valid && c.x >= 0 && c.x < g.B;
+  if (valid && !ok) mark_words[kMarkBatch] = gen;
+  const NarrowCands<KZ, KY, KX> cand(g, ng, c, ok);
+  const uint8_t mark = static_cast<uint8_t>(gen);
+  int32_t cnt = 0;
+  uint32_t packed = 0;
+  for_each_index(
+      [&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        const uint32_t cell = cand.template cell<k>();
+        const bool hit = cell < kFar;
+        if (hit) ((global_char*)bytes)[cell] = mark;
+        count_slot<k, KC>(cnt, packed, hit);
+      },
+      std::make_integer_sequence<int, KC>{});
+  const uint64_t with_pairs = __ballot(cand.any);
+  if (lane == 0) s_paired[w] = static_cast<int32_t>(__popcll(with_pairs));
+  if (lane < NW) s_cnt[w][lane] = cnt;
+  __syncthreads();
+  if (t == 0) {
+    int32_t sum = 0;
+#pragma unroll
+    for (int ww = 0; ww < kRows / kWave; ++ww) sum += s_paired[ww];
+    paired[blockIdx.x] = sum;
+  }
+  if (t < KC) {
+    int32_t sum = 0;
+#pragma unroll
+    for (int ww = 0; ww < kRows / kWave; ++ww) sum += count_field(s_cnt[ww][t / 3], t);
+    blk_cnt[(int64_t)t * nblk + blockIdx.x] = sum;
+  }
+}
+
+// strided_fill_kernel for narrow builds: the same lists, map and ids.  The
+// stores address per-slot scalar bases plus 32-bit lane offsets.
+template <int KZ, int KY, int KX>
+__global__ void __launch_bounds__(kRows) strided_fill_narrow_kernel(
+    const int4* __restrict__ coords, int64_t n, int K, StridedGeom g, NarrowGeom ng,
+    const uint2* __restrict__ wr, const int32_t* __restrict__ blk_off, int nblk, int64_t cap,
+    const int32_t* __restrict__ n_out_dev, int64_t out_cap, int32_t* __restrict__ nbr,
+    int32_t* __restrict__ pairs_in, int32_t* __restrict__ pairs_out,
+    int32_t* __restrict__ in_ids) {
+  constexpr int KC = KZ * KY * KX;
+  constexpr int NW = (KC + 2) / 3;
+  __shared__ int32_t s_cnt[kRows / kWave][NW];
+  __shared__ int32_t s_off[kRows / kWave][KC];
+  __shared__ int32_t s_paired[kRows / kWave];
+  const int32_t n_out = *n_out_dev;
+  const bool to_map = n_out <= out_cap;
+  const int t = threadIdx.x;
+  const int w = t / kWave;
+  const int lane = t & (kWave - 1);
+  const int64_t i = blockIdx.x * (int64_t)kRows + t;
+  const bool valid = i < n;
+  const int4 c = valid ? coords[i] : make_int4(-1, 0, 0, 0);
+  const bool ok = valid && c.x >= 0 && c.x < g.B;
+  const NarrowCands<KZ, KY, KX> cand(g, ng, c, ok);
+  // every slot's bitmap entry is loaded before any is used
+  uint2 e[KC];
+  int32_t cnt = 0;
+  uint32_t packed = 0;
+  for_each_index(
+      [&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        const uint32_t cell = cand.template cell<k>();
+        const bool hit = cell < kFar;
+        e[k] = wr[hit ? cell >> 5 : 0u];  // entry 0 exists
+        count_slot<k, KC>(cnt, packed, hit);
+      },
+      std::make_integer_sequence<int, KC>{});
+  const uint64_t with_pairs = __ballot(cand.any);
+  if (lane == 0) s_paired[w] = static_cast<int32_t>(__popcll(with_pairs));
+  if (lane < NW) s_cnt[w][lane] = cnt;
+  __syncthreads();
+  if (in_ids) {
+    // the row's id among the input rows with a pair: the block's first id
+    // from the scan of the mark's per-block counts, then waves, then lanes
+    int32_t id = blk_off[(int64_t)K * nblk + blockIdx.x];
+    for (int ww = 0; ww < w; ++ww) id += s_paired[ww];
+    if (valid) in_ids[i] = cand.any ? id + rank_in_wave(with_pairs) : -1;
+  }
+  if (t < KC) {
+    // block offset of each wave's slot-t pairs
+    int32_t run = blk_off[(int64_t)t * nblk + blockIdx.x];
+#pragma unroll
+    for (int ww = 0; ww < kRows / kWave; ++ww) {
+      s_off[ww][t] = run;
+      run += count_field(s_cnt[ww][t / 3], t);
+    }
+  }
+  __syncthreads();
+  const uint32_t row = static_cast<uint32_t>(i);
+  const uint32_t ucap = static_cast<uint32_t>(cap), un_out = static_cast<uint32_t>(n_out);
+  global_char* pin = (global_char*)pairs_in;
+  global_char* pout = (global_char*)pairs_out;
+  global_char* pmap = (global_char*)nbr;
+  const uint64_t list_bytes = static_cast<uint64_t>(cap) * sizeof(int32_t);
+  const uint64_t map_bytes = static_cast<uint64_t>(n_out) * sizeof(int32_t);
+  for_each_index(
+      [&](auto kc) {
+        constexpr int k = decltype(kc)::value;
+        const uint32_t cell = cand.template cell<k>();
+        const bool hit = cell < kFar;
+        const uint64_t hits = __ballot(hit);
+        const uint32_t base = static_cast<uint32_t>(s_off[w][k]);
+        const uint32_t rank = e[k].y + __popc(e[k].x & ~(0xffffffffu << (cell & 31u)));
+        const uint32_t pos = __builtin_amdgcn_mbcnt_hi(
+            static_cast<uint32_t>(hits >> 32),
+            __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(hits), base));
+        // both bounds hold by construction; the test keeps a bad count from
+        // turning into an out-of-bounds write
+        if (hit && pos < ucap && rank < un_out) {
+          *(global_int*)(pin + (pos << 2)) = static_cast<int32_t>(row);
+          *(global_int*)(pout + (pos << 2)) = static_cast<int32_t>(rank);
+          if (to_map) *(global_int*)(pmap + (rank << 2)) = static_cast<int32_t>(row);
+        }
+        pin += list_bytes;
+        pout += list_bytes;
+        pmap += map_bytes;
+        asm("" : "+s"(pin), "+s"(pout), "+s"(pmap));
+      },
+      std::make_integer_sequence<int, KC>{});
+}
+
 // Runs F<KZ, KY, KX> for the common kernel shapes, F<0, 0, 0> otherwise.
 template <template <int, int, int> class F, typename... A>
 int by_shape(const Box& ks, A... a) {
@@ -441,9 +681,17 @@ int by_shape(const Box& ks, A... a) {
 
 template <int KZ, int KY, int KX>
 struct LaunchMark {
-  static int run(const int4* c, int64_t n, int K, StridedGeom g, uint2* wr, uint8_t* bytes,
-                 uint32_t* mwords, uint32_t gen, int32_t* blk_cnt, int nblk, int32_t* status,
-                 int32_t* paired, hipStream_t s) {
+  static int run(const int4* c, int64_t n, int K, StridedGeom g, const NarrowGeom* ng, uint2* wr,
+                 uint8_t* bytes, uint32_t* mwords, uint32_t gen, int32_t* blk_cnt, int nblk,
+                 int32_t* status, int32_t* paired, hipStream_t s) {
+    if constexpr (KZ * KY * KX > 0) {
+      if (bytes && ng) {
+        strided_mark_narrow_kernel<KZ, KY, KX><<<nblk, kRows, 0, s>>>(
+            c, n, g, *ng, bytes, mwords, gen, blk_cnt, nblk, paired);
+        TSC_LAUNCH_CHECK("strided_mark");
+        return 0;
+      }
+    }
     if (bytes)
       strided_mark_kernel<KZ, KY, KX, true><<<nblk, kRows, 0, s>>>(
           c, n, K, g, wr, bytes, mwords, gen, blk_cnt, nblk, status, paired);
@@ -457,10 +705,18 @@ struct LaunchMark {
 
 template <int KZ, int KY, int KX>
 struct LaunchFill {
-  static int run(const int4* c, int64_t n, int K, StridedGeom g, const uint2* wr,
-                 const int32_t* blk_off, int nblk, int64_t cap, const int32_t* n_out_dev,
-                 int64_t out_cap, int32_t* nbr, int32_t* pin, int32_t* pout, int32_t* in_ids,
-                 hipStream_t s) {
+  static int run(const int4* c, int64_t n, int K, StridedGeom g, const NarrowGeom* ng,
+                 const uint2* wr, const int32_t* blk_off, int nblk, int64_t cap,
+                 const int32_t* n_out_dev, int64_t out_cap, int32_t* nbr, int32_t* pin,
+                 int32_t* pout, int32_t* in_ids, hipStream_t s) {
+    if constexpr (KZ * KY * KX > 0) {
+      if (ng) {
+        strided_fill_narrow_kernel<KZ, KY, KX><<<nblk, kRows, 0, s>>>(
+            c, n, K, g, *ng, wr, blk_off, nblk, cap, n_out_dev, out_cap, nbr, pin, pout, in_ids);
+        TSC_LAUNCH_CHECK("strided_fill");
+        return 0;
+      }
+    }
     strided_fill_kernel<KZ, KY, KX><<<nblk, kRows, 0, s>>>(c, n, K, g, wr, blk_off, nblk, cap,
                                                            n_out_dev, out_cap, nbr, pin, pout,
                                                            in_ids);
@@ -557,7 +813,10 @@ extern "C" int tsc_strided_count(const int32_t* coords, int64_t n, int32_t batch
   TSC_REQUIRE(coords != nullptr, "strided: coords is null");
   if (K > 64 && (rc = fill_u32(reinterpret_cast<uint32_t*>(b.blk_cnt), L.nblk * K, 0u, s)))
     return rc;
-  if ((rc = by_shape<LaunchMark>(g.ks, reinterpret_cast<const int4*>(coords), n, K, g, b.wr,
+  NarrowGeom ng;
+  const bool narrow = narrow_geom(g, n, L, &ng);
+  if ((rc = by_shape<LaunchMark>(g.ks, reinterpret_cast<const int4*>(coords), n, K, g,
+                                 narrow ? &ng : static_cast<const NarrowGeom*>(nullptr), b.wr,
                                  bytes, mwords, mark_gen, b.blk_cnt, (int)L.nblk, counts + K + 1,
                                  b.blk_cnt + (int64_t)K * L.nblk, s)))
     return rc;
@@ -605,7 +864,10 @@ extern "C" int tsc_strided_fill(const int32_t* coords, int64_t n, int32_t batch_
       b.wr, L.nwords, g, reinterpret_cast<int4*>(out_coords), counts + K, out_cap, emit_blocks,
       reinterpret_cast<uint32_t*>(nbr), K);
   TSC_LAUNCH_CHECK("strided_emit");
+  NarrowGeom ng;
+  const bool narrow = narrow_geom(g, n, L, &ng);
   return by_shape<LaunchFill>(g.ks, reinterpret_cast<const int4*>(coords), n, K, g,
+                              narrow ? &ng : static_cast<const NarrowGeom*>(nullptr),
                               static_cast<const uint2*>(b.wr), static_cast<const int32_t*>(b.blk_off),
                               (int)L.nblk, n, counts + K, out_cap, nbr, pairs_in, pairs_out, in_ids,
                               s);
