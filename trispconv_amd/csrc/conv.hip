@@ -1417,11 +1417,35 @@ __device__ __forceinline__ float param_or(const void* p, int dt, int64_t i, floa
 
 // PIECE: bytes per gather (16 or 8); NT: 16-column tiles per wave.  A group
 // is SG steps: 8 / NT gathers and 32 / NP weight registers per lane.
-template <typename T, int PIECE, int NT>
+// B32: layers whose features and map stay below 2^31 bytes (NarrowB32::fits).
+// The gathers and map loads then go through buffer loads with 32-bit
+// offsets: an offset past the buffer's end reads zeros, which gives absent
+// neighbours their zero row and the identity map (a buffer of no bytes) its
+// zero entries, and the slot of a reduction index is one multiply-high by
+// C_in's rounded-up reciprocal.  The 64-bit addresses and the division cost
+// each step about three times the vector instructions (a wave of the 20k-row
+// 16->16 fp32 layer executed 1,623 of them for 108 MFMAs).  Both forms sum
+// the same products in the same order.
+struct NarrowB32 {
+  uint32_t feat_bytes;  // n_in * C_in * sizeof(T)
+  uint32_t map_bytes;   // K * n_out * 4, 0 for the identity map
+  uint32_t row_bytes;   // C_in * sizeof(T)
+  uint32_t cin_mag;     // ceil(2^32 / C_in)
+  static bool fits(int64_t n_in, int c_in, int elem, int64_t n_out, int K, int64_t nsteps,
+                   int lv) {
+    const int64_t r_end = 4 * lv * nsteps;  // reduction indices stay below this
+    return n_in * c_in * elem < (int64_t(1) << 31) && (int64_t)K * n_out * 4 < (int64_t(1) << 31) &&
+           n_in < (int64_t(1) << 24) && (int64_t)c_in * elem < (int64_t(1) << 24) &&
+           r_end * c_in < (int64_t(1) << 32);
+  }
+};
+constexpr int kBufferWord3 = 0x00020000;  // raw buffer, 32-bit data (gfx9 family)
+
+template <typename T, int PIECE, int NT, bool B32>
 __global__ void __launch_bounds__(256) conv_narrow_kernel(
     const T* __restrict__ feat, int c_in, const T* __restrict__ W, Epilogue ep,
     const int32_t* __restrict__ nbr, const int32_t* __restrict__ order, int nbr_ordered,
-    int64_t n_out, int K, int c_out, int nsteps, T* __restrict__ out) {
+    int64_t n_out, int K, int c_out, int nsteps, NarrowB32 nb32, T* __restrict__ out) {
   using Op = Mfma16<T>;
   using Piece = typename VecOf<PIECE>::type;
   constexpr int LV = 16 / (int)sizeof(T);      // reduction values per lane and step
@@ -1470,6 +1494,14 @@ __global__ void __launch_bounds__(256) conv_narrow_kernel(
 #pragma unroll
   for (int n = 0; n < NT; ++n) acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // B32: buffers over the features and the map (no bytes for the identity map)
+  const __amdgpu_buffer_rsrc_t feat_rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<T*>(feat), 0, static_cast<int>(nb32.feat_bytes), kBufferWord3);
+  const __amdgpu_buffer_rsrc_t map_rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int32_t*>(nbr), 0, static_cast<int>(nb32.map_bytes), kBufferWord3);
+  const uint32_t col4 = static_cast<uint32_t>(col) * 4u;
+  const uint32_t n_out4 = static_cast<uint32_t>(n_out) * 4u;
+
   for (int i0 = 0; i0 < nsteps; i0 += SG) {
     int32_t j[SG * NP];
     uint32_t ch[SG * NP];
@@ -1477,13 +1509,19 @@ __global__ void __launch_bounds__(256) conv_narrow_kernel(
     for (int u = 0; u < SG * NP; ++u) {
       const int i = i0 + u / NP;
       const uint32_t r = 4u * LV * static_cast<uint32_t>(i) + LV * q + VPP * static_cast<uint32_t>(u % NP);
-      const uint32_t k = r / static_cast<uint32_t>(c_in);
+      const uint32_t k = B32 ? __umulhi(r, nb32.cin_mag) : r / static_cast<uint32_t>(c_in);
       ch[u] = r - k * static_cast<uint32_t>(c_in);
       const bool live = va && i < nsteps && k < static_cast<uint32_t>(K);
       // every lane loads (dead ones from slot K-1 of their column), so the
       // group's map loads issue back to back; dead lanes then use -1
-      const int64_t kk = live ? k : K - 1;
-      const int32_t e = map[(kk * n_out + col) & map_mask];
+      int32_t e;
+      if constexpr (B32) {
+        const uint32_t kk = live ? k : static_cast<uint32_t>(K - 1);
+        e = __builtin_amdgcn_raw_buffer_load_b32(map_rs, kk * n_out4 + col4, 0, 0);
+      } else {
+        const int64_t kk = live ? k : K - 1;
+        e = map[(kk * n_out + col) & map_mask];
+      }
       // an OR rather than a select: the load's value is then always used, and
       // the compiler keeps it unconditional instead of branching around it
       j[u] = (e + ident_row) | (live ? 0 : -1);
@@ -1491,10 +1529,21 @@ __global__ void __launch_bounds__(256) conv_narrow_kernel(
     Piece v[SG * NP];
 #pragma unroll
     for (int u = 0; u < SG * NP; ++u) {
-      const Piece* src = j[u] >= 0
-                             ? reinterpret_cast<const Piece*>(feat + (int64_t)j[u] * c_in + ch[u])
-                             : zero_piece;
-      v[u] = *src;
+      if constexpr (B32) {
+        // absent rows read past the buffer's end: zeros
+        const uint32_t off = j[u] >= 0 ? __umul24(static_cast<uint32_t>(j[u]), nb32.row_bytes) +
+                                             ch[u] * static_cast<uint32_t>(sizeof(T))
+                                       : 0x80000000u;
+        if constexpr (PIECE == 16)
+          v[u] = __builtin_bit_cast(Piece, __builtin_amdgcn_raw_buffer_load_b128(feat_rs, off, 0, 0));
+        else
+          v[u] = __builtin_bit_cast(Piece, __builtin_amdgcn_raw_buffer_load_b64(feat_rs, off, 0, 0));
+      } else {
+        const Piece* src = j[u] >= 0
+                               ? reinterpret_cast<const Piece*>(feat + (int64_t)j[u] * c_in + ch[u])
+                               : zero_piece;
+        v[u] = *src;
+      }
     }
     uint4 b[SG][NT];
 #pragma unroll
@@ -1676,7 +1725,7 @@ int dispatch_mfma(const void* feat, int c_in, const void* W, const Epilogue& ep,
 }
 
 template <typename T, int PIECE, int NT>
-int launch_narrow(const void* feat, int c_in, const void* W, const Epilogue& ep,
+int launch_narrow(const void* feat, int64_t n_in, int c_in, const void* W, const Epilogue& ep,
                   const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out, int K,
                   int c_out, void* out, hipStream_t s) {
   constexpr int dt = std::is_same<T, float>::value ? TSC_F32
@@ -1685,15 +1734,26 @@ int launch_narrow(const void* feat, int c_in, const void* W, const Epilogue& ep,
   TSC_REQUIRE(nsteps < (int64_t(1) << 26), "conv: K * C_in too large");
   dim3 grid(static_cast<unsigned>(ceil_div(n_out, 4 * kNarrowRows)),
             static_cast<unsigned>(c_out / 16 / NT));
-  conv_narrow_kernel<T, PIECE, NT><<<grid, 256, 0, s>>>(
-      static_cast<const T*>(feat), c_in, static_cast<const T*>(W), ep, nbr, order, nbr_ordered,
-      n_out, K, c_out, static_cast<int>(nsteps), static_cast<T*>(out));
+  constexpr int elem = static_cast<int>(sizeof(T));
+  if (NarrowB32::fits(n_in, c_in, elem, n_out, K, nsteps, 16 / elem)) {
+    const NarrowB32 nb32{static_cast<uint32_t>(n_in * c_in * elem),
+                         nbr ? static_cast<uint32_t>((int64_t)K * n_out * 4) : 0u,
+                         static_cast<uint32_t>(c_in * elem),
+                         static_cast<uint32_t>(((uint64_t(1) << 32) + c_in - 1) / c_in)};
+    conv_narrow_kernel<T, PIECE, NT, true><<<grid, 256, 0, s>>>(
+        static_cast<const T*>(feat), c_in, static_cast<const T*>(W), ep, nbr, order, nbr_ordered,
+        n_out, K, c_out, static_cast<int>(nsteps), nb32, static_cast<T*>(out));
+  } else {
+    conv_narrow_kernel<T, PIECE, NT, false><<<grid, 256, 0, s>>>(
+        static_cast<const T*>(feat), c_in, static_cast<const T*>(W), ep, nbr, order, nbr_ordered,
+        n_out, K, c_out, static_cast<int>(nsteps), NarrowB32{}, static_cast<T*>(out));
+  }
   TSC_LAUNCH_CHECK("conv_narrow");
   return 0;
 }
 
 template <typename T>
-int dispatch_narrow(const void* feat, int c_in, const void* W, const Epilogue& ep,
+int dispatch_narrow(const void* feat, int64_t n_in, int c_in, const void* W, const Epilogue& ep,
                     const int32_t* nbr, const int32_t* order, int nbr_ordered, int64_t n_out,
                     int K, int c_out, void* out, hipStream_t s) {
   // Column tiles per wave: up to 4, fewer while that leaves under 2048
@@ -1708,7 +1768,7 @@ int dispatch_narrow(const void* feat, int c_in, const void* W, const Epilogue& e
               "conv: features must be %d-byte and weights 16-byte aligned", piece);
 #define TSC_NARROW_CASE(P_, NT_)                                                             \
   if (piece == P_ && nt == NT_)                                                              \
-    return launch_narrow<T, P_, NT_>(feat, c_in, W, ep, nbr, order, nbr_ordered, n_out, K, \
+    return launch_narrow<T, P_, NT_>(feat, n_in, c_in, W, ep, nbr, order, nbr_ordered, n_out, K, \
                                      c_out, out, s);
   TSC_NARROW_CASE(16, 1)
   TSC_NARROW_CASE(16, 2)
@@ -1875,12 +1935,12 @@ static int conv_forward(const void* feat, int32_t dtype, int64_t n_in, int32_t c
   }
   if (path == kNarrow) {
     if (dtype == TSC_F32)
-      return dispatch_narrow<float>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out,
+      return dispatch_narrow<float>(feat, n_in, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out,
                                     k_vol, c_out, out, s);
     if (dtype == TSC_F16)
-      return dispatch_narrow<__half>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out,
+      return dispatch_narrow<__half>(feat, n_in, c_in, packed_w, ep, nbr, order, nbr_ordered, n_out,
                                      k_vol, c_out, out, s);
-    return dispatch_narrow<__hip_bfloat16>(feat, c_in, packed_w, ep, nbr, order, nbr_ordered,
+    return dispatch_narrow<__hip_bfloat16>(feat, n_in, c_in, packed_w, ep, nbr, order, nbr_ordered,
                                            n_out, k_vol, c_out, out, s);
   }
   if (dtype == TSC_F32)
