@@ -895,8 +895,27 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
     for (int m = 0; m < WD; ++m)
       dma_b128(src + m * 256, w_lds + P * SLAB_BYTES + (m * 256 + wave_u * 64) * 16);
   };
+  // DMA addresses.  A present row's is one 64-bit multiply-add (row times
+  // row bytes plus the lane's base), an absent row's the zero row, chosen by a
+  // lane-mask select: written as a C++ select, the compiler branches around
+  // the multiply, an exec-masked block with its own 64-bit arithmetic per DMA.
+  // Channel half hh of a stage is the same address plus 64 bytes, added in the
+  // address register: the DMA's immediate offset would move its LDS
+  // destination too.
+  const uint64_t row_bytes = static_cast<uint64_t>(c_in) * sizeof(T);
+  const uint64_t feat_lane = reinterpret_cast<uint64_t>(feat) + piece * 16;
+  const uint64_t zero_lane = reinterpret_cast<uint64_t>(zero_row) + piece * 16;
+  const uint64_t live_entries = __ballot(orow_l >= 0);
+  const uint64_t entry_lane = reinterpret_cast<uint64_t>(nbr + col_l);  // slot 0's entry
+  const uint64_t none_lane = reinterpret_cast<uint64_t>(no_row);
+  auto lane_select = [](uint64_t m, uint64_t a, uint64_t b) {
+    const uint32_t lo = select_lanes(m, static_cast<uint32_t>(a), static_cast<uint32_t>(b));
+    const uint32_t hi = select_lanes(m, static_cast<uint32_t>(a >> 32), static_cast<uint32_t>(b >> 32));
+    return reinterpret_cast<const char*>((static_cast<uint64_t>(hi) << 32) | lo);
+  };
   auto dma_entries = [&](int P, int k) {  // slot k's entries of the wave's rows into buffer P
-    dma_b32(orow_l >= 0 ? nbr + (int64_t)k * n_out + col_l : no_row, e_lds + P * 256);
+    const uint64_t a = entry_lane + static_cast<uint64_t>(k) * static_cast<uint64_t>(n_out) * 4u;
+    dma_b32(lane_select(live_entries, a, none_lane), e_lds + P * 256);
   };
   // chunk c of the rows named by entry buffer P, for the blocks in set (four
   // DMAs per 32-row block)
@@ -904,16 +923,14 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
     int32_t j[2 * RB];
 #pragma unroll
     for (int g = 0; g < 2 * RB; ++g) j[g] = s_e[P * 64 + 16 * g + q];
+    const uint64_t base = feat_lane + static_cast<uint64_t>(c) * (CK * sizeof(T));
 #pragma unroll
     for (int g = 0; g < 2 * RB; ++g) {
       if (!((set >> (g / 2)) & 1)) continue;
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const char* src =
-            j[g] >= 0 ? reinterpret_cast<const char*>(feat + (int64_t)j[g] * c_in + c * CK + hh * (CK / 2)) + piece * 16
-                      : zero_row + piece * 16;
-        dma_b128(src, a_lds + (2 * g + hh) * 1024);
-      }
+      const uint64_t a = static_cast<uint64_t>(static_cast<uint32_t>(j[g])) * row_bytes + base;
+      const char* src = lane_select(__ballot(j[g] >= 0), a, zero_lane);
+      dma_b128(src, a_lds + (2 * g) * 1024);
+      dma_b128(src + 64, a_lds + (2 * g + 1) * 1024);
     }
   };
   auto wait_vm0 = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
