@@ -146,6 +146,22 @@ __device__ __forceinline__ uint32_t select_lanes(uint64_t m, uint32_t a, uint32_
   return r;
 }
 
+// The same for 64-bit values (addresses): a C++ select of an address that
+// takes arithmetic makes the compiler branch around the arithmetic, one
+// exec-masked block per address.
+__device__ __forceinline__ uint64_t select_lanes64(uint64_t m, uint64_t a, uint64_t b) {
+  const uint32_t lo = select_lanes(m, static_cast<uint32_t>(a), static_cast<uint32_t>(b));
+  const uint32_t hi = select_lanes(m, static_cast<uint32_t>(a >> 32), static_cast<uint32_t>(b >> 32));
+  return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+// A pointer into global memory from an address, so that loads through it are
+// global loads rather than flat ones.
+template <typename T>
+__device__ __forceinline__ const T* global_ptr(uint64_t a) {
+  return (const T*)reinterpret_cast<const __attribute__((address_space(1))) T*>(a);
+}
+
 // f(std::integral_constant<int, Q>{}) for Q = 0, 1, ... in order.
 template <typename F, int... Q>
 __device__ __forceinline__ void for_each_index(F&& f, std::integer_sequence<int, Q...>) {

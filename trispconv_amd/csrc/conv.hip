@@ -498,8 +498,8 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
   // (otherwise it is reloaded from the GOT, with a wait, in every stage)
   uint64_t zero_addr = reinterpret_cast<uint64_t>(g_zero_row);
   asm volatile("" : "+s"(zero_addr));
-  const uint4* zero_row =
-      (const uint4*)reinterpret_cast<const __attribute__((address_space(1))) uint4*>(zero_addr);
+  const uint64_t feat_addr = reinterpret_cast<uint64_t>(feat);
+  const uint32_t row_bytes = static_cast<uint32_t>(c_in) * static_cast<uint32_t>(sizeof(T));
 
   f32x16 acc[2][NB];
 #pragma unroll
@@ -538,12 +538,12 @@ __global__ void __launch_bounds__(256, 2) conv_mfma_kernel(
     const int32_t j1 = live ? e1 : -1;
     const int coff = c * CK + h * (CK / 2);
     const bool pad = coff >= c_in;  // the upper half of a half-filled last chunk
-    const uint4* p0 = j0 >= 0 && !pad
-                          ? reinterpret_cast<const uint4*>(feat + (int64_t)j0 * c_in + coff)
-                          : zero_row;
-    const uint4* p1 = j1 >= 0 && !pad
-                          ? reinterpret_cast<const uint4*>(feat + (int64_t)j1 * c_in + coff)
-                          : zero_row;
+    // one 64-bit multiply-add per row, the zero row by a lane-mask select
+    const uint64_t base = feat_addr + static_cast<uint64_t>(coff) * sizeof(T);
+    const uint64_t a0 = static_cast<uint64_t>(static_cast<uint32_t>(j0)) * static_cast<uint64_t>(row_bytes) + base;
+    const uint64_t a1 = static_cast<uint64_t>(static_cast<uint32_t>(j1)) * static_cast<uint64_t>(row_bytes) + base;
+    const uint4* p0 = global_ptr<uint4>(select_lanes64(__ballot(j0 >= 0 && !pad), a0, zero_addr));
+    const uint4* p1 = global_ptr<uint4>(select_lanes64(__ballot(j1 >= 0 && !pad), a1, zero_addr));
 #pragma unroll
     for (int u = 0; u < UB; ++u) {
       ring[S][0][u] = p0[u];
@@ -909,9 +909,7 @@ __global__ void __launch_bounds__(256, 2) conv_dma_kernel(
   const uint64_t entry_lane = reinterpret_cast<uint64_t>(nbr + col_l);  // slot 0's entry
   const uint64_t none_lane = reinterpret_cast<uint64_t>(no_row);
   auto lane_select = [](uint64_t m, uint64_t a, uint64_t b) {
-    const uint32_t lo = select_lanes(m, static_cast<uint32_t>(a), static_cast<uint32_t>(b));
-    const uint32_t hi = select_lanes(m, static_cast<uint32_t>(a >> 32), static_cast<uint32_t>(b >> 32));
-    return reinterpret_cast<const char*>((static_cast<uint64_t>(hi) << 32) | lo);
+    return reinterpret_cast<const char*>(select_lanes64(m, a, b));
   };
   auto dma_entries = [&](int P, int k) {  // slot k's entries of the wave's rows into buffer P
     const uint64_t a = entry_lane + static_cast<uint64_t>(k) * static_cast<uint64_t>(n_out) * 4u;
@@ -1236,8 +1234,8 @@ __global__ void __launch_bounds__(256, 2) conv_split_kernel(
   const int nbt_all = c_out / 32;
   uint64_t zero_addr = reinterpret_cast<uint64_t>(g_zero_row);
   asm volatile("" : "+s"(zero_addr));
-  const uint4* zero_row =
-      (const uint4*)reinterpret_cast<const __attribute__((address_space(1))) uint4*>(zero_addr);
+  const uint64_t feat_addr = reinterpret_cast<uint64_t>(feat);
+  const uint32_t row_bytes = static_cast<uint32_t>(c_in) * static_cast<uint32_t>(sizeof(T));
 
   f32x16 acc[2][NB];
 #pragma unroll
@@ -1271,12 +1269,12 @@ __global__ void __launch_bounds__(256, 2) conv_split_kernel(
     const int32_t j1 = live ? e1 : -1;
     const int coff = c * CK + h * (CK / 2);
     const bool pad = coff >= c_in;  // the upper half of a half-filled last chunk
-    const uint4* p0 = j0 >= 0 && !pad
-                          ? reinterpret_cast<const uint4*>(feat + (int64_t)j0 * c_in + coff)
-                          : zero_row;
-    const uint4* p1 = j1 >= 0 && !pad
-                          ? reinterpret_cast<const uint4*>(feat + (int64_t)j1 * c_in + coff)
-                          : zero_row;
+    // one 64-bit multiply-add per row, the zero row by a lane-mask select
+    const uint64_t base = feat_addr + static_cast<uint64_t>(coff) * sizeof(T);
+    const uint64_t a0 = static_cast<uint64_t>(static_cast<uint32_t>(j0)) * static_cast<uint64_t>(row_bytes) + base;
+    const uint64_t a1 = static_cast<uint64_t>(static_cast<uint32_t>(j1)) * static_cast<uint64_t>(row_bytes) + base;
+    const uint4* p0 = global_ptr<uint4>(select_lanes64(__ballot(j0 >= 0 && !pad), a0, zero_addr));
+    const uint4* p1 = global_ptr<uint4>(select_lanes64(__ballot(j1 >= 0 && !pad), a1, zero_addr));
 #pragma unroll
     for (int u = 0; u < UB; ++u) {
       ring[S][0][u] = p0[u];
