@@ -401,7 +401,10 @@ def test_dma_kernels_own_m0(tmp_path):
     direct-to-LDS load, without telling the compiler; that is sound only while
     nothing else in those kernels uses M0.  The gfx950 assembly of every
     instantiation, built with the library's own flags, must show each
-    global_load_lds right after its own M0 write and no other M0 user."""
+    global_load_lds right after its own M0 write and no other M0 user.  No
+    global_load_lds may carry an immediate offset either: the offset moves
+    the LDS destination as well as the global address, so a load meant for
+    the next 64 bytes of a row lands 64 bytes past its slot."""
     import subprocess
 
     from trispconv_amd import build as B
@@ -424,6 +427,7 @@ def test_dma_kernels_own_m0(tmp_path):
             if ln.startswith("global_load_lds"):
                 n_dma += 1
                 assert lines[i - 1].startswith("s_mov_b32 m0,"), (name, lines[i - 1], ln)
+                assert "offset" not in ln, (name, ln)
             elif re.search(r"\bm0\b", ln):
                 assert ln.startswith("s_mov_b32 m0,") and lines[i + 1].startswith("global_load_lds"), \
                     (name, ln)
